@@ -1,0 +1,201 @@
+/*
+ * suffixgpu_amd -- C ABI of the MI355X (gfx950) SuffixGPU drafter kernels.
+ *
+ * Every entry point takes device pointers, plain integer sizes and a
+ * hipStream_t, enqueues work on that stream and returns without waiting.
+ * None of them allocates device or host memory, synchronises, or keeps
+ * state between calls: scratch memory is a caller-provided workspace whose
+ * size the matching *_workspace_size() function reports.  Workspaces of the
+ * fused step must be zero-filled once when allocated; the kernels leave
+ * them zeroed again at the end of every call.
+ *
+ * Return value: 0 on success, SFX_EINVAL (-1) for an argument the kernels
+ * cannot accept (reported before anything is enqueued), otherwise the
+ * hipError_t of the failing launch.
+ *
+ * Token contract (as in the reference): buffer tokens are int32 in
+ * [0, INT32_MAX).  -1 pads, -2 (SEP) separates documents in the global
+ * corpus, INT32_MAX (PAD) fills the corpus past its end.
+ */
+#ifndef SUFFIXGPU_AMD_H
+#define SUFFIXGPU_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SFX_EINVAL (-1)
+#define SFX_MAX_CANDIDATES 32
+#define SFX_ABI_VERSION 1
+
+/* Drafter configuration shared by the local and global paths.
+ * Mirrors the constructor arguments of SuffixGPUDrafter
+ * (suffix_gpu/proposer.py:33-108) and LocalMatchKernel
+ * (suffix_gpu/local_matcher.py:52-74). */
+typedef struct sfx_params {
+    int32_t k;               /* draft length K = chain depth              */
+    int32_t max_pattern_len; /* P (<= 255)                               */
+    int32_t max_occurrences; /* R (<= 2048)                              */
+    int32_t min_match_len;   /* already max(1, min_match_len)            */
+    int32_t num_thresholds;  /* C_l: local support thresholds            */
+    int32_t num_caps;        /* C_g: global length caps (0: local only)  */
+    int32_t has_spec_factor; /* 0: emission cap = k                      */
+    float spec_factor;       /* max_spec_factor (as fp32)                */
+    float spec_offset;       /* max_spec_offset (as fp32)                */
+    float min_token_prob;    /* as fp32                                  */
+    float alpha;             /* vote_smoothing_alpha (as fp32)           */
+    int32_t thresholds[SFX_MAX_CANDIDATES]; /* local support thresholds */
+    int32_t caps[SFX_MAX_CANDIDATES];       /* global caps, descending  */
+} sfx_params;
+
+/* Global index buffers (suffix_gpu/global_index.py:63-74). */
+typedef struct sfx_index {
+    const int32_t* corpus;    /* [capacity] PAD-filled ring               */
+    const int32_t* sa;        /* [capacity] suffix array of corpus        */
+    int64_t capacity;         /* N                                        */
+    const int32_t* delta;     /* [delta_capacity] append-only delta       */
+    int64_t delta_capacity;   /* D                                        */
+    const int64_t* delta_len; /* device scalar: committed delta length    */
+} sfx_index;
+
+/* One decode step's batch (suffix_gpu/proposer.py:135-214).
+ * sampled == NULL means propose() without a state update; then `mask`
+ * (optional bool [B]) selects the drafting rows. */
+typedef struct sfx_batch {
+    int32_t* tokens;          /* [B,S] resident token rows (updated)      */
+    int64_t batch;            /* B                                        */
+    int64_t seq;              /* S                                        */
+    const void* num_tokens;   /* [B] committed counts, int32 or int64     */
+    int32_t num_tokens_is64;
+    const int32_t* sampled;   /* [B,T] last step's ids, -1 padded, or NULL */
+    int64_t num_sampled;      /* T                                        */
+    const void* valid_count;  /* [B] optional count, int32 or int64       */
+    int32_t valid_count_is64;
+    const uint8_t* mask;      /* [B] optional rows allowed to draft       */
+    int64_t limit;            /* length limit: S or min(max_model_len, S) */
+} sfx_batch;
+
+int sfx_abi_version(void);
+
+/* ---- reference operator boundary (suffix_gpu/triton_kernels.py) ------- */
+
+/* triton_kernels.py:392-402 scatter_append + proposer.py:162-184:
+ * tokens[b, base+j] = sampled[b, j] for j < cnt, sampled != -1, base+j < S;
+ * new_counts[b] = base + cnt (cnt = #(sampled != -1) when valid_count is
+ * NULL).  new_counts may be NULL. */
+int sfx_scatter_append(const sfx_batch* batch, int32_t* new_counts,
+                       hipStream_t stream);
+
+/* triton_kernels.py:259-281 match_back: out[b,i] = number of leading t < P
+ * with x(i-1-t) == pat[b,t], x(j) = src[b*row_stride + j] (j >= 0) else -1.
+ * row_stride 0 shares one 1-D source (the delta). */
+int sfx_match_back(const int32_t* src, int64_t row_stride,
+                   const int32_t* pat, int64_t batch, int64_t pattern_len,
+                   int64_t n_out, int32_t* out, hipStream_t stream);
+
+/* triton_kernels.py:362-389 first_occurrences: the first R ascending
+ * columns with mb[b, i] >= thr[b*C + c] (thr > 0), zero padded; count
+ * clamped to R. */
+int sfx_first_occurrences(const int32_t* mb, int64_t n_cols,
+                          const int64_t* thr, int64_t rows, int64_t per_row,
+                          int64_t max_occ, int64_t* pos, int64_t* count,
+                          hipStream_t stream);
+
+/* triton_kernels.py:284-302 sa_search / sa_search.py:66-107: exact lower
+ * and upper bounds of each pattern (row-major [B, M], plen[b] valid) among
+ * the suffixes listed by sa; a corpus read at or past n compares as -1. */
+int sfx_sa_search(const int32_t* sa, const int32_t* corpus, int64_t n,
+                  const int32_t* pattern, int64_t batch, int64_t width,
+                  const int64_t* plen, int64_t* lower, int64_t* upper,
+                  hipStream_t stream);
+
+/* triton_kernels.py:305-338 expand_chain / expand.py:59-147: depth-wise
+ * majority vote with fp32 chain-probability scoring.  weights may be NULL
+ * (unit votes); cap may be NULL (cap = K). */
+int sfx_expand_chain(const int32_t* cont, int64_t rows, int64_t max_occ,
+                     int64_t k, const int64_t* num_occ, const int64_t* cap,
+                     const float* weights, float min_token_prob, float alpha,
+                     int32_t* chain, int64_t* num_valid, int64_t* num_emit,
+                     float* score, hipStream_t stream);
+
+/* ---- local path (suffix_gpu/local_matcher.py) ------------------------- */
+
+/* local_matcher.py:83-196 gather_candidates: cand [B,C_l] i64,
+ * cont [B,C_l,R,K] i32, occ [B,C_l] i64.  Any output may be NULL. */
+int sfx_local_gather(const sfx_params* p, const sfx_batch* batch,
+                     int64_t* cand, int32_t* cont, int64_t* occ,
+                     hipStream_t stream);
+
+/* local_matcher.py:198-242 forward: draft [B,K] i32 (padded past the
+ * emission count), num_valid [B] i32, match_len [B] i64, occ [B] i64,
+ * score [B] f32.  Outputs other than draft/num_valid may be NULL. */
+int sfx_local_forward(const sfx_params* p, const sfx_batch* batch,
+                      int32_t* draft, int32_t* num_valid, int64_t* match_len,
+                      int64_t* occ, float* score, hipStream_t stream);
+
+/* ---- global path (suffix_gpu/global_index.py, sa_search.py) ----------- */
+
+/* Queries are newest-last tails: query [B,Q] i32 with qlen [B] i64
+ * (global_index.py:286-370 _query_backoff, :465-546 _delta_match_backoff,
+ * sa_search.py:110-163 suffix_match_backoff, global_index.py:372-441
+ * draft).  Every output may be NULL:
+ *   sa_len/sa_start/sa_end  [B,C_g] i64  suffix_match_backoff
+ *   d_len/d_pos/d_cnt       [B,C_g] i64, [B,C_g,R] i64, [B,C_g] i64
+ *   len/cont/occ            [B,C_g] i64, [B,C_g,R,K] i32, [B,C_g] i64
+ *   draft/emit/dlen/docc/dscore  best-cap draft: [B,K] i32, [B] i64 x3,
+ *                                [B] f32
+ * workspace: sfx_global_query_workspace_size() bytes, zero-filled once. */
+typedef struct sfx_global_out {
+    int64_t* sa_len; int64_t* sa_start; int64_t* sa_end;
+    int64_t* d_len; int64_t* d_pos; int64_t* d_cnt;
+    int64_t* len; int32_t* cont; int64_t* occ;
+    int32_t* draft; int64_t* emit; int64_t* draft_len; int64_t* draft_occ;
+    float* draft_score;
+} sfx_global_out;
+
+size_t sfx_global_query_workspace_size(const sfx_params* p, int64_t batch);
+int sfx_global_query(const sfx_params* p, const sfx_index* index,
+                     const int32_t* query, int64_t batch, int64_t width,
+                     const int64_t* qlen, const sfx_global_out* out,
+                     void* workspace, size_t workspace_bytes,
+                     hipStream_t stream);
+
+/* ---- fused decode step (suffix_gpu/proposer.py:186-327) --------------- */
+
+/* propose_with_update (batch->sampled != NULL) or propose (== NULL).
+ * Local-only when index == NULL.  With an index the step is two kernels:
+ * the local kernel goes on `stream`, the global kernel on `side_stream`
+ * (which may equal `stream`); the caller orders side_stream after prior
+ * work on stream and joins it back.  The two kernels hand results over
+ * through the workspace; whichever finishes a row last writes that row's
+ * draft [B,K] i32 and num_valid [B] i32.  new_counts [B] i32 may be NULL.
+ * workspace: sfx_step_workspace_size() bytes, zero-filled once. */
+size_t sfx_step_workspace_size(const sfx_params* p, int64_t batch);
+int sfx_propose_step(const sfx_params* p, const sfx_index* index,
+                     const sfx_batch* batch, int32_t* draft,
+                     int32_t* num_valid, int32_t* new_counts,
+                     void* workspace, size_t workspace_bytes,
+                     hipStream_t stream, hipStream_t side_stream);
+
+/* ---- suffix-array rebuild (suffix_gpu/suffix_array.py:15-63,
+ *      global_index.py:217-223) ------------------------------------------ */
+
+/* sa[0:m] = suffix array of text[0:m] (signed int32 order, a proper prefix
+ * first); sa[m:n_total] = m .. n_total-1.  Prefix doubling with LSD radix
+ * sorts; rounds stop on the device once every rank is distinct, with no
+ * host synchronisation.  sa_is64 selects int64 output. */
+size_t sfx_sa_build_workspace_size(int64_t m);
+int sfx_sa_build(const int32_t* text, int64_t m, int64_t n_total, void* sa,
+                 int32_t sa_is64, void* workspace, size_t workspace_bytes,
+                 hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SUFFIXGPU_AMD_H */

@@ -74,7 +74,8 @@ def expand_chain(cont: np.ndarray, num_occ: np.ndarray, k: int,
         else:
             denom = np.where(act, weights.astype(F32), F32(0)).sum(
                 axis=1, dtype=F32)
-        cum = (cum * (cnt.astype(F32) / (denom + alpha32))).astype(F32)
+        with np.errstate(invalid="ignore", divide="ignore"):
+            cum = (cum * (cnt.astype(F32) / (denom + alpha32))).astype(F32)
         valid = (tok != sentinel) & (cnt > 0) & (cum >= minp)
         chain[:, d] = np.where(valid, tok, chain[:, d])
         score = (score + np.where(valid & (cap > d), cum, F32(0))).astype(F32)

@@ -1,0 +1,115 @@
+// Suffix-array interval search by a group of G lanes (k-ary search).
+//
+// The reference resolves each bound with ceil(log2(n+1)) dependent binary
+// probes (suffix_gpu/sa_search.py:66-107).  Here G lanes probe G ranks of
+// the current range at once, so one round trip to the SA and corpus cuts
+// the range (G+1)-fold; lower and upper bound share their probes until
+// their ranges separate, then each gets G/2 lanes.  Only the exact bounds
+// are returned, which is all the reference's result depends on.
+#pragma once
+
+#include "sfx_common.h"
+
+namespace sfx {
+
+// -1 / 0 / +1: suffix at sa[rank] < pattern / starts with it / > pattern.
+// Corpus reads at or past n compare as -1 (sa_search.py:25-63).
+template <class PatFn>
+__device__ __forceinline__ int cmp_suffix(const int32_t* __restrict__ sa,
+                                          const int32_t* __restrict__ corpus,
+                                          int64_t n, int64_t rank,
+                                          PatFn pat_at, int plen) {
+  const int64_t pos = sa[rank];
+  for (int j0 = 0; j0 < plen; j0 += 4) {
+    int32_t t[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int64_t idx = pos + j0 + u;
+      t[u] = idx < n ? corpus[idx > 0 ? idx : 0] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = j0 + u;
+      if (j >= plen) return 0;
+      const int32_t pj = pat_at(j);
+      if (t[u] != pj) return t[u] < pj ? -1 : 1;
+    }
+  }
+  return 0;
+}
+
+__device__ __forceinline__ int64_t kary_probe(int64_t lo, int64_t hi,
+                                              int k, int np) {
+  return lo + ((hi - lo) * (int64_t)(k + 1)) / (np + 1);
+}
+
+// Narrow [lo, hi] (answer inside; ranks < lo false, >= hi true) with the
+// predicate bits of np probes (bit k = probe k true).
+__device__ __forceinline__ void kary_update(int64_t& lo, int64_t& hi,
+                                            int np, uint32_t bits) {
+  if (bits == 0) {
+    lo = kary_probe(lo, hi, np - 1, np) + 1;
+    return;
+  }
+  const int k = __builtin_ctz(bits);
+  const int64_t nh = kary_probe(lo, hi, k, np);
+  if (k > 0) lo = kary_probe(lo, hi, k - 1, np) + 1;
+  hi = nh;
+}
+
+// Exact lower bound (first rank with cmp >= 0) and upper bound (first rank
+// with cmp > 0) of one pattern.  Called by all G lanes of an aligned group
+// with identical arguments; returns the bounds on every lane of the group.
+template <int G, class PatFn>
+__device__ void kary_bounds(const int32_t* __restrict__ sa,
+                            const int32_t* __restrict__ corpus, int64_t n,
+                            PatFn pat_at, int plen, int64_t& lower,
+                            int64_t& upper) {
+  static_assert(G >= 2 && G <= 32 && (64 % G) == 0, "group size");
+  const int ln = lane_id();
+  const int gl = ln % G;
+  const int gbase = ln - gl;
+  int64_t lo1 = 0, hi1 = n, lo2 = 0, hi2 = n;
+  while (lo1 < hi1 || lo2 < hi2) {
+    const bool shared = lo1 == lo2 && hi1 == hi2;
+    const bool only1 = !shared && lo2 == hi2;
+    const bool only2 = !shared && lo1 == hi1;
+    int64_t lo, hi;
+    int np, k;
+    bool upper_half = false;
+    if (shared || only1) {
+      lo = lo1; hi = hi1; np = G; k = gl;
+    } else if (only2) {
+      lo = lo2; hi = hi2; np = G; k = gl;
+    } else {
+      np = G / 2;
+      upper_half = gl >= np;
+      k = upper_half ? gl - np : gl;
+      lo = upper_half ? lo2 : lo1;
+      hi = upper_half ? hi2 : hi1;
+    }
+    const int64_t probe = kary_probe(lo, hi, k, np);
+    const int c = cmp_suffix(sa, corpus, n, probe, pat_at, plen);
+    const uint64_t m1 = ballot(c >= 0);
+    const uint64_t m2 = ballot(c > 0);
+    const uint32_t full = G == 32 ? 0xffffffffu : ((1u << G) - 1u);
+    const uint32_t g1 = (uint32_t)(m1 >> gbase) & full;
+    const uint32_t g2 = (uint32_t)(m2 >> gbase) & full;
+    if (shared) {
+      kary_update(lo1, hi1, G, g1);
+      kary_update(lo2, hi2, G, g2);
+    } else if (only1) {
+      kary_update(lo1, hi1, G, g1);
+    } else if (only2) {
+      kary_update(lo2, hi2, G, g2);
+    } else {
+      const uint32_t half = (1u << (G / 2)) - 1u;
+      kary_update(lo1, hi1, G / 2, g1 & half);
+      kary_update(lo2, hi2, G / 2, (g2 >> (G / 2)) & half);
+    }
+  }
+  lower = lo1;
+  upper = lo2;
+}
+
+}  // namespace sfx

@@ -1,0 +1,73 @@
+"""Frequency-ranked chain expansion (public helper API).
+
+Mirrors suffix_gpu/expand.py:16-147.  Both functions run the wave-level
+majority-vote kernel of libsuffixgpu_amd.so: per depth the most voted
+continuation token wins (ties to the smallest id), the chain probability is
+multiplied by votes / (active + alpha) in fp32, and the chain stops once it
+falls below ``min_token_prob``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from suffixgpu_amd import kernels
+from suffixgpu_amd._lib import require_gpu
+
+
+def _majority_token(values: torch.Tensor, active: torch.Tensor,
+                    sentinel: int, weights: torch.Tensor | None = None,
+                    ) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row majority token among active entries (expand.py:16-56).
+
+    Returns (token [B], count [B]); rows without an active entry get
+    (sentinel, 0).  Runs as a one-depth chain expansion.
+    """
+    require_gpu(values, active, weights)
+    b, r = values.shape
+    if (values[active] == -1).any().item() if values.numel() else False:
+        raise ValueError("_majority_token: -1 is reserved for inactive slots")
+    cont = torch.where(active, values.to(torch.int32),
+                       torch.full_like(values, -1, dtype=torch.int32))
+    occ = torch.full((b,), r, dtype=torch.int64, device=values.device)
+    cap = torch.ones(b, dtype=torch.int64, device=values.device)
+    chain, nv, _, score = kernels.expand_chain(
+        cont.unsqueeze(2).contiguous(), occ, 1, 0.0, cap, weights=weights)
+    act_n = active.sum(dim=1)
+    if weights is None:
+        count = torch.where(nv > 0,
+                            torch.round(score * act_n.clamp(min=1)).to(
+                                torch.int64),
+                            torch.zeros_like(nv))
+    else:
+        w = torch.where(active, weights.to(torch.float32),
+                        torch.zeros_like(weights, dtype=torch.float32))
+        eq = cont == chain[:, :1]
+        count = torch.where(nv > 0, (w * eq).sum(dim=1),
+                            torch.zeros(b, device=values.device))
+    token = torch.where(nv > 0, chain[:, 0].to(values.dtype),
+                        torch.full_like(chain[:, 0], sentinel).to(
+                            values.dtype))
+    return token, count
+
+
+def expand_chain(cont: torch.Tensor, num_occ: torch.Tensor, k: int,
+                 sentinel: int = -1, min_token_prob: float = 0.0,
+                 cap: torch.Tensor | None = None,
+                 weights: torch.Tensor | None = None, alpha: float = 0.0,
+                 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                            torch.Tensor]:
+    """Majority-vote chain expansion with fused scoring (expand.py:59-147).
+
+    Returns (chain [B, k] int32, num_valid [B] i64, num_emit [B] i64,
+    score [B] f32).  ``sentinel`` must be -1 (the padding value of every
+    continuation block in the drafter).
+    """
+    if sentinel != -1:
+        raise ValueError("expand_chain: only sentinel -1 is supported")
+    require_gpu(cont, num_occ, cap, weights)
+    b = cont.shape[0]
+    if cap is None:
+        cap = torch.full((b,), k, dtype=torch.int64, device=cont.device)
+    return kernels.expand_chain(cont, num_occ, k, min_token_prob, cap,
+                                weights=weights, alpha=alpha)

@@ -1,0 +1,394 @@
+"""Cross-request global memory: suffix array over finished responses.
+
+Mirrors suffix_gpu/global_index.py:34-553: a PAD-filled corpus ring of
+``capacity`` int32 tokens with its suffix array (immutable between
+rebuilds), an append-only delta of ``delta_capacity`` tokens whose
+documents end with SEP, and a double-buffered rebuild: eviction-trimmed
+active corpus + whole-document delta snapshot go to the staging buffers,
+the delta is compacted at launch, the staging suffix array is built on the
+rebuild stream (csrc/sa_build.hip, no host synchronisation), and
+``poll_rebuild`` swaps it in with in-place copies so captured graphs keep
+their tensor identities.
+
+Host bookkeeping (document lengths, eviction and snapshot arithmetic) is
+plain Python exactly as in the reference; every device operation is a
+stream-ordered copy/fill or a libsuffixgpu_amd kernel.  Queries run the
+fused SA-search + delta-scan + merge kernel (csrc/global.hip).
+"""
+
+from __future__ import annotations
+
+from collections import deque
+
+import torch
+
+from suffixgpu_amd import _lib
+from suffixgpu_amd._lib import check, lib, require_gpu, stream_of
+from suffixgpu_amd.expand import expand_chain
+from suffixgpu_amd.suffix_array import sa_workspace_bytes
+
+PAD_TOKEN = torch.iinfo(torch.int32).max
+# Written between documents; negative, so no query token (>= 0) can match
+# it and neither matches nor continuations cross document boundaries.
+SEP_TOKEN = -2
+
+
+class GlobalIndex:
+    """GPU-resident global suffix index with periodic rebuilds."""
+
+    def __init__(self, capacity: int, delta_capacity: int, k: int,
+                 max_occurrences: int = 32,
+                 rebuild_threshold: int | None = None,
+                 device: torch.device | str = "cuda",
+                 rebuild_stream: torch.cuda.Stream | None = None):
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise _lib.SuffixGPUError(
+                "GlobalIndex needs a ROCm GPU device; there is no CPU path")
+        if not 1 <= capacity <= 2 ** 31 - 1:
+            raise ValueError("capacity must be in [1, 2^31)")
+        if not 1 <= delta_capacity <= 2 ** 31 - 1:
+            raise ValueError("delta_capacity must be in [1, 2^31)")
+        self.capacity = capacity
+        self.delta_capacity = delta_capacity
+        self.k = k
+        self.max_occurrences = max_occurrences
+        self.rebuild_threshold = rebuild_threshold or max(
+            1, delta_capacity // 2)
+        self.rebuild_stream = rebuild_stream
+        # True: poll_rebuild waits for an in-flight build (deterministic
+        # swap points); False (default, as the reference): event.query().
+        self.blocking_poll = False
+
+        dev = self.device
+        self.corpus = torch.full((capacity,), PAD_TOKEN, dtype=torch.int32,
+                                 device=dev)
+        self.staging_corpus = self.corpus.clone()
+        self.sa = torch.arange(capacity, dtype=torch.int32, device=dev)
+        self.staging_sa = self.sa.clone()
+        self.delta = torch.zeros(delta_capacity, dtype=torch.int32,
+                                 device=dev)
+        self.delta_len_t = torch.zeros((), dtype=torch.int64, device=dev)
+        self._sa_ws: torch.Tensor | None = None
+        self._query_ws: dict = {}
+
+        self.active_len = 0
+        self.delta_len = 0
+        self.active_doc_lens: deque[int] = deque()
+        self.delta_doc_lens: list[int] = []
+        self._rebuild_event = None
+        self._pending = None
+
+    # ------------------------------------------------------------------
+    # device views
+    # ------------------------------------------------------------------
+    def index_struct(self) -> _lib.SfxIndex:
+        return _lib.SfxIndex(self.corpus.data_ptr(), self.sa.data_ptr(),
+                             self.capacity, self.delta.data_ptr(),
+                             self.delta_capacity,
+                             self.delta_len_t.data_ptr())
+
+    # ------------------------------------------------------------------
+    # writes (global_index.py:86-133)
+    # ------------------------------------------------------------------
+    def append_documents(self, docs: list[torch.Tensor]) -> None:
+        """Append token tensors to the delta, each followed by SEP_TOKEN.
+
+        Recorded doc lengths include the separator.
+        """
+        for doc in docs:
+            doc = doc.to(self.device).to(torch.int32).reshape(-1)
+            n = doc.shape[0]
+            if n == 0:
+                continue
+            if n + 1 > self.delta_capacity:
+                doc = doc[-(self.delta_capacity - 1):]
+                n = doc.shape[0]
+            if self.delta_len + n + 1 > self.delta_capacity:
+                self._make_room(n + 1)
+            self.delta[self.delta_len:self.delta_len + n].copy_(doc)
+            self.delta[self.delta_len + n] = SEP_TOKEN
+            self.delta_len += n + 1
+            self.delta_len_t.fill_(self.delta_len)
+            self.delta_doc_lens.append(n + 1)
+        self.maybe_rebuild()
+
+    def _make_room(self, needed: int) -> None:
+        self.poll_rebuild()
+        if self._rebuild_event is None:
+            self._launch_rebuild()
+        if self.delta_len + needed <= self.delta_capacity:
+            return
+        # A rebuild is in flight (staging buffers busy): drop oldest docs.
+        self._drop_oldest_docs(
+            self.delta_len + needed - self.delta_capacity)
+
+    def _drop_oldest_docs(self, drop: int) -> None:
+        acc = 0
+        dropped = 0
+        for ln in self.delta_doc_lens:
+            if acc >= drop:
+                break
+            acc += ln
+            dropped += 1
+        remaining = self.delta_len - acc
+        if remaining > 0:
+            self.delta[:remaining] = self.delta[acc:self.delta_len].clone()
+        self.delta_len = remaining
+        self.delta_len_t.fill_(remaining)
+        self.delta_doc_lens = self.delta_doc_lens[dropped:]
+
+    # ------------------------------------------------------------------
+    # rebuild (global_index.py:138-252)
+    # ------------------------------------------------------------------
+    def maybe_rebuild(self) -> None:
+        """Kick off a rebuild when the delta grew past the threshold."""
+        self.poll_rebuild()
+        if self._rebuild_event is not None or self.delta_len == 0:
+            return
+        if self.delta_len < self.rebuild_threshold:
+            return
+        self._launch_rebuild()
+
+    def _plan_rebuild(self) -> tuple[int, int, int, int]:
+        """(keep_start, n_active_keep, snap, n_new): evict oldest whole
+        docs until the snapshot fits, round the delta snapshot down to
+        whole docs (global_index.py:150-167)."""
+        keep_start = 0
+        for ln in self.active_doc_lens:
+            if self.active_len - keep_start + self.delta_len \
+                    <= self.capacity:
+                break
+            keep_start += ln
+        n_keep = self.active_len - keep_start
+        snap = min(self.delta_len, self.capacity - n_keep)
+        acc = 0
+        for ln in self.delta_doc_lens:
+            if acc + ln <= snap:
+                acc += ln
+            else:
+                break
+        return keep_start, n_keep, acc, n_keep + acc
+
+    def _launch_rebuild(self) -> None:
+        if self._rebuild_event is not None:
+            return
+        keep_start, n_keep, snap, n_new = self._plan_rebuild()
+        if n_new == 0:
+            return
+        dst = self.staging_corpus
+        dst.fill_(PAD_TOKEN)
+        if n_keep > 0:
+            dst[:n_keep].copy_(self.corpus[keep_start:self.active_len])
+        if snap > 0:
+            dst[n_keep:n_new].copy_(self.delta[:snap])
+
+        new_doc_lens: deque[int] = deque()
+        acc = 0
+        for ln in self.active_doc_lens:
+            acc += ln
+            if acc > keep_start:
+                new_doc_lens.append(ln)
+        acc = 0
+        for ln in self.delta_doc_lens:
+            acc += ln
+            if acc <= snap:
+                new_doc_lens.append(ln)
+
+        # Staging owns a copy of the snapshot: compact it out of the delta
+        # now so appends always see the full capacity.
+        absorbed = self._count_docs_within(snap)
+        remaining = self.delta_len - snap
+        if remaining > 0:
+            self.delta[:remaining] = self.delta[snap:self.delta_len].clone()
+        self.delta_len = remaining
+        self.delta_len_t.fill_(remaining)
+        self.delta_doc_lens = self.delta_doc_lens[absorbed:]
+
+        # Real prefix plus one PAD sentinel column, so build-time suffix
+        # order equals query-time comparison order.
+        m = min(n_new + 1, self.capacity)
+        if self.rebuild_stream is not None:
+            self.rebuild_stream.wait_stream(
+                torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(self.rebuild_stream):
+                self._build_staging_sa(dst, m)
+            event = torch.cuda.Event()
+            event.record(self.rebuild_stream)
+            self._pending = (n_new, new_doc_lens)
+            self._rebuild_event = event
+        else:
+            self._build_staging_sa(dst, m)
+            self._finish_swap(n_new, new_doc_lens)
+
+    def _build_staging_sa(self, dst: torch.Tensor, m: int) -> None:
+        """staging_sa[:m] = SA(dst[:m]); staging_sa[m:] = m .. N-1."""
+        need = sa_workspace_bytes(self.capacity)
+        if self._sa_ws is None or self._sa_ws.numel() < need:
+            self._sa_ws = torch.empty(max(need, 1), dtype=torch.uint8,
+                                      device=self.device)
+        check(lib().sfx_sa_build(dst.data_ptr(), m, self.capacity,
+                                 self.staging_sa.data_ptr(), 0,
+                                 self._sa_ws.data_ptr(), self._sa_ws.numel(),
+                                 stream_of(self.device)), "SA rebuild")
+
+    def _count_docs_within(self, tokens: int) -> int:
+        acc = 0
+        count = 0
+        for ln in self.delta_doc_lens:
+            acc += ln
+            if acc > tokens:
+                break
+            count += 1
+        return count
+
+    def _finish_swap(self, n_new: int, new_doc_lens: deque[int]) -> None:
+        # In-place copies: captured graphs bind the active tensors' storage.
+        self.corpus.copy_(self.staging_corpus)
+        self.sa.copy_(self.staging_sa)
+        self.active_len = n_new
+        self.active_doc_lens = new_doc_lens
+        self._rebuild_event = None
+        self._pending = None
+
+    def poll_rebuild(self) -> None:
+        """Swap in a finished background rebuild."""
+        ev = self._rebuild_event
+        if ev is None:
+            return
+        if self.blocking_poll and hasattr(ev, "synchronize"):
+            ev.synchronize()
+            done = True
+        else:
+            done = ev.query()
+        if done:
+            n_new, new_doc_lens = self._pending
+            self._finish_swap(n_new, new_doc_lens)
+
+    def load_documents(self, docs: list[torch.Tensor]) -> None:
+        """Make ``docs`` (oldest first) the active corpus in one rebuild.
+
+        The state equals what a rebuild whose active set is exactly these
+        documents leaves behind: corpus = docs each + SEP, then PAD; SA
+        over the first min(n + 1, capacity) positions.  The delta is left
+        untouched.  Synchronous on the current stream.
+        """
+        if self._rebuild_event is not None:
+            raise RuntimeError("load_documents: a rebuild is in flight")
+        lens = [int(d.numel()) + 1 for d in docs]
+        n = sum(lens)
+        if n > self.capacity:
+            raise ValueError("load_documents: documents exceed capacity")
+        dst = self.staging_corpus
+        dst.fill_(PAD_TOKEN)
+        off = 0
+        for d in docs:
+            d = d.to(self.device).to(torch.int32).reshape(-1)
+            dst[off:off + d.shape[0]].copy_(d)
+            dst[off + d.shape[0]] = SEP_TOKEN
+            off += d.shape[0] + 1
+        self._build_staging_sa(dst, min(n + 1, self.capacity))
+        self._finish_swap(n, deque(lens))
+
+    # ------------------------------------------------------------------
+    # queries (global_index.py:257-553)
+    # ------------------------------------------------------------------
+    def _run_query(self, query, query_len, max_len, caps, *, want,
+                   k=None, min_token_prob=0.0, max_spec_factor=None,
+                   max_spec_offset=0.0, alpha=0.0):
+        require_gpu(query, query_len)
+        b = query.shape[0]
+        dev = self.device
+        caps_l = ([int(x) for x in caps.tolist()]
+                  if isinstance(caps, torch.Tensor) else list(caps))
+        cnum = len(caps_l)
+        r = self.max_occurrences
+        kk = self.k if k is None else k
+        p = _lib.make_params(kk, max_len, r, 1, (1,), caps_l,
+                             max_spec_factor, max_spec_offset,
+                             min_token_prob, alpha)
+        q = query.to(torch.int32).contiguous()
+        ql = query_len.to(torch.int64).contiguous()
+        out = _lib.SfxGlobalOut()
+        res = {}
+
+        def alloc(name, shape, dtype):
+            t = torch.empty(*shape, dtype=dtype, device=dev)
+            setattr(out, name, t.data_ptr())
+            res[name] = t
+
+        shapes = {
+            "sa_len": ((b, cnum), torch.int64),
+            "sa_start": ((b, cnum), torch.int64),
+            "sa_end": ((b, cnum), torch.int64),
+            "d_len": ((b, cnum), torch.int64),
+            "d_pos": ((b, cnum, r), torch.int64),
+            "d_cnt": ((b, cnum), torch.int64),
+            "len": ((b, cnum), torch.int64),
+            "cont": ((b, cnum, r, kk), torch.int32),
+            "occ": ((b, cnum), torch.int64),
+            "draft": ((b, kk), torch.int32),
+            "emit": ((b,), torch.int64),
+            "draft_len": ((b,), torch.int64),
+            "draft_occ": ((b,), torch.int64),
+            "draft_score": ((b,), torch.float32),
+        }
+        for name in want:
+            alloc(name, *shapes[name])
+        nbytes = int(lib().sfx_global_query_workspace_size(p, b))
+        ws = self._query_ws.get((b, cnum, kk))
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.zeros(max(1, nbytes), dtype=torch.uint8, device=dev)
+            self._query_ws[(b, cnum, kk)] = ws
+        if b:
+            check(lib().sfx_global_query(p, self.index_struct(),
+                                         q.data_ptr(), b, q.shape[1],
+                                         ql.data_ptr(), out, ws.data_ptr(),
+                                         ws.numel(), stream_of(dev)),
+                  "GlobalIndex query")
+        return res
+
+    def query(self, query: torch.Tensor, query_len: torch.Tensor,
+              max_len: int):
+        """(match_len [B] i64, cont [B, R, k] int32, occ_count [B] i64)."""
+        res = self._run_query(query, query_len, max_len, [max_len],
+                              want=("len", "cont", "occ"))
+        return res["len"][:, 0], res["cont"][:, 0], res["occ"][:, 0]
+
+    def _query_backoff(self, query: torch.Tensor, query_len: torch.Tensor,
+                       max_len: int, caps):
+        """(match_len [B, C] i64, cont [B, C, R, k] int32, occ [B, C] i64)."""
+        res = self._run_query(query, query_len, max_len, caps,
+                              want=("len", "cont", "occ"))
+        return res["len"], res["cont"], res["occ"]
+
+    def _delta_match_backoff(self, query: torch.Tensor,
+                             query_len: torch.Tensor, max_len: int, caps):
+        """(match_len [B, C], starts [B, C, R], count [B, C]) in the delta."""
+        res = self._run_query(query, query_len, max_len, caps,
+                              want=("d_len", "d_pos", "d_cnt"))
+        return res["d_len"], res["d_pos"], res["d_cnt"]
+
+    def draft(self, query: torch.Tensor, query_len: torch.Tensor,
+              max_len: int, k: int, min_token_prob: float = 0.0,
+              max_spec_factor: float | None = None,
+              max_spec_offset: float = 0.0, caps=None, alpha: float = 0.0):
+        """(chain [B, k] int32, num_valid [B] i64, match_len [B] i64,
+        occ_count [B] i64, score [B] f32) of the best-scored cap."""
+        if caps is None:
+            caps = sorted({max_len, max(2, max_len // 2),
+                           max(2, max_len // 4), 2}, reverse=True)
+        res = self._run_query(
+            query, query_len, max_len, caps,
+            want=("draft", "emit", "draft_len", "draft_occ", "draft_score"),
+            k=k, min_token_prob=min_token_prob,
+            max_spec_factor=max_spec_factor,
+            max_spec_offset=max_spec_offset, alpha=alpha)
+        return (res["draft"], res["emit"], res["draft_len"],
+                res["draft_occ"], res["draft_score"])
+
+    def expand(self, cont: torch.Tensor, occ_count: torch.Tensor,
+               min_token_prob: float = 0.0):
+        chain, num_valid, _, _ = expand_chain(
+            cont, occ_count, self.k, min_token_prob=min_token_prob)
+        return chain, num_valid

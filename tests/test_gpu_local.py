@@ -1,0 +1,132 @@
+"""Local matcher on gfx950 vs the oracle (and the reference's goldens)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.drafter import DrafterOracle, backoff_thresholds
+from oracle.local import LocalMatcher
+from suffixgpu_amd import synth
+from tests.conftest import golden
+
+pytestmark = pytest.mark.gpu
+
+I32 = np.int32
+
+
+def T(a, dev, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return t if dtype is None else t.to(dtype)
+
+
+def N(t):
+    return t.cpu().numpy()
+
+
+def _pair(gpu, **kw):
+    from suffixgpu_amd.local_matcher import LocalMatchKernel
+    return LocalMatchKernel(**kw), LocalMatcher(**kw)
+
+
+def _check(gpu, g, o, nt, tok, mask):
+    cand, cont, occ = g.gather_candidates(T(nt, gpu), T(tok, gpu),
+                                          T(mask, gpu))
+    ec, econt, eocc = o.gather_candidates(nt, tok, mask)
+    np.testing.assert_array_equal(N(cand), ec)
+    np.testing.assert_array_equal(N(occ), eocc)
+    np.testing.assert_array_equal(N(cont), econt)
+    fw = g(T(nt, gpu), T(tok, gpu), T(mask, gpu))
+    efw = o.forward(nt, tok, mask)
+    for a, b, name in zip(fw, efw, ("draft", "nv", "len", "occ", "score")):
+        np.testing.assert_array_equal(N(a), b, err_msg=name)
+
+
+def test_local_uniform_golden(gpu):
+    z = golden("local_uniform")
+    from suffixgpu_amd.local_matcher import LocalMatchKernel
+    g = LocalMatchKernel(k=16, max_pattern_len=32, max_occurrences=128,
+                         support_thresholds=(1,))
+    cand, cont, occ = g.gather_candidates(
+        T(z["num_tokens"], gpu), T(z["tokens"], gpu),
+        torch.ones(8, dtype=torch.bool, device=gpu))
+    np.testing.assert_array_equal(N(cand), z["cand"])
+    np.testing.assert_array_equal(N(occ), z["occ"])
+    np.testing.assert_array_equal(N(cont), z["cont"])
+
+
+def test_local_zipf_forward_golden(gpu):
+    z = golden("local_zipf_update")
+    from suffixgpu_amd.local_matcher import LocalMatchKernel
+    g = LocalMatchKernel(k=16, max_pattern_len=32, max_occurrences=128,
+                         max_spec_factor=2.0, min_token_prob=0.1,
+                         support_thresholds=backoff_thresholds(8))
+    fw = g(T(z["new_counts"], gpu), T(z["tokens_after"], gpu),
+           torch.ones(12, dtype=torch.bool, device=gpu))
+    for a, key in zip(fw, ("fw_draft", "fw_nv", "fw_len", "fw_occ",
+                           "fw_score")):
+        np.testing.assert_array_equal(N(a), z[key], err_msg=key)
+
+
+def test_local_ties_golden(gpu):
+    z = golden("local_ties")
+    kw = dict(k=8, max_pattern_len=12, max_occurrences=16,
+              max_spec_factor=0.7, max_spec_offset=0.3, min_token_prob=0.05,
+              support_thresholds=backoff_thresholds(6),
+              vote_smoothing_alpha=0.5)
+    g, o = _pair(gpu, **kw)
+    fw = g(T(z["num_tokens"], gpu), T(z["tokens"], gpu), T(z["mask"], gpu))
+    np.testing.assert_array_equal(N(fw[2]), z["fw_len"])
+    np.testing.assert_array_equal(N(fw[3]), z["fw_occ"])
+    np.testing.assert_array_equal(N(fw[4]), z["fw_score"])
+    _check(gpu, g, o, z["num_tokens"], z["tokens"], z["mask"])
+
+
+@pytest.mark.parametrize("vocab,s,r,p", [(3, 200, 8, 6), (5, 1000, 16, 12),
+                                         (50, 3000, 128, 32),
+                                         (2, 257, 300, 40)])
+def test_local_random(gpu, vocab, s, r, p):
+    rng = np.random.default_rng(vocab * 1000 + s)
+    b = 9
+    tok = rng.integers(0, vocab, size=(b, s)).astype(I32)
+    nt = rng.integers(0, s + 1, size=b).astype(np.int64)
+    nt[0], nt[1], nt[2] = 0, 1, s + 7   # empty, one token, past the buffer
+    mask = rng.random(b) < 0.85
+    g, o = _pair(gpu, k=7, max_pattern_len=p, max_occurrences=r,
+                 max_spec_factor=1.5, max_spec_offset=0.5,
+                 min_token_prob=0.02,
+                 support_thresholds=(1, 2, 3, 8, 64, 1 << 20))
+    _check(gpu, g, o, nt, tok, mask)
+
+
+def test_local_synth_workloads(gpu):
+    for w, nb, f, minp in ((synth.local_uniform(seed=1), 1, None, 0.0),
+                           (synth.local_zipf(seed=2, b=16), 8, 2.0, 0.1)):
+        g, o = _pair(gpu, k=16, max_pattern_len=32, max_occurrences=128,
+                     max_spec_factor=f, min_token_prob=minp,
+                     support_thresholds=backoff_thresholds(nb))
+        _check(gpu, g, o, w.num_tokens, w.tokens,
+               np.ones(w.tokens.shape[0], bool))
+
+
+def test_local_drafter_propose_matches_oracle(gpu):
+    from suffixgpu_amd import SuffixGPUDrafter
+    w = synth.local_zipf(seed=2, b=32, s=8192)
+    kw = dict(k=16, max_pattern_len=32, max_occurrences=128, num_backoff=8,
+              max_spec_factor=2.0, min_token_prob=0.1)
+    d = SuffixGPUDrafter(device=gpu, **kw)
+    o = DrafterOracle(**kw)
+    tg = T(w.tokens, gpu)
+    draft, nv, new = d.propose_with_update(T(w.num_tokens, gpu), tg,
+                                           T(w.sampled, gpu))
+    to = w.tokens.copy()
+    ed, env, enew = o.propose_with_update(w.num_tokens, to, w.sampled)
+    np.testing.assert_array_equal(N(tg), to)
+    np.testing.assert_array_equal(N(new), enew)
+    np.testing.assert_array_equal(N(draft), ed)
+    np.testing.assert_array_equal(N(nv), env)
+    draft, nv = d.propose(new, tg)
+    ed, env = o.propose(enew, to)
+    np.testing.assert_array_equal(N(draft), ed)
+    np.testing.assert_array_equal(N(nv), env)

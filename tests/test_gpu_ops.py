@@ -1,0 +1,195 @@
+"""HIP operators vs the oracle: scatter, match_back, first occurrences,
+SA build and search, majority-vote expansion (bit-exact; weighted-vote
+scores within rtol 1e-4 as in the reference's own test)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import naive
+from oracle.drafter import DrafterOracle
+from oracle.expand import expand_chain as o_expand
+from oracle.local import first_occurrences as o_first_occ
+from oracle.local import match_back as o_match_back
+from oracle.local import newest_first_pattern
+from oracle.sa import build_suffix_array as o_build_sa
+from oracle.sa import search_interval as o_search
+from tests.conftest import golden
+
+pytestmark = pytest.mark.gpu
+
+I32 = np.int32
+
+
+def T(a, dev, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return t if dtype is None else t.to(dtype)
+
+
+def N(t):
+    return t.cpu().numpy()
+
+
+def test_scatter_append(gpu):
+    from suffixgpu_amd import SuffixGPUDrafter
+    rng = np.random.default_rng(0)
+    b, s, t = 33, 64, 9
+    tok = rng.integers(0, 50, size=(b, s)).astype(I32)
+    nt = rng.integers(0, s + 5, size=b).astype(I32)
+    samp = rng.integers(-1, 50, size=(b, t)).astype(I32)
+    samp[3] = -1
+    d = SuffixGPUDrafter(k=4, device=gpu, max_pattern_len=8)
+    o = DrafterOracle(k=4, max_pattern_len=8)
+    for vc in (None, rng.integers(0, t + 1, size=b).astype(np.int64)):
+        tg = T(tok, gpu)
+        new = d.update_state(T(nt, gpu), tg, T(samp, gpu),
+                             None if vc is None else T(vc, gpu))
+        to = tok.copy()
+        exp = o.update_state(nt, to, samp, vc)
+        np.testing.assert_array_equal(N(tg), to)
+        np.testing.assert_array_equal(N(new), exp)
+
+
+def test_match_back_rows_and_shared(gpu):
+    from suffixgpu_amd import kernels
+    rng = np.random.default_rng(1)
+    tok = rng.integers(0, 3, size=(7, 300)).astype(I32)
+    q = rng.integers(0, 320, size=7)
+    pat = newest_first_pattern(tok, q, 12, -2)
+    got = kernels.match_back(T(tok, gpu), T(pat, gpu), 300)
+    np.testing.assert_array_equal(N(got), o_match_back(tok, pat, 300))
+    delta = rng.integers(-2, 3, size=500).astype(I32)
+    got = kernels.match_back(T(delta, gpu), T(pat, gpu), 501)
+    np.testing.assert_array_equal(N(got), o_match_back(delta, pat, 501))
+
+
+def test_first_occurrences(gpu):
+    from suffixgpu_amd import kernels
+    rng = np.random.default_rng(2)
+    mb = rng.integers(0, 6, size=(5, 3000)).astype(I32)
+    thr = rng.integers(0, 7, size=(5, 4)).astype(np.int64)
+    for r in (1, 7, 128, 600):
+        pos, cnt = kernels.first_occurrences(T(mb, gpu), T(thr.reshape(-1),
+                                                           gpu), 4, r)
+        ep, ec = o_first_occ(mb, thr, r)
+        np.testing.assert_array_equal(N(pos), ep.reshape(-1, r))
+        np.testing.assert_array_equal(N(cnt), ec.reshape(-1))
+
+
+@pytest.mark.parametrize("n,vocab", [(1, 3), (2, 2), (7, 2), (64, 3),
+                                     (4095, 4), (4097, 50), (20000, 3),
+                                     (70000, 30000)])
+def test_build_suffix_array(gpu, n, vocab):
+    from suffixgpu_amd.suffix_array import build_suffix_array
+    rng = np.random.default_rng(n)
+    t = rng.integers(-2, vocab, size=n).astype(I32)
+    got = build_suffix_array(T(t, gpu))
+    np.testing.assert_array_equal(N(got), o_build_sa(t))
+
+
+def test_build_suffix_array_structured(gpu):
+    from suffixgpu_amd.suffix_array import build_suffix_array
+    for toks in ([1, 2, 3, 1, 2, 3, 1, 2], [5] * 5000, [0],
+                 [3, -2, 2147483647, 3, -2, 0, 2147483647],
+                 [1, 2] * 3000 + [1]):
+        got = build_suffix_array(T(np.array(toks, I32), gpu))
+        if len(toks) <= 64:
+            assert N(got).tolist() == naive.suffix_array(toks)
+        np.testing.assert_array_equal(N(got), o_build_sa(np.array(toks)))
+
+
+def test_build_suffix_array_identity_tail(gpu):
+    from suffixgpu_amd.suffix_array import build_suffix_array_into
+    rng = np.random.default_rng(4)
+    t = rng.integers(0, 9, size=1000).astype(I32)
+    out = torch.empty(1500, dtype=torch.int32, device=gpu)
+    build_suffix_array_into(T(t, gpu), 600, out)
+    exp = np.concatenate([o_build_sa(t[:600]), np.arange(600, 1500)])
+    np.testing.assert_array_equal(N(out), exp)
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_sa_search(gpu, seed):
+    from suffixgpu_amd.sa_search import search_interval
+    rng = np.random.default_rng(seed)
+    n = 3000
+    toks = rng.integers(0, 4, size=n).astype(I32)
+    sa = o_build_sa(toks).astype(I32)
+    pats = np.zeros((200, 10), I32)
+    lens = np.zeros(200, np.int64)
+    for i in range(200):
+        m = int(rng.integers(0, 11))
+        st = int(rng.integers(0, n - m + 1))
+        pats[i, :m] = toks[st:st + m]
+        if i % 5 == 0:
+            pats[i, :m] = rng.integers(0, 5, size=m)
+        lens[i] = m
+    s, e = search_interval(T(sa, gpu), T(toks, gpu), T(pats, gpu),
+                           T(lens, gpu))
+    es, ee = o_search(sa, toks, pats, lens)
+    np.testing.assert_array_equal(N(s), es)
+    np.testing.assert_array_equal(N(e), ee)
+
+
+def _rand_expand(rng, b, r, k, vocab=9):
+    cont = rng.integers(0, vocab, size=(b, r, k)).astype(I32)
+    tail = rng.integers(0, k + 1, size=(b, r))
+    cont = np.where(np.arange(k)[None, None, :] < tail[:, :, None], cont, -1)
+    occ = rng.integers(0, r + 1, size=b).astype(np.int64)
+    cap = rng.integers(-1, k + 2, size=b).astype(np.int64)
+    return cont.astype(I32), occ, cap
+
+
+@pytest.mark.parametrize("r", [1, 4, 30, 128, 256, 700])
+@pytest.mark.parametrize("minp", [0.0, 0.1])
+def test_expand_chain(gpu, r, minp):
+    from suffixgpu_amd.expand import expand_chain
+    rng = np.random.default_rng(1234 + r)
+    for k, vocab in ((16, 9), (5, 3), (12, 2000)):
+        cont, occ, cap = _rand_expand(rng, 37, r, k, vocab)
+        got = expand_chain(T(cont, gpu), T(occ, gpu), k,
+                           min_token_prob=minp, cap=T(cap, gpu))
+        exp = o_expand(cont, occ, k, min_token_prob=minp, cap=cap)
+        for g, e in zip(got, exp):
+            np.testing.assert_array_equal(N(g), e)
+
+
+@pytest.mark.parametrize("i", range(4))
+def test_expand_alpha_weights_golden(gpu, i):
+    from suffixgpu_amd.expand import expand_chain
+    z = golden("expand_alpha_weights")
+    cont, occ, cap = z[f"cont_{i}"], z[f"occ_{i}"], z[f"cap_{i}"]
+    k = cont.shape[2]
+    got = expand_chain(T(cont, gpu), T(occ, gpu), k, min_token_prob=0.05,
+                       cap=T(cap, gpu), alpha=float(z[f"alpha_{i}"]))
+    for g, key in zip(got, ("chain", "nv", "emit", "score")):
+        np.testing.assert_array_equal(N(g), z[f"{key}_{i}"], err_msg=key)
+    got = expand_chain(T(cont, gpu), T(occ, gpu), k, min_token_prob=0.05,
+                       cap=T(cap, gpu), weights=T(z[f"w_{i}"], gpu))
+    for g, key in zip(got[:3], ("wchain", "wnv", "wemit")):
+        np.testing.assert_array_equal(N(g), z[f"{key}_{i}"], err_msg=key)
+    np.testing.assert_allclose(N(got[3]), z[f"wscore_{i}"], rtol=1e-4,
+                               atol=1e-5)
+
+
+def test_expand_division_table(gpu):
+    """Every vote fraction v/n, 1 <= v <= n <= 128, is the IEEE fp32
+    quotient: a one-depth chain of n occurrences with v equal tokens."""
+    from suffixgpu_amd.expand import expand_chain
+    rows = [(v, n) for n in range(1, 129) for v in range(1, n + 1)]
+    b = len(rows)
+    cont = np.full((b, 128, 1), -1, I32)
+    occ = np.zeros(b, np.int64)
+    for i, (v, n) in enumerate(rows):
+        cont[i, :n, 0] = np.arange(1000, 1000 + n)
+        cont[i, :v, 0] = 7
+        occ[i] = n
+    for alpha in (0.0, 0.5):
+        _, _, _, score = expand_chain(T(cont, gpu), T(occ, gpu), 1,
+                                      alpha=alpha)
+        exp = np.array([np.float32(v) / (np.float32(max(n, 1)) +
+                                         np.float32(alpha))
+                        for v, n in rows], np.float32)
+        np.testing.assert_array_equal(N(score), exp)
