@@ -1,0 +1,331 @@
+"""Global index on gfx950 vs the oracle and the reference's goldens/KATs:
+write path state machine (append, rebuild, eviction, compaction, in-flight
+drops), SA rebuild, capped SA + delta queries, merge and draft."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import naive
+from oracle.global_index import GlobalIndexOracle
+from suffixgpu_amd import synth
+from tests.conftest import golden
+from tests.test_oracle_golden import _docs, trace_ops
+
+pytestmark = pytest.mark.gpu
+
+I32 = np.int32
+
+
+def T(a, dev, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return t if dtype is None else t.to(dtype)
+
+
+def N(t):
+    return t.cpu().numpy()
+
+
+def gpu_state_equal(gi, ref):
+    """ref: oracle index or a dict of golden arrays."""
+    if isinstance(ref, dict):
+        g = ref
+        assert gi.active_len == int(g["active_len"])
+        assert gi.delta_len == int(g["delta_len"])
+        assert list(gi.active_doc_lens) == g["active_doc_lens"].tolist()
+        assert list(gi.delta_doc_lens) == g["delta_doc_lens"].tolist()
+        np.testing.assert_array_equal(N(gi.corpus), g["corpus"])
+        np.testing.assert_array_equal(N(gi.sa), g["sa"])
+        np.testing.assert_array_equal(N(gi.delta)[:gi.delta_len], g["delta"])
+        assert int(gi.delta_len_t.item()) == gi.delta_len
+        return
+    assert gi.active_len == ref.active_len
+    assert gi.delta_len == ref.delta_len
+    assert list(gi.active_doc_lens) == list(ref.active_doc_lens)
+    assert list(gi.delta_doc_lens) == list(ref.delta_doc_lens)
+    np.testing.assert_array_equal(N(gi.corpus), ref.corpus)
+    np.testing.assert_array_equal(N(gi.sa), ref.sa)
+    np.testing.assert_array_equal(N(gi.delta)[:gi.delta_len],
+                                  ref.delta[:ref.delta_len])
+
+
+def _sub(z, suffix):
+    return {k: z[k + suffix] for k in ("active_len", "delta_len",
+                                       "active_doc_lens", "delta_doc_lens",
+                                       "corpus", "sa", "delta")}
+
+
+class _NeverDone:
+    def query(self) -> bool:
+        return False
+
+
+def test_index_trace_golden(gpu):
+    from suffixgpu_amd.global_index import GlobalIndex
+    z = golden("index_trace")
+    gi = GlobalIndex(capacity=96, delta_capacity=40, k=4, max_occurrences=8,
+                     rebuild_threshold=25, device=gpu)
+    for step, docs, infl in trace_ops(z):
+        if infl and gi._rebuild_event is None:
+            gi._rebuild_event = _NeverDone()
+            gi._pending = (gi.active_len, gi.active_doc_lens)
+        gi.append_documents([T(d, gpu) for d in docs])
+        if step in (14, 27):
+            gi._rebuild_event = None
+            gi._pending = None
+        gpu_state_equal(gi, _sub(z, f"_{step}"))
+
+
+def _ties_index(gpu):
+    from suffixgpu_amd import SuffixGPUDrafter
+    z = golden("global_ties")
+    docs = _docs(z)
+    d = SuffixGPUDrafter(k=6, device=gpu, max_pattern_len=10,
+                         max_occurrences=8, num_backoff=5, enable_global=True,
+                         global_capacity=2048, delta_capacity=300,
+                         rebuild_threshold=200)
+    d.harvest_rows([T(x, gpu) for x in docs[:20]], [len(x) for x in docs[:20]])
+    d.harvest_rows([T(x, gpu) for x in docs[20:]], [len(x) for x in docs[20:]])
+    return z, d
+
+
+def test_global_ties_golden(gpu):
+    z, d = _ties_index(gpu)
+    gi = d.global_index
+    gpu_state_equal(gi, _sub(z, ""))
+    q, ql, caps = T(z["query"], gpu), T(z["query_len"], gpu), T(z["caps"], gpu)
+    ml, cont, occ = gi._query_backoff(q, ql, 10, caps)
+    np.testing.assert_array_equal(N(ml), z["q_len"])
+    np.testing.assert_array_equal(N(occ), z["q_occ"])
+    np.testing.assert_array_equal(N(cont), z["q_cont"])
+    dl, dp, dc = gi._delta_match_backoff(q, ql, 10, caps)
+    np.testing.assert_array_equal(N(dl), z["d_len"])
+    np.testing.assert_array_equal(N(dp), z["d_pos"])
+    np.testing.assert_array_equal(N(dc), z["d_cnt"])
+    dr = gi.draft(q, ql, 10, 6, min_token_prob=0.05, max_spec_factor=1.5,
+                  max_spec_offset=1.0, caps=caps)
+    for g, key in zip(dr, ("dr_chain", "dr_emit", "dr_len", "dr_occ",
+                           "dr_score")):
+        np.testing.assert_array_equal(N(g), z[key], err_msg=key)
+    draft, nv = d.propose(T(z["query_len"].astype(I32), gpu),
+                          T(z["rows"], gpu))
+    np.testing.assert_array_equal(N(draft), z["draft"])
+    np.testing.assert_array_equal(N(nv), z["num_valid"])
+
+
+def test_global_drafter_golden(gpu):
+    from suffixgpu_amd import SuffixGPUDrafter
+    z = golden("global_drafter")
+    docs = _docs(z)
+    d = SuffixGPUDrafter(k=16, device=gpu, max_pattern_len=32,
+                         max_occurrences=128, num_backoff=8,
+                         max_spec_factor=2.0, min_token_prob=0.1,
+                         enable_global=True, global_capacity=1 << 13,
+                         delta_capacity=1 << 10, rebuild_threshold=700)
+    for step, lo in enumerate(range(0, len(docs), 8)):
+        chunk = docs[lo:lo + 8]
+        d.harvest_rows([T(x, gpu) for x in chunk], [len(x) for x in chunk])
+        d.poll()
+        tok = T(z["rows"], gpu)
+        draft, nv, _ = d.propose_with_update(T(z["num_tokens"], gpu), tok,
+                                             T(z["sampled"], gpu))
+        np.testing.assert_array_equal(N(draft), z[f"draft_{step}"])
+        np.testing.assert_array_equal(N(nv), z[f"nv_{step}"])
+        gpu_state_equal(d.global_index, _sub(z, f"_{step}"))
+
+
+# ---------------------------------------------------------------- KATs
+def _query(gi, query, gpu, p=8):
+    ml, cont, occ = gi.query(T(np.array([query], I32), gpu),
+                             T(np.array([len(query)]), gpu), p)
+    chain, nv = gi.expand(cont, occ)
+    return (N(chain)[0, :int(nv[0])].tolist(), int(ml[0]), int(occ[0]))
+
+
+def _gi(gpu, **kw):
+    from suffixgpu_amd.global_index import GlobalIndex
+    base = dict(capacity=1024, delta_capacity=256, k=4, max_occurrences=8,
+                rebuild_threshold=100000, device=gpu)
+    base.update(kw)
+    return GlobalIndex(**base)
+
+
+def _append(gi, docs, gpu):
+    gi.append_documents([T(np.array(d, I32), gpu) for d in docs])
+
+
+def test_kat_delta_sa_consistency(gpu):
+    doc = [5, 6, 7, 8, 9, 5, 6, 7, 8, 10]
+    for thr in (100000, 1):
+        gi = _gi(gpu, rebuild_threshold=thr)
+        _append(gi, [doc], gpu)
+        if thr == 1:
+            assert gi.active_len == len(doc) + 1 and gi.delta_len == 0
+        exp_chain, exp_len = naive.global_chain([doc], [5, 6, 7, 8], 4, 8, 8)
+        assert _query(gi, [5, 6, 7, 8], gpu) == (exp_chain, exp_len, 2)
+    docs = [[1, 2, 3, 4, 1, 2, 3, 9], [7, 1, 2, 3, 4, 8, 1, 2]]
+    res = []
+    for thr in (100000, 1):
+        gi = _gi(gpu, rebuild_threshold=thr)
+        _append(gi, docs, gpu)
+        res.append(_query(gi, [1, 2, 3, 4], gpu)[:2])
+    assert res[0] == res[1] == naive.global_chain(docs, [1, 2, 3, 4], 4, 8, 8)
+
+
+def test_kat_rebuilds_eviction_empty(gpu):
+    gi = _gi(gpu, rebuild_threshold=1)
+    docs = [[1, 1, 2], [1, 1, 3], [1, 1, 4], [1, 1, 5]]
+    for d in docs:
+        _append(gi, [d], gpu)
+    assert gi.active_len == sum(len(d) + 1 for d in docs)
+    assert _query(gi, [1, 1], gpu)[:2] == naive.global_chain(docs, [1, 1], 4,
+                                                             8, 8)
+    gi = _gi(gpu, capacity=12, delta_capacity=64, rebuild_threshold=1)
+    for t in (1, 2, 3, 4):
+        _append(gi, [[t] * 4], gpu)
+    assert gi.active_len <= 12
+    assert _query(gi, [4, 4], gpu)[1] == 2
+    assert _query(gi, [1, 1, 1, 1], gpu)[1] == 0
+    gi = _gi(gpu, capacity=64, delta_capacity=16, rebuild_threshold=None)
+    assert _query(gi, [1, 2, 3], gpu) == ([], 0, 0)
+
+
+def test_kat_regressions(gpu):
+    gi = _gi(gpu)
+    doc = [9, 7, 7, 101, 5, 5, 5, 5, 5, 3, 7, 7, 101, 6, 6, 6, 6, 6, 6, 7, 7,
+           101, 4]
+    _append(gi, [doc], gpu)
+    dl, dp, dc = gi._delta_match_backoff(
+        T(np.array([[7, 7] + [0] * 6], I32), gpu), T(np.array([2]), gpu), 8,
+        T(np.array([8]), gpu))
+    assert int(dl[0, 0]) == 2 and int(dc[0, 0]) == 3
+    assert N(dp)[0, 0, :3].tolist() == [1, 10, 19]
+    chain, ml, occ = _query(gi, [7, 7], gpu)
+    assert (ml, occ, chain[0]) == (2, 3, 101)
+    gi = _gi(gpu, max_occurrences=4)
+    _append(gi, [[1, 9] * 10 + [1, 2, 3, 4, 6]], gpu)
+    assert _query(gi, [1, 2, 3, 4], gpu) == ([6], 4, 1)
+
+
+def test_kat_overflow(gpu):
+    gi = _gi(gpu, capacity=64, delta_capacity=18)
+    _append(gi, [[1] * 6, [2] * 6], gpu)
+    gi._rebuild_event = _NeverDone()
+    gi._pending = (gi.active_len, gi.active_doc_lens)
+    _append(gi, [[3] * 10], gpu)
+    assert gi.delta_len <= gi.delta_capacity
+    assert _query(gi, [3, 3], gpu)[1] == 2
+    assert _query(gi, [2, 2], gpu)[1] == 2
+    assert _query(gi, [1, 1], gpu)[1] == 0
+    gi._rebuild_event = None
+    gi._pending = None
+    gi = _gi(gpu, capacity=64, delta_capacity=16)
+    _append(gi, [[1] * 12], gpu)
+    _append(gi, [[2] * 12], gpu)
+    assert gi.active_len == 13 and gi.delta_len == 13
+    assert _query(gi, [1, 1], gpu)[1] == 2
+    assert _query(gi, [2, 2], gpu)[1] == 2
+
+
+def test_kat_no_cross_document(gpu):
+    for thr in (100000, 1):
+        gi = _gi(gpu, capacity=256, delta_capacity=64, rebuild_threshold=thr)
+        _append(gi, [[1, 2, 3, 7, 8, 9], [100, 101, 102, 55, 56]], gpu)
+        assert _query(gi, [7, 8, 9], gpu) == ([], 3, 1)
+        assert _query(gi, [8, 9, 100], gpu) == ([101, 102, 55, 56], 1, 1)
+
+
+# ------------------------------------------------------ random vs oracle
+def _load_pair(gpu, docs, delta_docs, cap, dcap, r, k=16):
+    from suffixgpu_amd.global_index import GlobalIndex
+    g = GlobalIndex(capacity=cap, delta_capacity=dcap, k=k,
+                    max_occurrences=r, rebuild_threshold=10 ** 9, device=gpu)
+    o = GlobalIndexOracle(capacity=cap, delta_capacity=dcap, k=k,
+                          max_occurrences=r, rebuild_threshold=10 ** 9)
+    g.load_documents([T(d, gpu) for d in docs])
+    o.load_documents(docs)
+    g.append_documents([T(d, gpu) for d in delta_docs])
+    o.append_documents(delta_docs)
+    gpu_state_equal(g, o)
+    return g, o
+
+
+@pytest.mark.parametrize("vocab", [4, 0])
+def test_queries_vs_oracle(gpu, vocab):
+    rng = np.random.default_rng(31 + vocab)
+    if vocab:
+        docs = [rng.integers(0, vocab, size=int(rng.integers(1, 200))).astype(
+            I32) for _ in range(60)]
+        dd = [rng.integers(0, vocab, size=int(rng.integers(1, 90))).astype(I32)
+              for _ in range(6)]
+    else:
+        tc = synth.TemplateCorpus(seed=5, n_templates=12)
+        docs = [tc.sequence(lo=64, hi=500) for _ in range(40)]
+        dd = [tc.sequence(lo=64, hi=300) for _ in range(4)]
+    cap = sum(len(d) + 1 for d in docs) + 37
+    g, o = _load_pair(gpu, docs, dd, cap, 2048, 16, k=8)
+    b, p = 48, 12
+    q = np.zeros((b, p), I32)
+    ql = np.zeros(b, np.int64)
+    for i in range(b):
+        src = docs[i % len(docs)] if i % 3 else dd[i % len(dd)]
+        n = int(rng.integers(0, min(len(src), p) + 1))
+        st = int(rng.integers(0, len(src) - n + 1))
+        q[i, :n] = src[st:st + n]
+        ql[i] = n
+        if i % 7 == 0:
+            q[i, :n] = rng.integers(0, max(vocab, 50), size=n)
+    ql[0] = 0
+    ql[1] = p + 5   # longer than the query width: clamped gathers
+    caps = np.array([12, 6, 3, 2], np.int64)
+    tq, tl, tc_ = T(q, gpu), T(ql, gpu), T(caps, gpu)
+    for got, exp in zip(g._query_backoff(tq, tl, p, tc_),
+                        o._query_backoff(q, ql, p, caps)):
+        np.testing.assert_array_equal(N(got), exp)
+    for got, exp in zip(g._delta_match_backoff(tq, tl, p, tc_),
+                        o._delta_match_backoff(q, ql, p, caps)):
+        np.testing.assert_array_equal(N(got), exp)
+    for got, exp in zip(g.draft(tq, tl, p, 8, min_token_prob=0.05,
+                                max_spec_factor=0.7, max_spec_offset=0.3,
+                                caps=tc_, alpha=0.25),
+                        o.draft(q, ql, p, 8, min_token_prob=0.05,
+                                max_spec_factor=0.7, max_spec_offset=0.3,
+                                caps=caps, alpha=0.25)):
+        np.testing.assert_array_equal(N(got), exp)
+    from suffixgpu_amd.sa_search import suffix_match_backoff
+    from oracle.sa import suffix_match_backoff as o_smb
+    for got, exp in zip(suffix_match_backoff(g.sa, g.corpus, tq, tl, p, tc_),
+                        o_smb(o.sa, o.corpus, q, ql, p, caps)):
+        np.testing.assert_array_equal(N(got), exp)
+
+
+def test_async_rebuild_blocking_poll(gpu):
+    """Side-stream rebuilds swapped at deterministic points match the
+    oracle's done-at-next-poll schedule."""
+    from suffixgpu_amd.global_index import GlobalIndex
+    rng = np.random.default_rng(8)
+    side = torch.cuda.Stream(gpu)
+    g = GlobalIndex(capacity=3000, delta_capacity=400, k=4,
+                    max_occurrences=8, rebuild_threshold=150, device=gpu,
+                    rebuild_stream=side)
+    g.blocking_poll = True
+    o = GlobalIndexOracle(capacity=3000, delta_capacity=400, k=4,
+                          max_occurrences=8, rebuild_threshold=150,
+                          async_rebuild=True)
+    for step in range(40):
+        docs = [rng.integers(0, 6, size=int(rng.integers(1, 120))).astype(I32)
+                for _ in range(int(rng.integers(1, 4)))]
+        g.append_documents([T(d, gpu) for d in docs])
+        o.append_documents(docs)
+        if step % 3 == 0:
+            g.poll_rebuild()
+            o.poll_rebuild()
+        assert (g._rebuild_event is None) == (o._rebuild_event is None)
+        assert g.delta_len == o.delta_len
+        assert list(g.delta_doc_lens) == list(o.delta_doc_lens)
+    g.poll_rebuild()
+    o.poll_rebuild()
+    torch.cuda.synchronize()
+    gpu_state_equal(g, o)
