@@ -1,0 +1,451 @@
+"""Drafter benchmark: propose_with_update on one MI355X.
+
+Workload (the drafter's decode shape with global memory on): B=64 request
+rows of S=8192 int32 tokens, k=16, max_pattern_len=32, num_backoff=8,
+max_occurrences=128, max_spec_factor=2.0, min_token_prob=0.1, and a
+2^22-token corpus + SA built from 1024 template-sharing synthetic sequences
+plus a half-full 2^16-token delta; each row carries a geometric(0.3)+1
+accepted-token sampled block.  One step = update_state + local match +
+SA/delta match + merge + expansion + selection, captured once as a HIP
+graph and replayed; inputs stay resident in HBM.
+
+Printed: one JSON line with p50 us/step (value), the dominant kernel's
+roofline, the SA-build throughput and the CPU baseline (the oracle's numpy
+restatement of the same step on this host, on a bounded sample).
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = ("propose_with_update p50 µs/step (B=64,S=8192); HBM GB/s; "
+          "SA build Mtok/s")
+HBM_PEAK_GBPS = 8000.0
+CFG = dict(k=16, max_pattern_len=32, max_occurrences=128, num_backoff=8,
+           max_spec_factor=2.0, min_token_prob=0.1)
+B, S, T_SAMPLED = 64, 8192, 17
+CAPACITY, DELTA_CAP, DELTA_FILL = 1 << 22, 1 << 16, 1 << 15
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-steps", type=int, default=2)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel-reps", type=int, default=50)
+    return ap.parse_args()
+
+
+# --------------------------------------------------------------- roofline
+def local_algorithmic_bytes(new_counts, accepted, k) -> int:
+    """Rows scanned once + sampled block read + scatter writes + draft,
+    num_valid and counts (in/out)."""
+    n_eff = np.minimum(new_counts.astype(np.int64), S)
+    return int(4 * n_eff.sum() + 4 * B * T_SAMPLED + 4 * accepted.sum()
+               + 4 * B * (k + 3))
+
+
+def reference_probe_footprint(sa, corpus, rpat, plen, P):
+    """Distinct SA ranks and corpus positions the reference's merged
+    binary search (ceil(log2(N+1)) fixed probes per bound, every length
+    1..P) has to read to decide its comparisons."""
+    n = sa.shape[0]
+    iters = int(np.ceil(np.log2(n + 1)))
+    rows = []
+    for b in range(rpat.shape[0]):
+        for ln in range(1, int(plen[b]) + 1):
+            rows.append((b, ln))
+    rb = np.array([r[0] for r in rows])
+    rl = np.array([r[1] for r in rows])
+    m = rb.shape[0]
+    pats = np.zeros((m, P), np.int64)
+    for j in range(P):
+        t = rl - 1 - j
+        pats[:, j] = np.where(t >= 0, rpat[rb, np.maximum(t, 0)], 0)
+    pats2 = np.concatenate([pats, pats])
+    rl2 = np.concatenate([rl, rl])
+    upper = np.arange(2 * m) >= m
+    lo = np.zeros(2 * m, np.int64)
+    hi = np.full(2 * m, n, np.int64)
+    ranks, cpos = [], []
+    offs = np.arange(P)
+    for _ in range(iters):
+        mid = np.minimum((lo + hi) // 2, n - 1)
+        active = lo < hi
+        pos = sa[mid].astype(np.int64)
+        idx = pos[:, None] + offs[None, :]
+        tok = np.where(idx < n, corpus[np.minimum(idx, n - 1)], -1)
+        valid = offs[None, :] < rl2[:, None]
+        eq = (tok == pats2) | ~valid
+        lcp = np.minimum(np.cumprod(eq, axis=1).sum(1), rl2)
+        full = lcp >= rl2
+        sp = np.minimum(pos + lcp, n - 1)
+        sch = np.where(pos + lcp < n, corpus[sp], -1)
+        pch = pats2[np.arange(2 * m), np.minimum(lcp, P - 1)]
+        c = np.where(full, 0, np.where(sch < pch, -1, np.where(sch > pch, 1,
+                                                                0)))
+        go = (c < 0) | (upper & (c == 0))
+        ranks.append(mid[active])
+        need = np.minimum(lcp + 1, rl2)
+        for r in np.flatnonzero(active):
+            e = min(int(pos[r]) + int(need[r]), n)
+            cpos.append(np.arange(int(pos[r]), e))
+        lo = np.where(go, mid + 1, lo)
+        hi = np.where(go, hi, mid)
+    u_sa = np.unique(np.concatenate(ranks)) if ranks else np.zeros(0)
+    u_c = np.unique(np.concatenate(cpos)) if cpos else np.zeros(0)
+    return u_sa, u_c
+
+
+# ------------------------------------------------------------------ main
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this drafter benchmark runs on exactly "
+                          "one GPU (the workload is one GPU's rows); "
+                          f"--gpus {args.gpus} is not supported"}))
+        return 2
+    import torch
+
+    from suffixgpu_amd import SuffixGPUDrafter, synth
+    from suffixgpu_amd import _lib
+    from suffixgpu_amd.suffix_array import (build_suffix_array_into,
+                                            sa_workspace_bytes)
+
+    dev = torch.device("cuda", 0)
+    t0 = time.time()
+    w = synth.global_corpus(seed=3, capacity=CAPACITY, delta_fill=DELTA_FILL,
+                            n_docs=1024, b=B, s=S, t=T_SAMPLED)
+    log(f"workload generated in {time.time() - t0:.1f}s: "
+        f"{len(w.active_docs)} corpus docs, {len(w.delta_docs)} delta docs")
+
+    d = SuffixGPUDrafter(device=dev, enable_global=True,
+                         global_capacity=CAPACITY, delta_capacity=DELTA_CAP,
+                         rebuild_threshold=1 << 30, **CFG)
+    gi = d.global_index
+
+    # ---- SA build throughput (side stream, HIP events): corpus snapshot
+    # (docs + SEP + sentinel) and a uniform-random low-repeat corpus.
+    side = torch.cuda.Stream(dev)
+    flat = np.concatenate([np.append(x, -2) for x in w.active_docs]).astype(
+        np.int32)
+    m = min(flat.shape[0] + 1, CAPACITY)
+    rng = np.random.default_rng(4)
+    uniform = rng.integers(0, synth.VOCAB_LARGE, size=CAPACITY).astype(
+        np.int32)
+    ws = torch.empty(sa_workspace_bytes(CAPACITY), dtype=torch.uint8,
+                     device=dev)
+    build_ms = {}
+    for name, text_np, mm in (("corpus", flat, m), ("uniform", uniform,
+                                                     CAPACITY)):
+        text = torch.full((CAPACITY,), _lib_pad(), dtype=torch.int32,
+                          device=dev)
+        text[:text_np.shape[0]].copy_(torch.from_numpy(text_np))
+        out = torch.empty(CAPACITY, dtype=torch.int32, device=dev)
+        times = []
+        for rep in range(3):
+            torch.cuda.synchronize()
+            side.wait_stream(torch.cuda.current_stream(dev))
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(side):
+                e0.record(side)
+                build_suffix_array_into(text, mm, out, ws)
+                e1.record(side)
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1))
+        build_ms[name] = (min(times), mm)
+        log(f"SA build {name}: m={mm} {min(times):.2f} ms")
+    del ws
+
+    gi.load_documents([torch.from_numpy(x).to(dev) for x in w.active_docs])
+    gi.append_documents([torch.from_numpy(x).to(dev) for x in w.delta_docs])
+    torch.cuda.synchronize()
+    log(f"index: active_len={gi.active_len} delta_len={gi.delta_len}")
+
+    bt = w.batch
+    tokens0 = torch.from_numpy(bt.tokens).to(dev)
+    buf = tokens0.clone()
+    nt = torch.from_numpy(bt.num_tokens).to(dev)
+    sampled = torch.from_numpy(bt.sampled).to(dev)
+
+    # ---- capture one step; replays are identical (counts not fed back).
+    for _ in range(3):
+        d.propose_with_update(nt, buf.clone(), sampled)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = d.propose_with_update(nt, buf, sampled)
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    cur = torch.cuda.current_stream(dev)
+    torch.cuda.synchronize()
+    tw0 = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(cur)
+        graph.replay()
+        ends[i].record(cur)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - tw0) * 1e3
+    per_us = [s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends)]
+    p50 = statistics.median(per_us)
+    draft, num_valid, new_counts = (x.cpu().numpy() for x in out)
+    log(f"step p50 {p50:.2f} us, wall {wall_ms / args.steps * 1e3:.2f} "
+        f"us/step, drafting rows {(num_valid > 0).sum()}/{B}, "
+        f"mean num_valid {num_valid.mean():.2f}")
+
+    # ---- per-kernel durations (same kernels, launched alone).
+    acc = (bt.sampled != -1).sum(1)
+    k_local_us, k_global_us = kernel_timings(d, dev, tokens0, nt, sampled,
+                                             args.kernel_reps)
+    log(f"kernel avg: local {k_local_us:.2f} us, global {k_global_us:.2f} us")
+
+    a_local = local_algorithmic_bytes(new_counts, acc, CFG["k"])
+    a_global, fp = global_algorithmic_bytes(d, dev, buf, new_counts)
+    log(f"algorithmic bytes: local {a_local}, global {a_global} ({fp})")
+    kernels = {
+        "k_local": (a_local, k_local_us),
+        "k_global": (a_global, k_global_us),
+    }
+    dom = max(kernels, key=lambda kk: kernels[kk][1])
+    a_bytes, dur = kernels[dom]
+    achieved = a_bytes / (dur * 1e-6) / 1e9
+    step_bytes = a_local + a_global
+    traffic = load_traffic(dom)
+    roofline = {"bound": "hbm", "achieved": round(achieved, 2),
+                "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBPS, 6),
+                "traffic": traffic, "kernel": dom,
+                "algorithmic_bytes": a_bytes,
+                "avg_launch_us": round(dur, 3)}
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(d, w, args.cpu_steps)
+
+    sa_corpus_ms, sa_m = build_ms["corpus"]
+    sa_uni_ms, _ = build_ms["uniform"]
+    result = {
+        "metric": METRIC,
+        "value": round(p50, 3),
+        "unit": "us/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms / args.steps, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i32",
+        "data": "synthetic",
+        "config": {"workload": "propose_with_update, global memory on: "
+                   "B=64 S=8192 k=16 P=32 R=128 num_backoff=8 "
+                   "spec_factor=2.0 min_prob=0.1, corpus 2^22 (template "
+                   "sequences, SA prebuilt) + delta 2^15/2^16, hipGraph "
+                   "replay", "global_batch": B, "seq_len": S,
+                   "parallelism": "none (1 GPU)"},
+        "step_hbm_gbps": round(step_bytes / (p50 * 1e-6) / 1e9, 3),
+        "step_algorithmic_bytes": step_bytes,
+        "sa_build_mtok_s": round(sa_m / (sa_corpus_ms * 1e-3) / 1e6, 2),
+        "sa_build_uniform_mtok_s": round(CAPACITY / (sa_uni_ms * 1e-3) / 1e6,
+                                         2),
+        "sa_build_steps_equiv": round(sa_corpus_ms * 1e3 / p50, 1),
+        "kernels_us": {"k_local": round(k_local_us, 3),
+                       "k_global": round(k_global_us, 3)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def _lib_pad() -> int:
+    return 2 ** 31 - 1
+
+
+def kernel_timings(d, dev, tokens0, nt, sampled, reps):
+    """Average duration of the local and the global kernel, each launched
+    alone on the current stream between HIP events."""
+    import torch
+
+    from suffixgpu_amd import _lib
+    L = _lib.lib()
+    cur = torch.cuda.current_stream(dev)
+    b = tokens0.shape[0]
+    buf = tokens0.clone()
+    bt, keep = _lib.make_batch(buf, nt, sampled=sampled,
+                               limit=tokens0.shape[1])
+    draft = torch.empty(b, d.k, dtype=torch.int32, device=dev)
+    nv = torch.empty(b, dtype=torch.int32, device=dev)
+    newc = torch.empty(b, dtype=torch.int32, device=dev)
+    p_local = _lib.make_params(d.k, d.max_pattern_len,
+                               d.local_kernel.max_occurrences,
+                               d.local_kernel.min_match_len,
+                               d.local_kernel.support_thresholds, (),
+                               d.max_spec_factor, d.max_spec_offset,
+                               d.min_token_prob, d.vote_smoothing_alpha)
+
+    def local_launch():
+        _lib.check(L.sfx_propose_step(p_local, None, bt, draft.data_ptr(),
+                                      nv.data_ptr(), newc.data_ptr(), None,
+                                      0, cur.cuda_stream), "local")
+
+    # the global kernel, query form: tails of the updated rows
+    upd = tokens0.clone()
+    new = d.update_state(nt, upd, sampled)
+    tails, tail_len = d._gather_tails(new, upd)
+    tails = tails.to(torch.int32).contiguous()
+    gi = d.global_index
+    caps = [int(x) for x in d._global_caps.tolist()]
+    pg = _lib.make_params(d.k, d.max_pattern_len, gi.max_occurrences, 1,
+                          (1,), caps, d.max_spec_factor, d.max_spec_offset,
+                          d.min_token_prob, d.vote_smoothing_alpha)
+    outs = {n: torch.empty(sh, dtype=dt, device=dev) for n, sh, dt in (
+        ("draft", (b, d.k), torch.int32), ("emit", (b,), torch.int64),
+        ("draft_len", (b,), torch.int64), ("draft_occ", (b,), torch.int64),
+        ("draft_score", (b,), torch.float32))}
+    go = _lib.SfxGlobalOut()
+    for n, t in outs.items():
+        setattr(go, n, t.data_ptr())
+    nbytes = int(L.sfx_global_query_workspace_size(pg, b,
+                                                    gi.delta_capacity))
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    ix = gi.index_struct()
+
+    def global_launch():
+        _lib.check(L.sfx_global_query(pg, ix, tails.data_ptr(), b,
+                                      tails.shape[1], tail_len.data_ptr(),
+                                      go, ws.data_ptr(), nbytes,
+                                      cur.cuda_stream), "global")
+
+    res = []
+    for fn in (local_launch, global_launch):
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        evs = [(torch.cuda.Event(enable_timing=True),
+                torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for e0, e1 in evs:
+            e0.record(cur)
+            fn()
+            e1.record(cur)
+        torch.cuda.synchronize()
+        res.append(statistics.mean(e0.elapsed_time(e1) * 1e3
+                                   for e0, e1 in evs))
+    del keep
+    return res[0], res[1]
+
+
+def global_algorithmic_bytes(d, dev, buf, new_counts):
+    """4*delta_len + 4*|SA ranks| + 4*|corpus positions| the reference's
+    search and continuation gathers must read for this batch."""
+    import torch
+    gi = d.global_index
+    P = d.max_pattern_len
+    q = torch.from_numpy(new_counts.astype(np.int64)).to(dev)
+    tails, tail_len = d._gather_tails(q, buf)
+    tails = tails.to(torch.int32)
+    res = gi._run_query(tails, tail_len, P, d._global_caps,
+                        want=("len", "occ", "sa_start", "sa_end", "sa_len",
+                              "d_len"))
+    sa = gi.sa.cpu().numpy()
+    corpus = gi.corpus.cpu().numpy()
+    tl = tail_len.cpu().numpy()
+    tn = tails.cpu().numpy().astype(np.int64)
+    rpat = np.zeros((tn.shape[0], P), np.int64)
+    for j in range(P):
+        idx = tl - 1 - j
+        rpat[:, j] = np.where(idx >= 0, tn[np.arange(tn.shape[0]),
+                                           np.clip(idx, 0, P - 1)], -3)
+    u_sa, u_c = reference_probe_footprint(sa, corpus, rpat, np.minimum(tl, P),
+                                          P)
+    u_sa = set(u_sa.tolist())
+    u_c = set(u_c.tolist())
+    ml = res["len"].cpu().numpy()
+    sl = res["sa_len"].cpu().numpy()
+    dl = res["d_len"].cpu().numpy()
+    s0 = res["sa_start"].cpu().numpy()
+    s1 = res["sa_end"].cpu().numpy()
+    R, K, N = gi.max_occurrences, gi.k, gi.capacity
+    for b in range(ml.shape[0]):
+        for c in range(ml.shape[1]):
+            if ml[b, c] == 0 or not (sl[b, c] >= dl[b, c] and sl[b, c] > 0):
+                continue
+            ilen = int(s1[b, c] - s0[b, c])
+            cnt = min(ilen, R)
+            for r in range(cnt):
+                idx = (int(s0[b, c]) + (r * ilen) // R if ilen > R
+                       else int(s0[b, c]) + r)
+                u_sa.add(idx)
+                p0 = int(sa[idx]) + int(ml[b, c])
+                u_c.update(range(p0, min(p0 + K, N)))
+    a = 4 * gi.delta_len + 4 * len(u_sa) + 4 * len(u_c)
+    return int(a), {"delta_len": gi.delta_len, "u_sa": len(u_sa),
+                    "u_corpus": len(u_c)}
+
+
+def load_traffic(kernel: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary."""
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text()).get(kernel)
+    except (OSError, ValueError):
+        return None
+
+
+def cpu_baseline(d, w, steps):
+    """The oracle (numpy restatement of the reference's CPU path) timed on
+    this host on `steps` steps of the same batch and index state."""
+    from oracle.drafter import DrafterOracle
+    gi = d.global_index
+    o = DrafterOracle(enable_global=True, global_capacity=CAPACITY,
+                      delta_capacity=DELTA_CAP, rebuild_threshold=1 << 30,
+                      **CFG)
+    og = o.global_index
+    og.corpus[:] = gi.corpus.cpu().numpy()
+    og.sa[:] = gi.sa.cpu().numpy()
+    og.delta[:] = gi.delta.cpu().numpy()
+    og.active_len = gi.active_len
+    og.delta_len = gi.delta_len
+    bt = w.batch
+    times = []
+    for _ in range(steps):
+        tok = bt.tokens.copy()
+        t0 = time.perf_counter()
+        o.propose_with_update(bt.num_tokens, tok, bt.sampled)
+        times.append(time.perf_counter() - t0)
+    us = statistics.median(times) * 1e6
+    log(f"cpu baseline: {us / 1e3:.1f} ms/step")
+    return {"value": round(us, 1), "unit": "us/step", "cores": 1,
+            "kind": "port",
+            "sample": f"{steps} propose_with_update steps of the same B=64 "
+                      "batch and index (numpy oracle, one thread); "
+                      f"host has {os.cpu_count()} logical CPUs"}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

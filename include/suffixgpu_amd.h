@@ -31,7 +31,7 @@ extern "C" {
 
 #define SFX_EINVAL (-1)
 #define SFX_MAX_CANDIDATES 32
-#define SFX_ABI_VERSION 1
+#define SFX_ABI_VERSION 3
 
 /* Drafter configuration shared by the local and global paths.
  * Mirrors the constructor arguments of SuffixGPUDrafter
@@ -53,7 +53,10 @@ typedef struct sfx_params {
     int32_t caps[SFX_MAX_CANDIDATES];       /* global caps, descending  */
 } sfx_params;
 
-/* Global index buffers (suffix_gpu/global_index.py:63-74). */
+/* Global index buffers (suffix_gpu/global_index.py:63-74), plus the key
+ * array of the suffix array (no reference counterpart): row r holds the
+ * first key_width tokens of the suffix at sa[r] (-1 past the end), built
+ * by sfx_sa_keys() with every suffix array; NULL disables it. */
 typedef struct sfx_index {
     const int32_t* corpus;    /* [capacity] PAD-filled ring               */
     const int32_t* sa;        /* [capacity] suffix array of corpus        */
@@ -61,6 +64,8 @@ typedef struct sfx_index {
     const int32_t* delta;     /* [delta_capacity] append-only delta       */
     int64_t delta_capacity;   /* D                                        */
     const int64_t* delta_len; /* device scalar: committed delta length    */
+    const int32_t* sa_key;    /* [capacity, key_width] or NULL            */
+    int64_t key_width;        /* 4..32, a multiple of 4                   */
 } sfx_index;
 
 /* One decode step's batch (suffix_gpu/proposer.py:135-214).
@@ -149,7 +154,8 @@ int sfx_local_forward(const sfx_params* p, const sfx_batch* batch,
  *   len/cont/occ            [B,C_g] i64, [B,C_g,R,K] i32, [B,C_g] i64
  *   draft/emit/dlen/docc/dscore  best-cap draft: [B,K] i32, [B] i64 x3,
  *                                [B] f32
- * workspace: sfx_global_query_workspace_size() bytes, zero-filled once. */
+ * workspace: sfx_global_query_workspace_size() bytes, zero-filled once
+ * (its size depends on the index's delta capacity; 0 for local-only). */
 typedef struct sfx_global_out {
     int64_t* sa_len; int64_t* sa_start; int64_t* sa_end;
     int64_t* d_len; int64_t* d_pos; int64_t* d_cnt;
@@ -158,7 +164,8 @@ typedef struct sfx_global_out {
     float* draft_score;
 } sfx_global_out;
 
-size_t sfx_global_query_workspace_size(const sfx_params* p, int64_t batch);
+size_t sfx_global_query_workspace_size(const sfx_params* p, int64_t batch,
+                                       int64_t delta_capacity);
 int sfx_global_query(const sfx_params* p, const sfx_index* index,
                      const int32_t* query, int64_t batch, int64_t width,
                      const int64_t* qlen, const sfx_global_out* out,
@@ -167,20 +174,21 @@ int sfx_global_query(const sfx_params* p, const sfx_index* index,
 
 /* ---- fused decode step (suffix_gpu/proposer.py:186-327) --------------- */
 
-/* propose_with_update (batch->sampled != NULL) or propose (== NULL).
- * Local-only when index == NULL.  With an index the step is two kernels:
- * the local kernel goes on `stream`, the global kernel on `side_stream`
- * (which may equal `stream`); the caller orders side_stream after prior
- * work on stream and joins it back.  The two kernels hand results over
- * through the workspace; whichever finishes a row last writes that row's
- * draft [B,K] i32 and num_valid [B] i32.  new_counts [B] i32 may be NULL.
- * workspace: sfx_step_workspace_size() bytes, zero-filled once. */
-size_t sfx_step_workspace_size(const sfx_params* p, int64_t batch);
+/* propose_with_update (batch->sampled != NULL) or propose (== NULL), one
+ * kernel launch on `stream`.  Local-only when index == NULL.  With an
+ * index, every row runs an SA-search, a delta-scan and a local workgroup
+ * that hand results over through the workspace; whichever finishes a row
+ * last writes that row's draft [B,K] i32 and num_valid [B] i32.
+ * new_counts [B] i32 may be NULL.  workspace: sfx_step_workspace_size()
+ * bytes (0 for local-only), zero-filled once; calls sharing a workspace
+ * must not overlap. */
+size_t sfx_step_workspace_size(const sfx_params* p, int64_t batch,
+                               int64_t delta_capacity);
 int sfx_propose_step(const sfx_params* p, const sfx_index* index,
                      const sfx_batch* batch, int32_t* draft,
                      int32_t* num_valid, int32_t* new_counts,
                      void* workspace, size_t workspace_bytes,
-                     hipStream_t stream, hipStream_t side_stream);
+                     hipStream_t stream);
 
 /* ---- suffix-array rebuild (suffix_gpu/suffix_array.py:15-63,
  *      global_index.py:217-223) ------------------------------------------ */
@@ -190,6 +198,11 @@ int sfx_propose_step(const sfx_params* p, const sfx_index* index,
  * sorts; rounds stop on the device once every rank is distinct, with no
  * host synchronisation.  sa_is64 selects int64 output. */
 size_t sfx_sa_build_workspace_size(int64_t m);
+
+/* keys[r * width + j] = j-th token of the suffix at sa[r] (corpus reads at
+ * or past n give -1), for r < n and j < width (4..32, multiple of 4). */
+int sfx_sa_keys(const int32_t* corpus, const int32_t* sa, int64_t n,
+                int64_t width, int32_t* keys, hipStream_t stream);
 int sfx_sa_build(const int32_t* text, int64_t m, int64_t n_total, void* sa,
                  int32_t sa_is64, void* workspace, size_t workspace_bytes,
                  hipStream_t stream);

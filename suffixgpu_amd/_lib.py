@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsuffixgpu_amd.so"
 MAX_CANDIDATES = 32
-ABI_VERSION = 1
+ABI_VERSION = 3
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -40,6 +40,7 @@ class SfxIndex(ctypes.Structure):
     _fields_ = [
         ("corpus", c_p), ("sa", c_p), ("capacity", c_i64),
         ("delta", c_p), ("delta_capacity", c_i64), ("delta_len", c_p),
+        ("sa_key", c_p), ("key_width", c_i64),
     ]
 
 
@@ -80,18 +81,20 @@ SIGNATURES = {
                                   ctypes.POINTER(SfxBatch), c_p, c_p, c_p,
                                   c_p, c_p, c_p]),
     "sfx_global_query_workspace_size": (ctypes.c_size_t,
-                                        [ctypes.POINTER(SfxParams), c_i64]),
+                                        [ctypes.POINTER(SfxParams), c_i64,
+                                         c_i64]),
     "sfx_global_query": (c_i32, [ctypes.POINTER(SfxParams),
                                  ctypes.POINTER(SfxIndex), c_p, c_i64, c_i64,
                                  c_p, ctypes.POINTER(SfxGlobalOut), c_p,
                                  ctypes.c_size_t, c_p]),
     "sfx_step_workspace_size": (ctypes.c_size_t,
-                                [ctypes.POINTER(SfxParams), c_i64]),
+                                [ctypes.POINTER(SfxParams), c_i64, c_i64]),
     "sfx_propose_step": (c_i32, [ctypes.POINTER(SfxParams),
                                  ctypes.POINTER(SfxIndex),
                                  ctypes.POINTER(SfxBatch), c_p, c_p, c_p,
-                                 c_p, ctypes.c_size_t, c_p, c_p]),
+                                 c_p, ctypes.c_size_t, c_p]),
     "sfx_sa_build_workspace_size": (ctypes.c_size_t, [c_i64]),
+    "sfx_sa_keys": (c_i32, [c_p, c_p, c_i64, c_i64, c_p, c_p]),
     "sfx_sa_build": (c_i32, [c_p, c_i64, c_i64, c_p, c_i32, c_p,
                              ctypes.c_size_t, c_p]),
 }

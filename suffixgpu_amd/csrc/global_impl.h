@@ -1,0 +1,474 @@
+// Global-role device code: SA-search and delta-scan workgroups per query
+// row, and the merge run by whichever of the two finishes second.
+// Included by global.hip (standalone kernel) and step.hip (fused step).
+#pragma once
+
+#include "pick.h"
+#include "sa_search.h"
+#include "sfx_common.h"
+#include "step_ws.h"
+
+namespace sfx {
+
+constexpr int kGlobalThreads = 512;
+constexpr int kSearchGroup = 16;
+
+struct GlobalArgs {
+  sfx_params p;
+  sfx_index ix;
+  int64_t B;
+  int step;
+  sfx_batch bt;
+  const int32_t* query;
+  int64_t qwidth;
+  const int64_t* qlen;
+  sfx_global_out out;
+  int need_expand;
+  int32_t* draft;
+  int32_t* num_valid;
+  StepWs ws;
+  int merge_waves;
+  int mb_lds;  // bytes of LDS for the delta match_back array (0: workspace)
+};
+
+struct GlobalLayout {
+  int rpat, lb, ub, found, scan, red, misc, lo, dtok, dmb, mpos, mcache, mA,
+      chain, nv, score, rlen, rocc, total;
+};
+
+// Delta tokens staged per chunk (after a halo of P rounded up to 4
+// tokens); the per-row match_back bytes stay in LDS up to kMbLdsMax
+// positions, longer deltas keep them in the workspace.
+constexpr int kDeltaChunk = 8192;
+constexpr int kMbLdsMax = (int)kDeltaMbLdsMax;
+
+__host__ __device__ inline int g_take(int& off, int bytes) {
+  const int o = off;
+  off += (bytes + 15) & ~15;
+  return o;
+}
+
+// Shared header, then a union: the SA/delta role buffers are dead by the
+// time the block (if it arrives second) merges the row.
+__host__ __device__ inline GlobalLayout global_layout(int P, int C, int R,
+                                                      int K, int nmw,
+                                                      int mb_lds) {
+  constexpr int NW = kGlobalThreads / kWave;
+  const int Rp = (R + 3) & ~3;
+  GlobalLayout L;
+  int off = 0;
+  L.rpat = g_take(off, P * 4);
+  L.lb = g_take(off, P * 8);
+  L.ub = g_take(off, P * 8);
+  L.found = g_take(off, C * 4);
+  L.scan = g_take(off, 4 * NW * 8);
+  L.red = g_take(off, NW * 4);
+  L.misc = g_take(off, 64);
+  L.lo = g_take(off, C * 4);
+  L.chain = g_take(off, C * K * 4);
+  L.nv = g_take(off, C * 4);
+  L.score = g_take(off, C * 4);
+  L.rlen = g_take(off, C * 4);
+  L.rocc = g_take(off, C * 4);
+  const int ubase = off;
+  L.dtok = g_take(off, (kDeltaChunk + ((P + 3) & ~3)) * 4);
+  L.dmb = g_take(off, mb_lds);
+  const int delta_end = off;
+  off = ubase;
+  L.mpos = g_take(off, nmw * Rp * 4);
+  L.mcache = g_take(off, nmw * R * K * 4);
+  L.mA = g_take(off, nmw * Rp * 4);
+  L.total = off > delta_end ? off : delta_end;
+  return L;
+}
+
+// ---- Delta role: match_back over ends i in [0, delta_len] with the delta
+// staged through LDS in 16-byte words (chunks of kDeltaChunk positions
+// after a halo of P rounded up to 4), kept as u8 in LDS (kMbLds) or the
+// workspace, then one ordered pass extracts the first R ends per cap with
+// mb >= min(max mb, cap) (global_index.py:465-546).
+template <bool kMbLds>
+__device__ __forceinline__ void delta_role(const GlobalArgs& a,
+                                           const GlobalLayout& L,
+                                           unsigned char* smem, int b,
+                                           const int32_t* rpat) {
+  constexpr int NT = kGlobalThreads;
+  constexpr int NW = NT / kWave;
+  const sfx_params& p = a.p;
+  const int tid = threadIdx.x;
+  const int wv = tid / kWave;
+  const int ln = tid % kWave;
+  const int P = p.max_pattern_len;
+  const int C = p.num_caps;
+  const int R = p.max_occurrences;
+  const int64_t D = a.ix.delta_capacity;
+  int32_t* found = (int32_t*)(smem + L.found);
+  uint32_t* scan = (uint32_t*)(smem + L.scan);
+  int32_t* red = (int32_t*)(smem + L.red);
+  int* misc = (int*)(smem + L.misc);
+  int32_t* lo_lds = (int32_t*)(smem + L.lo);
+  int32_t* dtok = (int32_t*)(smem + L.dtok);
+  uint8_t* mb = kMbLds ? (uint8_t*)(smem + L.dmb)
+                       : a.ws.d_mb + (int64_t)b * delta_mb_stride(D);
+  int64_t dl = *a.ix.delta_len;
+  dl = dl < 0 ? 0 : (dl > D ? D : dl);
+  const int64_t n = dl + 1;
+  const int halo = (P + 3) & ~3;
+  const int4* d4 = reinterpret_cast<const int4*>(a.ix.delta);
+  // Staged words per chunk: x(j0 .. cend - 2) with j0 = c0 - halo, in
+  // int4 words; a thread holds at most kStage4 of them in registers so the
+  // next chunk's loads are in flight while the current one is scanned.
+  constexpr int kStage4 = (kDeltaChunk + 256) / 4 / NT + 1;
+  auto chunk_words = [&](int64_t c0) -> int {
+    const int64_t cend = c0 + kDeltaChunk < n ? c0 + kDeltaChunk : n;
+    return (int)((cend - 1 - (c0 - halo) + 3) / 4);
+  };
+  auto load_chunk = [&](int64_t c0, int4 (&v)[kStage4]) {
+    const int nk4 = chunk_words(c0);
+    const int64_t j0 = c0 - halo;
+#pragma unroll
+    for (int u = 0; u < kStage4; ++u) {
+      const int k4 = tid + u * NT;
+      const int64_t j = j0 + 4 * (int64_t)k4;
+      if (k4 < nk4) {
+        if (j >= 0 && j + 3 < D) {
+          v[u] = d4[j >> 2];
+        } else {
+          v[u].x = j < 0 ? -1 : (j < D ? a.ix.delta[j] : 0);
+          v[u].y = j + 1 < 0 ? -1 : (j + 1 < D ? a.ix.delta[j + 1] : 0);
+          v[u].z = j + 2 < 0 ? -1 : (j + 2 < D ? a.ix.delta[j + 2] : 0);
+          v[u].w = j + 3 < 0 ? -1 : (j + 3 < D ? a.ix.delta[j + 3] : 0);
+        }
+      }
+    }
+  };
+  const int32_t r0 = rpat[0];
+  int4 stage[kStage4];
+  load_chunk(0, stage);
+  int mx = 0;
+  for (int64_t c0 = 0; c0 < n; c0 += kDeltaChunk) {
+    const int64_t cend = c0 + kDeltaChunk < n ? c0 + kDeltaChunk : n;
+    {
+      const int nk4 = chunk_words(c0);
+#pragma unroll
+      for (int u = 0; u < kStage4; ++u) {
+        const int k4 = tid + u * NT;
+        if (k4 < nk4) reinterpret_cast<int4*>(dtok)[k4] = stage[u];
+      }
+    }
+    __syncthreads();
+    if (c0 + kDeltaChunk < n) load_chunk(c0 + kDeltaChunk, stage);
+    // Ends i0 .. i0 + 3 (i0 = c0 + 4g) test x(i - 1) against the newest
+    // pattern token first; only ends that pass walk further back.
+    const int ng = (int)((cend - c0 + 3) / 4);
+    for (int g = tid; g < ng; g += NT) {
+      const int k = 4 * g + halo;  // dtok index of x(i0)
+      const int4 lo4 = reinterpret_cast<const int4*>(dtok)[(k >> 2) - 1];
+      const int4 hi4 = reinterpret_cast<const int4*>(dtok)[k >> 2];
+      const int32_t prev[4] = {lo4.w, hi4.x, hi4.y, hi4.z};  // x(i - 1)
+      const int64_t i0 = c0 + 4 * (int64_t)g;
+      uint32_t word = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (prev[q] == r0 && i0 + q < cend) {
+          int m = 1;
+          const int base = k - 1 + q;
+          while (m < P && dtok[base - m] == rpat[m]) ++m;
+          word |= (uint32_t)m << (8 * q);
+          mx = max(mx, m);
+        }
+      }
+      *reinterpret_cast<uint32_t*>(mb + i0) = word;
+    }
+    __syncthreads();
+  }
+  mx = wave_max_i32(mx);
+  if (ln == 0) red[wv] = mx;
+  __syncthreads();
+  if (tid == 0) {
+    int m = 0;
+    for (int w = 0; w < NW; ++w) m = max(m, red[w]);
+    misc[0] = m;
+  }
+  __syncthreads();
+  const int lo_full = misc[0];
+  SFX_TRACE_POINT(2);
+  for (int c = tid; c < C; c += NT) lo_lds[c] = min(lo_full, p.caps[c]);
+  __syncthreads();
+  for (int g0 = 0; g0 < C; g0 += 8)
+    compact_first_r<NT>(mb, n, lo_lds + g0, min(8, C - g0), R,
+                        a.ws.d_end + ((int64_t)b * C + g0) * R, found + g0,
+                        scan);
+  __syncthreads();
+  SFX_TRACE_POINT(3);
+  for (int c = tid; c < C; c += NT) {
+    const int lo = lo_lds[c];
+    const int cnt = lo > 0 ? found[c] : 0;
+    a.ws.d_len[(int64_t)b * C + c] = lo;
+    a.ws.d_cnt[(int64_t)b * C + c] = cnt;
+    if (a.out.d_len) a.out.d_len[(int64_t)b * C + c] = lo;
+    if (a.out.d_cnt) a.out.d_cnt[(int64_t)b * C + c] = cnt;
+  }
+  if (a.out.d_pos) {
+    for (int e = tid; e < C * R; e += NT) {
+      const int c = e / R;
+      const int r = e % R;
+      const int lo = lo_lds[c];
+      const int cnt = lo > 0 ? found[c] : 0;
+      const int64_t end =
+          r < cnt ? (int64_t)a.ws.d_end[((int64_t)b * C + c) * R + r] : 0;
+      int64_t v = end - lo;
+      v = v < 0 ? 0 : v;
+      a.out.d_pos[((int64_t)b * C + c) * R + r] = v;
+    }
+  }
+}
+
+__device__ __forceinline__ void global_body(const GlobalArgs& a,
+                                            unsigned char* smem, int b,
+                                            bool sa_role) {
+  constexpr int NT = kGlobalThreads;
+  constexpr int NW = NT / kWave;
+  const sfx_params& p = a.p;
+  const int tid = threadIdx.x;
+  const int wv = tid / kWave;
+  const int ln = tid % kWave;
+  const int P = p.max_pattern_len;
+  const int C = p.num_caps;
+  const int R = p.max_occurrences;
+  const int K = p.k;
+  const int Rp = (R + 3) & ~3;
+  const GlobalLayout L = global_layout(P, C, R, K, a.merge_waves, a.mb_lds);
+  int32_t* rpat = (int32_t*)(smem + L.rpat);
+  int64_t* lbs = (int64_t*)(smem + L.lb);
+  int64_t* ubs = (int64_t*)(smem + L.ub);
+  int32_t* found = (int32_t*)(smem + L.found);
+  uint32_t* scan = (uint32_t*)(smem + L.scan);
+  int32_t* red = (int32_t*)(smem + L.red);
+  int* misc = (int*)(smem + L.misc);
+  const int64_t N = a.ix.capacity;
+  const int64_t D = a.ix.delta_capacity;
+  SFX_TRACE_POINT(0);
+
+  // Query tail, newest first: rpat[t] = tail token t back from the end;
+  // -3 past the start (global_index.py:493-501).
+  int64_t qlen;
+  if (a.step) {
+    const RowState st = row_state(a.bt, b);
+    if (!st.mask) return;  // masked rows: the local kernel writes them
+    const int64_t q = st.q;
+    qlen = q < P ? q : P;
+    for (int t = tid; t < P; t += NT) {
+      const int64_t idx = q - 1 - t;
+      int32_t v = -3;
+      if (idx >= 0) {
+        const int64_t x = idx < a.bt.seq - 1 ? idx : a.bt.seq - 1;
+        v = updated_token(a.bt, b, st, x);
+      }
+      rpat[t] = v;
+    }
+  } else {
+    qlen = a.qlen[b];
+    const int64_t Q = a.qwidth;
+    for (int t = tid; t < P; t += NT) {
+      const int64_t idx = qlen - 1 - t;
+      int32_t v = -3;
+      if (idx >= 0) v = a.query[(int64_t)b * Q + (idx < Q - 1 ? idx : Q - 1)];
+      rpat[t] = v;
+    }
+  }
+  const int plen = (int)(qlen < 0 ? 0 : (qlen < P ? qlen : P));
+  __syncthreads();
+  SFX_TRACE_POINT(1);
+
+  if (sa_role) {
+    // ---- SA interval search for every suffix length of the tail.
+    constexpr int G = kSearchGroup;
+    const int ngroups = NT / G;
+    const int g = tid / G;
+    for (int l = g + 1; l <= P; l += ngroups) {
+      int64_t lo = 0, hi = 0;
+      if (l <= plen) {
+        auto pat_at = [&](int j) -> int32_t { return rpat[l - 1 - j]; };
+        kary_bounds<G>(a.ix.sa, a.ix.corpus, N, a.ix.sa_key,
+                       (int)a.ix.key_width, pat_at, l, lo, hi);
+      }
+      if (tid % G == 0) {
+        lbs[l - 1] = lo;
+        ubs[l - 1] = hi;
+      }
+    }
+    __syncthreads();
+    SFX_TRACE_POINT(2);
+    if (wv == 0) {
+      for (int c = 0; c < C; ++c) {
+        const int cap = p.caps[c];
+        int best = 0;
+        for (int base = 1; base <= P; base += kWave) {
+          const int l = base + ln;
+          const bool f = l <= P && l <= cap && l <= plen &&
+                         ubs[l - 1] > lbs[l - 1];
+          const uint64_t m = ballot(f);
+          if (m) best = base + 63 - __builtin_clzll(m);
+        }
+        if (ln == 0) {
+          const int64_t s0 = best ? lbs[best - 1] : 0;
+          const int64_t e0 = best ? ubs[best - 1] : 0;
+          a.ws.sa_len[(int64_t)b * C + c] = best;
+          a.ws.sa_s[(int64_t)b * C + c] = (int32_t)s0;
+          a.ws.sa_e[(int64_t)b * C + c] = (int32_t)e0;
+          if (a.out.sa_len) a.out.sa_len[(int64_t)b * C + c] = best;
+          if (a.out.sa_start) a.out.sa_start[(int64_t)b * C + c] = s0;
+          if (a.out.sa_end) a.out.sa_end[(int64_t)b * C + c] = e0;
+        }
+      }
+    }
+  } else {
+    if (a.mb_lds)
+      delta_role<true>(a, L, smem, b, rpat);
+    else
+      delta_role<false>(a, L, smem, b, rpat);
+  }
+
+  // ---- Handover: the second role to finish merges the row.
+  SFX_TRACE_POINT(4);
+  if (!block_arrive(a.ws.join + b, 2u, misc + 1)) return;
+  SFX_TRACE_POINT(5);
+
+  const int nmw = a.merge_waves;
+  int32_t* chain = (int32_t*)(smem + L.chain);
+  int32_t* res_nv = (int32_t*)(smem + L.nv);
+  float* res_score = (float*)(smem + L.score);
+  int32_t* res_len = (int32_t*)(smem + L.rlen);
+  int32_t* res_occ = (int32_t*)(smem + L.rocc);
+  int64_t dl_live = *a.ix.delta_len;
+  for (int c = wv; c < C && wv < nmw; c += nmw) {
+    // Source selection per cap, before and after dedup (:321-337).
+    auto pre = [&](int cc, int& len, int& src) {
+      const int sl = a.ws.sa_len[(int64_t)b * C + cc];
+      const int dlen = a.ws.d_len[(int64_t)b * C + cc];
+      const bool use_sa = sl >= dlen && sl > 0;
+      const bool use_d = dlen > sl && dlen > 0;
+      len = use_sa ? sl : (use_d ? dlen : 0);
+      src = (use_sa ? 1 : 0) + (use_d ? 2 : 0);
+    };
+    int len, src;
+    pre(c, len, src);
+    if (c > 0) {
+      int plen0, psrc;
+      pre(c - 1, plen0, psrc);
+      if (len == plen0 && src == psrc && len > 0) {
+        len = 0;
+        src = 0;
+      }
+    }
+    const int64_t sa_s = a.ws.sa_s[(int64_t)b * C + c];
+    const int64_t ilen = (int64_t)a.ws.sa_e[(int64_t)b * C + c] - sa_s;
+    int occ = 0;
+    if (src == 1) occ = (int)(ilen < R ? ilen : R);
+    if (src == 2) occ = a.ws.d_cnt[(int64_t)b * C + c];
+    int32_t* mpos = (int32_t*)(smem + L.mpos) + wv * Rp;
+    int32_t* mcache = (int32_t*)(smem + L.mcache) + (int64_t)wv * R * K;
+    // Occurrence starts: strided SA sample (:339-352) or delta ends - len.
+    for (int r = ln; r < occ; r += kWave) {
+      int32_t pos;
+      if (src == 1) {
+        int64_t idx = ilen > R ? sa_s + ((int64_t)r * ilen) / R : sa_s + r;
+        idx = idx < 0 ? 0 : (idx > N - 1 ? N - 1 : idx);
+        pos = a.ix.sa[idx];
+      } else {
+        const int64_t e =
+            (int64_t)a.ws.d_end[((int64_t)b * C + c) * R + r] - len;
+        pos = (int32_t)(e < 0 ? 0 : e);
+      }
+      mpos[r] = pos;
+    }
+    wave_lds_sync();
+    SFX_TRACE_POINT(10);
+    // Continuations (:443-463): in range, not PAD, not negative.
+    const int32_t* srcbuf = src == 1 ? a.ix.corpus : a.ix.delta;
+    const int64_t nbuf = src == 1 ? N : D;
+    const int64_t slen = src == 1 ? N : dl_live;
+    // One occurrence row per lane: its K tokens are independent loads.
+    for (int r = ln; r < occ; r += kWave) {
+      const int64_t base = (int64_t)mpos[r] + len;
+      int32_t* dst = mcache + r * K;
+      for (int j0 = 0; j0 < K; j0 += 16) {
+        int32_t v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int64_t idx = base + j0 + u;
+          v[u] = -1;
+          if (j0 + u < K && idx < slen && idx >= 0)
+            v[u] = srcbuf[idx < nbuf - 1 ? idx : nbuf - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+          if (j0 + u < K) dst[j0 + u] = (v[u] != kPad && v[u] >= 0) ? v[u] : -1;
+      }
+    }
+    wave_lds_sync();
+    SFX_TRACE_POINT(11);
+    if (a.out.len && ln == 0) a.out.len[(int64_t)b * C + c] = len;
+    if (a.out.occ && ln == 0) a.out.occ[(int64_t)b * C + c] = occ;
+    if (a.out.cont) {
+      int32_t* o = a.out.cont + ((int64_t)b * C + c) * R * K;
+      for (int e = ln; e < R * K; e += kWave)
+        o[e] = e < occ * K ? mcache[e] : -1;
+    }
+    if (a.need_expand) {
+      const int64_t cap = spec_cap(p, len);
+      auto cont_at = [&](int r, int d) -> int32_t { return mcache[r * K + d]; };
+      const ExpandResult er = expand_wave<false>(
+          cont_at, NoWeight(), R, occ, K, cap, p.min_token_prob, p.alpha,
+          (int32_t*)(smem + L.mA) + wv * Rp, nullptr, chain + c * K);
+      SFX_TRACE_POINT(12);
+      if (ln == 0) {
+        res_nv[c] = er.nv;
+        res_score[c] = er.score;
+        res_len[c] = len;
+        res_occ[c] = occ;
+      }
+    }
+  }
+  if (!a.need_expand) return;
+  __syncthreads();
+  SFX_TRACE_POINT(6);
+  // Best cap: first argmax of the raw score (proposer.py:308-314,
+  // global_index.py:427-436).
+  if (tid == 0) {
+    int best = 0;
+    for (int c = 1; c < C; ++c)
+      if (res_score[c] > res_score[best]) best = c;
+    const int64_t cap = spec_cap(p, res_len[best]);
+    const int64_t cap0 = cap > 0 ? cap : 0;
+    misc[2] = best;
+    misc[3] = (int)((int64_t)res_nv[best] < cap0 ? res_nv[best] : cap0);
+  }
+  __syncthreads();
+  const int best = misc[2];
+  const int emit = misc[3];
+  const int32_t* bchain = chain + best * K;
+  if (!a.step) {
+    if (a.out.draft)
+      for (int j = tid; j < K; j += NT)
+        a.out.draft[(int64_t)b * K + j] = j < emit ? bchain[j] : -1;
+    if (tid == 0) {
+      if (a.out.emit) a.out.emit[b] = emit;
+      if (a.out.draft_len) a.out.draft_len[b] = res_len[best];
+      if (a.out.draft_occ) a.out.draft_occ[b] = res_occ[best];
+      if (a.out.draft_score) a.out.draft_score[b] = res_score[best];
+    }
+    return;
+  }
+  for (int j = tid; j < K; j += NT)
+    a.ws.g_chain[(int64_t)b * K + j] = bchain[j];
+  if (tid == 0) {
+    a.ws.g_emit[b] = emit;
+    a.ws.g_score[b] = res_score[best];
+  }
+  if (block_arrive(a.ws.pick + b, 2u, misc + 4))
+    pick_row(b, K, a.ws, a.draft, a.num_valid);
+}
+
+}  // namespace sfx

@@ -1,0 +1,307 @@
+// Local-role device code: one 512-thread workgroup per request row.
+// Included by local.hip (standalone kernel) and step.hip (fused step).
+#pragma once
+
+#include "pick.h"
+#include "sfx_common.h"
+#include "step_ws.h"
+
+namespace sfx {
+
+enum LocalMode { kLocalGather = 0, kLocalForward = 1, kLocalStep = 2 };
+
+struct LocalArgs {
+  sfx_params p;
+  sfx_batch bt;
+  int mode;
+  int global_on;
+  int64_t* cand_out;   // gather
+  int32_t* cont_out;
+  int64_t* occ_out;
+  int32_t* draft;      // forward / step
+  int32_t* num_valid;
+  int64_t* len_out;    // forward
+  int64_t* occ1_out;
+  float* score_out;
+  int32_t* new_counts;  // step
+  StepWs ws;
+};
+
+struct LocalLayout {
+  int row, mb, pat, hist, cand, found, scan, occ, A, chain, nv, score, misc,
+      total;
+};
+
+__host__ __device__ inline int lds_take(int& off, int bytes) {
+  const int o = off;
+  off += (bytes + 15) & ~15;
+  return o;
+}
+
+// compact_first_r reads whole 16-byte words of every thread's segment.
+__host__ __device__ inline int mb_bytes(int n, int nthreads) {
+  const int seg = (((n + nthreads - 1) / nthreads) + 15) & ~15;
+  return seg * nthreads;
+}
+
+__host__ __device__ inline LocalLayout local_layout(int S, int P, int C,
+                                                    int R, int K,
+                                                    int nwaves) {
+  const int nthreads = nwaves * kWave;
+  LocalLayout L;
+  int off = 0;
+  L.row = lds_take(off, S * 4);
+  L.mb = lds_take(off, mb_bytes(S, nthreads));
+  L.pat = lds_take(off, P * 4);
+  L.hist = lds_take(off, (P + 1) * 4);
+  L.cand = lds_take(off, C * 4);
+  L.found = lds_take(off, C * 4);
+  L.scan = lds_take(off, 4 * nwaves * 8);
+  L.occ = lds_take(off, C * R * 4);
+  L.A = lds_take(off, nwaves * ((R + 3) & ~3) * 4);
+  L.chain = lds_take(off, C * K * 4);
+  L.nv = lds_take(off, C * 4);
+  L.score = lds_take(off, C * 4);
+  L.misc = lds_take(off, 64);
+  L.total = off;
+  return L;
+}
+
+constexpr int kLocalThreads = 512;
+
+__device__ __forceinline__ void local_body(const LocalArgs& a,
+                                           unsigned char* smem, int b) {
+  constexpr int NT = kLocalThreads;
+  constexpr int NW = NT / kWave;
+  const sfx_params& p = a.p;
+  const int tid = threadIdx.x;
+  const int wv = tid / kWave;
+  const int ln = tid % kWave;
+  const int S = (int)a.bt.seq;
+  const int P = p.max_pattern_len;
+  const int C = p.num_thresholds;
+  const int R = p.max_occurrences;
+  const int K = p.k;
+  const LocalLayout L = local_layout(S, P, C, R, K, NW);
+  int32_t* row = (int32_t*)(smem + L.row);
+  uint8_t* mbuf = (uint8_t*)(smem + L.mb);
+  int32_t* pat = (int32_t*)(smem + L.pat);
+  int32_t* hist = (int32_t*)(smem + L.hist);
+  int32_t* cand = (int32_t*)(smem + L.cand);
+  int32_t* found = (int32_t*)(smem + L.found);
+  uint32_t* scan = (uint32_t*)(smem + L.scan);
+  int32_t* occ = (int32_t*)(smem + L.occ);
+  int32_t* Abuf = (int32_t*)(smem + L.A);
+  int32_t* chain = (int32_t*)(smem + L.chain);
+  int32_t* res_nv = (int32_t*)(smem + L.nv);
+  float* res_score = (float*)(smem + L.score);
+  int* misc = (int*)(smem + L.misc);
+
+  SFX_TRACE_POINT(0);
+  const RowState st = row_state(a.bt, b);
+  const int64_t q = st.q;
+
+  // Stage the row, then apply this step's scatter (proposer.py:162-184).
+  int32_t* grow = a.bt.tokens + (int64_t)b * S;
+  if ((S & 3) == 0 && (((uintptr_t)grow) & 15) == 0) {
+    const int4* src = reinterpret_cast<const int4*>(grow);
+    int4* dst = reinterpret_cast<int4*>(row);
+    for (int i = tid; i < S / 4; i += NT) dst[i] = src[i];
+  } else {
+    for (int i = tid; i < S; i += NT) row[i] = grow[i];
+  }
+  __syncthreads();
+  if (a.bt.sampled) {
+    const int32_t* sp = a.bt.sampled + (int64_t)b * a.bt.num_sampled;
+    for (int64_t j = tid; j < a.bt.num_sampled; j += NT) {
+      const int64_t pos = st.base + j;
+      const int32_t v = sp[j];
+      if (j < st.cnt && v != -1 && pos < S && pos >= 0) {
+        row[pos] = v;
+        grow[pos] = v;
+      }
+    }
+    if (a.new_counts && tid == 0) a.new_counts[b] = (int32_t)q;
+  }
+  __syncthreads();
+
+  if (a.mode == kLocalStep && !st.mask) {
+    for (int j = tid; j < K; j += NT) a.draft[(int64_t)b * K + j] = -1;
+    if (tid == 0) a.num_valid[b] = 0;
+    return;
+  }
+
+  SFX_TRACE_POINT(1);
+  // Newest-first pattern, -2 fill (local_matcher.py:103-112).
+  for (int t = tid; t < P; t += NT) {
+    const int64_t idx = q - 1 - t;
+    pat[t] = idx >= 0 ? row[idx < S - 1 ? idx : S - 1] : -2;
+  }
+  for (int i = tid; i <= P; i += NT) hist[i] = 0;
+  __syncthreads();
+
+  // match_back, zero at i >= q (local_matcher.py:114-132).
+  for (int i = tid; i < S; i += NT) {
+    int m = 0;
+    if ((int64_t)i < q) {
+      for (int t = 0; t < P; ++t) {
+        const int j = i - 1 - t;
+        const int32_t x = j >= 0 ? row[j] : -1;
+        if (x != pat[t]) break;
+        ++m;
+      }
+    }
+    mbuf[i] = (uint8_t)m;
+    if (m > 0) atomicAdd(&hist[m], 1);
+  }
+  __syncthreads();
+
+  SFX_TRACE_POINT(2);
+  // Candidates: thr-th largest match_back = largest L with #{mb >= L} >=
+  // thr; zero below min_match_len or when masked; adjacent duplicates
+  // zeroed (local_matcher.py:134-157).  Wave 0: suffix sums of the
+  // histogram, then one ballot per threshold (#{mb >= L} is monotone in L,
+  // so the largest qualifying L is the number of qualifying L).
+  if (wv == 0) {
+    int carry = 0;
+    for (int top = P; top >= 1; top -= kWave) {
+      const int Lv = top - ln;
+      int x = Lv >= 1 ? hist[Lv] : 0;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const int y = __shfl_up(x, o);
+        if (ln >= o) x += y;
+      }
+      x += carry;
+      if (Lv >= 1) hist[Lv] = x;
+      carry = __shfl(x, kWave - 1);
+    }
+    wave_lds_sync();
+    int maxthr = p.thresholds[0];
+    for (int c = 1; c < C; ++c) maxthr = max(maxthr, p.thresholds[c]);
+    const int w = min(maxthr, S);
+    int prev_raw = -1;
+    for (int c = 0; c < C; ++c) {
+      const int thr = p.thresholds[c];
+      int v = 0;
+      if (thr <= w) {
+        const int t = thr < 1 ? 1 : thr;
+        for (int base = 1; base <= P; base += kWave) {
+          const int Lv = base + ln;
+          v += popc(ballot(Lv <= P && hist[Lv] >= t));
+        }
+      }
+      if (!(v >= p.min_match_len && st.mask)) v = 0;
+      const int raw = v;
+      if (c > 0 && raw == prev_raw) v = 0;
+      prev_raw = raw;
+      if (ln == 0) cand[c] = v;
+    }
+  }
+  __syncthreads();
+
+  SFX_TRACE_POINT(3);
+  // First R ascending ends per candidate (triton_kernels.py:217-243
+  // semantics): one ordered pass per group of 8 candidates.
+  for (int g0 = 0; g0 < C; g0 += 8)
+    compact_first_r<NT>(mbuf, S, cand + g0, min(8, C - g0), R, occ + g0 * R,
+                        found + g0, scan);
+  __syncthreads();
+
+  SFX_TRACE_POINT(4);
+  if (a.mode == kLocalGather) {
+    for (int c = tid; c < C; c += NT) {
+      if (a.cand_out) a.cand_out[(int64_t)b * C + c] = cand[c];
+      if (a.occ_out) a.occ_out[(int64_t)b * C + c] = min(found[c], R);
+    }
+    if (a.cont_out) {
+      const int total = C * R * K;
+      int32_t* out = a.cont_out + (int64_t)b * total;
+      for (int e = tid; e < total; e += NT) {
+        const int c = e / (R * K);
+        const int r = (e / K) % R;
+        const int j = e % K;
+        int32_t v = -1;
+        if (r < min(found[c], R)) {
+          const int64_t idx = (int64_t)occ[c * R + r] + j;
+          if (idx < q) v = row[idx < S - 1 ? idx : S - 1];
+        }
+        out[e] = v;
+      }
+    }
+    return;
+  }
+
+  // One wave per candidate: majority-vote expansion from the LDS row.
+  for (int c = wv; c < C; c += NW) {
+    const int cv = cand[c];
+    const int64_t oc = cv > 0 ? (int64_t)min(found[c], R) : 0;
+    const int64_t cap = spec_cap(p, cv);
+    const int32_t* oc_list = occ + c * R;
+    auto cont_at = [&](int r, int d) -> int32_t {
+      const int64_t idx = (int64_t)oc_list[r] + d;
+      return idx < q ? row[idx < S - 1 ? idx : S - 1] : -1;
+    };
+    const ExpandResult er = expand_wave<false>(
+        cont_at, NoWeight(), R, oc, K, cap, p.min_token_prob, p.alpha,
+        Abuf + wv * ((R + 3) & ~3), nullptr, chain + c * K);
+    if (ln == 0) {
+      res_nv[c] = er.nv;
+      res_score[c] = er.score;
+    }
+  }
+  __syncthreads();
+
+  SFX_TRACE_POINT(5);
+  // select_local_best (local_matcher.py:245-263).
+  if (tid == 0) {
+    int best = 0;
+    float bkey = local_key(res_score[0], cand[0]);
+    for (int c = 1; c < C; ++c) {
+      const float key = local_key(res_score[c], cand[c]);
+      if (key > bkey) {
+        bkey = key;
+        best = c;
+      }
+    }
+    const int64_t cap = spec_cap(p, cand[best]);
+    const int64_t cap0 = cap > 0 ? cap : 0;
+    misc[0] = best;
+    misc[1] = (int)((int64_t)res_nv[best] < cap0 ? res_nv[best] : cap0);
+  }
+  __syncthreads();
+  const int best = misc[0];
+  const int emit = misc[1];
+  const int32_t* bchain = chain + best * K;
+
+  if (a.mode == kLocalForward) {
+    for (int j = tid; j < K; j += NT)
+      a.draft[(int64_t)b * K + j] = j < emit ? bchain[j] : -1;
+    if (tid == 0) {
+      a.num_valid[b] = emit;
+      if (a.len_out) a.len_out[b] = cand[best];
+      if (a.occ1_out)
+        a.occ1_out[b] = cand[best] > 0 ? min(found[best], R) : 0;
+      if (a.score_out) a.score_out[b] = res_score[best];
+    }
+    return;
+  }
+
+  // Decode step.
+  if (!a.global_on) {
+    for (int j = tid; j < K; j += NT)
+      a.draft[(int64_t)b * K + j] = j < emit ? bchain[j] : -1;
+    if (tid == 0) a.num_valid[b] = emit;
+    return;
+  }
+  for (int j = tid; j < K; j += NT)
+    a.ws.l_chain[(int64_t)b * K + j] = bchain[j];
+  if (tid == 0) {
+    a.ws.l_emit[b] = emit;
+    a.ws.l_score[b] = res_score[best];
+  }
+  if (block_arrive(a.ws.pick + b, 2u, misc + 2))
+    pick_row(b, K, a.ws, a.draft, a.num_valid);
+}
+
+}  // namespace sfx

@@ -111,7 +111,7 @@ __global__ __launch_bounds__(kSearchThreads) void k_sa_search(
   pl = pl < 0 ? 0 : (pl > width ? width : pl);
   auto pat_at = [&](int j) -> int32_t { return pr[j]; };
   int64_t lo, hi;
-  kary_bounds<kOpGroup>(sa, corpus, n, pat_at, (int)pl, lo, hi);
+  kary_bounds<kOpGroup>(sa, corpus, n, nullptr, 0, pat_at, (int)pl, lo, hi);
   if (threadIdx.x % kOpGroup == 0) {
     lower[row] = lo;
     upper[row] = hi;
@@ -187,6 +187,17 @@ __global__ __launch_bounds__(256) void k_expand(ExpandArgs a) {
 }  // namespace sfx
 
 using namespace sfx;
+
+#ifdef SFX_TRACE
+__device__ uint64_t* sfx_trace_buf = nullptr;
+
+// Profiling builds only: point the phase-timestamp buffer (device memory,
+// 16 u64 per block) at `buf`, or disable with NULL.
+extern "C" int sfx_trace_set(uint64_t* buf) {
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(sfx_trace_buf), &buf,
+                                sizeof(buf));
+}
+#endif
 
 extern "C" int sfx_abi_version(void) { return SFX_ABI_VERSION; }
 

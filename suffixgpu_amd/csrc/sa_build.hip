@@ -309,6 +309,18 @@ __global__ __launch_bounds__(kSortThreads) void k_grp_rank(
   }
 }
 
+// keys[r * W + j] = corpus[sa[r] + j] (-1 at or past n).
+__global__ __launch_bounds__(256) void k_rank_keys(const int32_t* corpus,
+                                                 const int32_t* sa, int64_t n,
+                                                 int W, int32_t* keys) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= n * W) return;
+  const int64_t r = e / W;
+  const int j = (int)(e - r * W);
+  const int64_t pos = (int64_t)sa[r] + j;
+  keys[e] = pos < n && pos >= 0 ? corpus[pos] : -1;
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void k_sa_out(const uint32_t* sa, int64_t m,
                                                 int64_t n_total, T* out) {
@@ -326,6 +338,18 @@ static int bits_for(uint64_t maxval) {
 }  // namespace sfx
 
 using namespace sfx;
+
+extern "C" int sfx_sa_keys(const int32_t* corpus, const int32_t* sa,
+                           int64_t n, int64_t width, int32_t* keys,
+                           hipStream_t stream) {
+  if (n < 0 || width < 4 || width > 32 || (width & 3)) return SFX_EINVAL;
+  if (n == 0) return 0;
+  if (!corpus || !sa || !keys) return SFX_EINVAL;
+  const int64_t total = n * width;
+  hipLaunchKernelGGL(k_rank_keys, dim3((unsigned)((total + 255) / 256)),
+                     dim3(256), 0, stream, corpus, sa, n, (int)width, keys);
+  return (int)hipGetLastError();
+}
 
 extern "C" size_t sfx_sa_build_workspace_size(int64_t m) {
   if (m < 0) return 0;

@@ -1,11 +1,14 @@
 // Suffix-array interval search by a group of G lanes (k-ary search).
 //
 // The reference resolves each bound with ceil(log2(n+1)) dependent binary
-// probes (suffix_gpu/sa_search.py:66-107).  Here G lanes probe G ranks of
-// the current range at once, so one round trip to the SA and corpus cuts
-// the range (G+1)-fold; lower and upper bound share their probes until
-// their ranges separate, then each gets G/2 lanes.  Only the exact bounds
-// are returned, which is all the reference's result depends on.
+// probes, each an SA read followed by corpus reads (suffix_gpu/
+// sa_search.py:66-107).  Here G lanes probe G ranks of the current range
+// at once, so one round of loads cuts the range (G+1)-fold; lower and
+// upper bound share their probes until their ranges separate, then each
+// gets G/2 lanes.  With a key array (the first kw tokens of every rank's
+// suffix, built with the suffix array) a probe is a single row load.  Only
+// the exact bounds are returned, which is all the reference's result
+// depends on.
 #pragma once
 
 #include "sfx_common.h"
@@ -38,6 +41,43 @@ __device__ __forceinline__ int cmp_suffix(const int32_t* __restrict__ sa,
   return 0;
 }
 
+// The same comparison from the rank's key row: keys[rank * kw + j] holds
+// corpus[sa[rank] + j] (or -1 past the end) for j < kw, so patterns of up
+// to kw tokens are decided by one row load (kw * 4 bytes, one line for
+// kw = 32); longer patterns continue in the corpus.
+template <class PatFn>
+__device__ __forceinline__ int cmp_suffix_key(
+    const int32_t* __restrict__ keys, int kw,
+    const int32_t* __restrict__ sa, const int32_t* __restrict__ corpus,
+    int64_t n, int64_t rank, PatFn pat_at, int plen) {
+  const int4* row = reinterpret_cast<const int4*>(keys + rank * kw);
+  const int kn = plen < kw ? plen : kw;
+  int4 w[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    if (4 * q < kn) w[q] = row[q];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    const int t4[4] = {w[q].x, w[q].y, w[q].z, w[q].w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = 4 * q + u;
+      if (j >= kn) break;
+      const int32_t pj = pat_at(j);
+      if (t4[u] != pj) return t4[u] < pj ? -1 : 1;
+    }
+  }
+  if (plen <= kw) return 0;
+  const int64_t pos = sa[rank];
+  for (int j = kw; j < plen; ++j) {
+    const int64_t idx = pos + j;
+    const int32_t t = idx < n ? corpus[idx] : -1;
+    const int32_t pj = pat_at(j);
+    if (t != pj) return t < pj ? -1 : 1;
+  }
+  return 0;
+}
+
 __device__ __forceinline__ int64_t kary_probe(int64_t lo, int64_t hi,
                                               int k, int np) {
   return lo + ((hi - lo) * (int64_t)(k + 1)) / (np + 1);
@@ -60,11 +100,13 @@ __device__ __forceinline__ void kary_update(int64_t& lo, int64_t& hi,
 // Exact lower bound (first rank with cmp >= 0) and upper bound (first rank
 // with cmp > 0) of one pattern.  Called by all G lanes of an aligned group
 // with identical arguments; returns the bounds on every lane of the group.
+// keys (kw = key width, 4 <= kw <= 32, kw % 4 == 0) may be NULL: then the
+// comparison reads sa and the corpus.
 template <int G, class PatFn>
-__device__ void kary_bounds(const int32_t* __restrict__ sa,
-                            const int32_t* __restrict__ corpus, int64_t n,
-                            PatFn pat_at, int plen, int64_t& lower,
-                            int64_t& upper) {
+__device__ __forceinline__ void kary_bounds(
+    const int32_t* __restrict__ sa, const int32_t* __restrict__ corpus,
+    int64_t n, const int32_t* __restrict__ keys, int kw, PatFn pat_at,
+    int plen, int64_t& lower, int64_t& upper) {
   static_assert(G >= 2 && G <= 32 && (64 % G) == 0, "group size");
   const int ln = lane_id();
   const int gl = ln % G;
@@ -89,7 +131,9 @@ __device__ void kary_bounds(const int32_t* __restrict__ sa,
       hi = upper_half ? hi2 : hi1;
     }
     const int64_t probe = kary_probe(lo, hi, k, np);
-    const int c = cmp_suffix(sa, corpus, n, probe, pat_at, plen);
+    const int c =
+        keys ? cmp_suffix_key(keys, kw, sa, corpus, n, probe, pat_at, plen)
+             : cmp_suffix(sa, corpus, n, probe, pat_at, plen);
     const uint64_t m1 = ballot(c >= 0);
     const uint64_t m2 = ballot(c > 0);
     const uint32_t full = G == 32 ? 0xffffffffu : ((1u << G) - 1u);

@@ -8,6 +8,21 @@
 
 #include "suffixgpu_amd.h"
 
+// Phase timestamps for profiling builds (-DSFX_TRACE): thread 0 of each
+// block stores wall_clock64() into sfx_trace_buf[block * 16 + slot].
+#ifdef SFX_TRACE
+extern __device__ uint64_t* sfx_trace_buf;
+#define SFX_TRACE_POINT(slot)                                          \
+  do {                                                                 \
+    if (threadIdx.x == 0 && sfx_trace_buf)                             \
+      sfx_trace_buf[(uint64_t)blockIdx.x * 16 + (slot)] = wall_clock64(); \
+  } while (0)
+#else
+#define SFX_TRACE_POINT(slot) \
+  do {                        \
+  } while (0)
+#endif
+
 namespace sfx {
 
 constexpr int kWave = 64;
@@ -82,103 +97,199 @@ struct ExpandResult {
   float score;  // sum of the chain probability over valid slots < cap
 };
 
+// max votes first, then the smallest (signed) token
+__device__ __forceinline__ bool vote_better(int cnt, int tok, int bcnt,
+                                            int btok) {
+  return cnt > bcnt || (cnt == bcnt && tok < btok);
+}
+
+// Smallest v in [1, nact] with fl32(prob * fl32(v / denom)) >= min_prob,
+// or nact + 1 when none (the product is monotone in v for denom > 0 and
+// prob >= 0).  Returns 1 when the early exit does not apply.
+__device__ __forceinline__ int min_votes(float prob, float denom,
+                                         float min_prob, int nact) {
+  if (!(min_prob > 0.0f) || !(denom > 0.0f) || !(prob > 0.0f)) return 1;
+  auto pass = [&](int v) {
+    return __fmul_rn(prob, __fdiv_rn((float)v, denom)) >= min_prob;
+  };
+  if (!pass(nact)) return nact + 1;
+  // Binary search for the first passing v in [1, nact].
+  int lo = 1, hi = nact;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (pass(mid)) hi = mid; else lo = mid + 1;
+  }
+  return lo;
+}
+
 // Wave-cooperative depth-wise majority vote of one candidate
 // (suffix_gpu/expand.py:59-147 == triton_kernels.py:139-215).
 //
 // Occurrence r (< R) is row r of the candidate's continuation block;
 // cont_at(r, d) returns its token at depth d and is only called for rows
 // still on the chain (r < occ and every earlier depth voted for them).
-// Per depth the active rows (token != -1) are compacted into A (in row
-// order), every lane counts the votes of its compacted entries by
-// broadcast LDS reads, and a 64-bit wave max picks (max votes, min token).
 // chain_out[0..K) receives the chain (-1 past the first invalid depth).
+//
+// Unit votes with R <= 128 (two rows per lane) count each distinct active
+// value with two ballots: the first unprocessed lane's value is broadcast,
+// its matches are counted and retired, and the loop stops once the
+// unprocessed rows cannot outvote the best so far -- one iteration per
+// distinct token, usually a handful.  Larger R and weighted votes compact
+// the active rows into A (row order) and count by broadcast LDS reads.
 // A holds R ints; W (weighted votes only) R floats, both LDS.
 template <bool kWeighted, class ContFn, class WeightFn>
-__device__ ExpandResult expand_wave(ContFn cont_at, WeightFn weight_at,
+__device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
+                                                    WeightFn weight_at,
                                     int R, int64_t occ, int K, int64_t cap,
                                     float min_prob, float alpha, int* A,
                                     float* W, int32_t* chain_out) {
   const int ln = lane_id();
-  const int nslot = (R + kWave - 1) / kWave;  // <= 32 (R <= 2048)
-  uint32_t ok = 0;
-  for (int s = 0; s < nslot; ++s) {
-    int r = s * kWave + ln;
-    if (r < R && (int64_t)r < occ) ok |= 1u << s;
-  }
   float prob = 1.0f;
   float score = 0.0f;
   int nv = 0;
   int d = 0;
-  for (; d < K; ++d) {
-    int nact = 0;
-    for (int s = 0; s < nslot; ++s) {
-      const int r = s * kWave + ln;
-      const bool okr = (ok >> s) & 1u;
-      int c = -1;
-      if (okr) c = cont_at(r, d);
-      const bool act = okr && c != -1;
-      const uint64_t m = ballot(act);
-      if (act) {
-        const int pos = nact + rank_lt(m);
-        A[pos] = c;
-        if (kWeighted) W[pos] = weight_at(r);
-      }
-      nact += popc(m);
-      if (!act) ok &= ~(1u << s);
-    }
-    wave_lds_sync();
-    if (nact == 0) break;
-    uint64_t best = 0;
-    for (int i = ln; i < nact; i += kWave) {
-      const int x = A[i];
-      uint32_t vbits;
-      if (!kWeighted) {
-        int v = 0;
-        int j = 0;
-        for (; j + 4 <= nact; j += 4) {
-          const int4 q = *reinterpret_cast<const int4*>(A + j);
-          v += (q.x == x) + (q.y == x) + (q.z == x) + (q.w == x);
+  if (!kWeighted && R <= 2 * kWave) {
+    const int r0 = ln;
+    const int r1 = ln + kWave;
+    bool ok0 = r0 < R && (int64_t)r0 < occ;
+    bool ok1 = r1 < R && (int64_t)r1 < occ;
+    int v0 = ok0 && K > 0 ? cont_at(r0, 0) : -1;
+    int v1 = ok1 && K > 0 ? cont_at(r1, 0) : -1;
+    for (; d < K; ++d) {
+      const bool a0 = ok0 && v0 != -1;
+      const bool a1 = ok1 && v1 != -1;
+      // next depth's tokens for every row still on the chain (a superset
+      // of the survivors), loaded while this depth votes
+      const int n0 = a0 && d + 1 < K ? cont_at(r0, d + 1) : -1;
+      const int n1 = a1 && d + 1 < K ? cont_at(r1, d + 1) : -1;
+      uint64_t rem0 = ballot(a0);
+      uint64_t rem1 = ballot(a1);
+      const int nact = popc(rem0) + popc(rem1);
+      if (nact == 0) break;
+      const float denom = __fadd_rn((float)(nact > 1 ? nact : 1), alpha);
+      int bcnt = 0;
+      int btok = 0x7fffffff;
+      int vmin = 0;  // 0: not needed yet
+      bool dead = false;
+      while (rem0 | rem1) {
+        const int left = popc(rem0) + popc(rem1);
+        if (left < bcnt) break;
+        if (bcnt > 0 && vmin == 0) {
+          // Fewest votes that keep the chain probability >= min_prob; if
+          // neither the best so far nor the rest can reach it the chain
+          // ends here whichever token wins.
+          vmin = min_votes(prob, denom, min_prob, nact);
+          if (vmin > nact) {
+            dead = true;
+            break;
+          }
         }
-        for (; j < nact; ++j) v += (A[j] == x);
-        vbits = (uint32_t)v;
-      } else {
-        float v = 0.0f;
-        for (int j = 0; j < nact; ++j)
-          if (A[j] == x) v = __fadd_rn(v, W[j]);
-        vbits = __float_as_uint(v);
+        if (left < vmin && bcnt < vmin) break;
+        int x;
+        if (rem0)
+          x = __builtin_amdgcn_readlane(v0, __builtin_ctzll(rem0));
+        else
+          x = __builtin_amdgcn_readlane(v1, __builtin_ctzll(rem1));
+        const uint64_t e0 = ballot(a0 && v0 == x);
+        const uint64_t e1 = ballot(a1 && v1 == x);
+        const int cnt = popc(e0) + popc(e1);
+        if (vote_better(cnt, x, bcnt, btok)) {
+          bcnt = cnt;
+          btok = x;
+        }
+        rem0 &= ~e0;
+        rem1 &= ~e1;
       }
-      // max votes first, then the smallest (signed) token
-      const uint64_t key =
-          ((uint64_t)vbits << 32) |
-          (uint64_t)(0xffffffffu - ((uint32_t)x ^ 0x80000000u));
-      best = key > best ? key : best;
+      if (dead) break;
+      const float vf = (float)bcnt;
+      prob = __fmul_rn(prob, __fdiv_rn(vf, denom));
+      const bool valid = (vf > 0.0f) && (prob >= min_prob);
+      if (!valid) break;
+      if (ln == 0) chain_out[d] = btok;
+      if ((int64_t)d < cap) score = __fadd_rn(score, prob);
+      ++nv;
+      ok0 = a0 && v0 == btok;
+      ok1 = a1 && v1 == btok;
+      v0 = n0;
+      v1 = n1;
     }
-    best = wave_max_u64(best);
-    const uint32_t vbits = (uint32_t)(best >> 32);
-    const int tok = (int)((0xffffffffu - (uint32_t)best) ^ 0x80000000u);
-    float vf;
-    float denom;
-    if (!kWeighted) {
-      vf = (float)(int)vbits;
-      denom = __fadd_rn((float)(nact > 1 ? nact : 1), alpha);
-    } else {
-      vf = __uint_as_float(vbits);
-      float a = 0.0f;
-      for (int j = 0; j < nact; ++j) a = __fadd_rn(a, W[j]);
-      denom = __fadd_rn(a, alpha);
-    }
-    prob = __fmul_rn(prob, __fdiv_rn(vf, denom));
-    const bool valid = (vf > 0.0f) && (prob >= min_prob);
-    if (!valid) break;
-    if (ln == 0) chain_out[d] = tok;
-    if ((int64_t)d < cap) score = __fadd_rn(score, prob);
-    ++nv;
+  } else {
+    const int nslot = (R + kWave - 1) / kWave;  // <= 32 (R <= 2048)
+    uint32_t ok = 0;
     for (int s = 0; s < nslot; ++s) {
-      if ((ok >> s) & 1u) {
-        if (cont_at(s * kWave + ln, d) != tok) ok &= ~(1u << s);
-      }
+      int r = s * kWave + ln;
+      if (r < R && (int64_t)r < occ) ok |= 1u << s;
     }
-    wave_lds_sync();
+    for (; d < K; ++d) {
+      int nact = 0;
+      for (int s = 0; s < nslot; ++s) {
+        const int r = s * kWave + ln;
+        const bool okr = (ok >> s) & 1u;
+        int c = -1;
+        if (okr) c = cont_at(r, d);
+        const bool act = okr && c != -1;
+        const uint64_t m = ballot(act);
+        if (act) {
+          const int pos = nact + rank_lt(m);
+          A[pos] = c;
+          if (kWeighted) W[pos] = weight_at(r);
+        }
+        nact += popc(m);
+        if (!act) ok &= ~(1u << s);
+      }
+      wave_lds_sync();
+      if (nact == 0) break;
+      uint64_t best = 0;
+      for (int i = ln; i < nact; i += kWave) {
+        const int x = A[i];
+        uint32_t vbits;
+        if (!kWeighted) {
+          int v = 0;
+          int j = 0;
+          for (; j + 4 <= nact; j += 4) {
+            const int4 q = *reinterpret_cast<const int4*>(A + j);
+            v += (q.x == x) + (q.y == x) + (q.z == x) + (q.w == x);
+          }
+          for (; j < nact; ++j) v += (A[j] == x);
+          vbits = (uint32_t)v;
+        } else {
+          float v = 0.0f;
+          for (int j = 0; j < nact; ++j)
+            if (A[j] == x) v = __fadd_rn(v, W[j]);
+          vbits = __float_as_uint(v);
+        }
+        const uint64_t key =
+            ((uint64_t)vbits << 32) |
+            (uint64_t)(0xffffffffu - ((uint32_t)x ^ 0x80000000u));
+        best = key > best ? key : best;
+      }
+      best = wave_max_u64(best);
+      const uint32_t vbits = (uint32_t)(best >> 32);
+      const int tok = (int)((0xffffffffu - (uint32_t)best) ^ 0x80000000u);
+      float vf;
+      float denom;
+      if (!kWeighted) {
+        vf = (float)(int)vbits;
+        denom = __fadd_rn((float)(nact > 1 ? nact : 1), alpha);
+      } else {
+        vf = __uint_as_float(vbits);
+        float a = 0.0f;
+        for (int j = 0; j < nact; ++j) a = __fadd_rn(a, W[j]);
+        denom = __fadd_rn(a, alpha);
+      }
+      prob = __fmul_rn(prob, __fdiv_rn(vf, denom));
+      const bool valid = (vf > 0.0f) && (prob >= min_prob);
+      if (!valid) break;
+      if (ln == 0) chain_out[d] = tok;
+      if ((int64_t)d < cap) score = __fadd_rn(score, prob);
+      ++nv;
+      for (int s = 0; s < nslot; ++s) {
+        if ((ok >> s) & 1u) {
+          if (cont_at(s * kWave + ln, d) != tok) ok &= ~(1u << s);
+        }
+      }
+      wave_lds_sync();
+    }
   }
   for (int dd = d + ln; dd < K; dd += kWave) chain_out[dd] = -1;
   ExpandResult res;
@@ -190,6 +301,174 @@ __device__ ExpandResult expand_wave(ContFn cont_at, WeightFn weight_at,
 struct NoWeight {
   __device__ float operator()(int) const { return 0.0f; }
 };
+
+// ------------------------------------------------- ordered compaction
+// Inclusive prefix sum over the 64 lanes of a wave with DPP row shifts and
+// row broadcasts (no LDS traffic).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf,
+                                             false);  // row_shr:1
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf,
+                                             false);  // row_shr:2
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf,
+                                             false);  // row_shr:4
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf,
+                                             false);  // row_shr:8
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf,
+                                             false);  // row_bcast:15
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf,
+                                             false);  // row_bcast:31
+  return v;
+}
+
+// Block-wide exclusive prefix sums of 8 per-thread counters.  `scratch`
+// holds 8 * (NT/64) u32 in LDS.  Two barriers.
+template <int NT>
+__device__ __forceinline__ void block_exscan8(const uint32_t (&v)[8],
+                                              uint32_t (&pre)[8],
+                                              uint32_t (&tot)[8],
+                                              uint32_t* scratch) {
+  constexpr int NW = NT / kWave;
+  const int ln = lane_id();
+  const int wv = threadIdx.x / kWave;
+  uint32_t inc[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    inc[c] = wave_incl_scan(v[c]);
+    if (ln == kWave - 1) scratch[wv * 8 + c] = inc[c];
+  }
+  __syncthreads();
+  uint32_t before[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  uint32_t all[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int w = 0; w < NW; ++w) {
+    const uint4 lo = *reinterpret_cast<const uint4*>(scratch + w * 8);
+    const uint4 hi = *reinterpret_cast<const uint4*>(scratch + w * 8 + 4);
+    const uint32_t t8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      if (w < wv) before[c] += t8[c];
+      all[c] += t8[c];
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    pre[c] = before[c] + inc[c] - v[c];
+    tot[c] = all[c];
+  }
+  __syncthreads();
+}
+
+// Per-byte test x >= t (1 <= t <= 255) on four u8 match lengths at once,
+// as 0x80 flags.  With s = (x & 0x7f) + add (add = 128 - t for t < 128,
+// 256 - t otherwise; never carries out of the byte), bit 7 of s is the
+// carry of the low seven bits of x - t, and the carry out of the byte --
+// no borrow, x >= t -- is x7 | s7 for t < 128 and x7 & s7 for t >= 128.
+struct ByteGe {
+  uint32_t add;  // per-byte constant replicated into all four bytes
+  bool hi;       // t >= 128
+  bool on;       // t >= 1
+};
+__device__ __forceinline__ ByteGe byte_ge_init(int t) {
+  ByteGe g;
+  g.on = t > 0;
+  g.hi = t >= 128;
+  const uint32_t a = t <= 0 ? 0u : (g.hi ? 256u - t : 128u - t);
+  g.add = a * 0x01010101u;
+  return g;
+}
+__device__ __forceinline__ uint32_t bytes_ge(uint32_t x, const ByteGe& g) {
+  const uint32_t s = (x & 0x7f7f7f7fu) + g.add;
+  return (g.hi ? (x & s) : (x | s)) & 0x80808080u;
+}
+
+// Clears the bytes of a 16-byte word from byte r (0 < r < 16) on.
+__device__ __forceinline__ uint4 clear_from(uint4 q, int r) {
+  uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int keep = r - 4 * k;
+    if (keep <= 0) w[k] = 0u;
+    else if (keep < 4) w[k] &= (1u << (8 * keep)) - 1u;
+  }
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// First R ascending positions i in [0, n) with mb[i] >= thr[c], for up to
+// 8 thresholds (thr[c] <= 0 disables c).  mb holds u8 match lengths, is
+// 16-byte aligned and readable up to the last thread segment's end (bytes
+// from n on are ignored).  One ordered
+// pass: every thread owns a 16-byte-aligned segment read as uint4 words,
+// counts bytes >= thr four at a time (all-zero words skipped), one block
+// scan gives each thread its output offsets, then it writes its hits
+// below R.  out[c * R + slot]; count[c] = min(hits, R).  thr, out and
+// count may be LDS or global.  All threads of the block must call it.
+template <int NT, typename MbPtr>
+__device__ __forceinline__ void compact_first_r(MbPtr mb, int64_t n,
+                                                const int* thr, int nthr,
+                                                int R, int32_t* out,
+                                                int* count,
+                                                uint32_t* scratch) {
+  int64_t seg = (n + NT - 1) / NT;
+  seg = (seg + 15) & ~(int64_t)15;
+  const int64_t beg = (int64_t)threadIdx.x * seg;
+  const int64_t end = beg + seg < n ? beg + seg : n;
+  ByteGe ge[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) ge[c] = byte_ge_init(c < nthr ? thr[c] : 0);
+  uint32_t cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int64_t i0 = beg; i0 < end; i0 += 16) {
+    uint4 q = *reinterpret_cast<const uint4*>(mb + i0);
+    if (i0 + 16 > end) q = clear_from(q, (int)(end - i0));
+    if ((q.x | q.y | q.z | q.w) == 0u) continue;  // no match ends here
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      if (ge[c].on) {
+        cnt[c] += __popc(bytes_ge(q.x, ge[c])) + __popc(bytes_ge(q.y, ge[c])) +
+                  __popc(bytes_ge(q.z, ge[c])) + __popc(bytes_ge(q.w, ge[c]));
+      }
+    }
+  }
+  uint32_t off[8], tot[8];
+  SFX_TRACE_POINT(7);
+  block_exscan8<NT>(cnt, off, tot, scratch);
+  SFX_TRACE_POINT(8);
+  bool more = false;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) more |= ge[c].on && off[c] < (uint32_t)R;
+  for (int64_t i0 = beg; more && i0 < end; i0 += 16) {
+    uint4 q = *reinterpret_cast<const uint4*>(mb + i0);
+    if (i0 + 16 > end) q = clear_from(q, (int)(end - i0));
+    if ((q.x | q.y | q.z | q.w) == 0u) continue;
+    const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+    more = false;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      if (ge[c].on && off[c] < (uint32_t)R) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          uint32_t m = bytes_ge(w4[k], ge[c]);
+          while (m) {
+            const int byte = __builtin_ctz(m) >> 3;
+            if (off[c] < (uint32_t)R)
+              out[c * R + off[c]] = (int32_t)(i0 + 4 * k + byte);
+            ++off[c];
+            m &= m - 1;
+          }
+        }
+        more |= off[c] < (uint32_t)R;
+      }
+    }
+  }
+  if (threadIdx.x < (unsigned)nthr) {
+    const int c = threadIdx.x;
+    uint32_t total = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k == c) total = tot[k];
+    count[c] = total < (uint32_t)R ? (int)total : R;
+  }
+  SFX_TRACE_POINT(9);
+}
 
 // -------------------------------------------------- block-level handover
 // Publish this block's global writes, count its arrival on ctr and return

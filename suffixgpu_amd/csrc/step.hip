@@ -1,48 +1,105 @@
-// Fused decode step (suffix_gpu/proposer.py:186-327): the local kernel on
-// the caller's stream, the global kernel on the side stream; rows meet in
-// the workspace and the later of the two writes the row's draft.
+// Fused decode step (suffix_gpu/proposer.py:186-327) in one launch.
+//
+// With global memory each request row gets three 512-thread workgroups,
+// interleaved: SA interval search, delta scan, local match.  The first two
+// hand over through the workspace and the later of them merges the row's
+// global candidates; local and global results meet the same way and the
+// later one writes the row's draft.  Nothing waits on another workgroup,
+// so any scheduling order completes.  Local-only drafting is one workgroup
+// per row.  One kernel node per step keeps a captured HIP graph minimal.
 
+#include "global_impl.h"
 #include "launch.h"
-#include "step_ws.h"
+#include "local_impl.h"
+
+namespace sfx {
+
+static_assert(kLocalThreads == kGlobalThreads,
+              "the fused step runs every role with one block size");
+
+struct StepArgs {
+  LocalArgs l;
+  GlobalArgs g;
+  int global_on;
+};
+
+__global__ __launch_bounds__(kGlobalThreads) void k_step(StepArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  if (!a.global_on) {
+    local_body(a.l, smem, blockIdx.x);
+    return;
+  }
+  const int b = blockIdx.x / 3;
+  const int role = blockIdx.x % 3;  // 0: SA search, 1: delta scan, 2: local
+  if (role == 2)
+    local_body(a.l, smem, b);
+  else
+    global_body(a.g, smem, b, role == 0);
+}
+
+}  // namespace sfx
 
 using namespace sfx;
 
 extern "C" size_t sfx_step_workspace_size(const sfx_params* p,
-                                          int64_t batch) {
+                                          int64_t batch,
+                                          int64_t delta_capacity) {
   if (!p || batch < 0) return 0;
-  return step_ws_layout(*p, batch, nullptr, nullptr);
+  return step_ws_layout(*p, batch, delta_capacity, nullptr, nullptr);
 }
 
 extern "C" int sfx_propose_step(const sfx_params* p, const sfx_index* ix,
                                 const sfx_batch* bt, int32_t* draft,
                                 int32_t* num_valid, int32_t* new_counts,
                                 void* workspace, size_t workspace_bytes,
-                                hipStream_t stream, hipStream_t side_stream) {
+                                hipStream_t stream) {
   if (!p || !bt || !draft || !num_valid) return SFX_EINVAL;
   int rc = check_local(*p, *bt);
   if (rc) return rc;
   if (bt->sampled && bt->limit < 0) return SFX_EINVAL;
   const bool global_on = ix != nullptr;
+  StepArgs a = {};
+  a.global_on = global_on ? 1 : 0;
+  a.l.p = *p;
+  a.l.bt = *bt;
+  a.l.mode = kLocalStep;
+  a.l.global_on = a.global_on;
+  a.l.draft = draft;
+  a.l.num_valid = num_valid;
+  a.l.new_counts = new_counts;
+  size_t lds = local_lds_bytes(*p, bt->seq);
   if (global_on) {
     rc = check_global(*p, *ix);
     if (rc) return rc;
-  }
-  StepWs ws = {};
-  if (global_on) {
-    const size_t need = step_ws_layout(*p, bt->batch, nullptr, nullptr);
+    const size_t need =
+        step_ws_layout(*p, bt->batch, ix->delta_capacity, nullptr, nullptr);
     if (!workspace || workspace_bytes < need) return SFX_EINVAL;
-    step_ws_layout(*p, bt->batch, workspace, &ws);
+    step_ws_layout(*p, bt->batch, ix->delta_capacity, workspace, &a.l.ws);
+    a.g.p = *p;
+    a.g.ix = *ix;
+    a.g.B = bt->batch;
+    a.g.step = 1;
+    a.g.bt = *bt;
+    a.g.need_expand = 1;
+    a.g.draft = draft;
+    a.g.num_valid = num_valid;
+    a.g.ws = a.l.ws;
+    size_t glds = 0;
+    a.g.merge_waves = merge_waves_for(*p, *ix, &glds);
+    a.g.mb_lds = mb_lds_bytes(*ix);
+    lds = lds > glds ? lds : glds;
   }
-  // The global kernel reads each row's tail through the step's sampled ids
-  // (pick.h updated_token), so it does not wait for the local kernel's
-  // scatter; the two only meet in the workspace.
-  rc = local_step(*p, *bt, global_on, draft, num_valid, new_counts, ws,
-                  stream);
-  if (rc) return rc;
-  if (global_on) {
-    rc = global_step(*p, *ix, *bt, draft, num_valid, ws,
-                     side_stream ? side_stream : stream);
-    if (rc) return rc;
+  if (lds > kMaxLds) return SFX_EINVAL;
+  if (bt->batch == 0) return 0;
+  static bool attr_done = false;
+  if (!attr_done) {
+    hipFuncSetAttribute((const void*)k_step,
+                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                        (int)kMaxLds);
+    attr_done = true;
   }
-  return 0;
+  const unsigned blocks = (unsigned)(bt->batch * (global_on ? 3 : 1));
+  hipLaunchKernelGGL(k_step, dim3(blocks), dim3(kGlobalThreads), lds, stream,
+                     a);
+  return (int)hipGetLastError();
 }

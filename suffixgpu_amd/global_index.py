@@ -28,6 +28,9 @@ from suffixgpu_amd.expand import expand_chain
 from suffixgpu_amd.suffix_array import sa_workspace_bytes
 
 PAD_TOKEN = torch.iinfo(torch.int32).max
+# Tokens of every suffix kept next to the suffix array (one 128-byte row
+# per rank) so an interval-search probe is a single row load.
+KEY_WIDTH = 32
 # Written between documents; negative, so no query token (>= 0) can match
 # it and neither matches nor continuations cross document boundaries.
 SEP_TOKEN = -2
@@ -69,6 +72,10 @@ class GlobalIndex:
         self.delta = torch.zeros(delta_capacity, dtype=torch.int32,
                                  device=dev)
         self.delta_len_t = torch.zeros((), dtype=torch.int64, device=dev)
+        self.sa_key = torch.empty(capacity * KEY_WIDTH, dtype=torch.int32,
+                                  device=dev)
+        self.staging_sa_key = torch.empty_like(self.sa_key)
+        self._build_keys(self.corpus, self.sa, self.sa_key)
         self._sa_ws: torch.Tensor | None = None
         self._query_ws: dict = {}
 
@@ -86,7 +93,13 @@ class GlobalIndex:
         return _lib.SfxIndex(self.corpus.data_ptr(), self.sa.data_ptr(),
                              self.capacity, self.delta.data_ptr(),
                              self.delta_capacity,
-                             self.delta_len_t.data_ptr())
+                             self.delta_len_t.data_ptr(),
+                             self.sa_key.data_ptr(), KEY_WIDTH)
+
+    def _build_keys(self, corpus, sa, keys) -> None:
+        check(lib().sfx_sa_keys(corpus.data_ptr(), sa.data_ptr(),
+                                self.capacity, KEY_WIDTH, keys.data_ptr(),
+                                stream_of(self.device)), "SA key rows")
 
     # ------------------------------------------------------------------
     # writes (global_index.py:86-133)
@@ -231,6 +244,7 @@ class GlobalIndex:
                                  self.staging_sa.data_ptr(), 0,
                                  self._sa_ws.data_ptr(), self._sa_ws.numel(),
                                  stream_of(self.device)), "SA rebuild")
+        self._build_keys(dst, self.staging_sa, self.staging_sa_key)
 
     def _count_docs_within(self, tokens: int) -> int:
         acc = 0
@@ -246,6 +260,7 @@ class GlobalIndex:
         # In-place copies: captured graphs bind the active tensors' storage.
         self.corpus.copy_(self.staging_corpus)
         self.sa.copy_(self.staging_sa)
+        self.sa_key.copy_(self.staging_sa_key)
         self.active_len = n_new
         self.active_doc_lens = new_doc_lens
         self._rebuild_event = None
@@ -335,7 +350,8 @@ class GlobalIndex:
         }
         for name in want:
             alloc(name, *shapes[name])
-        nbytes = int(lib().sfx_global_query_workspace_size(p, b))
+        nbytes = int(lib().sfx_global_query_workspace_size(
+            p, b, self.delta_capacity))
         ws = self._query_ws.get((b, cnum, kk))
         if ws is None or ws.numel() < nbytes:
             ws = torch.zeros(max(1, nbytes), dtype=torch.uint8, device=dev)

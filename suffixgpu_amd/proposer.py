@@ -3,9 +3,9 @@
 Mirrors suffix_gpu/proposer.py:26-393 (constructor, update_state,
 propose_with_update, propose, poll, harvest_finished, harvest_rows,
 ingest_active, load_model).  Device tensors in and out, no host
-synchronisation on the step, static shapes: a step is one local kernel on
-the current stream plus (with global memory) one global kernel on a side
-stream joined back by events, so ``torch.cuda.graph`` can capture it.
+synchronisation on the step, static shapes: a step is one kernel launch on
+the current stream (local, SA-search and delta-scan workgroups per row), so
+``torch.cuda.graph`` captures it as a single node.
 
 Local candidates use support thresholds 2^0..2^(C-1); global candidates use
 length caps max(2, P >> i) for i < C-1 plus 2, deduplicated, descending
@@ -73,10 +73,9 @@ class SuffixGPUDrafter:
         self.min_token_prob = min_token_prob
         self.num_backoff = max(1, int(num_backoff))
         self.vote_smoothing_alpha = float(vote_smoothing_alpha)
+        # The local and global paths always run concurrently: they are
+        # workgroups of the same launch.  Kept for API compatibility.
         self.parallel_paths = bool(parallel_paths)
-        self._ps_stream: torch.cuda.Stream | None = None
-        self._ps_fork: torch.cuda.Event | None = None
-        self._ps_join: torch.cuda.Event | None = None
         support_thresholds = backoff_thresholds(self.num_backoff)
         caps = global_caps(max_pattern_len, self.num_backoff)
         self._global_caps = torch.tensor(caps, dtype=torch.int64,
@@ -175,7 +174,10 @@ class SuffixGPUDrafter:
     def _workspace(self, b: int) -> torch.Tensor:
         ws = self._ws.get(b)
         if ws is None:
-            nbytes = int(lib().sfx_step_workspace_size(self._params, b))
+            dcap = (self.global_index.delta_capacity
+                    if self.global_index is not None else 0)
+            nbytes = int(lib().sfx_step_workspace_size(self._params, b,
+                                                       dcap))
             ws = torch.zeros(max(1, nbytes), dtype=torch.uint8,
                              device=self.device)
             self._ws[b] = ws
@@ -194,38 +196,22 @@ class SuffixGPUDrafter:
         if b == 0:
             return draft, num_valid, new
         L = lib()
-        cur = torch.cuda.current_stream(dev)
+        cur = torch.cuda.current_stream(dev).cuda_stream
         if self.global_index is None:
             check(L.sfx_propose_step(self._params, None, bt,
                                      draft.data_ptr(), num_valid.data_ptr(),
-                                     _lib.ptr(new), None, 0,
-                                     cur.cuda_stream, cur.cuda_stream),
+                                     _lib.ptr(new), None, 0, cur),
                   "propose")
             del keep
             return draft, num_valid, new
         ws = self._workspace(b)
-        ix = self.global_index.index_struct()
-        if self.parallel_paths:
-            if self._ps_stream is None:
-                self._ps_stream = torch.cuda.Stream(dev)
-                self._ps_fork = torch.cuda.Event()
-                self._ps_join = torch.cuda.Event()
-            self._ps_fork.record(cur)
-            self._ps_stream.wait_event(self._ps_fork)
-            side = self._ps_stream.cuda_stream
-        else:
-            side = cur.cuda_stream
-        rc = L.sfx_propose_step(self._params, ix, bt, draft.data_ptr(),
-                                num_valid.data_ptr(), _lib.ptr(new),
-                                ws.data_ptr(), ws.numel(), cur.cuda_stream,
-                                side)
-        if self.parallel_paths:
-            # Join even on failure so the side stream never dangles.
-            self._ps_join.record(self._ps_stream)
-            cur.wait_event(self._ps_join)
+        rc = L.sfx_propose_step(self._params,
+                                self.global_index.index_struct(), bt,
+                                draft.data_ptr(), num_valid.data_ptr(),
+                                _lib.ptr(new), ws.data_ptr(), ws.numel(),
+                                cur)
         if rc != 0:
-            # A partial launch can leave handover counters set.
-            ws.zero_()
+            ws.zero_()  # never leave handover counters half set
         check(rc, "propose")
         del keep
         return draft, num_valid, new

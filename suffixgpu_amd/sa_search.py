@@ -52,7 +52,7 @@ def suffix_match_backoff(sa: torch.Tensor, corpus: torch.Tensor,
     out.sa_len = out_len.data_ptr()
     out.sa_start = out_s.data_ptr()
     out.sa_end = out_e.data_ptr()
-    nbytes = lib().sfx_global_query_workspace_size(p, b)
+    nbytes = lib().sfx_global_query_workspace_size(p, b, 1)
     ws = torch.zeros(max(1, nbytes), dtype=torch.uint8, device=dev)
     if b:
         check(lib().sfx_global_query(p, ix, q.data_ptr(), b, q.shape[1],
