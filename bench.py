@@ -49,9 +49,16 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--cpu-steps", type=int, default=2)
+    ap.add_argument("--cpu-steps", type=int, default=40)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=50)
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="for rocprofv3 --pmc passes: a copy of known size, "
+                    "then a few step launches; prints no JSON")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR",
+                                                         "WRITE_DIR"),
+                    help="turn two rocprofv3 --pmc outputs (FETCH_SIZE, "
+                    "WRITE_SIZE) of --pmc-workload into HBM bytes/launch")
     return ap.parse_args()
 
 
@@ -116,36 +123,14 @@ def reference_probe_footprint(sa, corpus, rpat, plen, P):
     return u_sa, u_c
 
 
-# ------------------------------------------------------------------ main
-def main() -> int:
-    args = parse()
-    if args.gpus != 1:
-        print(json.dumps({"error": "this drafter benchmark runs on exactly "
-                          "one GPU (the workload is one GPU's rows); "
-                          f"--gpus {args.gpus} is not supported"}))
-        return 2
+def time_sa_builds(w, dev, side):
+    """SA build throughput on a side stream (HIP events): the corpus
+    snapshot (docs + SEP + sentinel) and a uniform-random low-repeat
+    corpus of the same capacity."""
     import torch
-
-    from suffixgpu_amd import SuffixGPUDrafter, synth
-    from suffixgpu_amd import _lib
+    from suffixgpu_amd import synth
     from suffixgpu_amd.suffix_array import (build_suffix_array_into,
                                             sa_workspace_bytes)
-
-    dev = torch.device("cuda", 0)
-    t0 = time.time()
-    w = synth.global_corpus(seed=3, capacity=CAPACITY, delta_fill=DELTA_FILL,
-                            n_docs=1024, b=B, s=S, t=T_SAMPLED)
-    log(f"workload generated in {time.time() - t0:.1f}s: "
-        f"{len(w.active_docs)} corpus docs, {len(w.delta_docs)} delta docs")
-
-    d = SuffixGPUDrafter(device=dev, enable_global=True,
-                         global_capacity=CAPACITY, delta_capacity=DELTA_CAP,
-                         rebuild_threshold=1 << 30, **CFG)
-    gi = d.global_index
-
-    # ---- SA build throughput (side stream, HIP events): corpus snapshot
-    # (docs + SEP + sentinel) and a uniform-random low-repeat corpus.
-    side = torch.cuda.Stream(dev)
     flat = np.concatenate([np.append(x, -2) for x in w.active_docs]).astype(
         np.int32)
     m = min(flat.shape[0] + 1, CAPACITY)
@@ -176,11 +161,50 @@ def main() -> int:
         build_ms[name] = (min(times), mm)
         log(f"SA build {name}: m={mm} {min(times):.2f} ms")
     del ws
+    return build_ms
+
+
+# ------------------------------------------------------------------ main
+def main() -> int:
+    args = parse()
+    if args.summarize_pmc:
+        print(json.dumps(summarize_pmc(*args.summarize_pmc), indent=1))
+        return 0
+    if args.gpus != 1:
+        print(json.dumps({"error": "this drafter benchmark runs on exactly "
+                          "one GPU (the workload is one GPU's rows); "
+                          f"--gpus {args.gpus} is not supported"}))
+        return 2
+    import torch
+
+    from suffixgpu_amd import SuffixGPUDrafter, synth
+    from suffixgpu_amd import _lib
+    from suffixgpu_amd.suffix_array import (build_suffix_array_into,
+                                            sa_workspace_bytes)
+
+    dev = torch.device("cuda", 0)
+    t0 = time.time()
+    w = synth.global_corpus(seed=3, capacity=CAPACITY, delta_fill=DELTA_FILL,
+                            n_docs=1024, b=B, s=S, t=T_SAMPLED)
+    log(f"workload generated in {time.time() - t0:.1f}s: "
+        f"{len(w.active_docs)} corpus docs, {len(w.delta_docs)} delta docs")
+
+    d = SuffixGPUDrafter(device=dev, enable_global=True,
+                         global_capacity=CAPACITY, delta_capacity=DELTA_CAP,
+                         rebuild_threshold=1 << 30, **CFG)
+    gi = d.global_index
+
+    side = torch.cuda.Stream(dev)
+    build_ms = None
+    if not args.pmc_workload:
+        build_ms = time_sa_builds(w, dev, side)
 
     gi.load_documents([torch.from_numpy(x).to(dev) for x in w.active_docs])
     gi.append_documents([torch.from_numpy(x).to(dev) for x in w.delta_docs])
     torch.cuda.synchronize()
     log(f"index: active_len={gi.active_len} delta_len={gi.delta_len}")
+    if args.pmc_workload:
+        return pmc_workload(d, w, dev)
 
     bt = w.batch
     tokens0 = torch.from_numpy(bt.tokens).to(dev)
@@ -216,30 +240,26 @@ def main() -> int:
         f"us/step, drafting rows {(num_valid > 0).sum()}/{B}, "
         f"mean num_valid {num_valid.mean():.2f}")
 
-    # ---- per-kernel durations (same kernels, launched alone).
+    # ---- the step kernel launched directly (no graph) between HIP events
+    # on its stream, then the local and global kernels launched alone.
+    step_us = step_kernel_us(d, dev, tokens0, nt, sampled, args.kernel_reps)
     acc = (bt.sampled != -1).sum(1)
     k_local_us, k_global_us = kernel_timings(d, dev, tokens0, nt, sampled,
                                              args.kernel_reps)
-    log(f"kernel avg: local {k_local_us:.2f} us, global {k_global_us:.2f} us")
+    log(f"kernel avg: step {step_us:.2f} us (local alone {k_local_us:.2f}, "
+        f"global alone {k_global_us:.2f})")
 
     a_local = local_algorithmic_bytes(new_counts, acc, CFG["k"])
     a_global, fp = global_algorithmic_bytes(d, dev, buf, new_counts)
     log(f"algorithmic bytes: local {a_local}, global {a_global} ({fp})")
-    kernels = {
-        "k_local": (a_local, k_local_us),
-        "k_global": (a_global, k_global_us),
-    }
-    dom = max(kernels, key=lambda kk: kernels[kk][1])
-    a_bytes, dur = kernels[dom]
-    achieved = a_bytes / (dur * 1e-6) / 1e9
     step_bytes = a_local + a_global
-    traffic = load_traffic(dom)
+    achieved = step_bytes / (step_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 2),
                 "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBPS, 6),
-                "traffic": traffic, "kernel": dom,
-                "algorithmic_bytes": a_bytes,
-                "avg_launch_us": round(dur, 3)}
+                "traffic": load_traffic("k_step"), "kernel": "k_step",
+                "algorithmic_bytes": step_bytes,
+                "avg_launch_us": round(step_us, 3)}
 
     cpu = None
     if not args.no_cpu:
@@ -272,8 +292,9 @@ def main() -> int:
         "sa_build_uniform_mtok_s": round(CAPACITY / (sa_uni_ms * 1e-3) / 1e6,
                                          2),
         "sa_build_steps_equiv": round(sa_corpus_ms * 1e3 / p50, 1),
-        "kernels_us": {"k_local": round(k_local_us, 3),
-                       "k_global": round(k_global_us, 3)},
+        "kernels_us": {"k_step": round(step_us, 3),
+                       "k_local_alone": round(k_local_us, 3),
+                       "k_global_alone": round(k_global_us, 3)},
         "roofline": roofline,
         "cpu_baseline": cpu,
     }
@@ -283,6 +304,96 @@ def main() -> int:
 
 def _lib_pad() -> int:
     return 2 ** 31 - 1
+
+
+def step_kernel_us(d, dev, tokens0, nt, sampled, reps):
+    """Average duration of the fused step kernel: propose_with_update
+    launched directly on the current stream `reps` times between HIP
+    events recorded on that stream (launches queue ahead of the GPU, so
+    the events bracket the kernel alone)."""
+    import torch
+    cur = torch.cuda.current_stream(dev)
+    buf = tokens0.clone()
+    for _ in range(5):
+        d.propose_with_update(nt, buf, sampled)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True),
+            torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for e0, e1 in evs:
+        e0.record(cur)
+        d.propose_with_update(nt, buf, sampled)
+        e1.record(cur)
+    torch.cuda.synchronize()
+    return statistics.mean(e0.elapsed_time(e1) * 1e3 for e0, e1 in evs)
+
+
+# Calibration copy for the PMC passes: bitwise_not over 2^26 int32 reads
+# and writes exactly 256 MiB each.
+PMC_COPY_ELEMS = 1 << 26
+PMC_STEP_LAUNCHES = 10
+
+
+def pmc_workload(d, w, dev) -> int:
+    import torch
+    src = torch.randint(0, 1 << 30, (PMC_COPY_ELEMS,), dtype=torch.int32,
+                        device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        torch.bitwise_not(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    bt = w.batch
+    buf = torch.from_numpy(bt.tokens).to(dev)
+    nt = torch.from_numpy(bt.num_tokens).to(dev)
+    sampled = torch.from_numpy(bt.sampled).to(dev)
+    for _ in range(PMC_STEP_LAUNCHES):
+        d.propose_with_update(nt, buf, sampled)
+    torch.cuda.synchronize()
+    log(f"pmc workload done: 3 calibration copies of {PMC_COPY_ELEMS * 4} "
+        f"bytes, {PMC_STEP_LAUNCHES} step launches")
+    return 0
+
+
+def _pmc_rows(out_dir: str, counter: str):
+    """(kernel name, value) per dispatch of one counter from a rocprofv3
+    --pmc CSV output directory."""
+    import csv
+    files = sorted(Path(out_dir).rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {out_dir}")
+    rows = []
+    for f in files:
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                if r.get("Counter_Name") == counter:
+                    rows.append((r["Kernel_Name"], float(r["Counter_Value"])))
+    return rows
+
+
+def summarize_pmc(fetch_dir: str, write_dir: str) -> dict:
+    """HBM bytes per step launch from FETCH_SIZE / WRITE_SIZE (KiB per
+    dispatch), each scaled by what it reads for the calibration copy of
+    known size (256 MiB read, 256 MiB written)."""
+    known = PMC_COPY_ELEMS * 4
+    out = {}
+    for name, d_, counter in (("fetch", fetch_dir, "FETCH_SIZE"),
+                              ("write", write_dir, "WRITE_SIZE")):
+        rows = _pmc_rows(d_, counter)
+        cal = [v for k, v in rows if "bitwise_not" in k]
+        step = [v for k, v in rows if "k_step" in k]
+        if not cal or not step:
+            raise SystemExit(f"{counter}: calibration or k_step dispatches "
+                             "missing")
+        cal_b = statistics.median(cal) * 1024.0
+        scale = known / cal_b
+        step_b = statistics.mean(step) * 1024.0
+        out[name] = {"counter": counter, "calibration_bytes": cal_b,
+                     "scale": scale, "step_raw_bytes": step_b,
+                     "step_bytes": step_b * scale,
+                     "dispatches": len(step)}
+    total = out["fetch"]["step_bytes"] + out["write"]["step_bytes"]
+    return {"k_step": round(total), "detail": out}
 
 
 def kernel_timings(d, dev, tokens0, nt, sampled, reps):

@@ -1,18 +1,21 @@
 // Suffix-array construction on the GPU: prefix doubling over LSD radix
-// sorts, with no host synchronisation.
+// sorts of the still-unsorted suffixes only, with no host synchronisation.
 //
-// Round 0 sorts positions by token (signed order, 4 passes of 8 bits).
-// Round h sorts them by (rank[i], rank[i+h]+1 or 0), rank = SA position of
-// the first suffix of the same h-prefix group; a proper prefix sorts first,
-// as in suffix_gpu/suffix_array.py:15-63.  After each sort a device-wide
-// max-scan of group-start flags yields the new ranks and a device flag
-// records whether every rank is distinct; all later rounds then return at
-// their first instruction, so the fixed launch sequence (capturable, no
-// host reads) costs only empty launches once the array is final.
+// Round 0 sorts all positions by token (signed order, 4 passes of 8 bits).
+// Every later round h = 1, 2, 4, ... re-sorts only the suffixes whose
+// group still has more than one member, by the key
+// (group head, rank[i+h]+1 or 0) -- a proper prefix sorts first, as in
+// suffix_gpu/suffix_array.py:15-63 -- and writes them back into the SA
+// positions their groups occupy, in order.  rank[i] is the SA position of
+// the first suffix of i's group (for a finished suffix, its final
+// position).  When no group of two or more is left the device sets a done
+// flag and every later launch returns at its first instruction, so the
+// fixed launch sequence (capturable, no host reads) is safe for any input.
 //
-// Each LSD pass is histogram -> single-block exclusive scan -> stable
-// scatter; the scatter ranks equal digits inside a wave with eight ballots
-// (wave64 match) and across waves through LDS, keeping tile order.
+// Each LSD pass is histogram (per 4096-element tile) -> per-digit row scan
+// across tiles -> stable scatter.  The scatter ranks equal digits inside a
+// wave with eight ballots (wave64 match) and across waves through LDS, so
+// tile order and element order are kept.
 
 #include "launch.h"
 #include "sfx_common.h"
@@ -23,19 +26,25 @@ constexpr int kSortThreads = 256;
 constexpr int kSortItems = 16;
 constexpr int kTile = kSortThreads * kSortItems;  // 4096
 constexpr int kRadix = 256;
+constexpr int kSortWaves = kSortThreads / kWave;  // 4
+constexpr int kWaveSpan = kTile / kSortWaves;     // 1024 per wave
 
 struct SaWs {
   uint64_t* keyA;
   uint64_t* keyB;
   uint32_t* valA;
   uint32_t* valB;
-  uint32_t* rank;
-  uint32_t* sa;
-  uint32_t* hist;    // [256 * NB]
-  uint32_t* blkmax;  // [NB]
-  uint32_t* blkcnt;  // [NB]
-  uint32_t* carry;   // [NB]
-  uint32_t* state;   // [0] done, [1] pending
+  uint32_t* pos;     // SA positions of the active suffixes, ascending
+  uint32_t* rank;    // [m] group head of text position i
+  uint32_t* sa;      // [m] current suffix order
+  uint32_t* grp;     // [m] group head of SA position j
+  uint32_t* hist;    // [256][NB] digit counts per tile, then offsets
+  uint32_t* rowsum;  // [256] digit totals
+  uint32_t* tcnt;    // [NB] active suffixes per tile
+  uint32_t* toff;    // [NB] their exclusive prefix
+  uint32_t* blkmax;  // [NB] last group start per tile
+  uint32_t* carry;   // [NB] group start carried into the tile
+  uint32_t* state;   // [0] done, [1] active count
 };
 
 static size_t sa_ws_layout(int64_t n, void* base, SaWs* w) {
@@ -53,50 +62,60 @@ static size_t sa_ws_layout(int64_t n, void* base, SaWs* w) {
   s.keyB = (uint64_t*)take(N * 8);
   s.valA = (uint32_t*)take(N * 4);
   s.valB = (uint32_t*)take(N * 4);
+  s.pos = (uint32_t*)take(N * 4);
   s.rank = (uint32_t*)take(N * 4);
   s.sa = (uint32_t*)take(N * 4);
+  s.grp = (uint32_t*)take(N * 4);
   s.hist = (uint32_t*)take((size_t)kRadix * NB * 4);
+  s.rowsum = (uint32_t*)take(kRadix * 4);
+  s.tcnt = (uint32_t*)take(NB * 4);
+  s.toff = (uint32_t*)take(NB * 4);
   s.blkmax = (uint32_t*)take(NB * 4);
-  s.blkcnt = (uint32_t*)take(NB * 4);
   s.carry = (uint32_t*)take(NB * 4);
   s.state = (uint32_t*)take(256);
   if (w) *w = s;
   return off;
 }
 
-__global__ void k_sa_reset(uint32_t* state) {
-  if (threadIdx.x == 0) {
-    state[0] = 0;
-    state[1] = 0;
-  }
+__device__ __forceinline__ int64_t tiles_of(int64_t a) {
+  return (a + kTile - 1) / kTile;
 }
 
-__global__ void k_sa_commit(uint32_t* state) {
-  if (threadIdx.x == 0 && state[0] == 0) state[0] = state[1];
+// Block-wide exclusive scan of one u32 per thread (NT threads); `red`
+// holds NT/64 u32 in LDS.  Returns the prefix; *total gets the sum.
+template <int NT>
+__device__ __forceinline__ uint32_t block_exscan1(uint32_t v, uint32_t* red,
+                                                  uint32_t* total) {
+  constexpr int NW = NT / kWave;
+  const int wv = threadIdx.x / kWave;
+  const uint32_t inc = wave_incl_scan(v);
+  if (lane_id() == kWave - 1) red[wv] = inc;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const uint32_t t = red[w];
+    if (w < wv) before += t;
+    all += t;
+  }
+  __syncthreads();
+  *total = all;
+  return before + inc - v;
 }
 
 __global__ __launch_bounds__(256) void k_sa_init(const int32_t* text,
                                                  int64_t n, uint64_t* key,
-                                                 uint32_t* val) {
+                                                 uint32_t* val, uint32_t* pos,
+                                                 uint32_t* state) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i == 0) {
+    state[0] = 0;
+    state[1] = (uint32_t)n;
+  }
   if (i >= n) return;
   key[i] = (uint64_t)((uint32_t)text[i] ^ 0x80000000u);
   val[i] = (uint32_t)i;
-}
-
-__global__ __launch_bounds__(256) void k_sa_keys(const uint32_t* sa,
-                                                 const uint32_t* rank,
-                                                 int64_t n, int64_t h,
-                                                 uint64_t* key, uint32_t* val,
-                                                 const uint32_t* state) {
-  if (state[0]) return;
-  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (j >= n) return;
-  const uint32_t i = sa[j];
-  const uint64_t k1 = rank[i];
-  const uint64_t k2 = (int64_t)i + h < n ? (uint64_t)rank[i + h] + 1 : 0;
-  key[j] = k1 * (uint64_t)(n + 1) + k2;
-  val[j] = i;
+  pos[i] = (uint32_t)i;
 }
 
 // Lanes of the wave holding the same 8-bit digit as the calling lane.
@@ -111,88 +130,104 @@ __device__ __forceinline__ uint64_t match_digit(bool act, uint32_t d) {
   return peers;
 }
 
+// ---------------------------------------------------------------- radix
+// Element e of a tile is base + r * 256 + tid (r < 16): this r-major order
+// is the element order the scatter keeps.
+
 __global__ __launch_bounds__(kSortThreads) void k_rs_hist(
-    const uint64_t* __restrict__ key, int64_t n, int sh, uint32_t* hist,
-    int64_t nb, const uint32_t* state) {
+    const uint64_t* __restrict__ key, int sh, uint32_t* hist, int64_t nb,
+    const uint32_t* state) {
   if (state[0]) return;
+  const int64_t A = state[1];
+  const int64_t base = (int64_t)blockIdx.x * kTile;
+  if (base >= A) return;
   __shared__ uint32_t h[kRadix];
   const int tid = threadIdx.x;
   h[tid] = 0;
-  __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * kTile;
+  uint32_t d[kSortItems];
+#pragma unroll
   for (int r = 0; r < kSortItems; ++r) {
     const int64_t idx = base + (int64_t)r * kSortThreads + tid;
-    const bool act = idx < n;
-    const uint32_t d = act ? (uint32_t)(key[idx] >> sh) & 255u : 0u;
-    const uint64_t peers = match_digit(act, d);
-    if (act && rank_lt(peers) == 0) atomicAdd(&h[d], (uint32_t)popc(peers));
+    d[r] = idx < A ? (uint32_t)(key[idx] >> sh) & 255u : 0u;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kSortItems; ++r) {
+    const bool act = base + (int64_t)r * kSortThreads + tid < A;
+    const uint64_t peers = match_digit(act, d[r]);
+    if (act && rank_lt(peers) == 0)
+      atomicAdd(&h[d[r]], (uint32_t)popc(peers));
   }
   __syncthreads();
   hist[(int64_t)tid * nb + blockIdx.x] = h[tid];
 }
 
-// In-place exclusive scan of `total` u32 by one 1024-thread block.
-__global__ __launch_bounds__(1024) void k_scan_excl(uint32_t* a,
-                                                    int64_t total,
-                                                    const uint32_t* state) {
-  if (state && state[0]) return;
-  __shared__ uint32_t part[1024];
-  const int tid = threadIdx.x;
-  const int64_t per = (total + 1023) / 1024;
-  const int64_t lo = (int64_t)tid * per;
-  const int64_t hi = lo + per < total ? lo + per : total;
-  uint32_t s = 0;
-  for (int64_t i = lo; i < hi; ++i) s += a[i];
-  part[tid] = s;
-  __syncthreads();
-  for (int o = 1; o < 1024; o <<= 1) {
-    const uint32_t v = tid >= o ? part[tid - o] : 0u;
-    __syncthreads();
-    part[tid] += v;
-    __syncthreads();
+// Row d of the histogram (tiles 0 .. ceil(A/4096)) becomes its exclusive
+// prefix; rowsum[d] the digit total.  One block per digit.
+__global__ __launch_bounds__(kSortThreads) void k_rs_rowscan(
+    uint32_t* hist, int64_t nb, uint32_t* rowsum, const uint32_t* state) {
+  if (state[0]) return;
+  __shared__ uint32_t red[kSortWaves];
+  const int64_t nbA = tiles_of(state[1]);
+  uint32_t* row = hist + (int64_t)blockIdx.x * nb;
+  uint32_t carry = 0;
+  for (int64_t c0 = 0; c0 < nbA; c0 += kSortThreads) {
+    const int64_t t = c0 + threadIdx.x;
+    const uint32_t v = t < nbA ? row[t] : 0u;
+    uint32_t tot;
+    const uint32_t ex = block_exscan1<kSortThreads>(v, red, &tot);
+    if (t < nbA) row[t] = carry + ex;
+    carry += tot;
   }
-  uint32_t run = part[tid] - s;
-  for (int64_t i = lo; i < hi; ++i) {
-    const uint32_t v = a[i];
-    a[i] = run;
-    run += v;
-  }
+  if (threadIdx.x == 0) rowsum[blockIdx.x] = carry;
 }
 
 __global__ __launch_bounds__(kSortThreads) void k_rs_scatter(
     const uint64_t* __restrict__ kin, const uint32_t* __restrict__ vin,
-    uint64_t* __restrict__ kout, uint32_t* __restrict__ vout, int64_t n,
-    int sh, const uint32_t* __restrict__ offs, int64_t nb,
-    const uint32_t* state) {
+    uint64_t* __restrict__ kout, uint32_t* __restrict__ vout, int sh,
+    const uint32_t* __restrict__ hist, int64_t nb,
+    const uint32_t* __restrict__ rowsum, const uint32_t* state) {
   if (state[0]) return;
-  constexpr int NW = kSortThreads / kWave;
+  const int64_t A = state[1];
+  const int64_t base = (int64_t)blockIdx.x * kTile;
+  if (base >= A) return;
   __shared__ uint32_t gofs[kRadix];
-  __shared__ uint32_t whist[NW][kRadix];
+  __shared__ uint32_t whist[kSortWaves][kRadix];
+  __shared__ uint32_t red[kSortWaves];
   const int tid = threadIdx.x;
   const int wv = tid / kWave;
-  gofs[tid] = offs[(int64_t)tid * nb + blockIdx.x];
-  for (int w = 0; w < NW; ++w) whist[w][tid] = 0;
-  __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * kTile;
+  uint64_t k[kSortItems];
+  uint32_t v[kSortItems];
+#pragma unroll
   for (int r = 0; r < kSortItems; ++r) {
     const int64_t idx = base + (int64_t)r * kSortThreads + tid;
-    const bool act = idx < n;
-    const uint64_t k = act ? kin[idx] : 0;
-    const uint32_t v = act ? vin[idx] : 0;
-    const uint32_t d = (uint32_t)(k >> sh) & 255u;
+    k[r] = idx < A ? kin[idx] : 0;
+    v[r] = idx < A ? vin[idx] : 0;
+  }
+  uint32_t tot;
+  const uint32_t dbase = block_exscan1<kSortThreads>(rowsum[tid], red, &tot);
+  gofs[tid] = dbase + hist[(int64_t)tid * nb + blockIdx.x];
+#pragma unroll
+  for (int w = 0; w < kSortWaves; ++w) whist[w][tid] = 0;
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kSortItems; ++r) {
+    const bool act = base + (int64_t)r * kSortThreads + tid < A;
+    const uint32_t d = (uint32_t)(k[r] >> sh) & 255u;
     const uint64_t peers = match_digit(act, d);
     const int rk = rank_lt(peers);
     if (act && rk == 0) whist[wv][d] = (uint32_t)popc(peers);
     __syncthreads();
     if (act) {
-      uint32_t pos = gofs[d] + (uint32_t)rk;
-      for (int w = 0; w < wv; ++w) pos += whist[w][d];
-      kout[pos] = k;
-      vout[pos] = v;
+      uint32_t p = gofs[d] + (uint32_t)rk;
+      for (int w = 0; w < wv; ++w) p += whist[w][d];
+      kout[p] = k[r];
+      vout[p] = v[r];
     }
     __syncthreads();
     uint32_t add = 0;
-    for (int w = 0; w < NW; ++w) {
+#pragma unroll
+    for (int w = 0; w < kSortWaves; ++w) {
       add += whist[w][tid];
       whist[w][tid] = 0;
     }
@@ -201,114 +236,224 @@ __global__ __launch_bounds__(kSortThreads) void k_rs_scatter(
   }
 }
 
-// Group starts: flag[j] = j == 0 || key[j] != key[j-1].
+// ----------------------------------------------------------- group heads
+// Over the sorted active list: slot t starts a group when its key differs
+// from slot t-1's; the group's head is pos[start] (pos ascends with t, so
+// the head of slot t is the largest start position at or before t).  Wave
+// w of a tile owns slots base + w*1024 .. +1024, 64 consecutive per step.
+
+__device__ __forceinline__ bool starts_group(const uint64_t* key, int64_t t,
+                                             uint64_t kt) {
+  return t == 0 || key[t - 1] != kt;
+}
+
 __global__ __launch_bounds__(kSortThreads) void k_grp_reduce(
-    const uint64_t* __restrict__ key, int64_t n, uint32_t* blkmax,
-    uint32_t* blkcnt, const uint32_t* state) {
+    const uint64_t* __restrict__ key, const uint32_t* __restrict__ pos,
+    uint32_t* blkmax, const uint32_t* state) {
   if (state[0]) return;
-  __shared__ uint32_t smax[kSortThreads / kWave];
-  __shared__ uint32_t scnt[kSortThreads / kWave];
-  const int tid = threadIdx.x;
+  const int64_t A = state[1];
   const int64_t base = (int64_t)blockIdx.x * kTile;
-  uint32_t mx = 0, cnt = 0;
-  for (int r = 0; r < kSortItems; ++r) {
-    const int64_t j = base + (int64_t)r * kSortThreads + tid;
-    if (j < n && (j == 0 || key[j] != key[j - 1])) {
-      mx = (uint32_t)j;
-      ++cnt;
+  if (base >= A) return;
+  __shared__ uint32_t smax[kSortWaves];
+  const int wv = threadIdx.x / kWave;
+  const int ln = lane_id();
+  const int64_t wbase = base + (int64_t)wv * kWaveSpan;
+  uint32_t mx = 0;
+#pragma unroll 4
+  for (int s = 0; s < kWaveSpan / kWave; ++s) {
+    const int64_t t = wbase + s * kWave + ln;
+    if (t < A) {
+      const uint64_t kt = key[t];
+      if (starts_group(key, t, kt)) mx = max(mx, pos[t]);
     }
   }
-  for (int o = 32; o > 0; o >>= 1) {
-    mx = max(mx, (uint32_t)__shfl_xor((int)mx, o));
-    cnt += (uint32_t)__shfl_xor((int)cnt, o);
-  }
-  if (lane_id() == 0) {
-    smax[tid / kWave] = mx;
-    scnt[tid / kWave] = cnt;
-  }
+  mx = (uint32_t)wave_max_i32((int)mx);
+  if (ln == 0) smax[wv] = mx;
   __syncthreads();
-  if (tid == 0) {
-    uint32_t m = 0, c = 0;
-    for (int w = 0; w < kSortThreads / kWave; ++w) {
-      m = max(m, smax[w]);
-      c += scnt[w];
-    }
+  if (threadIdx.x == 0) {
+    uint32_t m = 0;
+    for (int w = 0; w < kSortWaves; ++w) m = max(m, smax[w]);
     blkmax[blockIdx.x] = m;
-    blkcnt[blockIdx.x] = c;
   }
 }
 
-// Carry-in of the max-scan per block and the all-distinct flag.
+// Exclusive max-scan of blkmax over the active tiles (one block).
 __global__ __launch_bounds__(1024) void k_grp_carry(const uint32_t* blkmax,
-                                                    const uint32_t* blkcnt,
                                                     uint32_t* carry,
-                                                    int64_t nb, int64_t n,
-                                                    uint32_t* state) {
+                                                    const uint32_t* state) {
   if (state[0]) return;
-  __shared__ uint32_t pm[1024];
-  __shared__ uint64_t pc[1024];
+  __shared__ uint32_t wmax[16];
+  const int64_t nbA = tiles_of(state[1]);
   const int tid = threadIdx.x;
-  const int64_t per = (nb + 1023) / 1024;
-  const int64_t lo = (int64_t)tid * per;
-  const int64_t hi = lo + per < nb ? lo + per : nb;
-  uint32_t m = 0;
-  uint64_t c = 0;
-  for (int64_t i = lo; i < hi; ++i) {
-    m = max(m, blkmax[i]);
-    c += blkcnt[i];
-  }
-  pm[tid] = m;
-  pc[tid] = c;
-  __syncthreads();
-  for (int o = 1; o < 1024; o <<= 1) {
-    const uint32_t vm = tid >= o ? pm[tid - o] : 0u;
-    const uint64_t vc = tid >= o ? pc[tid - o] : 0u;
+  const int wv = tid / kWave;
+  uint32_t run = 0;
+  for (int64_t c0 = 0; c0 < nbA; c0 += 1024) {
+    const int64_t t = c0 + tid;
+    const uint32_t v = t < nbA ? blkmax[t] : 0u;
+    const uint32_t inc = wave_incl_max(v);
+    if (lane_id() == kWave - 1) wmax[wv] = inc;
     __syncthreads();
-    pm[tid] = max(pm[tid], vm);
-    pc[tid] += vc;
+    uint32_t before = run, all = run;
+    for (int w = 0; w < 16; ++w) {
+      if (w < wv) before = max(before, wmax[w]);
+      all = max(all, wmax[w]);
+    }
+    // the max over earlier tiles only
+    const uint32_t prev = (uint32_t)__shfl_up((int)inc, 1);
+    const uint32_t ex = lane_id() == 0 ? before : max(before, prev);
+    if (t < nbA) carry[t] = ex;
+    run = all;
     __syncthreads();
   }
-  uint32_t run = tid > 0 ? pm[tid - 1] : 0u;
-  for (int64_t i = lo; i < hi; ++i) {
-    carry[i] = run;
-    run = max(run, blkmax[i]);
-  }
-  if (tid == 1023) state[1] = pc[1023] == (uint64_t)n ? 1u : 0u;
 }
 
-// head[j] = last group start <= j; rank[sa[j]] = head[j].
+// rank[val[t]] = head, sa[pos[t]] = val[t], grp[pos[t]] = head.
 __global__ __launch_bounds__(kSortThreads) void k_grp_rank(
     const uint64_t* __restrict__ key, const uint32_t* __restrict__ val,
-    int64_t n, const uint32_t* __restrict__ carry, uint32_t* rank,
-    uint32_t* sa, const uint32_t* state) {
+    const uint32_t* __restrict__ pos, const uint32_t* __restrict__ carry,
+    uint32_t* rank, uint32_t* sa, uint32_t* grp, const uint32_t* state) {
   if (state[0]) return;
-  __shared__ uint32_t part[kSortThreads];
-  const int tid = threadIdx.x;
-  const int64_t base = (int64_t)blockIdx.x * kTile + (int64_t)tid * kSortItems;
+  const int64_t A = state[1];
+  const int64_t base = (int64_t)blockIdx.x * kTile;
+  if (base >= A) return;
+  __shared__ uint32_t smax[kSortWaves];
+  const int wv = threadIdx.x / kWave;
+  const int ln = lane_id();
+  const int64_t wbase = base + (int64_t)wv * kWaveSpan;
+  constexpr int kSteps = kWaveSpan / kWave;  // 16
+  uint32_t st[kSteps];  // start position of a group beginning here, or 0
   uint32_t mx = 0;
-  for (int u = 0; u < kSortItems; ++u) {
-    const int64_t j = base + u;
-    if (j < n && (j == 0 || key[j] != key[j - 1])) mx = (uint32_t)j;
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    const int64_t t = wbase + s * kWave + ln;
+    st[s] = 0;
+    if (t < A) {
+      const uint64_t kt = key[t];
+      if (starts_group(key, t, kt)) st[s] = pos[t];
+    }
+    mx = max(mx, st[s]);
   }
-  part[tid] = mx;
+  mx = (uint32_t)wave_max_i32((int)mx);
+  if (ln == 0) smax[wv] = mx;
   __syncthreads();
-  for (int o = 1; o < kSortThreads; o <<= 1) {
-    const uint32_t v = tid >= o ? part[tid - o] : 0u;
-    __syncthreads();
-    part[tid] = max(part[tid], v);
-    __syncthreads();
-  }
-  uint32_t run = max(carry[blockIdx.x], tid > 0 ? part[tid - 1] : 0u);
-  for (int u = 0; u < kSortItems; ++u) {
-    const int64_t j = base + u;
-    if (j >= n) break;
-    if (j == 0 || key[j] != key[j - 1]) run = (uint32_t)j;
-    const uint32_t i = val[j];
-    rank[i] = run;
-    sa[j] = i;
+  uint32_t run = carry[blockIdx.x];
+  for (int w = 0; w < wv; ++w) run = max(run, smax[w]);
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    const int64_t t = wbase + s * kWave + ln;
+    const uint32_t head = max(run, wave_incl_max(st[s]));
+    run = max(run, (uint32_t)__builtin_amdgcn_readlane((int)head, kWave - 1));
+    if (t < A) {
+      const uint32_t i = val[t];
+      const uint32_t j = pos[t];
+      rank[i] = head;
+      sa[j] = i;
+      grp[j] = head;
+    }
   }
 }
 
+// ------------------------------------------------------ active suffixes
+// SA position j is finished when its group is the singleton {j}.
+__device__ __forceinline__ bool unfinished(const uint32_t* grp, int64_t j,
+                                           int64_t m) {
+  const bool single =
+      grp[j] == (uint32_t)j && (j + 1 == m || grp[j + 1] == (uint32_t)(j + 1));
+  return !single;
+}
+
+__global__ __launch_bounds__(kSortThreads) void k_sa_mark(
+    const uint32_t* __restrict__ grp, int64_t m, uint32_t* tcnt,
+    const uint32_t* state) {
+  if (state[0]) return;
+  __shared__ uint32_t scnt[kSortWaves];
+  const int wv = threadIdx.x / kWave;
+  const int ln = lane_id();
+  const int64_t wbase = (int64_t)blockIdx.x * kTile + (int64_t)wv * kWaveSpan;
+  uint32_t cnt = 0;
+#pragma unroll 4
+  for (int s = 0; s < kWaveSpan / kWave; ++s) {
+    const int64_t j = wbase + s * kWave + ln;
+    cnt += (uint32_t)popc(ballot(j < m && unfinished(grp, j, m)));
+  }
+  if (ln == 0) scnt[wv] = cnt;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t c = 0;
+    for (int w = 0; w < kSortWaves; ++w) c += scnt[w];
+    tcnt[blockIdx.x] = c;
+  }
+}
+
+// Exclusive scan of the per-tile active counts (one block); the total is
+// the round's active count, and none left means the array is final.
+__global__ __launch_bounds__(1024) void k_sa_tilescan(const uint32_t* tcnt,
+                                                      uint32_t* toff,
+                                                      int64_t nb,
+                                                      uint32_t* state) {
+  if (state[0]) return;
+  __shared__ uint32_t red[16];
+  uint32_t carry = 0;
+  for (int64_t c0 = 0; c0 < nb; c0 += 1024) {
+    const int64_t t = c0 + threadIdx.x;
+    const uint32_t v = t < nb ? tcnt[t] : 0u;
+    uint32_t tot;
+    const uint32_t ex = block_exscan1<1024>(v, red, &tot);
+    if (t < nb) toff[t] = carry + ex;
+    carry += tot;
+  }
+  if (threadIdx.x == 0) {
+    state[1] = carry;
+    if (carry == 0) state[0] = 1;
+  }
+}
+
+// Active suffixes of the tile, in SA order, with their sort keys:
+// key = head * (m + 1) + (rank[i + h] + 1, or 0 past the end).
+__global__ __launch_bounds__(kSortThreads) void k_sa_gather(
+    const uint32_t* __restrict__ sa, const uint32_t* __restrict__ rank,
+    const uint32_t* __restrict__ grp, int64_t m, int64_t h,
+    const uint32_t* __restrict__ toff, uint64_t* key, uint32_t* val,
+    uint32_t* pos, const uint32_t* state) {
+  if (state[0]) return;
+  __shared__ uint32_t scnt[kSortWaves];
+  const int wv = threadIdx.x / kWave;
+  const int ln = lane_id();
+  const int64_t wbase = (int64_t)blockIdx.x * kTile + (int64_t)wv * kWaveSpan;
+  constexpr int kSteps = kWaveSpan / kWave;
+  uint32_t flags = 0;
+  uint32_t cnt = 0;
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    const int64_t j = wbase + s * kWave + ln;
+    const bool a = j < m && unfinished(grp, j, m);
+    flags |= (uint32_t)a << s;
+    cnt += (uint32_t)popc(ballot(a));
+  }
+  if (ln == 0) scnt[wv] = cnt;
+  __syncthreads();
+  uint32_t out = toff[blockIdx.x];
+  for (int w = 0; w < wv; ++w) out += scnt[w];
+  const uint64_t M1 = (uint64_t)m + 1;
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    const int64_t j = wbase + s * kWave + ln;
+    const bool a = (flags >> s) & 1u;
+    const uint64_t bm = ballot(a);
+    if (a) {
+      const uint32_t o = out + (uint32_t)rank_lt(bm);
+      const uint32_t i = sa[j];
+      const uint64_t k2 =
+          (int64_t)i + h < m ? (uint64_t)rank[i + h] + 1 : 0;
+      key[o] = (uint64_t)grp[j] * M1 + k2;
+      val[o] = i;
+      pos[o] = (uint32_t)j;
+    }
+    out += (uint32_t)popc(bm);
+  }
+}
+
+// ------------------------------------------------------------ outputs
 // keys[r * W + j] = corpus[sa[r] + j] (-1 at or past n).
 __global__ __launch_bounds__(256) void k_rank_keys(const int32_t* corpus,
                                                  const int32_t* sa, int64_t n,
@@ -317,8 +462,8 @@ __global__ __launch_bounds__(256) void k_rank_keys(const int32_t* corpus,
   if (e >= n * W) return;
   const int64_t r = e / W;
   const int j = (int)(e - r * W);
-  const int64_t pos = (int64_t)sa[r] + j;
-  keys[e] = pos < n && pos >= 0 ? corpus[pos] : -1;
+  const int64_t p = (int64_t)sa[r] + j;
+  keys[e] = p < n && p >= 0 ? corpus[p] : -1;
 }
 
 template <typename T>
@@ -333,6 +478,38 @@ static int bits_for(uint64_t maxval) {
   int b = 0;
   while (b < 64 && (maxval >> b) != 0) ++b;
   return b;
+}
+
+// LSD radix sort of the active (key, val) pairs by the low `nbits` bits,
+// then the group heads of the sorted order.
+static int sort_and_rank(SaWs& w, int64_t nb, int nbits, hipStream_t stream) {
+  uint64_t* kin = w.keyA;
+  uint32_t* vin = w.valA;
+  uint64_t* kout = w.keyB;
+  uint32_t* vout = w.valB;
+  for (int sh = 0; sh < nbits; sh += 8) {
+    hipLaunchKernelGGL(k_rs_hist, dim3((unsigned)nb), dim3(kSortThreads), 0,
+                       stream, kin, sh, w.hist, nb, w.state);
+    hipLaunchKernelGGL(k_rs_rowscan, dim3(kRadix), dim3(kSortThreads), 0,
+                       stream, w.hist, nb, w.rowsum, w.state);
+    hipLaunchKernelGGL(k_rs_scatter, dim3((unsigned)nb), dim3(kSortThreads),
+                       0, stream, kin, vin, kout, vout, sh, w.hist, nb,
+                       w.rowsum, w.state);
+    uint64_t* tk = kin;
+    kin = kout;
+    kout = tk;
+    uint32_t* tv = vin;
+    vin = vout;
+    vout = tv;
+  }
+  hipLaunchKernelGGL(k_grp_reduce, dim3((unsigned)nb), dim3(kSortThreads), 0,
+                     stream, kin, w.pos, w.blkmax, w.state);
+  hipLaunchKernelGGL(k_grp_carry, dim3(1), dim3(1024), 0, stream, w.blkmax,
+                     w.carry, w.state);
+  hipLaunchKernelGGL(k_grp_rank, dim3((unsigned)nb), dim3(kSortThreads), 0,
+                     stream, kin, vin, w.pos, w.carry, w.rank, w.sa, w.grp,
+                     w.state);
+  return (int)hipGetLastError();
 }
 
 }  // namespace sfx
@@ -382,50 +559,21 @@ extern "C" int sfx_sa_build(const int32_t* text, int64_t m, int64_t n_total,
   sa_ws_layout(m, workspace, &w);
   const int64_t nb = (m + kTile - 1) / kTile;
   const unsigned eb = (unsigned)((m + 255) / 256);
-  hipLaunchKernelGGL(k_sa_reset, dim3(1), dim3(64), 0, stream, w.state);
   hipLaunchKernelGGL(k_sa_init, dim3(eb), dim3(256), 0, stream, text, m,
-                     w.keyA, w.valA);
-  int rounds = 0;
-  while ((1LL << rounds) < m) ++rounds;  // ceil(log2 m)
-  for (int round = 0; round <= rounds; ++round) {
-    int nbits;
-    if (round == 0) {
-      nbits = 32;
-    } else {
-      const int64_t h = 1LL << (round - 1);
-      hipLaunchKernelGGL(k_sa_keys, dim3(eb), dim3(256), 0, stream, w.sa,
-                         w.rank, m, h, w.keyA, w.valA, w.state);
-      const uint64_t maxkey =
-          (uint64_t)(m - 1) * (uint64_t)(m + 1) + (uint64_t)m;
-      nbits = bits_for(maxkey);
-    }
-    uint64_t* kin = w.keyA;
-    uint32_t* vin = w.valA;
-    uint64_t* kout = w.keyB;
-    uint32_t* vout = w.valB;
-    for (int sh = 0; sh < nbits; sh += 8) {
-      hipLaunchKernelGGL(k_rs_hist, dim3((unsigned)nb), dim3(kSortThreads), 0,
-                         stream, kin, m, sh, w.hist, nb, w.state);
-      hipLaunchKernelGGL(k_scan_excl, dim3(1), dim3(1024), 0, stream, w.hist,
-                         (int64_t)kRadix * nb, (const uint32_t*)w.state);
-      hipLaunchKernelGGL(k_rs_scatter, dim3((unsigned)nb),
-                         dim3(kSortThreads), 0, stream, kin, vin, kout, vout,
-                         m, sh, w.hist, nb, w.state);
-      uint64_t* tk = kin;
-      kin = kout;
-      kout = tk;
-      uint32_t* tv = vin;
-      vin = vout;
-      vout = tv;
-    }
-    hipLaunchKernelGGL(k_grp_reduce, dim3((unsigned)nb), dim3(kSortThreads),
-                       0, stream, kin, m, w.blkmax, w.blkcnt, w.state);
-    hipLaunchKernelGGL(k_grp_carry, dim3(1), dim3(1024), 0, stream, w.blkmax,
-                       w.blkcnt, w.carry, nb, m, w.state);
-    hipLaunchKernelGGL(k_grp_rank, dim3((unsigned)nb), dim3(kSortThreads), 0,
-                       stream, kin, vin, m, w.carry, w.rank, w.sa, w.state);
-    hipLaunchKernelGGL(k_sa_commit, dim3(1), dim3(64), 0, stream, w.state);
-    int rc = (int)hipGetLastError();
+                     w.keyA, w.valA, w.pos, w.state);
+  int rc = sort_and_rank(w, nb, 32, stream);
+  if (rc) return rc;
+  const uint64_t maxkey = (uint64_t)(m - 1) * (uint64_t)(m + 1) + (uint64_t)m;
+  const int nbits = bits_for(maxkey);
+  for (int64_t h = 1; h < m; h <<= 1) {
+    hipLaunchKernelGGL(k_sa_mark, dim3((unsigned)nb), dim3(kSortThreads), 0,
+                       stream, w.grp, m, w.tcnt, w.state);
+    hipLaunchKernelGGL(k_sa_tilescan, dim3(1), dim3(1024), 0, stream, w.tcnt,
+                       w.toff, nb, w.state);
+    hipLaunchKernelGGL(k_sa_gather, dim3((unsigned)nb), dim3(kSortThreads), 0,
+                       stream, w.sa, w.rank, w.grp, m, h, w.toff, w.keyA,
+                       w.valA, w.pos, w.state);
+    rc = sort_and_rank(w, nb, nbits, stream);
     if (rc) return rc;
   }
   if (sa_is64)

@@ -93,11 +93,25 @@ def test_build_suffix_array_structured(gpu):
     from suffixgpu_amd.suffix_array import build_suffix_array
     for toks in ([1, 2, 3, 1, 2, 3, 1, 2], [5] * 5000, [0],
                  [3, -2, 2147483647, 3, -2, 0, 2147483647],
+                 [-2147483648, 0, -2147483648, 5, -2147483648],
                  [1, 2] * 3000 + [1]):
         got = build_suffix_array(T(np.array(toks, I32), gpu))
         if len(toks) <= 64:
             assert N(got).tolist() == naive.suffix_array(toks)
         np.testing.assert_array_equal(N(got), o_build_sa(np.array(toks)))
+
+
+def test_build_suffix_array_template_corpus(gpu):
+    """Sequences sharing template spans: long repeats, many rounds, most
+    suffixes finished early (the active set shrinks round by round)."""
+    from suffixgpu_amd import synth
+    from suffixgpu_amd.suffix_array import build_suffix_array
+    tc = synth.TemplateCorpus(seed=11)
+    docs = [np.append(tc.sequence(lo=1024, hi=4096), -2) for _ in range(90)]
+    t = np.concatenate(docs + [np.array([2147483647])]).astype(I32)
+    t = np.concatenate([t, t[:5000]])  # one 5000-token exact repeat
+    got = build_suffix_array(T(t, gpu))
+    np.testing.assert_array_equal(N(got), o_build_sa(t))
 
 
 def test_build_suffix_array_identity_tail(gpu):
