@@ -31,7 +31,7 @@ extern "C" {
 
 #define SFX_EINVAL (-1)
 #define SFX_MAX_CANDIDATES 32
-#define SFX_ABI_VERSION 3
+#define SFX_ABI_VERSION 4
 
 /* Drafter configuration shared by the local and global paths.
  * Mirrors the constructor arguments of SuffixGPUDrafter
@@ -195,7 +195,8 @@ int sfx_propose_step(const sfx_params* p, const sfx_index* index,
 
 /* sa[0:m] = suffix array of text[0:m] (signed int32 order, a proper prefix
  * first); sa[m:n_total] = m .. n_total-1.  Prefix doubling with LSD radix
- * sorts; rounds stop on the device once every rank is distinct, with no
+ * sorts; each round re-sorts only the suffixes whose group is not yet a
+ * singleton, and the rounds stop on the device once none is left, with no
  * host synchronisation.  sa_is64 selects int64 output. */
 size_t sfx_sa_build_workspace_size(int64_t m);
 
@@ -206,6 +207,15 @@ int sfx_sa_keys(const int32_t* corpus, const int32_t* sa, int64_t n,
 int sfx_sa_build(const int32_t* text, int64_t m, int64_t n_total, void* sa,
                  int32_t sa_is64, void* workspace, size_t workspace_bytes,
                  hipStream_t stream);
+
+/* global_index.py:235-240 _finish_swap: in-place copy of a finished
+ * rebuild into the live buffers (corpus, sa: capacity int32 each; sa_key:
+ * capacity * key_width int32, skipped when key_width is 0), one launch, so
+ * graphs captured over the live buffers keep their pointers. */
+int sfx_index_swap(int32_t* corpus, int32_t* sa, int32_t* sa_key,
+                   const int32_t* new_corpus, const int32_t* new_sa,
+                   const int32_t* new_sa_key, int64_t capacity,
+                   int64_t key_width, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsuffixgpu_amd.so"
 MAX_CANDIDATES = 32
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -64,6 +64,8 @@ class SfxGlobalOut(ctypes.Structure):
 # name -> (restype, argtypes)
 SIGNATURES = {
     "sfx_abi_version": (c_i32, []),
+    "sfx_index_swap": (c_i32, [c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64,
+                               c_p]),
     "sfx_scatter_append": (c_i32, [ctypes.POINTER(SfxBatch), c_p, c_p]),
     "sfx_match_back": (c_i32, [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p,
                                c_p]),

@@ -74,13 +74,8 @@ static int launch_global(GlobalArgs& a, hipStream_t stream) {
   size_t lds = 0;
   a.merge_waves = merge_waves_for(a.p, a.ix, &lds);
   a.mb_lds = mb_lds_bytes(a.ix);
-  static bool attr_done = false;
-  if (!attr_done) {
-    hipFuncSetAttribute((const void*)k_global,
-                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)kMaxLds);
-    attr_done = true;
-  }
+  static std::atomic<uint64_t> lds_opt{0};
+  allow_max_lds((const void*)k_global, lds_opt);
   hipLaunchKernelGGL(k_global, dim3((unsigned)(2 * a.B)),
                      dim3(kGlobalThreads), lds, stream, a);
   return (int)hipGetLastError();

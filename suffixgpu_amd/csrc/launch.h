@@ -3,6 +3,9 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+#include <cstdint>
+
 #include "step_ws.h"
 #include "suffixgpu_amd.h"
 
@@ -10,6 +13,22 @@ namespace sfx {
 
 // LDS available to one workgroup on gfx950 (160 KiB per CU).
 constexpr size_t kMaxLds = 160 * 1024;
+
+// Opts `fn` into the full LDS of a CU on the current device, once per
+// device (`done` holds one bit per device ordinal).
+inline void allow_max_lds(const void* fn, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                        (int)kMaxLds);
+    return;
+  }
+  const uint64_t bit = 1ull << dev;
+  if (done.load(std::memory_order_acquire) & bit) return;
+  hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                      (int)kMaxLds);
+  done.fetch_or(bit, std::memory_order_release);
+}
 
 int check_local(const sfx_params& p, const sfx_batch& bt);
 size_t local_lds_bytes(const sfx_params& p, int64_t S);

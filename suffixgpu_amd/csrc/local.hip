@@ -46,13 +46,8 @@ int check_local(const sfx_params& p, const sfx_batch& bt) {
 int launch_local(const LocalArgs& a, hipStream_t stream) {
   if (a.bt.batch == 0) return 0;
   const size_t lds = local_lds_bytes(a.p, a.bt.seq);
-  static bool attr_done = false;
-  if (!attr_done) {
-    hipFuncSetAttribute((const void*)k_local,
-                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)kMaxLds);
-    attr_done = true;
-  }
+  static std::atomic<uint64_t> lds_opt{0};
+  allow_max_lds((const void*)k_local, lds_opt);
   hipLaunchKernelGGL(k_local, dim3((unsigned)a.bt.batch), dim3(kLocalThreads),
                      lds, stream, a);
   return (int)hipGetLastError();

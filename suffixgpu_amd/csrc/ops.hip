@@ -27,6 +27,36 @@ __global__ __launch_bounds__(64) void k_scatter(sfx_batch bt,
   if (new_counts && threadIdx.x == 0) new_counts[b] = (int32_t)st.q;
 }
 
+// ---------------------------------------------------------- index swap
+// Up to three buffer copies in one grid-stride launch: 16-byte words where
+// both sides are 16-byte aligned, single words for the rest.
+struct CopySpan {
+  int32_t* dst;
+  const int32_t* src;
+  int64_t n;
+};
+
+__device__ __forceinline__ void copy_span(const CopySpan& c, int64_t tid,
+                                          int64_t nthreads) {
+  if (c.n <= 0) return;
+  const bool vec = ((reinterpret_cast<uintptr_t>(c.dst) |
+                     reinterpret_cast<uintptr_t>(c.src)) & 15u) == 0;
+  const int64_t n4 = vec ? c.n / 4 : 0;
+  const int4* s4 = reinterpret_cast<const int4*>(c.src);
+  int4* d4 = reinterpret_cast<int4*>(c.dst);
+  for (int64_t i = tid; i < n4; i += nthreads) d4[i] = s4[i];
+  for (int64_t i = 4 * n4 + tid; i < c.n; i += nthreads) c.dst[i] = c.src[i];
+}
+
+__global__ __launch_bounds__(256) void k_swap(CopySpan a, CopySpan b,
+                                              CopySpan c) {
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nth = (int64_t)gridDim.x * blockDim.x;
+  copy_span(a, tid, nth);
+  copy_span(b, tid, nth);
+  copy_span(c, tid, nth);
+}
+
 // -------------------------------------------------------------- match_back
 __global__ __launch_bounds__(256) void k_match_back(
     const int32_t* __restrict__ src, int64_t row_stride,
@@ -201,6 +231,25 @@ extern "C" int sfx_trace_set(uint64_t* buf) {
 
 extern "C" int sfx_abi_version(void) { return SFX_ABI_VERSION; }
 
+extern "C" int sfx_index_swap(int32_t* corpus, int32_t* sa, int32_t* sa_key,
+                              const int32_t* new_corpus,
+                              const int32_t* new_sa,
+                              const int32_t* new_sa_key, int64_t capacity,
+                              int64_t key_width, hipStream_t stream) {
+  if (capacity < 0 || key_width < 0 || (key_width > 0 && !sa_key) ||
+      (key_width > 0 && !new_sa_key))
+    return SFX_EINVAL;
+  if (capacity == 0) return 0;
+  if (!corpus || !sa || !new_corpus || !new_sa) return SFX_EINVAL;
+  const CopySpan a{corpus, new_corpus, capacity};
+  const CopySpan b{sa, new_sa, capacity};
+  const CopySpan c{sa_key, new_sa_key, key_width > 0 ? capacity * key_width
+                                                     : 0};
+  // enough 256-thread blocks to keep every CU streaming
+  hipLaunchKernelGGL(k_swap, dim3(2048), dim3(256), 0, stream, a, b, c);
+  return (int)hipGetLastError();
+}
+
 extern "C" int sfx_scatter_append(const sfx_batch* bt, int32_t* new_counts,
                                   hipStream_t stream) {
   if (!bt || bt->batch < 0 || bt->seq < 1 || !bt->tokens ||
@@ -293,16 +342,10 @@ extern "C" int sfx_expand_chain(const int32_t* cont, int64_t rows,
   a.waves_per_block = wpb;
   const int64_t blocks = (rows + wpb - 1) / wpb;
   const size_t lds = per_wave * (size_t)wpb;
-  static bool attr_done = false;
-  if (!attr_done) {
-    hipFuncSetAttribute((const void*)k_expand<true>,
-                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)kMaxLds);
-    hipFuncSetAttribute((const void*)k_expand<false>,
-                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)kMaxLds);
-    attr_done = true;
-  }
+  static std::atomic<uint64_t> lds_opt_w{0};
+  allow_max_lds((const void*)k_expand<true>, lds_opt_w);
+  static std::atomic<uint64_t> lds_opt_u{0};
+  allow_max_lds((const void*)k_expand<false>, lds_opt_u);
   if (weights)
     hipLaunchKernelGGL(k_expand<true>, dim3((unsigned)blocks), dim3(256),
                        lds, stream, a);

@@ -91,13 +91,8 @@ extern "C" int sfx_propose_step(const sfx_params* p, const sfx_index* ix,
   }
   if (lds > kMaxLds) return SFX_EINVAL;
   if (bt->batch == 0) return 0;
-  static bool attr_done = false;
-  if (!attr_done) {
-    hipFuncSetAttribute((const void*)k_step,
-                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)kMaxLds);
-    attr_done = true;
-  }
+  static std::atomic<uint64_t> lds_opt{0};
+  allow_max_lds((const void*)k_step, lds_opt);
   const unsigned blocks = (unsigned)(bt->batch * (global_on ? 3 : 1));
   hipLaunchKernelGGL(k_step, dim3(blocks), dim3(kGlobalThreads), lds, stream,
                      a);

@@ -258,9 +258,11 @@ class GlobalIndex:
 
     def _finish_swap(self, n_new: int, new_doc_lens: deque[int]) -> None:
         # In-place copies: captured graphs bind the active tensors' storage.
-        self.corpus.copy_(self.staging_corpus)
-        self.sa.copy_(self.staging_sa)
-        self.sa_key.copy_(self.staging_sa_key)
+        check(lib().sfx_index_swap(
+            self.corpus.data_ptr(), self.sa.data_ptr(),
+            self.sa_key.data_ptr(), self.staging_corpus.data_ptr(),
+            self.staging_sa.data_ptr(), self.staging_sa_key.data_ptr(),
+            self.capacity, KEY_WIDTH, stream_of(self.device)), "swap")
         self.active_len = n_new
         self.active_doc_lens = new_doc_lens
         self._rebuild_event = None

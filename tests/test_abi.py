@@ -1,0 +1,127 @@
+"""The C ABI without a GPU: the library loads, exports every function the
+header declares, reports the header's ABI version, and the ctypes mirrors
+of the header structs have the C layout (checked against gcc's sizeof /
+offsetof of the header itself).  No kernel is launched."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from suffixgpu_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "suffixgpu_amd.h"
+ROCM_INCLUDE = Path("/opt/rocm/include")
+
+
+def header_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sfx_\w+)\s*\(", text)))
+
+
+def header_define(name: str) -> int:
+    m = re.search(rf"#define\s+{name}\s+\(?(-?\d+)\)?", HEADER.read_text())
+    assert m, name
+    return int(m.group(1))
+
+
+@pytest.fixture(scope="module")
+def so():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f"{_lib.LIB_PATH} missing: run `python -m "
+                    "suffixgpu_amd.build` first")
+    return ctypes.CDLL(str(_lib.LIB_PATH))
+
+
+def test_header_declares_the_reference_operator_set():
+    fns = header_functions()
+    for name in ("sfx_scatter_append", "sfx_match_back",
+                 "sfx_first_occurrences", "sfx_sa_search", "sfx_expand_chain",
+                 "sfx_local_gather", "sfx_local_forward", "sfx_global_query",
+                 "sfx_propose_step", "sfx_sa_build", "sfx_sa_keys",
+                 "sfx_index_swap"):
+        assert name in fns
+
+
+def test_library_exports_every_declared_function(so):
+    missing = [f for f in header_functions() if not hasattr(so, f)]
+    assert not missing, missing
+
+
+def test_ctypes_signatures_cover_the_header():
+    assert sorted(_lib.SIGNATURES) == header_functions()
+
+
+def test_abi_version_and_constants(so):
+    so.sfx_abi_version.restype = ctypes.c_int32
+    assert so.sfx_abi_version() == header_define("SFX_ABI_VERSION")
+    assert _lib.ABI_VERSION == header_define("SFX_ABI_VERSION")
+    assert _lib.MAX_CANDIDATES == header_define("SFX_MAX_CANDIDATES")
+
+
+def test_workspace_sizes_are_host_only(so):
+    lib = _lib.lib()
+    p = _lib.make_params(16, 32, 128, 1, [1, 2, 4, 8, 16, 32, 64, 128],
+                         [32, 16, 8, 4, 2], 2.0, 0.0, 0.1, 0.0)
+    assert lib.sfx_step_workspace_size(p, 64, 1 << 16) > 0
+    assert lib.sfx_global_query_workspace_size(p, 64, 1 << 16) > 0
+    assert lib.sfx_sa_build_workspace_size(1 << 22) >= 40 * (1 << 22)
+    assert lib.sfx_sa_build_workspace_size(-1) == 0
+
+
+def test_argument_errors_are_reported_before_any_launch():
+    lib = _lib.lib()
+    # invalid sizes are rejected on the host: nothing is enqueued
+    assert lib.sfx_sa_keys(None, None, 16, 3, None, None) == -1
+    assert lib.sfx_sa_build(None, -1, 0, None, 0, None, 0, None) == -1
+    assert lib.sfx_index_swap(None, None, None, None, None, None, -1, 0,
+                              None) == -1
+
+
+STRUCT_PROBE = r"""
+#include <stddef.h>
+#include <stdio.h>
+#include "suffixgpu_amd.h"
+#define F(T, f) printf(#T "." #f " %zu\n", offsetof(T, f))
+#define S(T) printf(#T " %zu\n", sizeof(T))
+int main(void) {
+  S(sfx_params); F(sfx_params, k); F(sfx_params, spec_factor);
+  F(sfx_params, alpha); F(sfx_params, thresholds); F(sfx_params, caps);
+  S(sfx_index); F(sfx_index, delta_len); F(sfx_index, sa_key);
+  F(sfx_index, key_width);
+  S(sfx_batch); F(sfx_batch, num_tokens_is64); F(sfx_batch, sampled);
+  F(sfx_batch, valid_count_is64); F(sfx_batch, mask); F(sfx_batch, limit);
+  S(sfx_global_out); F(sfx_global_out, draft_score);
+  return 0;
+}
+"""
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None
+                    or not (ROCM_INCLUDE / "hip").is_dir(),
+                    reason="needs gcc and the ROCm headers")
+def test_struct_layouts_match_the_header(tmp_path):
+    src = tmp_path / "probe.c"
+    src.write_text(STRUCT_PROBE)
+    exe = tmp_path / "probe"
+    subprocess.run(["gcc", "-D__HIP_PLATFORM_AMD__", f"-I{ROOT / 'include'}",
+                    f"-I{ROCM_INCLUDE}", str(src), "-o", str(exe)],
+                   check=True, capture_output=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True,
+                         text=True).stdout
+    c = dict(line.rsplit(" ", 1) for line in out.strip().splitlines())
+    mirrors = {"sfx_params": _lib.SfxParams, "sfx_index": _lib.SfxIndex,
+               "sfx_batch": _lib.SfxBatch, "sfx_global_out": _lib.SfxGlobalOut}
+    for key, val in c.items():
+        if "." in key:
+            t, f = key.split(".")
+            assert getattr(mirrors[t], f).offset == int(val), key
+        else:
+            assert ctypes.sizeof(mirrors[key]) == int(val), key
