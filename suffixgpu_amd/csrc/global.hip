@@ -1,15 +1,17 @@
 // Global (cross-request) match: SA interval search + delta scan + merge.
 //
-// Grid: two 512-thread workgroups per query row, interleaved.
+// Grid: 1 + dparts 512-thread workgroups per query row, interleaved.
 //   * SA role: for every length l = 1..min(qlen, P) the suffix of length l
 //     of the query is searched by an 8-lane k-ary interval search
 //     (sa_search.h); each cap then takes its longest non-empty interval
 //     (suffix_gpu/sa_search.py:110-163).
-//   * Delta role: match_back over the committed delta with an early-exit
-//     compare per position, a block max, and the ordered compaction of the
-//     first R ends per cap (global_index.py:465-546).
-// Whichever role finishes a row second (atomic handover in the workspace)
-// merges the two sources per cap (global_index.py:311-370): SA vs delta
+//   * Delta roles: each takes an equal share of the committed delta:
+//     match_back with an early-exit compare per position, a block max, and
+//     the ordered compaction of its first R ends per cap
+//     (global_index.py:465-546).
+// Whichever workgroup finishes a row last (atomic handover in the
+// workspace) combines the delta parts and merges the two sources per cap
+// (global_index.py:311-370): SA vs delta
 // choice, adjacent-duplicate zeroing, strided SA sampling, continuation
 // gather into LDS, and (decode step / draft) one wave per cap running the
 // majority-vote expansion, then the first-argmax cap.  In the decode step
@@ -22,18 +24,20 @@ namespace sfx {
 
 __global__ __launch_bounds__(kGlobalThreads) void k_global(GlobalArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  global_body(a, smem, (int)(blockIdx.x >> 1), (blockIdx.x & 1) == 0);
+  const int per = 1 + a.dparts;
+  global_body(a, smem, (int)(blockIdx.x / per), (int)(blockIdx.x % per));
 }
 
 
-int mb_lds_bytes(const sfx_index& ix) {
-  if (ix.delta_capacity + 1 > kMbLdsMax) return 0;
-  const int n = (int)ix.delta_capacity + 1;
+int mb_lds_bytes(const sfx_index& ix, int parts) {
+  const int64_t cap = delta_part_cap(ix.delta_capacity, parts);
+  if (cap > kMbLdsMax) return 0;
+  const int n = (int)cap;
   const int seg = (((n + kGlobalThreads - 1) / kGlobalThreads) + 15) & ~15;
   return seg * kGlobalThreads;
 }
 
-int merge_waves_for(const sfx_params& p, const sfx_index& ix,
+int merge_waves_for(const sfx_params& p, const sfx_index& ix, int parts,
                     size_t* lds) {
   const int NW = kGlobalThreads / kWave;
   const int C = p.num_caps;
@@ -42,7 +46,7 @@ int merge_waves_for(const sfx_params& p, const sfx_index& ix,
   for (; nmw >= 1; --nmw) {
     const GlobalLayout L = global_layout(p.max_pattern_len, C,
                                          p.max_occurrences, p.k, nmw,
-                                         mb_lds_bytes(ix));
+                                         mb_lds_bytes(ix, parts));
     if ((size_t)L.total <= kMaxLds) {
       *lds = (size_t)L.total;
       return nmw;
@@ -51,7 +55,7 @@ int merge_waves_for(const sfx_params& p, const sfx_index& ix,
   return 0;
 }
 
-int check_global(const sfx_params& p, const sfx_index& ix) {
+int check_global(const sfx_params& p, const sfx_index& ix, int64_t batch) {
   if (p.num_caps < 1 || p.num_caps > SFX_MAX_CANDIDATES) return SFX_EINVAL;
   if (p.k < 1 || p.k > 4096 || p.max_pattern_len < 1 ||
       p.max_pattern_len > 255 || p.max_occurrences < 1 ||
@@ -65,19 +69,23 @@ int check_global(const sfx_params& p, const sfx_index& ix) {
       (ix.key_width < 4 || ix.key_width > 32 || (ix.key_width & 3)))
     return SFX_EINVAL;
   size_t lds = 0;
-  if (merge_waves_for(p, ix, &lds) < 1) return SFX_EINVAL;
+  const int parts = delta_parts_for(batch, ix.delta_capacity);
+  if (merge_waves_for(p, ix, parts, &lds) < 1) return SFX_EINVAL;
   return 0;
 }
 
 static int launch_global(GlobalArgs& a, hipStream_t stream) {
   if (a.B == 0) return 0;
   size_t lds = 0;
-  a.merge_waves = merge_waves_for(a.p, a.ix, &lds);
-  a.mb_lds = mb_lds_bytes(a.ix);
+  a.dparts = delta_parts_for(a.B, a.ix.delta_capacity);
+  a.merge_waves = merge_waves_for(a.p, a.ix, a.dparts, &lds);
+  a.mb_lds = mb_lds_bytes(a.ix, a.dparts);
   static std::atomic<uint64_t> lds_opt{0};
   allow_max_lds((const void*)k_global, lds_opt);
-  hipLaunchKernelGGL(k_global, dim3((unsigned)(2 * a.B)),
-                     dim3(kGlobalThreads), lds, stream, a);
+  const unsigned blocks = (unsigned)((1 + a.dparts) * a.B);
+  lds = one_per_cu_lds(lds, blocks);
+  hipLaunchKernelGGL(k_global, dim3(blocks), dim3(kGlobalThreads), lds,
+                     stream, a);
   return (int)hipGetLastError();
 }
 
@@ -98,7 +106,7 @@ extern "C" int sfx_global_query(const sfx_params* p, const sfx_index* ix,
                                 const sfx_global_out* out, void* workspace,
                                 size_t workspace_bytes, hipStream_t stream) {
   if (!p || !ix || !out || batch < 0) return SFX_EINVAL;
-  int rc = check_global(*p, *ix);
+  int rc = check_global(*p, *ix, batch);
   if (rc) return rc;
   if (batch > 0 && (!query || !qlen || width < 1)) return SFX_EINVAL;
   const size_t need =

@@ -28,17 +28,18 @@ struct GlobalArgs {
   int32_t* num_valid;
   StepWs ws;
   int merge_waves;
-  int mb_lds;  // bytes of LDS for the delta match_back array (0: workspace)
+  int mb_lds;  // bytes of LDS for a delta part's match lengths (0: workspace)
+  int dparts;  // delta workgroups per row (delta_parts_for)
 };
 
 struct GlobalLayout {
-  int rpat, lb, ub, found, scan, red, misc, lo, dtok, dmb, mpos, mcache, mA,
-      chain, nv, score, rlen, rocc, total;
+  int rpat, lb, ub, found, scan, red, misc, lo, dlen, dcnt, dpc, dtok, dmb,
+      mpos, mcache, mA, chain, nv, score, rlen, rocc, total;
 };
 
 // Delta tokens staged per chunk (after a halo of P rounded up to 4
-// tokens); the per-row match_back bytes stay in LDS up to kMbLdsMax
-// positions, longer deltas keep them in the workspace.
+// tokens); a part's match_back bytes stay in LDS up to kMbLdsMax
+// positions, longer parts keep them in the workspace.
 constexpr int kDeltaChunk = 8192;
 constexpr int kMbLdsMax = (int)kDeltaMbLdsMax;
 
@@ -65,6 +66,9 @@ __host__ __device__ inline GlobalLayout global_layout(int P, int C, int R,
   L.red = g_take(off, NW * 4);
   L.misc = g_take(off, 64);
   L.lo = g_take(off, C * 4);
+  L.dlen = g_take(off, C * 4);
+  L.dcnt = g_take(off, C * 4);
+  L.dpc = g_take(off, C * kMaxDeltaParts * 4);
   L.chain = g_take(off, C * K * 4);
   L.nv = g_take(off, C * 4);
   L.score = g_take(off, C * 4);
@@ -82,16 +86,19 @@ __host__ __device__ inline GlobalLayout global_layout(int P, int C, int R,
   return L;
 }
 
-// ---- Delta role: match_back over ends i in [0, delta_len] with the delta
-// staged through LDS in 16-byte words (chunks of kDeltaChunk positions
-// after a halo of P rounded up to 4), kept as u8 in LDS (kMbLds) or the
-// workspace, then one ordered pass extracts the first R ends per cap with
-// mb >= min(max mb, cap) (global_index.py:465-546).
+// ---- Delta role, one part of the row: match_back over ends i in
+// [lo, hi) of 0 .. delta_len, with the delta staged through LDS in 16-byte
+// words (chunks of kDeltaChunk positions after a halo of P rounded up to
+// 4), kept as u8 in LDS (kMbLds) or the workspace; then one ordered pass
+// extracts the part's first R ends per cap with mb >= min(part max, cap).
+// The merge keeps a part's list only where that threshold equals the
+// row's min(max mb, cap) -- any other part has no end that reaches it --
+// and concatenates the kept lists in part order (global_index.py:465-546).
 template <bool kMbLds>
 __device__ __forceinline__ void delta_role(const GlobalArgs& a,
                                            const GlobalLayout& L,
                                            unsigned char* smem, int b,
-                                           const int32_t* rpat) {
+                                           int part, const int32_t* rpat) {
   constexpr int NT = kGlobalThreads;
   constexpr int NW = NT / kWave;
   const sfx_params& p = a.p;
@@ -101,6 +108,7 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
   const int P = p.max_pattern_len;
   const int C = p.num_caps;
   const int R = p.max_occurrences;
+  const int KD = a.dparts;
   const int64_t D = a.ix.delta_capacity;
   int32_t* found = (int32_t*)(smem + L.found);
   uint32_t* scan = (uint32_t*)(smem + L.scan);
@@ -108,11 +116,14 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
   int* misc = (int*)(smem + L.misc);
   int32_t* lo_lds = (int32_t*)(smem + L.lo);
   int32_t* dtok = (int32_t*)(smem + L.dtok);
+  const int64_t slot = (int64_t)b * KD + part;
   uint8_t* mb = kMbLds ? (uint8_t*)(smem + L.dmb)
-                       : a.ws.d_mb + (int64_t)b * delta_mb_stride(D);
+                       : a.ws.d_mb + slot * delta_mb_stride(
+                                                delta_part_cap(D, KD));
   int64_t dl = *a.ix.delta_len;
   dl = dl < 0 ? 0 : (dl > D ? D : dl);
-  const int64_t n = dl + 1;
+  int64_t plo, phi;
+  delta_part_range(dl + 1, KD, part, &plo, &phi);
   const int halo = (P + 3) & ~3;
   const int4* d4 = reinterpret_cast<const int4*>(a.ix.delta);
   // Staged words per chunk: x(j0 .. cend - 2) with j0 = c0 - halo, in
@@ -120,7 +131,7 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
   // next chunk's loads are in flight while the current one is scanned.
   constexpr int kStage4 = (kDeltaChunk + 256) / 4 / NT + 1;
   auto chunk_words = [&](int64_t c0) -> int {
-    const int64_t cend = c0 + kDeltaChunk < n ? c0 + kDeltaChunk : n;
+    const int64_t cend = c0 + kDeltaChunk < phi ? c0 + kDeltaChunk : phi;
     return (int)((cend - 1 - (c0 - halo) + 3) / 4);
   };
   auto load_chunk = [&](int64_t c0, int4 (&v)[kStage4]) {
@@ -144,10 +155,10 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
   };
   const int32_t r0 = rpat[0];
   int4 stage[kStage4];
-  load_chunk(0, stage);
+  if (plo < phi) load_chunk(plo, stage);
   int mx = 0;
-  for (int64_t c0 = 0; c0 < n; c0 += kDeltaChunk) {
-    const int64_t cend = c0 + kDeltaChunk < n ? c0 + kDeltaChunk : n;
+  for (int64_t c0 = plo; c0 < phi; c0 += kDeltaChunk) {
+    const int64_t cend = c0 + kDeltaChunk < phi ? c0 + kDeltaChunk : phi;
     {
       const int nk4 = chunk_words(c0);
 #pragma unroll
@@ -157,7 +168,7 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
       }
     }
     __syncthreads();
-    if (c0 + kDeltaChunk < n) load_chunk(c0 + kDeltaChunk, stage);
+    if (c0 + kDeltaChunk < phi) load_chunk(c0 + kDeltaChunk, stage);
     // Ends i0 .. i0 + 3 (i0 = c0 + 4g) test x(i - 1) against the newest
     // pattern token first; only ends that pass walk further back.
     const int ng = (int)((cend - c0 + 3) / 4);
@@ -178,7 +189,7 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
           mx = max(mx, m);
         }
       }
-      *reinterpret_cast<uint32_t*>(mb + i0) = word;
+      *reinterpret_cast<uint32_t*>(mb + (i0 - plo)) = word;
     }
     __syncthreads();
   }
@@ -191,42 +202,68 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
     misc[0] = m;
   }
   __syncthreads();
-  const int lo_full = misc[0];
+  const int part_max = misc[0];
   SFX_TRACE_POINT(2);
-  for (int c = tid; c < C; c += NT) lo_lds[c] = min(lo_full, p.caps[c]);
+  for (int c = tid; c < C; c += NT) lo_lds[c] = min(part_max, p.caps[c]);
   __syncthreads();
   for (int g0 = 0; g0 < C; g0 += 8)
-    compact_first_r<NT>(mb, n, lo_lds + g0, min(8, C - g0), R,
-                        a.ws.d_end + ((int64_t)b * C + g0) * R, found + g0,
-                        scan);
+    compact_first_r<NT>(mb, phi - plo, lo_lds + g0, min(8, C - g0), R,
+                        a.ws.d_end + (slot * C + g0) * R, (int32_t)plo,
+                        found + g0, scan);
   __syncthreads();
   SFX_TRACE_POINT(3);
-  for (int c = tid; c < C; c += NT) {
-    const int lo = lo_lds[c];
-    const int cnt = lo > 0 ? found[c] : 0;
-    a.ws.d_len[(int64_t)b * C + c] = lo;
-    a.ws.d_cnt[(int64_t)b * C + c] = cnt;
-    if (a.out.d_len) a.out.d_len[(int64_t)b * C + c] = lo;
-    if (a.out.d_cnt) a.out.d_cnt[(int64_t)b * C + c] = cnt;
-  }
-  if (a.out.d_pos) {
-    for (int e = tid; e < C * R; e += NT) {
-      const int c = e / R;
-      const int r = e % R;
-      const int lo = lo_lds[c];
-      const int cnt = lo > 0 ? found[c] : 0;
-      const int64_t end =
-          r < cnt ? (int64_t)a.ws.d_end[((int64_t)b * C + c) * R + r] : 0;
-      int64_t v = end - lo;
-      v = v < 0 ? 0 : v;
-      a.out.d_pos[((int64_t)b * C + c) * R + r] = v;
+  for (int c = tid; c < C; c += NT)
+    a.ws.d_cnt[slot * C + c] = lo_lds[c] > 0 ? found[c] : 0;
+  if (tid == 0) a.ws.d_mx[slot] = part_max;
+}
+
+// Row-level delta result per cap from the parts (run by the merging
+// workgroup): dlen[c] = min(max mb, cap), dpc[c][k] = part k's kept hits,
+// dcnt[c] = min(sum, R).
+__device__ __forceinline__ void delta_combine(const GlobalArgs& a, int b,
+                                              int32_t* dlen, int32_t* dcnt,
+                                              int32_t* dpc) {
+  const int C = a.p.num_caps;
+  const int R = a.p.max_occurrences;
+  const int KD = a.dparts;
+  for (int c = threadIdx.x; c < C; c += blockDim.x) {
+    const int cap = a.p.caps[c];
+    int mx = 0;
+    for (int k = 0; k < KD; ++k) mx = max(mx, a.ws.d_mx[(int64_t)b * KD + k]);
+    const int lo = min(mx, cap);
+    int total = 0;
+    for (int k = 0; k < KD; ++k) {
+      const int64_t slot = (int64_t)b * KD + k;
+      const bool keep = lo > 0 && min(a.ws.d_mx[slot], cap) == lo;
+      const int h = keep ? a.ws.d_cnt[slot * C + c] : 0;
+      dpc[c * kMaxDeltaParts + k] = h;
+      total += h;
     }
+    dlen[c] = lo;
+    dcnt[c] = total < R ? total : R;
   }
 }
 
+// End position of the row's r-th delta hit for cap c (r < dcnt[c]).
+__device__ __forceinline__ int32_t delta_end_at(const GlobalArgs& a, int b,
+                                                int c, int r,
+                                                const int32_t* dpc) {
+  const int C = a.p.num_caps;
+  const int R = a.p.max_occurrences;
+  const int KD = a.dparts;
+  int k = 0;
+  while (k < KD - 1 && r >= dpc[c * kMaxDeltaParts + k]) {
+    r -= dpc[c * kMaxDeltaParts + k];
+    ++k;
+  }
+  const int64_t slot = (int64_t)b * KD + k;
+  return a.ws.d_end[(slot * C + c) * R + r];
+}
+
+// role 0: SA search; role 1 .. dparts: delta part role - 1.
 __device__ __forceinline__ void global_body(const GlobalArgs& a,
                                             unsigned char* smem, int b,
-                                            bool sa_role) {
+                                            int role) {
   constexpr int NT = kGlobalThreads;
   constexpr int NW = NT / kWave;
   const sfx_params& p = a.p;
@@ -281,7 +318,7 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
   __syncthreads();
   SFX_TRACE_POINT(1);
 
-  if (sa_role) {
+  if (role == 0) {
     // ---- SA interval search for every suffix length of the tail.
     constexpr int G = kSearchGroup;
     const int ngroups = NT / G;
@@ -325,15 +362,34 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
     }
   } else {
     if (a.mb_lds)
-      delta_role<true>(a, L, smem, b, rpat);
+      delta_role<true>(a, L, smem, b, role - 1, rpat);
     else
-      delta_role<false>(a, L, smem, b, rpat);
+      delta_role<false>(a, L, smem, b, role - 1, rpat);
   }
 
   // ---- Handover: the second role to finish merges the row.
   SFX_TRACE_POINT(4);
-  if (!block_arrive(a.ws.join + b, 2u, misc + 1)) return;
+  if (!block_arrive(a.ws.join + b, 1u + (unsigned)a.dparts, misc + 1))
+    return;
   SFX_TRACE_POINT(5);
+  int32_t* dlen = (int32_t*)(smem + L.dlen);
+  int32_t* dcnt = (int32_t*)(smem + L.dcnt);
+  int32_t* dpc = (int32_t*)(smem + L.dpc);
+  delta_combine(a, b, dlen, dcnt, dpc);
+  __syncthreads();
+  if (a.out.d_len || a.out.d_cnt)
+    for (int c = tid; c < C; c += NT) {
+      if (a.out.d_len) a.out.d_len[(int64_t)b * C + c] = dlen[c];
+      if (a.out.d_cnt) a.out.d_cnt[(int64_t)b * C + c] = dcnt[c];
+    }
+  if (a.out.d_pos)
+    for (int e = tid; e < C * R; e += NT) {
+      const int c = e / R;
+      const int r = e % R;
+      int64_t v = 0;
+      if (r < dcnt[c]) v = (int64_t)delta_end_at(a, b, c, r, dpc) - dlen[c];
+      a.out.d_pos[((int64_t)b * C + c) * R + r] = v < 0 ? 0 : v;
+    }
 
   const int nmw = a.merge_waves;
   int32_t* chain = (int32_t*)(smem + L.chain);
@@ -346,10 +402,10 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
     // Source selection per cap, before and after dedup (:321-337).
     auto pre = [&](int cc, int& len, int& src) {
       const int sl = a.ws.sa_len[(int64_t)b * C + cc];
-      const int dlen = a.ws.d_len[(int64_t)b * C + cc];
-      const bool use_sa = sl >= dlen && sl > 0;
-      const bool use_d = dlen > sl && dlen > 0;
-      len = use_sa ? sl : (use_d ? dlen : 0);
+      const int dl_c = dlen[cc];
+      const bool use_sa = sl >= dl_c && sl > 0;
+      const bool use_d = dl_c > sl && dl_c > 0;
+      len = use_sa ? sl : (use_d ? dl_c : 0);
       src = (use_sa ? 1 : 0) + (use_d ? 2 : 0);
     };
     int len, src;
@@ -366,7 +422,7 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
     const int64_t ilen = (int64_t)a.ws.sa_e[(int64_t)b * C + c] - sa_s;
     int occ = 0;
     if (src == 1) occ = (int)(ilen < R ? ilen : R);
-    if (src == 2) occ = a.ws.d_cnt[(int64_t)b * C + c];
+    if (src == 2) occ = dcnt[c];
     int32_t* mpos = (int32_t*)(smem + L.mpos) + wv * Rp;
     int32_t* mcache = (int32_t*)(smem + L.mcache) + (int64_t)wv * R * K;
     // Occurrence starts: strided SA sample (:339-352) or delta ends - len.
@@ -377,8 +433,7 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
         idx = idx < 0 ? 0 : (idx > N - 1 ? N - 1 : idx);
         pos = a.ix.sa[idx];
       } else {
-        const int64_t e =
-            (int64_t)a.ws.d_end[((int64_t)b * C + c) * R + r] - len;
+        const int64_t e = (int64_t)delta_end_at(a, b, c, r, dpc) - len;
         pos = (int32_t)(e < 0 ? 0 : e);
       }
       mpos[r] = pos;

@@ -30,11 +30,35 @@ inline void allow_max_lds(const void* fn, std::atomic<uint64_t>& done) {
   done.fetch_or(bit, std::memory_order_release);
 }
 
+// Compute units of the current device (cached per device ordinal).
+inline int device_cus() {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount,
+                            dev) != hipSuccess ||
+      n < 1)
+    n = 256;
+  cus[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+// When a grid fits the device one workgroup per CU, ask for more than half
+// of a CU's LDS so no two of them share a CU.
+inline size_t one_per_cu_lds(size_t lds, unsigned blocks) {
+  const size_t half = kMaxLds / 2 + 1024;
+  if (blocks <= (unsigned)device_cus() && lds < half) return half;
+  return lds;
+}
+
 int check_local(const sfx_params& p, const sfx_batch& bt);
 size_t local_lds_bytes(const sfx_params& p, int64_t S);
 
-int check_global(const sfx_params& p, const sfx_index& ix);
-int mb_lds_bytes(const sfx_index& ix);
-int merge_waves_for(const sfx_params& p, const sfx_index& ix, size_t* lds);
+int check_global(const sfx_params& p, const sfx_index& ix, int64_t batch);
+int mb_lds_bytes(const sfx_index& ix, int parts);
+int merge_waves_for(const sfx_params& p, const sfx_index& ix, int parts,
+                    size_t* lds);
 
 }  // namespace sfx

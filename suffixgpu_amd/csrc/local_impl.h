@@ -205,7 +205,7 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
   // semantics): one ordered pass per group of 8 candidates.
   for (int g0 = 0; g0 < C; g0 += 8)
     compact_first_r<NT>(mbuf, S, cand + g0, min(8, C - g0), R, occ + g0 * R,
-                        found + g0, scan);
+                        0, found + g0, scan);
   __syncthreads();
 
   SFX_TRACE_POINT(4);

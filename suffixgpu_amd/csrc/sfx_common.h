@@ -419,13 +419,14 @@ __device__ __forceinline__ uint4 clear_from(uint4 q, int r) {
 // pass: every thread owns a 16-byte-aligned segment read as uint4 words,
 // counts bytes >= thr four at a time (all-zero words skipped), one block
 // scan gives each thread its output offsets, then it writes its hits
-// below R.  out[c * R + slot]; count[c] = min(hits, R).  thr, out and
-// count may be LDS or global.  All threads of the block must call it.
+// below R.  out[c * R + slot] = out_base + position; count[c] =
+// min(hits, R).  thr, out and count may be LDS or global.  All threads of
+// the block must call it.
 template <int NT, typename MbPtr>
 __device__ __forceinline__ void compact_first_r(MbPtr mb, int64_t n,
                                                 const int* thr, int nthr,
                                                 int R, int32_t* out,
-                                                int* count,
+                                                int32_t out_base, int* count,
                                                 uint32_t* scratch) {
   int64_t seg = (n + NT - 1) / NT;
   seg = (seg + 15) & ~(int64_t)15;
@@ -469,7 +470,7 @@ __device__ __forceinline__ void compact_first_r(MbPtr mb, int64_t n,
           while (m) {
             const int byte = __builtin_ctz(m) >> 3;
             if (off[c] < (uint32_t)R)
-              out[c * R + off[c]] = (int32_t)(i0 + 4 * k + byte);
+              out[c * R + off[c]] = out_base + (int32_t)(i0 + 4 * k + byte);
             ++off[c];
             m &= m - 1;
           }
@@ -494,21 +495,30 @@ __device__ __forceinline__ void compact_first_r(MbPtr mb, int64_t n,
 // (to every thread) whether it was the last of `expected` arrivals.  The
 // last arriver resets the counter, so the workspace is zero again after
 // every call.  Call from uniform control flow.
+//
+// The fences are device-scope and cost a write-back (release) or an
+// invalidation (acquire) of the XCD's whole L2, so each is issued once per
+// workgroup, by thread 0, and split into its release and acquire halves:
+// the barrier first completes every wave's stores into the L2, thread 0's
+// release writes that L2 back before the counter update, and only the last
+// arriver's thread 0 invalidates (its CU's L1 and XCD's L2) before the
+// barrier that lets the block read the other workgroups' results.
 __device__ __forceinline__ bool block_arrive(unsigned* ctr,
                                              unsigned expected,
                                              int* lds_flag) {
-  __threadfence();
   __syncthreads();
   if (threadIdx.x == 0) {
-    unsigned old = atomicAdd(ctr, 1u);
-    int last = (old == expected - 1);
-    if (last) atomicExch(ctr, 0u);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const unsigned old = atomicAdd(ctr, 1u);
+    const int last = old == expected - 1;
+    if (last) {
+      atomicExch(ctr, 0u);
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
     *lds_flag = last;
   }
   __syncthreads();
-  const bool last = *lds_flag != 0;
-  if (last) __threadfence();
-  return last;
+  return *lds_flag != 0;
 }
 
 }  // namespace sfx

@@ -1,10 +1,11 @@
 // Fused decode step (suffix_gpu/proposer.py:186-327) in one launch.
 //
-// With global memory each request row gets three 512-thread workgroups,
-// interleaved: SA interval search, delta scan, local match.  The first two
-// hand over through the workspace and the later of them merges the row's
-// global candidates; local and global results meet the same way and the
-// later one writes the row's draft.  Nothing waits on another workgroup,
+// With global memory each request row gets 2 + dparts 512-thread
+// workgroups, interleaved: SA interval search, dparts delta-scan parts,
+// local match.  The SA and delta workgroups hand over through the
+// workspace and the last of them merges the row's global candidates;
+// local and global results meet the same way and the later one writes the
+// row's draft.  Nothing waits on another workgroup,
 // so any scheduling order completes.  Local-only drafting is one workgroup
 // per row.  One kernel node per step keeps a captured HIP graph minimal.
 
@@ -29,12 +30,13 @@ __global__ __launch_bounds__(kGlobalThreads) void k_step(StepArgs a) {
     local_body(a.l, smem, blockIdx.x);
     return;
   }
-  const int b = blockIdx.x / 3;
-  const int role = blockIdx.x % 3;  // 0: SA search, 1: delta scan, 2: local
-  if (role == 2)
+  const int per = 2 + a.g.dparts;
+  const int b = (int)(blockIdx.x / per);
+  const int role = (int)(blockIdx.x % per);  // 0: SA, 1..dparts: delta
+  if (role == per - 1)
     local_body(a.l, smem, b);
   else
-    global_body(a.g, smem, b, role == 0);
+    global_body(a.g, smem, b, role);
 }
 
 }  // namespace sfx
@@ -69,7 +71,7 @@ extern "C" int sfx_propose_step(const sfx_params* p, const sfx_index* ix,
   a.l.new_counts = new_counts;
   size_t lds = local_lds_bytes(*p, bt->seq);
   if (global_on) {
-    rc = check_global(*p, *ix);
+    rc = check_global(*p, *ix, bt->batch);
     if (rc) return rc;
     const size_t need =
         step_ws_layout(*p, bt->batch, ix->delta_capacity, nullptr, nullptr);
@@ -85,15 +87,18 @@ extern "C" int sfx_propose_step(const sfx_params* p, const sfx_index* ix,
     a.g.num_valid = num_valid;
     a.g.ws = a.l.ws;
     size_t glds = 0;
-    a.g.merge_waves = merge_waves_for(*p, *ix, &glds);
-    a.g.mb_lds = mb_lds_bytes(*ix);
+    a.g.dparts = delta_parts_for(bt->batch, ix->delta_capacity);
+    a.g.merge_waves = merge_waves_for(*p, *ix, a.g.dparts, &glds);
+    a.g.mb_lds = mb_lds_bytes(*ix, a.g.dparts);
     lds = lds > glds ? lds : glds;
   }
   if (lds > kMaxLds) return SFX_EINVAL;
   if (bt->batch == 0) return 0;
   static std::atomic<uint64_t> lds_opt{0};
   allow_max_lds((const void*)k_step, lds_opt);
-  const unsigned blocks = (unsigned)(bt->batch * (global_on ? 3 : 1));
+  const unsigned blocks =
+      (unsigned)(bt->batch * (global_on ? 2 + a.g.dparts : 1));
+  lds = one_per_cu_lds(lds, blocks);
   hipLaunchKernelGGL(k_step, dim3(blocks), dim3(kGlobalThreads), lds, stream,
                      a);
   return (int)hipGetLastError();

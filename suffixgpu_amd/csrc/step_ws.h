@@ -14,7 +14,7 @@
 namespace sfx {
 
 struct StepWs {
-  unsigned* join;    // [B] SA-search + delta-scan arrivals
+  unsigned* join;    // [B] SA-search + delta-part arrivals
   unsigned* pick;    // [B] local + global arrivals
   int32_t* l_chain;  // [B,K] best local chain (uncapped)
   int32_t* l_emit;   // [B]
@@ -25,20 +25,53 @@ struct StepWs {
   int32_t* sa_len;   // [B,C]
   int32_t* sa_s;     // [B,C]
   int32_t* sa_e;     // [B,C]
-  int32_t* d_len;    // [B,C]
-  int32_t* d_cnt;    // [B,C]
-  int32_t* d_end;    // [B,C,R] ascending end positions in the delta
-  uint8_t* d_mb;     // [B,D+1] delta match_back when it does not fit LDS
+  int32_t* d_mx;     // [B,KD] largest match length in each delta part
+  int32_t* d_cnt;    // [B,KD,C] hits (<= R) at the part's own threshold
+  int32_t* d_end;    // [B,KD,C,R] ascending end positions in the delta
+  uint8_t* d_mb;     // [B*KD, stride] match lengths when LDS is too small
 };
 
-// Largest delta (capacity + 1 positions) whose per-row match_back bytes
-// stay in LDS; longer deltas use StepWs::d_mb.
+// The delta scan of a row is split over up to kMaxDeltaParts workgroups,
+// each taking an equal share of the live delta (a device value).  The
+// split stops where the step's grid would exceed kGridSlots workgroups:
+// one per CU of an MI355X (256 CUs), since two co-resident workgroups of
+// these latency-bound roles slow each other down more than a split gains.
+constexpr int kMaxDeltaParts = 4;
+constexpr int64_t kDeltaPartSpan = 16384;
+constexpr int64_t kGridSlots = 256;
+
+__host__ __device__ inline int delta_parts_for(int64_t B,
+                                               int64_t delta_capacity) {
+  const int64_t n = (delta_capacity > 0 ? delta_capacity : 0) + 1;
+  int64_t parts = (n + kDeltaPartSpan - 1) / kDeltaPartSpan;
+  parts = parts < 1 ? 1 : (parts > kMaxDeltaParts ? kMaxDeltaParts : parts);
+  while (parts > 1 && B * (2 + parts) > kGridSlots) --parts;
+  return (int)parts;
+}
+
+// Most positions one part can hold: its share of the capacity plus the
+// 16-position alignment of the part bounds.
+__host__ __device__ inline int64_t delta_part_cap(int64_t delta_capacity,
+                                                  int parts) {
+  const int64_t n = (delta_capacity > 0 ? delta_capacity : 0) + 1;
+  return (n + parts - 1) / parts + 16;
+}
+
+// [lo, hi) of part k of the positions 0 .. n-1; lo is a multiple of 16.
+__host__ __device__ inline void delta_part_range(int64_t n, int parts, int k,
+                                                 int64_t* lo, int64_t* hi) {
+  *lo = k == 0 ? 0 : ((k * n / parts) & ~(int64_t)15);
+  *hi = k == parts - 1 ? n : (((k + 1) * n / parts) & ~(int64_t)15);
+}
+
+// Largest delta part (positions) whose match_back bytes stay in LDS;
+// longer parts use StepWs::d_mb.
 constexpr int64_t kDeltaMbLdsMax = 65540;
 
-// Bytes per row of delta match_back: the positions plus the tail that the
+// Bytes per delta part of match_back: its positions plus the tail that the
 // 16-byte-word segment reads of a <= 1024-thread block may touch.
-__host__ __device__ inline int64_t delta_mb_stride(int64_t delta_capacity) {
-  return ((delta_capacity + 1 + 15) & ~(int64_t)15) + 16 * 1024;
+__host__ __device__ inline int64_t delta_mb_stride(int64_t part_cap) {
+  return ((part_cap + 15) & ~(int64_t)15) + 16 * 1024;
 }
 
 inline size_t ws_align(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -70,12 +103,13 @@ inline size_t step_ws_layout(const sfx_params& p, int64_t B,
   w.sa_len = (int32_t*)take(b * C * 4);
   w.sa_s = (int32_t*)take(b * C * 4);
   w.sa_e = (int32_t*)take(b * C * 4);
-  w.d_len = (int32_t*)take(b * C * 4);
-  w.d_cnt = (int32_t*)take(b * C * 4);
-  w.d_end = (int32_t*)take(b * C * R * 4);
-  const int64_t dcap = delta_capacity > 0 ? delta_capacity : 0;
-  w.d_mb = (uint8_t*)take(dcap + 1 > kDeltaMbLdsMax
-                              ? b * (size_t)delta_mb_stride(dcap)
+  const int KD = delta_parts_for(B, delta_capacity);
+  w.d_mx = (int32_t*)take(b * KD * 4);
+  w.d_cnt = (int32_t*)take(b * KD * C * 4);
+  w.d_end = (int32_t*)take(b * KD * C * R * 4);
+  const int64_t pcap = delta_part_cap(delta_capacity, KD);
+  w.d_mb = (uint8_t*)take(pcap > kDeltaMbLdsMax
+                              ? b * KD * (size_t)delta_mb_stride(pcap)
                               : 0);
   if (ws) *ws = w;
   return off;

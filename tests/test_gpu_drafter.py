@@ -49,6 +49,22 @@ def _global_pair(gpu, seed=3, b=24, s=2048, **over):
     return w, d, o
 
 
+def test_global_step_split_delta_vs_oracle(gpu):
+    """A 2^16 delta capacity splits every row's delta scan over several
+    workgroups of the fused step (B=24 rows)."""
+    w, d, o = _global_pair(gpu, seed=6, delta_capacity=1 << 16)
+    assert d.global_index.delta_len > 20000
+    bt = w.batch
+    tg = T(bt.tokens, gpu)
+    draft, nv, new = d.propose_with_update(T(bt.num_tokens, gpu), tg,
+                                           T(bt.sampled, gpu))
+    to = bt.tokens.copy()
+    ed, env, enew = o.propose_with_update(bt.num_tokens, to, bt.sampled)
+    np.testing.assert_array_equal(N(new), enew)
+    np.testing.assert_array_equal(N(draft), ed)
+    np.testing.assert_array_equal(N(nv), env)
+
+
 def test_global_step_vs_oracle(gpu):
     w, d, o = _global_pair(gpu)
     bt = w.batch

@@ -301,6 +301,50 @@ def test_queries_vs_oracle(gpu, vocab):
         np.testing.assert_array_equal(N(got), exp)
 
 
+@pytest.mark.parametrize("mode", ["small_vocab", "templates", "short"])
+def test_split_delta_vs_oracle(gpu, mode):
+    """A 2^16-token delta is scanned by several workgroups per row; their
+    lists are combined in part order.  Queries whose longest delta match
+    lies in a late part exercise the per-part threshold check."""
+    rng = np.random.default_rng({"small_vocab": 1, "templates": 2,
+                                 "short": 3}[mode])
+    tc = synth.TemplateCorpus(seed=9, n_templates=10)
+    docs = [tc.sequence(lo=64, hi=400) for _ in range(30)]
+    if mode == "small_vocab":
+        dd = [rng.integers(0, 5, size=int(rng.integers(200, 4000))).astype(I32)
+              for _ in range(14)]
+    elif mode == "templates":
+        dd = [tc.sequence(lo=1024, hi=6000) for _ in range(10)]
+    else:
+        dd = [tc.sequence(lo=20, hi=60) for _ in range(2)]
+    cap = sum(len(d) + 1 for d in docs) + 11
+    g, o = _load_pair(gpu, docs, dd, cap, 1 << 16, 32, k=8)
+    assert g.delta_len == o.delta_len
+    b, p = 40, 24
+    q = np.zeros((b, p), I32)
+    ql = np.zeros(b, np.int64)
+    for i in range(b):
+        # late delta docs first: their longest matches sit in the last parts
+        src = dd[-1 - (i % len(dd))] if i % 4 else docs[i % len(docs)]
+        n = int(rng.integers(1, min(len(src), p) + 1))
+        st = int(rng.integers(0, len(src) - n + 1))
+        q[i, :n] = src[st:st + n]
+        ql[i] = n
+    caps = np.array([24, 12, 6, 3, 2], np.int64)
+    tq, tl, tc_ = T(q, gpu), T(ql, gpu), T(caps, gpu)
+    for got, exp in zip(g._delta_match_backoff(tq, tl, p, tc_),
+                        o._delta_match_backoff(q, ql, p, caps)):
+        np.testing.assert_array_equal(N(got), exp)
+    for got, exp in zip(g._query_backoff(tq, tl, p, tc_),
+                        o._query_backoff(q, ql, p, caps)):
+        np.testing.assert_array_equal(N(got), exp)
+    for got, exp in zip(g.draft(tq, tl, p, 8, min_token_prob=0.05,
+                                caps=tc_),
+                        o.draft(q, ql, p, 8, min_token_prob=0.05,
+                                caps=caps)):
+        np.testing.assert_array_equal(N(got), exp)
+
+
 def test_async_rebuild_blocking_poll(gpu):
     """Side-stream rebuilds swapped at deterministic points match the
     oracle's done-at-next-poll schedule."""
