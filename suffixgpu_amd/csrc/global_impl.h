@@ -33,8 +33,9 @@ struct GlobalArgs {
 };
 
 struct GlobalLayout {
-  int rpat, lb, ub, found, scan, red, misc, lo, dlen, dcnt, dpc, dtok, dmb,
-      mpos, mcache, mA, chain, nv, score, rlen, rocc, total;
+  int rpat, lb, ub, found, scan, red, misc, lo, dlen, dcnt, dpc, sal, sas,
+      sae, dtok, dmb, mpos, mcache, mA, mH, chain, nv, score, rlen, rocc,
+      total;
 };
 
 // Delta tokens staged per chunk (after a halo of P rounded up to 4
@@ -69,6 +70,9 @@ __host__ __device__ inline GlobalLayout global_layout(int P, int C, int R,
   L.dlen = g_take(off, C * 4);
   L.dcnt = g_take(off, C * 4);
   L.dpc = g_take(off, C * kMaxDeltaParts * 4);
+  L.sal = g_take(off, C * 4);
+  L.sas = g_take(off, C * 4);
+  L.sae = g_take(off, C * 4);
   L.chain = g_take(off, C * K * 4);
   L.nv = g_take(off, C * 4);
   L.score = g_take(off, C * 4);
@@ -82,6 +86,7 @@ __host__ __device__ inline GlobalLayout global_layout(int P, int C, int R,
   L.mpos = g_take(off, nmw * Rp * 4);
   L.mcache = g_take(off, nmw * R * K * 4);
   L.mA = g_take(off, nmw * Rp * 4);
+  L.mH = g_take(off, nmw * 2 * kHashSlots * 4);
   L.total = off > delta_end ? off : delta_end;
   return L;
 }
@@ -260,6 +265,135 @@ __device__ __forceinline__ int32_t delta_end_at(const GlobalArgs& a, int b,
   return a.ws.d_end[(slot * C + c) * R + r];
 }
 
+// One wave: the continuation block of one candidate (src 1: the SA
+// interval [sa_s, sa_s + ilen), sampled with stride ilen / R when longer
+// than R (global_index.py:339-352); src 2: the row's delta ends minus len)
+// gathered into LDS -- tokens in range, not PAD, not negative, else -1
+// (:443-463) -- optionally copied to cont_out [R, K], then (expand) the
+// majority-vote expansion into chain_out.
+__device__ __forceinline__ ExpandResult gather_expand(
+    const GlobalArgs& a, const GlobalLayout& L, unsigned char* smem, int b,
+    int c, int src, int len, int occ, int64_t sa_s, int64_t ilen,
+    const int32_t* dpc, int32_t* cont_out, bool expand, int32_t* chain_out) {
+  const sfx_params& p = a.p;
+  const int ln = lane_id();
+  const int wv = threadIdx.x / kWave;
+  const int R = p.max_occurrences;
+  const int K = p.k;
+  const int Rp = (R + 3) & ~3;
+  const int64_t N = a.ix.capacity;
+  const int64_t D = a.ix.delta_capacity;
+  int32_t* mpos = (int32_t*)(smem + L.mpos) + wv * Rp;
+  int32_t* mcache = (int32_t*)(smem + L.mcache) + (int64_t)wv * R * K;
+  for (int r = ln; r < occ; r += kWave) {
+    int32_t pos;
+    if (src == 1) {
+      int64_t idx = ilen > R ? sa_s + ((int64_t)r * ilen) / R : sa_s + r;
+      idx = idx < 0 ? 0 : (idx > N - 1 ? N - 1 : idx);
+      pos = a.ix.sa[idx];
+    } else {
+      const int64_t e = (int64_t)delta_end_at(a, b, c, r, dpc) - len;
+      pos = (int32_t)(e < 0 ? 0 : e);
+    }
+    mpos[r] = pos;
+  }
+  wave_lds_sync();
+  SFX_TRACE_POINT(10);
+  const int32_t* srcbuf = src == 1 ? a.ix.corpus : a.ix.delta;
+  const int64_t nbuf = src == 1 ? N : D;
+  int64_t slen = N;
+  if (src == 2) {
+    slen = *a.ix.delta_len;
+    slen = slen < 0 ? 0 : (slen > D ? D : slen);
+  }
+  // One occurrence row per lane: its K tokens are independent loads.
+  for (int r = ln; r < occ; r += kWave) {
+    const int64_t base = (int64_t)mpos[r] + len;
+    int32_t* dst = mcache + r * K;
+    for (int j0 = 0; j0 < K; j0 += 16) {
+      int32_t v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int64_t idx = base + j0 + u;
+        v[u] = -1;
+        if (j0 + u < K && idx < slen && idx >= 0)
+          v[u] = srcbuf[idx < nbuf - 1 ? idx : nbuf - 1];
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (j0 + u < K) dst[j0 + u] = (v[u] != kPad && v[u] >= 0) ? v[u] : -1;
+    }
+  }
+  wave_lds_sync();
+  SFX_TRACE_POINT(11);
+  if (cont_out)
+    for (int e = ln; e < R * K; e += kWave)
+      cont_out[e] = e < occ * K ? mcache[e] : -1;
+  ExpandResult er{0, 0.0f};
+  if (expand) {
+    const int64_t cap = spec_cap(p, len);
+    auto cont_at = [&](int r, int d) -> int32_t { return mcache[r * K + d]; };
+    er = expand_wave<false>(cont_at, NoWeight(), R, occ, K, cap,
+                            p.min_token_prob, p.alpha,
+                            (int32_t*)(smem + L.mA) + wv * Rp, nullptr,
+                            (int32_t*)(smem + L.mH) + wv * 2 * kHashSlots,
+                            chain_out);
+  }
+  SFX_TRACE_POINT(12);
+  return er;
+}
+
+// Decode step: expansions of one source's candidate for every cap
+// (src 1: SA, lens/s/e per cap in LDS; src 2: delta, lens/counts per cap
+// and the per-part hit counts).  Caps with the same length share one
+// candidate, so each run of equal lengths is expanded once (one wave per
+// run) and its result written for every cap of the run to nv/score/chain
+// [B,C(,K)] in the workspace.  Called by the whole block.
+__device__ __forceinline__ void source_expand(
+    const GlobalArgs& a, const GlobalLayout& L, unsigned char* smem, int b,
+    int src, const int32_t* lens, const int32_t* aux0, const int32_t* aux1,
+    const int32_t* dpc, int32_t* nv_out, float* score_out,
+    int32_t* chain_out) {
+  const sfx_params& p = a.p;
+  const int C = p.num_caps;
+  const int R = p.max_occurrences;
+  const int K = p.k;
+  const int wv = threadIdx.x / kWave;
+  const int ln = lane_id();
+  const int nmw = a.merge_waves;
+  int32_t* chain = (int32_t*)(smem + L.chain);
+  for (int c = wv; c < C && wv < nmw; c += nmw) {
+    const int len = lens[c];
+    if (c > 0 && lens[c - 1] == len) continue;  // expanded by the run head
+    int end = c + 1;
+    while (end < C && lens[end] == len) ++end;
+    ExpandResult er{0, 0.0f};
+    if (len > 0) {
+      int occ;
+      int64_t s0 = 0, ilen = 0;
+      if (src == 1) {
+        s0 = aux0[c];
+        ilen = (int64_t)aux1[c] - s0;
+        occ = (int)(ilen < R ? ilen : R);
+      } else {
+        occ = aux0[c];
+      }
+      er = gather_expand(a, L, smem, b, c, src, len, occ, s0, ilen, dpc,
+                         nullptr, true, chain + c * K);
+    }
+    wave_lds_sync();  // lane 0 wrote the chain
+    for (int cc = c; cc < end; ++cc) {
+      const int64_t i = (int64_t)b * C + cc;
+      for (int d = ln; d < K; d += kWave)
+        if (d < er.nv) chain_out[i * K + d] = chain[c * K + d];
+      if (ln == 0) {
+        nv_out[i] = er.nv;
+        score_out[i] = er.score;
+      }
+    }
+  }
+}
+
 // role 0: SA search; role 1 .. dparts: delta part role - 1.
 __device__ __forceinline__ void global_body(const GlobalArgs& a,
                                             unsigned char* smem, int b,
@@ -337,6 +471,11 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
     }
     __syncthreads();
     SFX_TRACE_POINT(2);
+    // Each cap takes its longest non-empty interval (sa_search.py:
+    // 137-163).
+    int32_t* sal = (int32_t*)(smem + L.sal);
+    int32_t* sas = (int32_t*)(smem + L.sas);
+    int32_t* sae = (int32_t*)(smem + L.sae);
     if (wv == 0) {
       for (int c = 0; c < C; ++c) {
         const int cap = p.caps[c];
@@ -351,6 +490,9 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
         if (ln == 0) {
           const int64_t s0 = best ? lbs[best - 1] : 0;
           const int64_t e0 = best ? ubs[best - 1] : 0;
+          sal[c] = best;
+          sas[c] = (int32_t)s0;
+          sae[c] = (int32_t)e0;
           a.ws.sa_len[(int64_t)b * C + c] = best;
           a.ws.sa_s[(int64_t)b * C + c] = (int32_t)s0;
           a.ws.sa_e[(int64_t)b * C + c] = (int32_t)e0;
@@ -360,14 +502,49 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
         }
       }
     }
+    if (a.step) {
+      // Decode step: expand the SA candidate of every cap now, while the
+      // delta and local workgroups are still running.
+      __syncthreads();
+      source_expand(a, L, smem, b, 1, sal, sas, sae, nullptr,
+                    a.ws.sa_nv, a.ws.sa_score, a.ws.sa_chain);
+      SFX_TRACE_POINT(4);
+      if (block_arrive(a.ws.pick + b, 3u, misc + 1))
+        final_pick(p, a.ws, b, a.draft, a.num_valid, misc + 4);
+      return;
+    }
   } else {
     if (a.mb_lds)
       delta_role<true>(a, L, smem, b, role - 1, rpat);
     else
       delta_role<false>(a, L, smem, b, role - 1, rpat);
+    if (a.step) {
+      // Decode step: the last delta part combines the parts and expands
+      // the delta candidate of every cap.
+      if (a.dparts > 1) {
+        if (!block_arrive(a.ws.djoin + b, (unsigned)a.dparts, misc + 1))
+          return;
+      } else {
+        __syncthreads();  // this block's own part results
+      }
+      SFX_TRACE_POINT(4);
+      int32_t* dlen = (int32_t*)(smem + L.dlen);
+      int32_t* dcnt = (int32_t*)(smem + L.dcnt);
+      int32_t* dpc = (int32_t*)(smem + L.dpc);
+      delta_combine(a, b, dlen, dcnt, dpc);
+      __syncthreads();
+      for (int c = tid; c < C; c += NT) a.ws.dl_c[(int64_t)b * C + c] = dlen[c];
+      SFX_TRACE_POINT(5);
+      source_expand(a, L, smem, b, 2, dlen, dcnt, nullptr, dpc, a.ws.dn_nv,
+                    a.ws.dn_score, a.ws.dn_chain);
+      SFX_TRACE_POINT(6);
+      if (block_arrive(a.ws.pick + b, 3u, misc + 2))
+        final_pick(p, a.ws, b, a.draft, a.num_valid, misc + 4);
+      return;
+    }
   }
 
-  // ---- Handover: the second role to finish merges the row.
+  // ---- Query: the last of the SA and delta workgroups merges the row.
   SFX_TRACE_POINT(4);
   if (!block_arrive(a.ws.join + b, 1u + (unsigned)a.dparts, misc + 1))
     return;
@@ -397,7 +574,6 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
   float* res_score = (float*)(smem + L.score);
   int32_t* res_len = (int32_t*)(smem + L.rlen);
   int32_t* res_occ = (int32_t*)(smem + L.rocc);
-  int64_t dl_live = *a.ix.delta_len;
   for (int c = wv; c < C && wv < nmw; c += nmw) {
     // Source selection per cap, before and after dedup (:321-337).
     auto pre = [&](int cc, int& len, int& src) {
@@ -423,74 +599,24 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
     int occ = 0;
     if (src == 1) occ = (int)(ilen < R ? ilen : R);
     if (src == 2) occ = dcnt[c];
-    int32_t* mpos = (int32_t*)(smem + L.mpos) + wv * Rp;
-    int32_t* mcache = (int32_t*)(smem + L.mcache) + (int64_t)wv * R * K;
-    // Occurrence starts: strided SA sample (:339-352) or delta ends - len.
-    for (int r = ln; r < occ; r += kWave) {
-      int32_t pos;
-      if (src == 1) {
-        int64_t idx = ilen > R ? sa_s + ((int64_t)r * ilen) / R : sa_s + r;
-        idx = idx < 0 ? 0 : (idx > N - 1 ? N - 1 : idx);
-        pos = a.ix.sa[idx];
-      } else {
-        const int64_t e = (int64_t)delta_end_at(a, b, c, r, dpc) - len;
-        pos = (int32_t)(e < 0 ? 0 : e);
-      }
-      mpos[r] = pos;
-    }
-    wave_lds_sync();
-    SFX_TRACE_POINT(10);
-    // Continuations (:443-463): in range, not PAD, not negative.
-    const int32_t* srcbuf = src == 1 ? a.ix.corpus : a.ix.delta;
-    const int64_t nbuf = src == 1 ? N : D;
-    const int64_t slen = src == 1 ? N : dl_live;
-    // One occurrence row per lane: its K tokens are independent loads.
-    for (int r = ln; r < occ; r += kWave) {
-      const int64_t base = (int64_t)mpos[r] + len;
-      int32_t* dst = mcache + r * K;
-      for (int j0 = 0; j0 < K; j0 += 16) {
-        int32_t v[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-          const int64_t idx = base + j0 + u;
-          v[u] = -1;
-          if (j0 + u < K && idx < slen && idx >= 0)
-            v[u] = srcbuf[idx < nbuf - 1 ? idx : nbuf - 1];
-        }
-#pragma unroll
-        for (int u = 0; u < 16; ++u)
-          if (j0 + u < K) dst[j0 + u] = (v[u] != kPad && v[u] >= 0) ? v[u] : -1;
-      }
-    }
-    wave_lds_sync();
-    SFX_TRACE_POINT(11);
-    if (a.out.len && ln == 0) a.out.len[(int64_t)b * C + c] = len;
-    if (a.out.occ && ln == 0) a.out.occ[(int64_t)b * C + c] = occ;
-    if (a.out.cont) {
-      int32_t* o = a.out.cont + ((int64_t)b * C + c) * R * K;
-      for (int e = ln; e < R * K; e += kWave)
-        o[e] = e < occ * K ? mcache[e] : -1;
-    }
-    if (a.need_expand) {
-      const int64_t cap = spec_cap(p, len);
-      auto cont_at = [&](int r, int d) -> int32_t { return mcache[r * K + d]; };
-      const ExpandResult er = expand_wave<false>(
-          cont_at, NoWeight(), R, occ, K, cap, p.min_token_prob, p.alpha,
-          (int32_t*)(smem + L.mA) + wv * Rp, nullptr, chain + c * K);
-      SFX_TRACE_POINT(12);
-      if (ln == 0) {
-        res_nv[c] = er.nv;
-        res_score[c] = er.score;
-        res_len[c] = len;
-        res_occ[c] = occ;
-      }
+    int32_t* cont_out =
+        a.out.cont ? a.out.cont + ((int64_t)b * C + c) * R * K : nullptr;
+    const ExpandResult er =
+        gather_expand(a, L, smem, b, c, src, len, occ, sa_s, ilen, dpc,
+                      cont_out, a.need_expand != 0, chain + c * K);
+    if (ln == 0) {
+      if (a.out.len) a.out.len[(int64_t)b * C + c] = len;
+      if (a.out.occ) a.out.occ[(int64_t)b * C + c] = occ;
+      res_nv[c] = er.nv;
+      res_score[c] = er.score;
+      res_len[c] = len;
+      res_occ[c] = occ;
     }
   }
   if (!a.need_expand) return;
   __syncthreads();
   SFX_TRACE_POINT(6);
-  // Best cap: first argmax of the raw score (proposer.py:308-314,
-  // global_index.py:427-436).
+  // Best cap: first argmax of the raw score (global_index.py:427-436).
   if (tid == 0) {
     int best = 0;
     for (int c = 1; c < C; ++c)
@@ -504,26 +630,15 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
   const int best = misc[2];
   const int emit = misc[3];
   const int32_t* bchain = chain + best * K;
-  if (!a.step) {
-    if (a.out.draft)
-      for (int j = tid; j < K; j += NT)
-        a.out.draft[(int64_t)b * K + j] = j < emit ? bchain[j] : -1;
-    if (tid == 0) {
-      if (a.out.emit) a.out.emit[b] = emit;
-      if (a.out.draft_len) a.out.draft_len[b] = res_len[best];
-      if (a.out.draft_occ) a.out.draft_occ[b] = res_occ[best];
-      if (a.out.draft_score) a.out.draft_score[b] = res_score[best];
-    }
-    return;
-  }
-  for (int j = tid; j < K; j += NT)
-    a.ws.g_chain[(int64_t)b * K + j] = bchain[j];
+  if (a.out.draft)
+    for (int j = tid; j < K; j += NT)
+      a.out.draft[(int64_t)b * K + j] = j < emit ? bchain[j] : -1;
   if (tid == 0) {
-    a.ws.g_emit[b] = emit;
-    a.ws.g_score[b] = res_score[best];
+    if (a.out.emit) a.out.emit[b] = emit;
+    if (a.out.draft_len) a.out.draft_len[b] = res_len[best];
+    if (a.out.draft_occ) a.out.draft_occ[b] = res_occ[best];
+    if (a.out.draft_score) a.out.draft_score[b] = res_score[best];
   }
-  if (block_arrive(a.ws.pick + b, 2u, misc + 4))
-    pick_row(b, K, a.ws, a.draft, a.num_valid);
 }
 
 }  // namespace sfx

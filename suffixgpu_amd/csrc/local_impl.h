@@ -28,8 +28,8 @@ struct LocalArgs {
 };
 
 struct LocalLayout {
-  int row, mb, pat, hist, cand, found, scan, occ, A, chain, nv, score, misc,
-      total;
+  int row, mb, pat, hist, cand, found, scan, occ, A, H, chain, nv, score,
+      misc, total;
 };
 
 __host__ __device__ inline int lds_take(int& off, int bytes) {
@@ -59,6 +59,7 @@ __host__ __device__ inline LocalLayout local_layout(int S, int P, int C,
   L.scan = lds_take(off, 4 * nwaves * 8);
   L.occ = lds_take(off, C * R * 4);
   L.A = lds_take(off, nwaves * ((R + 3) & ~3) * 4);
+  L.H = lds_take(off, nwaves * 2 * kHashSlots * 4);
   L.chain = lds_take(off, C * K * 4);
   L.nv = lds_take(off, C * 4);
   L.score = lds_take(off, C * 4);
@@ -244,7 +245,8 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
     };
     const ExpandResult er = expand_wave<false>(
         cont_at, NoWeight(), R, oc, K, cap, p.min_token_prob, p.alpha,
-        Abuf + wv * ((R + 3) & ~3), nullptr, chain + c * K);
+        Abuf + wv * ((R + 3) & ~3), nullptr,
+        (int32_t*)(smem + L.H) + wv * 2 * kHashSlots, chain + c * K);
     if (ln == 0) {
       res_nv[c] = er.nv;
       res_score[c] = er.score;
@@ -300,8 +302,8 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
     a.ws.l_emit[b] = emit;
     a.ws.l_score[b] = res_score[best];
   }
-  if (block_arrive(a.ws.pick + b, 2u, misc + 2))
-    pick_row(b, K, a.ws, a.draft, a.num_valid);
+  if (block_arrive(a.ws.pick + b, 3u, misc + 2))
+    final_pick(p, a.ws, b, a.draft, a.num_valid, misc + 4);
 }
 
 }  // namespace sfx

@@ -171,7 +171,8 @@ __host__ __device__ inline int round16(int x) { return (x + 15) & ~15; }
 // Per-wave LDS: continuation cache [R*K], vote buffer A [R], weights W [R],
 // chain [K]; every region 16-byte aligned.
 __host__ __device__ inline int expand_wave_bytes(int R, int K) {
-  return round16(R * K * 4) + 2 * round16(R * 4) + round16(K * 4);
+  return round16(R * K * 4) + 2 * round16(R * 4) + round16(K * 4) +
+         2 * kHashSlots * 4;
 }
 
 template <bool kWeighted>
@@ -189,6 +190,8 @@ __global__ __launch_bounds__(256) void k_expand(ExpandArgs a) {
   float* W = (float*)(base + round16(R * K * 4) + round16(R * 4));
   int32_t* chain =
       (int32_t*)(base + round16(R * K * 4) + 2 * round16(R * 4));
+  int32_t* H = (int32_t*)(base + round16(R * K * 4) + 2 * round16(R * 4) +
+                          round16(K * 4));
   const int32_t* src = a.cont + row * R * K;
   for (int e = ln; e < R * K; e += kWave) cache[e] = src[e];
   wave_lds_sync();
@@ -200,10 +203,10 @@ __global__ __launch_bounds__(256) void k_expand(ExpandArgs a) {
   ExpandResult er;
   if (kWeighted)
     er = expand_wave<true>(cont_at, w_at, R, occ, K, cap, a.min_prob,
-                           a.alpha, A, W, chain);
+                           a.alpha, A, W, H, chain);
   else
     er = expand_wave<false>(cont_at, NoWeight(), R, occ, K, cap, a.min_prob,
-                            a.alpha, A, W, chain);
+                            a.alpha, A, W, H, chain);
   wave_lds_sync();
   for (int d = ln; d < K; d += kWave) a.chain[row * K + d] = chain[d];
   if (ln == 0) {

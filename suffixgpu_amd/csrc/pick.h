@@ -8,15 +8,62 @@
 
 namespace sfx {
 
-// Executed by the whole block of whichever kernel arrived last for row b.
-__device__ __forceinline__ void pick_row(int b, int K, const StepWs& ws,
-                                         int32_t* draft, int32_t* num_valid) {
-  const float ls = ws.l_score[b];
-  const float gs = ws.g_score[b];
-  const bool g = gs > ls;
-  const int nv = g ? ws.g_emit[b] : ws.l_emit[b];
-  const int32_t* chain = g ? ws.g_chain + (int64_t)b * K
-                           : ws.l_chain + (int64_t)b * K;
+// Executed by the whole block of whichever of row b's SA, last delta and
+// local workgroups arrives last.  Global candidate per cap: SA when its
+// length is at least the delta's, else the delta (global_index.py:
+// 321-325); a cap repeating the previous cap's (length, source) is dropped
+// (:329-337); the global winner is the first argmax of the raw score
+// (proposer.py:308-314) and replaces the local one only on a strictly
+// greater score; the chain is padded with -1 past the emission count
+// (:322-327).  misc: 3 ints of LDS.
+__device__ __forceinline__ void final_pick(const sfx_params& p,
+                                           const StepWs& ws, int b,
+                                           int32_t* draft, int32_t* num_valid,
+                                           int* misc) {
+  const int C = p.num_caps;
+  const int K = p.k;
+  if (threadIdx.x == 0) {
+    int plen = 0, psrc = 0;
+    int best = 0, bnv = 0, blen = 0, bsrc = 0;
+    float bscore = 0.0f;
+    for (int c = 0; c < C; ++c) {
+      const int64_t i = (int64_t)b * C + c;
+      const int sl = ws.sa_len[i];
+      const int dl = ws.dl_c[i];
+      const bool use_sa = sl >= dl && sl > 0;
+      const bool use_d = dl > sl && dl > 0;
+      const int len = use_sa ? sl : (use_d ? dl : 0);
+      const int src = (use_sa ? 1 : 0) + (use_d ? 2 : 0);
+      int esrc = src, elen = len;
+      if (c > 0 && len == plen && src == psrc && len > 0) esrc = elen = 0;
+      plen = len;
+      psrc = src;
+      const float sc =
+          esrc == 1 ? ws.sa_score[i] : (esrc == 2 ? ws.dn_score[i] : 0.0f);
+      const int nv = esrc == 1 ? ws.sa_nv[i] : (esrc == 2 ? ws.dn_nv[i] : 0);
+      if (c == 0 || sc > bscore) {
+        best = c;
+        bscore = sc;
+        bnv = nv;
+        blen = elen;
+        bsrc = esrc;
+      }
+    }
+    const int64_t cap = spec_cap(p, blen);
+    const int64_t cap0 = cap > 0 ? cap : 0;
+    const int gemit = (int)((int64_t)bnv < cap0 ? bnv : cap0);
+    const bool g = bscore > ws.l_score[b];
+    misc[0] = g ? gemit : ws.l_emit[b];
+    misc[1] = g ? bsrc : 0;
+    misc[2] = best;
+  }
+  __syncthreads();
+  const int nv = misc[0];
+  const int which = misc[1];
+  const int64_t i = (int64_t)b * C + misc[2];
+  const int32_t* chain = which == 0   ? ws.l_chain + (int64_t)b * K
+                         : which == 1 ? ws.sa_chain + i * K
+                                      : ws.dn_chain + i * K;
   for (int j = threadIdx.x; j < K; j += blockDim.x)
     draft[(int64_t)b * K + j] = j < nv ? chain[j] : -1;
   if (threadIdx.x == 0) num_valid[b] = nv;

@@ -58,6 +58,43 @@ __device__ __forceinline__ int wave_max_i32(int v) {
 }
 
 // Order LDS traffic of the calling wave (writes before later reads).
+// Inclusive prefix sum over the 64 lanes of a wave with DPP row shifts and
+// row broadcasts (no LDS traffic).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf,
+                                             false);  // row_shr:1
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf,
+                                             false);  // row_shr:2
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf,
+                                             false);  // row_shr:4
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf,
+                                             false);  // row_shr:8
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf,
+                                             false);  // row_bcast:15
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf,
+                                             false);  // row_bcast:31
+  return v;
+}
+
+// Inclusive max-scan over the 64 lanes of a wave (unsigned; lanes shifted
+// in from outside a row contribute 0).
+__device__ __forceinline__ uint32_t wave_incl_max(uint32_t v) {
+  uint32_t t;
+  t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false);
+  v = v > t ? v : t;
+  t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false);
+  v = v > t ? v : t;
+  t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false);
+  v = v > t ? v : t;
+  t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false);
+  v = v > t ? v : t;
+  t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);
+  v = v > t ? v : t;
+  t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);
+  v = v > t ? v : t;
+  return v;
+}
+
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
   __builtin_amdgcn_wave_barrier();
@@ -105,7 +142,10 @@ __device__ __forceinline__ bool vote_better(int cnt, int tok, int bcnt,
 
 // Smallest v in [1, nact] with fl32(prob * fl32(v / denom)) >= min_prob,
 // or nact + 1 when none (the product is monotone in v for denom > 0 and
-// prob >= 0).  Returns 1 when the early exit does not apply.
+// prob >= 0).  Returns 1 when the early exit does not apply.  The rounded
+// product stays within a few ulps of prob * v / denom while consecutive v
+// differ by a factor of at least 1 + 1/nact, so the real-valued threshold
+// rounded up is within one of the answer; exact checks settle it.
 __device__ __forceinline__ int min_votes(float prob, float denom,
                                          float min_prob, int nact) {
   if (!(min_prob > 0.0f) || !(denom > 0.0f) || !(prob > 0.0f)) return 1;
@@ -113,13 +153,95 @@ __device__ __forceinline__ int min_votes(float prob, float denom,
     return __fmul_rn(prob, __fdiv_rn((float)v, denom)) >= min_prob;
   };
   if (!pass(nact)) return nact + 1;
-  // Binary search for the first passing v in [1, nact].
-  int lo = 1, hi = nact;
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (pass(mid)) hi = mid; else lo = mid + 1;
+  float t = __fdividef(min_prob, prob) * denom;
+  t = t < (float)nact ? t : (float)nact;
+  int v = (int)ceilf(t);
+  v = v < 1 ? 1 : v;
+  while (v > 1 && pass(v - 1)) --v;
+  while (!pass(v)) ++v;  // ends: pass(nact) holds
+  return v;
+}
+
+// ---------------------------------------------------------- vote helpers
+// Uniform maximum of an unsigned value over the wave.
+__device__ __forceinline__ uint32_t wave_all_max(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)wave_incl_max(v),
+                                             kWave - 1);
+}
+
+// Uniform minimum of a signed value over the wave.
+__device__ __forceinline__ int32_t wave_all_min(int32_t v) {
+  const uint32_t m = wave_all_max(~((uint32_t)v ^ 0x80000000u));
+  return (int32_t)(~m ^ 0x80000000u);
+}
+
+constexpr int kHashSlots = 256;  // per wave: keys then counts (2 KiB)
+constexpr int kQuickVotes = 4;   // distinct values counted one at a time
+
+__device__ __forceinline__ int hash_slot(int32_t v) {
+  return (int)(((uint32_t)v * 0x9E3779B1u) >> 24);
+}
+
+// Slot of v (!= INT32_MIN) in an open-addressing table of kHashSlots
+// keys (INT32_MIN = empty) with its count incremented.
+__device__ __forceinline__ int hash_add(int32_t* keys, int32_t* cnts,
+                                        int32_t v) {
+  int h = hash_slot(v);
+  while (true) {
+    const int32_t old = atomicCAS(&keys[h], (int32_t)0x80000000, v);
+    if (old == (int32_t)0x80000000 || old == v) {
+      atomicAdd(&cnts[h], 1);
+      return h;
+    }
+    h = (h + 1) & (kHashSlots - 1);
   }
-  return lo;
+}
+
+// Folds the remaining rows' values (lane masks rem0 over v0, rem1 over v1;
+// every row of a value is remaining or none is) into the running vote
+// (bcnt, btok): all their counts at once in the LDS table H.
+__device__ __forceinline__ void hash_vote(int32_t v0, int32_t v1,
+                                          uint64_t rem0, uint64_t rem1,
+                                          int32_t* H, int& bcnt, int& btok) {
+  const int ln = lane_id();
+  const uint64_t me = 1ull << ln;
+  // INT32_MIN marks empty slots: count that value, if present, directly.
+  {
+    const uint64_t e0 = ballot(v0 == (int32_t)0x80000000) & rem0;
+    const uint64_t e1 = ballot(v1 == (int32_t)0x80000000) & rem1;
+    const int cnt = popc(e0) + popc(e1);
+    if (cnt > 0 && vote_better(cnt, (int32_t)0x80000000, bcnt, btok)) {
+      bcnt = cnt;
+      btok = (int32_t)0x80000000;
+    }
+    rem0 &= ~e0;
+    rem1 &= ~e1;
+  }
+  if ((rem0 | rem1) == 0) return;
+  int32_t* keys = H;
+  int32_t* cnts = H + kHashSlots;
+  reinterpret_cast<int4*>(keys)[ln] =
+      make_int4((int32_t)0x80000000, (int32_t)0x80000000,
+                (int32_t)0x80000000, (int32_t)0x80000000);
+  reinterpret_cast<int4*>(cnts)[ln] = make_int4(0, 0, 0, 0);
+  wave_lds_sync();
+  const bool in0 = (rem0 & me) != 0;
+  const bool in1 = (rem1 & me) != 0;
+  int h0 = 0, h1 = 0;
+  if (in0) h0 = hash_add(keys, cnts, v0);
+  if (in1) h1 = hash_add(keys, cnts, v1);
+  wave_lds_sync();
+  const uint32_t c0 = in0 ? (uint32_t)cnts[h0] : 0u;
+  const uint32_t c1 = in1 ? (uint32_t)cnts[h1] : 0u;
+  const uint32_t mc = wave_all_max(c0 > c1 ? c0 : c1);
+  const int32_t t0 = c0 == mc ? v0 : 0x7fffffff;
+  const int32_t t1 = c1 == mc ? v1 : 0x7fffffff;
+  const int32_t mt = wave_all_min(t0 < t1 ? t0 : t1);
+  if (vote_better((int)mc, mt, bcnt, btok)) {
+    bcnt = (int)mc;
+    btok = mt;
+  }
+  wave_lds_sync();  // the table is rewritten by the next depth
 }
 
 // Wave-cooperative depth-wise majority vote of one candidate
@@ -130,19 +252,23 @@ __device__ __forceinline__ int min_votes(float prob, float denom,
 // still on the chain (r < occ and every earlier depth voted for them).
 // chain_out[0..K) receives the chain (-1 past the first invalid depth).
 //
-// Unit votes with R <= 128 (two rows per lane) count each distinct active
-// value with two ballots: the first unprocessed lane's value is broadcast,
-// its matches are counted and retired, and the loop stops once the
-// unprocessed rows cannot outvote the best so far -- one iteration per
-// distinct token, usually a handful.  Larger R and weighted votes compact
-// the active rows into A (row order) and count by broadcast LDS reads.
-// A holds R ints; W (weighted votes only) R floats, both LDS.
+// Unit votes with R <= 128 (two rows per lane): up to kQuickVotes distinct
+// values are counted one at a time with two ballots (the first remaining
+// row's value is broadcast, its matches counted and retired), stopping as
+// soon as the remaining rows cannot outvote the best -- which settles most
+// depths, where the rows mostly agree.  Otherwise the min_prob bound may
+// already end the chain, and if not, every remaining value is counted at
+// once in a per-wave LDS hash table H (2 * kHashSlots ints).  Larger R and
+// weighted votes compact the active rows into A (row order) and count by
+// broadcast LDS reads.  A holds R ints; W (weighted votes only) R floats,
+// both LDS.
 template <bool kWeighted, class ContFn, class WeightFn>
 __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
                                                     WeightFn weight_at,
                                     int R, int64_t occ, int K, int64_t cap,
                                     float min_prob, float alpha, int* A,
-                                    float* W, int32_t* chain_out) {
+                                    float* W, int32_t* H,
+                                    int32_t* chain_out) {
   const int ln = lane_id();
   float prob = 1.0f;
   float score = 0.0f;
@@ -169,29 +295,15 @@ __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
       const float denom = __fadd_rn((float)(nact > 1 ? nact : 1), alpha);
       int bcnt = 0;
       int btok = 0x7fffffff;
-      int vmin = 0;  // 0: not needed yet
-      bool dead = false;
-      while (rem0 | rem1) {
-        const int left = popc(rem0) + popc(rem1);
-        if (left < bcnt) break;
-        if (bcnt > 0 && vmin == 0) {
-          // Fewest votes that keep the chain probability >= min_prob; if
-          // neither the best so far nor the rest can reach it the chain
-          // ends here whichever token wins.
-          vmin = min_votes(prob, denom, min_prob, nact);
-          if (vmin > nact) {
-            dead = true;
-            break;
-          }
-        }
-        if (left < vmin && bcnt < vmin) break;
+      int left = nact;
+      for (int it = 0; it < kQuickVotes && left > 0 && left >= bcnt; ++it) {
         int x;
         if (rem0)
           x = __builtin_amdgcn_readlane(v0, __builtin_ctzll(rem0));
         else
           x = __builtin_amdgcn_readlane(v1, __builtin_ctzll(rem1));
-        const uint64_t e0 = ballot(a0 && v0 == x);
-        const uint64_t e1 = ballot(a1 && v1 == x);
+        const uint64_t e0 = ballot(v0 == x) & rem0;
+        const uint64_t e1 = ballot(v1 == x) & rem1;
         const int cnt = popc(e0) + popc(e1);
         if (vote_better(cnt, x, bcnt, btok)) {
           bcnt = cnt;
@@ -199,8 +311,16 @@ __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
         }
         rem0 &= ~e0;
         rem1 &= ~e1;
+        left -= cnt;
       }
-      if (dead) break;
+      if (left > 0 && left >= bcnt) {
+        // Fewest votes that keep the chain probability >= min_prob: if
+        // neither the best so far nor any remaining value can reach it,
+        // the chain ends here whichever token wins.
+        const int vmin = min_votes(prob, denom, min_prob, nact);
+        if (vmin > nact || (left < vmin && bcnt < vmin)) break;
+        hash_vote(v0, v1, rem0, rem1, H, bcnt, btok);
+      }
       const float vf = (float)bcnt;
       prob = __fmul_rn(prob, __fdiv_rn(vf, denom));
       const bool valid = (vf > 0.0f) && (prob >= min_prob);
@@ -303,43 +423,6 @@ struct NoWeight {
 };
 
 // ------------------------------------------------- ordered compaction
-// Inclusive prefix sum over the 64 lanes of a wave with DPP row shifts and
-// row broadcasts (no LDS traffic).
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf,
-                                             false);  // row_shr:1
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf,
-                                             false);  // row_shr:2
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf,
-                                             false);  // row_shr:4
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf,
-                                             false);  // row_shr:8
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf,
-                                             false);  // row_bcast:15
-  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf,
-                                             false);  // row_bcast:31
-  return v;
-}
-
-// Inclusive max-scan over the 64 lanes of a wave (unsigned; lanes shifted
-// in from outside a row contribute 0).
-__device__ __forceinline__ uint32_t wave_incl_max(uint32_t v) {
-  uint32_t t;
-  t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false);
-  v = v > t ? v : t;
-  t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false);
-  v = v > t ? v : t;
-  t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false);
-  v = v > t ? v : t;
-  t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false);
-  v = v > t ? v : t;
-  t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false);
-  v = v > t ? v : t;
-  t = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false);
-  v = v > t ? v : t;
-  return v;
-}
-
 // Block-wide exclusive prefix sums of 8 per-thread counters.  `scratch`
 // holds 8 * (NT/64) u32 in LDS.  Two barriers.
 template <int NT>

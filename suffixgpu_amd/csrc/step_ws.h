@@ -1,8 +1,8 @@
 // Workspace layout shared by the fused-step kernels and the global query.
 //
 // Per row b (B rows), C = number of global caps, K = draft length,
-// R = max occurrences.  The two handover counters must be zero before a
-// call; the kernels leave them zero.
+// R = max occurrences.  The handover counters must be zero before a call;
+// the kernels leave them zero.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -14,21 +14,26 @@
 namespace sfx {
 
 struct StepWs {
-  unsigned* join;    // [B] SA-search + delta-part arrivals
-  unsigned* pick;    // [B] local + global arrivals
-  int32_t* l_chain;  // [B,K] best local chain (uncapped)
-  int32_t* l_emit;   // [B]
-  float* l_score;    // [B]
-  int32_t* g_chain;  // [B,K] best global chain (uncapped)
-  int32_t* g_emit;   // [B]
-  float* g_score;    // [B]
-  int32_t* sa_len;   // [B,C]
-  int32_t* sa_s;     // [B,C]
-  int32_t* sa_e;     // [B,C]
-  int32_t* d_mx;     // [B,KD] largest match length in each delta part
-  int32_t* d_cnt;    // [B,KD,C] hits (<= R) at the part's own threshold
-  int32_t* d_end;    // [B,KD,C,R] ascending end positions in the delta
-  uint8_t* d_mb;     // [B*KD, stride] match lengths when LDS is too small
+  unsigned* join;     // [B] SA-search + delta-part arrivals (query)
+  unsigned* djoin;    // [B] delta-part arrivals (step)
+  unsigned* pick;     // [B] step: SA, last delta part and local arrivals
+  int32_t* l_chain;   // [B,K] best local chain (uncapped)
+  int32_t* l_emit;    // [B]
+  float* l_score;     // [B]
+  int32_t* sa_len;    // [B,C]
+  int32_t* sa_s;      // [B,C]
+  int32_t* sa_e;      // [B,C]
+  int32_t* sa_nv;     // [B,C] step: expansion of the SA candidate per cap
+  float* sa_score;    // [B,C]
+  int32_t* sa_chain;  // [B,C,K]
+  int32_t* dl_c;      // [B,C] step: row delta length per cap
+  int32_t* dn_nv;     // [B,C] step: expansion of the delta candidate
+  float* dn_score;    // [B,C]
+  int32_t* dn_chain;  // [B,C,K]
+  int32_t* d_mx;      // [B,KD] largest match length in each delta part
+  int32_t* d_cnt;     // [B,KD,C] hits (<= R) at the part's own threshold
+  int32_t* d_end;     // [B,KD,C,R] ascending end positions in the delta
+  uint8_t* d_mb;      // [B*KD, stride] match lengths when LDS is too small
 };
 
 // The delta scan of a row is split over up to kMaxDeltaParts workgroups,
@@ -93,16 +98,21 @@ inline size_t step_ws_layout(const sfx_params& p, int64_t B,
   };
   StepWs w;
   w.join = (unsigned*)take(b * 4);
+  w.djoin = (unsigned*)take(b * 4);
   w.pick = (unsigned*)take(b * 4);
   w.l_chain = (int32_t*)take(b * K * 4);
   w.l_emit = (int32_t*)take(b * 4);
   w.l_score = (float*)take(b * 4);
-  w.g_chain = (int32_t*)take(b * K * 4);
-  w.g_emit = (int32_t*)take(b * 4);
-  w.g_score = (float*)take(b * 4);
   w.sa_len = (int32_t*)take(b * C * 4);
   w.sa_s = (int32_t*)take(b * C * 4);
   w.sa_e = (int32_t*)take(b * C * 4);
+  w.sa_nv = (int32_t*)take(b * C * 4);
+  w.sa_score = (float*)take(b * C * 4);
+  w.sa_chain = (int32_t*)take(b * C * K * 4);
+  w.dl_c = (int32_t*)take(b * C * 4);
+  w.dn_nv = (int32_t*)take(b * C * 4);
+  w.dn_score = (float*)take(b * C * 4);
+  w.dn_chain = (int32_t*)take(b * C * K * 4);
   const int KD = delta_parts_for(B, delta_capacity);
   w.d_mx = (int32_t*)take(b * KD * 4);
   w.d_cnt = (int32_t*)take(b * KD * C * 4);
