@@ -52,6 +52,9 @@ def parse():
     ap.add_argument("--cpu-steps", type=int, default=40)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=50)
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="skip the B=256 S=16384 1000-step decode loop")
+    ap.add_argument("--e2e-steps", type=int, default=1000)
     ap.add_argument("--pmc-workload", action="store_true",
                     help="for rocprofv3 --pmc passes: a copy of known size, "
                     "then a few step launches; prints no JSON")
@@ -261,6 +264,16 @@ def main() -> int:
                 "algorithmic_bytes": step_bytes,
                 "avg_launch_us": round(step_us, 3)}
 
+    copy_gbps = copy_peak_gbps(dev)
+    cold_p50 = cold_step_p50(graph, dev)
+    conc = concurrent_rebuild(graph, w, dev)
+    log(f"copy peak {copy_gbps:.0f} GB/s; cold-cache step p50 "
+        f"{cold_p50:.2f} us; rebuild during replays: {conc}")
+    e2e = None
+    if not args.no_e2e:
+        e2e = e2e_loop(dev, args.e2e_steps)
+        log(f"e2e decode loop: {e2e}")
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(d, w, args.cpu_steps)
@@ -296,6 +309,11 @@ def main() -> int:
                        "k_local_alone": round(k_local_us, 3),
                        "k_global_alone": round(k_global_us, 3)},
         "roofline": roofline,
+        "copy_peak_gbps": round(copy_gbps, 1),
+        "roofline_frac_of_copy_peak": round(achieved / copy_gbps, 6),
+        "cold_cache_step_p50_us": round(cold_p50, 3),
+        "sa_rebuild_concurrent": conc,
+        "e2e_decode_loop": e2e,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
@@ -304,6 +322,173 @@ def main() -> int:
 
 def _lib_pad() -> int:
     return 2 ** 31 - 1
+
+
+
+def copy_peak_gbps(dev) -> float:
+    """Measured device-to-device copy bandwidth (read + write bytes / s)
+    over a 1 GiB int32 buffer, best of 10."""
+    import torch
+    n = 1 << 28
+    src = torch.ones(n, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    times = []
+    for _ in range(12):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        dst.copy_(src)
+        e1.record()
+        e1.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e-3)
+    del src, dst
+    return 2 * 4 * n / min(times[2:]) / 1e9
+
+
+def cold_step_p50(graph, dev, reps: int = 40) -> float:
+    """p50 µs of a replay after a 512 MiB scratch write (outside the timed
+    region) has pushed the index, delta and rows out of L2 and MALL."""
+    import torch
+    scratch = torch.empty(1 << 27, dtype=torch.int32, device=dev)
+    per = []
+    for i in range(reps):
+        scratch.fill_(i)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        e1.synchronize()
+        per.append(e0.elapsed_time(e1) * 1e3)
+    del scratch
+    return statistics.median(per)
+
+
+def concurrent_rebuild(graph, w, dev) -> dict:
+    """A full 4.19M-token SA rebuild enqueued on a side stream while the
+    captured step replays on the main stream: build time, decode steps
+    completed before the build's end event, and the step p50 meanwhile."""
+    import torch
+    from suffixgpu_amd.suffix_array import (build_suffix_array_into,
+                                            sa_workspace_bytes)
+    flat = np.concatenate([np.append(x, -2) for x in w.active_docs]).astype(
+        np.int32)
+    m = min(flat.shape[0] + 1, CAPACITY)
+    text = torch.full((CAPACITY,), 2 ** 31 - 1, dtype=torch.int32,
+                      device=dev)
+    text[:flat.shape[0]].copy_(torch.from_numpy(flat))
+    out = torch.empty(CAPACITY, dtype=torch.int32, device=dev)
+    ws = torch.empty(sa_workspace_bytes(CAPACITY), dtype=torch.uint8,
+                     device=dev)
+    side = torch.cuda.Stream(dev)
+    main = torch.cuda.current_stream(dev)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t0.record(main)
+    side.wait_stream(main)
+    b0 = torch.cuda.Event(enable_timing=True)
+    b1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(side):
+        b0.record(side)
+        build_suffix_array_into(text, m, out, ws)
+        b1.record(side)
+    ends = []
+    starts = []
+    while len(ends) < 4000:
+        s0 = torch.cuda.Event(enable_timing=True)
+        s1 = torch.cuda.Event(enable_timing=True)
+        s0.record(main)
+        graph.replay()
+        s1.record(main)
+        starts.append(s0)
+        ends.append(s1)
+        if len(ends) % 8 == 0 and b1.query():
+            break
+    torch.cuda.synchronize()
+    build_ms = b0.elapsed_time(b1)
+    done_at = t0.elapsed_time(b1)
+    fin = [t0.elapsed_time(e) for e in ends]
+    during = [a.elapsed_time(e) * 1e3 for a, e, f in zip(starts, ends, fin)
+              if f <= done_at]
+    steps = len(during)
+    del text, out, ws
+    return {"build_ms": round(build_ms, 3), "m": int(m),
+            "steps_during_build": steps,
+            "step_p50_us_during_build":
+                round(statistics.median(during), 3) if during else None}
+
+
+def e2e_loop(dev, steps: int) -> dict:
+    """Scripted decode loop (B=256, S=16384): captured propose_with_update
+    per step with the sampled block and counts fed back on the device,
+    16 longest rows harvested into global memory every 64 steps and reset,
+    background rebuilds at delta_capacity // 2 on a side stream, poll()
+    every step."""
+    import torch
+    from suffixgpu_amd import SuffixGPUDrafter, synth
+    t0 = time.time()
+    lp = synth.decode_loop(steps=steps)
+    gen_s = time.time() - t0
+    side = torch.cuda.Stream(dev)
+    d = SuffixGPUDrafter(device=dev, enable_global=True,
+                         global_capacity=CAPACITY, delta_capacity=DELTA_CAP,
+                         rebuild_threshold=DELTA_CAP // 2,
+                         rebuild_stream=side, **CFG)
+    gi = d.global_index
+    tok = torch.from_numpy(lp.tokens).to(dev)
+    nt = torch.from_numpy(lp.num_tokens).to(dev)
+    samp_all = torch.from_numpy(lp.sampled).to(dev)
+    samp = samp_all[0].clone()
+    for _ in range(3):
+        d.propose_with_update(nt, tok, samp)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = d.propose_with_update(nt, tok, samp)
+    torch.cuda.synchronize()
+    main = torch.cuda.current_stream(dev)
+    evs = []
+    swaps = 0
+    launches = 0
+    nv_log = torch.zeros(steps, lp.tokens.shape[0], dtype=torch.int32,
+                         device=dev)
+    tw = time.perf_counter()
+    for i in range(steps):
+        samp.copy_(samp_all[i])
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(main)
+        graph.replay()
+        e1.record(main)
+        evs.append((e0, e1))
+        nt.copy_(out[2])
+        nv_log[i].copy_(out[1])
+        hv = lp.harvests.get(i)
+        if hv is not None:
+            rows, lengths, new_rows, new_nt = hv
+            had = gi._rebuild_event is not None
+            d.harvest_finished(rows, lengths, tok)
+            launches += int(not had and gi._rebuild_event is not None)
+            idx = torch.tensor(rows, dtype=torch.int64, device=dev)
+            tok[idx] = torch.from_numpy(new_rows).to(dev)
+            nt[idx] = torch.from_numpy(new_nt).to(dev)
+        pending = gi._rebuild_event is not None
+        d.poll()
+        swaps += int(pending and gi._rebuild_event is None)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - tw
+    per = [a.elapsed_time(b) * 1e3 for a, b in evs]
+    return {"workload": "B=256 S=16384 k=16 nb=8 R=128, 1000-step "
+                        "captured decode loop, harvest 16 rows / 64 steps, "
+                        "rebuild at delta_capacity/2 on a side stream",
+            "steps": steps, "replay_p50_us": round(statistics.median(per), 3),
+            "replay_p99_us": round(float(np.percentile(per, 99)), 3),
+            "wall_us_per_step": round(wall / steps * 1e6, 3),
+            "mean_drafted_tokens_per_step":
+                round(float(nv_log.sum().item()) / steps, 2),
+            "harvests": len(lp.harvests), "rebuilds_launched": launches,
+            "swaps": swaps, "active_len": gi.active_len,
+            "generate_s": round(gen_s, 2)}
 
 
 def step_kernel_us(d, dev, tokens0, nt, sampled, reps):

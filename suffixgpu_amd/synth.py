@@ -198,3 +198,55 @@ def global_corpus(seed: int = 3, capacity: int = 1 << 22,
         sampled[i, :seg.shape[0]] = seg
     return GlobalWorkload(keep, delta,
                           DecodeBatch(rows, nt, sampled, {"vocab": VOCAB_LARGE}))
+
+
+@dataclass
+class DecodeLoop:
+    """A scripted decode loop: initial rows, per-step sampled blocks and the
+    harvests (every ``every`` steps the ``harvest`` longest rows, ties to
+    the lower index, are harvested at their host-mirrored lengths and reset
+    to fresh prefixes)."""
+    tokens: np.ndarray              # [B, S] int32 initial rows
+    num_tokens: np.ndarray          # [B] int32
+    sampled: np.ndarray             # [steps, B, T] int32, -1 padded
+    harvests: dict                  # step -> (rows, lengths, new rows, new counts)
+
+
+def decode_loop(seed: int = 5, b: int = 256, s: int = 16384,
+                steps: int = 1000, t: int = 17, every: int = 64,
+                harvest: int = 16, lo: int = 2048, hi: int = 8192
+                ) -> DecodeLoop:
+    """Config-2-style rows (Zipf tokens, copy/fresh spans) whose every step
+    accepts min(geometric(0.3) - 1, T - 1) + 1 tokens of the row's own
+    hidden continuation; the host mirrors each row's count exactly as
+    update_state advances it (base + accepted, not clipped)."""
+    rng = np.random.default_rng(seed)
+    z = ZipfTokens(rng)
+    hidden = np.stack([build_row(rng, s + t, z.draw) for _ in range(b)])
+    q = rng.integers(lo, hi, size=b, endpoint=True).astype(np.int64)
+    tokens = hidden[:, :s].copy()
+    num_tokens = q.astype(np.int32)
+    sampled = np.full((steps, b, t), -1, dtype=np.int32)
+    harvests = {}
+    for i in range(steps):
+        acc = np.minimum(rng.geometric(0.3, size=b) - 1, t - 1) + 1
+        for r in range(b):
+            n = int(acc[r])
+            st = int(q[r])
+            seg = hidden[r, st:st + n] if st < hidden.shape[1] else hidden[r, :0]
+            if seg.shape[0] < n:
+                seg = np.concatenate([seg, z.draw(rng, n - seg.shape[0])])
+            sampled[i, r, :n] = seg
+        q += acc
+        if (i + 1) % every == 0:
+            order = np.lexsort((np.arange(b), -q))[:harvest]
+            rows = [int(r) for r in order]
+            lengths = [int(min(q[r], s)) for r in rows]
+            new_rows = np.stack([build_row(rng, s + t, z.draw) for _ in rows])
+            new_q = rng.integers(lo, hi, size=len(rows), endpoint=True)
+            for j, r in enumerate(rows):
+                hidden[r] = new_rows[j]
+                q[r] = new_q[j]
+            harvests[i] = (rows, lengths, new_rows[:, :s].copy(),
+                           new_q.astype(np.int32))
+    return DecodeLoop(tokens, num_tokens, sampled, harvests)
