@@ -1,7 +1,7 @@
 // Suffix-array construction on the GPU: prefix doubling over LSD radix
 // sorts of the still-unsorted suffixes only, with no host synchronisation.
 //
-// Round 0 sorts all positions by token (signed order, 4 passes of 8 bits).
+// Round 0 sorts all positions by token (signed order, 4 passes of 9 bits).
 // Every later round h = 1, 2, 4, ... re-sorts only the suffixes whose
 // group still has more than one member, by the key
 // (group head, rank[i+h]+1 or 0) -- a proper prefix sorts first, as in
@@ -14,8 +14,8 @@
 //
 // Each LSD pass is histogram (per 4096-element tile) -> per-digit row scan
 // across tiles -> stable scatter.  The scatter ranks equal digits inside a
-// wave with eight ballots (wave64 match) and across waves through LDS, so
-// tile order and element order are kept.
+// wave with eight ballots (wave64 match) and across waves by per-wave digit
+// counts, so tile order and element order are kept.
 
 #include "launch.h"
 #include "sfx_common.h"
@@ -25,7 +25,9 @@ namespace sfx {
 constexpr int kSortThreads = 256;
 constexpr int kSortItems = 16;
 constexpr int kTile = kSortThreads * kSortItems;  // 4096
-constexpr int kRadix = 256;
+constexpr int kDigitBits = 9;
+constexpr int kRadix = 1 << kDigitBits;                 // 512
+constexpr int kDigitsPerThread = kRadix / kSortThreads;  // 2
 constexpr int kSortWaves = kSortThreads / kWave;  // 4
 constexpr int kWaveSpan = kTile / kSortWaves;     // 1024 per wave
 
@@ -41,9 +43,7 @@ struct SaWs {
   uint32_t* hist;    // [256][NB] digit counts per tile, then offsets
   uint32_t* rowsum;  // [256] digit totals
   uint32_t* tcnt;    // [NB] active suffixes per tile
-  uint32_t* toff;    // [NB] their exclusive prefix
   uint32_t* blkmax;  // [NB] last group start per tile
-  uint32_t* carry;   // [NB] group start carried into the tile
   uint32_t* state;   // [0] done, [1] active count
 };
 
@@ -69,9 +69,7 @@ static size_t sa_ws_layout(int64_t n, void* base, SaWs* w) {
   s.hist = (uint32_t*)take((size_t)kRadix * NB * 4);
   s.rowsum = (uint32_t*)take(kRadix * 4);
   s.tcnt = (uint32_t*)take(NB * 4);
-  s.toff = (uint32_t*)take(NB * 4);
   s.blkmax = (uint32_t*)take(NB * 4);
-  s.carry = (uint32_t*)take(NB * 4);
   s.state = (uint32_t*)take(256);
   if (w) *w = s;
   return off;
@@ -118,11 +116,11 @@ __global__ __launch_bounds__(256) void k_sa_init(const int32_t* text,
   pos[i] = (uint32_t)i;
 }
 
-// Lanes of the wave holding the same 8-bit digit as the calling lane.
+// Lanes of the wave holding the same digit as the calling lane.
 __device__ __forceinline__ uint64_t match_digit(bool act, uint32_t d) {
   uint64_t peers = ballot(act);
 #pragma unroll
-  for (int bit = 0; bit < 8; ++bit) {
+  for (int bit = 0; bit < kDigitBits; ++bit) {
     const bool set = (d >> bit) & 1u;
     const uint64_t m = ballot(act && set);
     peers &= set ? m : ~m;
@@ -130,9 +128,28 @@ __device__ __forceinline__ uint64_t match_digit(bool act, uint32_t d) {
   return peers;
 }
 
+__device__ __forceinline__ uint32_t digit_of(uint64_t k, int sh) {
+  return (uint32_t)(k >> sh) & (kRadix - 1u);
+}
+
+// Block-wide exclusive scan of the kRadix digit counts held
+// kDigitsPerThread per thread (digits tid * kDigitsPerThread + j).
+__device__ __forceinline__ void digit_exscan(const uint32_t (&c)[kDigitsPerThread],
+                                             uint32_t (&ex)[kDigitsPerThread],
+                                             uint32_t* red) {
+  uint32_t sum = 0;
+#pragma unroll
+  for (int j = 0; j < kDigitsPerThread; ++j) sum += c[j];
+  uint32_t tot;
+  uint32_t run = block_exscan1<kSortThreads>(sum, red, &tot);
+#pragma unroll
+  for (int j = 0; j < kDigitsPerThread; ++j) {
+    ex[j] = run;
+    run += c[j];
+  }
+}
+
 // ---------------------------------------------------------------- radix
-// Element e of a tile is base + r * 256 + tid (r < 16): this r-major order
-// is the element order the scatter keeps.
 
 __global__ __launch_bounds__(kSortThreads) void k_rs_hist(
     const uint64_t* __restrict__ key, int sh, uint32_t* hist, int64_t nb,
@@ -141,25 +158,35 @@ __global__ __launch_bounds__(kSortThreads) void k_rs_hist(
   const int64_t A = state[1];
   const int64_t base = (int64_t)blockIdx.x * kTile;
   if (base >= A) return;
-  __shared__ uint32_t h[kRadix];
+  // One histogram per wave (LDS atomics of a wave only collide on equal
+  // digits), summed at the end.
+  __shared__ uint32_t h[kSortWaves][kRadix];
   const int tid = threadIdx.x;
-  h[tid] = 0;
+  const int wv = tid / kWave;
+#pragma unroll
+  for (int w = 0; w < kSortWaves; ++w)
+#pragma unroll
+    for (int j = 0; j < kDigitsPerThread; ++j)
+      h[w][tid * kDigitsPerThread + j] = 0;
   uint32_t d[kSortItems];
 #pragma unroll
   for (int r = 0; r < kSortItems; ++r) {
     const int64_t idx = base + (int64_t)r * kSortThreads + tid;
-    d[r] = idx < A ? (uint32_t)(key[idx] >> sh) & 255u : 0u;
+    d[r] = idx < A ? digit_of(key[idx], sh) : kRadix;
   }
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < kSortItems; ++r) {
-    const bool act = base + (int64_t)r * kSortThreads + tid < A;
-    const uint64_t peers = match_digit(act, d[r]);
-    if (act && rank_lt(peers) == 0)
-      atomicAdd(&h[d[r]], (uint32_t)popc(peers));
-  }
+  for (int r = 0; r < kSortItems; ++r)
+    if (d[r] < kRadix) atomicAdd(&h[wv][d[r]], 1u);
   __syncthreads();
-  hist[(int64_t)tid * nb + blockIdx.x] = h[tid];
+#pragma unroll
+  for (int j = 0; j < kDigitsPerThread; ++j) {
+    const int dg = tid * kDigitsPerThread + j;
+    uint32_t sum = 0;
+#pragma unroll
+    for (int w = 0; w < kSortWaves; ++w) sum += h[w][dg];
+    hist[(int64_t)dg * nb + blockIdx.x] = sum;
+  }
 }
 
 // Row d of the histogram (tiles 0 .. ceil(A/4096)) becomes its exclusive
@@ -182,6 +209,12 @@ __global__ __launch_bounds__(kSortThreads) void k_rs_rowscan(
   if (threadIdx.x == 0) rowsum[blockIdx.x] = carry;
 }
 
+// Stable scatter of one tile.  Wave w owns the tile's elements
+// base + w*1024 + s*64 + lane (s < 16), i.e. a contiguous quarter, so the
+// element order is (wave, step, lane).  The waves first count their digits
+// (LDS atomics), one scan gives every (wave, digit) its output offset, and
+// then each wave places its elements step by step with an eight-ballot
+// digit match, advancing only its own offsets: three barriers per tile.
 __global__ __launch_bounds__(kSortThreads) void k_rs_scatter(
     const uint64_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint64_t* __restrict__ kout, uint32_t* __restrict__ vout, int sh,
@@ -191,48 +224,63 @@ __global__ __launch_bounds__(kSortThreads) void k_rs_scatter(
   const int64_t A = state[1];
   const int64_t base = (int64_t)blockIdx.x * kTile;
   if (base >= A) return;
-  __shared__ uint32_t gofs[kRadix];
-  __shared__ uint32_t whist[kSortWaves][kRadix];
+  __shared__ uint32_t woff[kSortWaves][kRadix];
   __shared__ uint32_t red[kSortWaves];
   const int tid = threadIdx.x;
   const int wv = tid / kWave;
-  uint64_t k[kSortItems];
-  uint32_t v[kSortItems];
+  const int ln = lane_id();
+  constexpr int kSteps = kWaveSpan / kWave;  // 16
+  const int64_t wbase = base + (int64_t)wv * kWaveSpan;
+  uint64_t k[kSteps];
+  uint32_t v[kSteps];
 #pragma unroll
-  for (int r = 0; r < kSortItems; ++r) {
-    const int64_t idx = base + (int64_t)r * kSortThreads + tid;
-    k[r] = idx < A ? kin[idx] : 0;
-    v[r] = idx < A ? vin[idx] : 0;
+  for (int s = 0; s < kSteps; ++s) {
+    const int64_t idx = wbase + s * kWave + ln;
+    k[s] = idx < A ? kin[idx] : 0;
+    v[s] = idx < A ? vin[idx] : 0;
   }
-  uint32_t tot;
-  const uint32_t dbase = block_exscan1<kSortThreads>(rowsum[tid], red, &tot);
-  gofs[tid] = dbase + hist[(int64_t)tid * nb + blockIdx.x];
 #pragma unroll
-  for (int w = 0; w < kSortWaves; ++w) whist[w][tid] = 0;
+  for (int w = 0; w < kSortWaves; ++w)
+#pragma unroll
+    for (int j = 0; j < kDigitsPerThread; ++j)
+      woff[w][tid * kDigitsPerThread + j] = 0;
+  uint32_t rs[kDigitsPerThread], dbase[kDigitsPerThread];
+#pragma unroll
+  for (int j = 0; j < kDigitsPerThread; ++j)
+    rs[j] = rowsum[tid * kDigitsPerThread + j];
+  digit_exscan(rs, dbase, red);  // ends with a barrier: counters zeroed
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    if (wbase + s * kWave + ln < A)
+      atomicAdd(&woff[wv][digit_of(k[s], sh)], 1u);
+  }
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < kSortItems; ++r) {
-    const bool act = base + (int64_t)r * kSortThreads + tid < A;
-    const uint32_t d = (uint32_t)(k[r] >> sh) & 255u;
-    const uint64_t peers = match_digit(act, d);
-    const int rk = rank_lt(peers);
-    if (act && rk == 0) whist[wv][d] = (uint32_t)popc(peers);
-    __syncthreads();
-    if (act) {
-      uint32_t p = gofs[d] + (uint32_t)rk;
-      for (int w = 0; w < wv; ++w) p += whist[w][d];
-      kout[p] = k[r];
-      vout[p] = v[r];
-    }
-    __syncthreads();
-    uint32_t add = 0;
+  for (int j = 0; j < kDigitsPerThread; ++j) {
+    const int dg = tid * kDigitsPerThread + j;
+    uint32_t run = dbase[j] + hist[(int64_t)dg * nb + blockIdx.x];
 #pragma unroll
     for (int w = 0; w < kSortWaves; ++w) {
-      add += whist[w][tid];
-      whist[w][tid] = 0;
+      const uint32_t c = woff[w][dg];
+      woff[w][dg] = run;
+      run += c;
     }
-    gofs[tid] += add;
-    __syncthreads();
+  }
+  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < kSteps; ++s) {
+    const bool act = wbase + s * kWave + ln < A;
+    const uint32_t d = digit_of(k[s], sh);
+    const uint64_t peers = match_digit(act, d);
+    const int rk = rank_lt(peers);
+    if (act) {
+      const uint32_t p = woff[wv][d] + (uint32_t)rk;
+      kout[p] = k[s];
+      vout[p] = v[s];
+    }
+    wave_lds_sync();  // every lane has read its offset
+    if (act && rk == 0) woff[wv][d] += (uint32_t)popc(peers);
+    wave_lds_sync();
   }
 }
 
@@ -277,46 +325,24 @@ __global__ __launch_bounds__(kSortThreads) void k_grp_reduce(
   }
 }
 
-// Exclusive max-scan of blkmax over the active tiles (one block).
-__global__ __launch_bounds__(1024) void k_grp_carry(const uint32_t* blkmax,
-                                                    uint32_t* carry,
-                                                    const uint32_t* state) {
-  if (state[0]) return;
-  __shared__ uint32_t wmax[16];
-  const int64_t nbA = tiles_of(state[1]);
-  const int tid = threadIdx.x;
-  const int wv = tid / kWave;
-  uint32_t run = 0;
-  for (int64_t c0 = 0; c0 < nbA; c0 += 1024) {
-    const int64_t t = c0 + tid;
-    const uint32_t v = t < nbA ? blkmax[t] : 0u;
-    const uint32_t inc = wave_incl_max(v);
-    if (lane_id() == kWave - 1) wmax[wv] = inc;
-    __syncthreads();
-    uint32_t before = run, all = run;
-    for (int w = 0; w < 16; ++w) {
-      if (w < wv) before = max(before, wmax[w]);
-      all = max(all, wmax[w]);
-    }
-    // the max over earlier tiles only
-    const uint32_t prev = (uint32_t)__shfl_up((int)inc, 1);
-    const uint32_t ex = lane_id() == 0 ? before : max(before, prev);
-    if (t < nbA) carry[t] = ex;
-    run = all;
-    __syncthreads();
-  }
-}
-
 // rank[val[t]] = head, sa[pos[t]] = val[t], grp[pos[t]] = head.
+// The group start carried into a tile is the largest start of all earlier
+// tiles: each block reduces blkmax[0 .. tile) itself.
 __global__ __launch_bounds__(kSortThreads) void k_grp_rank(
     const uint64_t* __restrict__ key, const uint32_t* __restrict__ val,
-    const uint32_t* __restrict__ pos, const uint32_t* __restrict__ carry,
+    const uint32_t* __restrict__ pos, const uint32_t* __restrict__ blkmax,
     uint32_t* rank, uint32_t* sa, uint32_t* grp, const uint32_t* state) {
   if (state[0]) return;
   const int64_t A = state[1];
   const int64_t base = (int64_t)blockIdx.x * kTile;
   if (base >= A) return;
   __shared__ uint32_t smax[kSortWaves];
+  __shared__ uint32_t cred[kSortWaves];
+  uint32_t cm = 0;
+  for (int t = threadIdx.x; t < (int)blockIdx.x; t += kSortThreads)
+    cm = max(cm, blkmax[t]);
+  cm = (uint32_t)wave_max_i32((int)cm);
+  if (lane_id() == 0) cred[threadIdx.x / kWave] = cm;
   const int wv = threadIdx.x / kWave;
   const int ln = lane_id();
   const int64_t wbase = base + (int64_t)wv * kWaveSpan;
@@ -336,7 +362,8 @@ __global__ __launch_bounds__(kSortThreads) void k_grp_rank(
   mx = (uint32_t)wave_max_i32((int)mx);
   if (ln == 0) smax[wv] = mx;
   __syncthreads();
-  uint32_t run = carry[blockIdx.x];
+  uint32_t run = 0;
+  for (int w = 0; w < kSortWaves; ++w) run = max(run, cred[w]);
   for (int w = 0; w < wv; ++w) run = max(run, smax[w]);
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
@@ -385,38 +412,36 @@ __global__ __launch_bounds__(kSortThreads) void k_sa_mark(
   }
 }
 
-// Exclusive scan of the per-tile active counts (one block); the total is
-// the round's active count, and none left means the array is final.
-__global__ __launch_bounds__(1024) void k_sa_tilescan(const uint32_t* tcnt,
-                                                      uint32_t* toff,
-                                                      int64_t nb,
-                                                      uint32_t* state) {
-  if (state[0]) return;
-  __shared__ uint32_t red[16];
-  uint32_t carry = 0;
-  for (int64_t c0 = 0; c0 < nb; c0 += 1024) {
-    const int64_t t = c0 + threadIdx.x;
-    const uint32_t v = t < nb ? tcnt[t] : 0u;
-    uint32_t tot;
-    const uint32_t ex = block_exscan1<1024>(v, red, &tot);
-    if (t < nb) toff[t] = carry + ex;
-    carry += tot;
-  }
-  if (threadIdx.x == 0) {
-    state[1] = carry;
-    if (carry == 0) state[0] = 1;
-  }
-}
-
 // Active suffixes of the tile, in SA order, with their sort keys:
 // key = head * (m + 1) + (rank[i + h] + 1, or 0 past the end).
+// Each block sums the earlier tiles' counts for its output offset; block 0
+// also sums them all: that is the round's active count, and none left
+// means the array is final (the done flag).
 __global__ __launch_bounds__(kSortThreads) void k_sa_gather(
     const uint32_t* __restrict__ sa, const uint32_t* __restrict__ rank,
-    const uint32_t* __restrict__ grp, int64_t m, int64_t h,
-    const uint32_t* __restrict__ toff, uint64_t* key, uint32_t* val,
-    uint32_t* pos, const uint32_t* state) {
+    const uint32_t* __restrict__ grp, int64_t m, int64_t h, int64_t nb,
+    const uint32_t* __restrict__ tcnt, uint64_t* key, uint32_t* val,
+    uint32_t* pos, uint32_t* state) {
   if (state[0]) return;
   __shared__ uint32_t scnt[kSortWaves];
+  __shared__ uint32_t ored[kSortWaves];
+  {
+    const int64_t upto = blockIdx.x == 0 ? nb : (int64_t)blockIdx.x;
+    uint32_t c = 0;
+    for (int64_t t = threadIdx.x; t < upto; t += kSortThreads) c += tcnt[t];
+    uint32_t tot;
+    block_exscan1<kSortThreads>(c, ored, &tot);
+    if (blockIdx.x == 0) {
+      if (threadIdx.x == 0) {
+        state[1] = tot;
+        if (tot == 0) state[0] = 1;
+      }
+      if (tot == 0) return;
+      ored[0] = 0;  // block 0's own offset (the barrier below publishes it)
+    } else if (threadIdx.x == 0) {
+      ored[0] = tot;
+    }
+  }
   const int wv = threadIdx.x / kWave;
   const int ln = lane_id();
   const int64_t wbase = (int64_t)blockIdx.x * kTile + (int64_t)wv * kWaveSpan;
@@ -432,7 +457,7 @@ __global__ __launch_bounds__(kSortThreads) void k_sa_gather(
   }
   if (ln == 0) scnt[wv] = cnt;
   __syncthreads();
-  uint32_t out = toff[blockIdx.x];
+  uint32_t out = ored[0];
   for (int w = 0; w < wv; ++w) out += scnt[w];
   const uint64_t M1 = (uint64_t)m + 1;
 #pragma unroll
@@ -487,7 +512,7 @@ static int sort_and_rank(SaWs& w, int64_t nb, int nbits, hipStream_t stream) {
   uint32_t* vin = w.valA;
   uint64_t* kout = w.keyB;
   uint32_t* vout = w.valB;
-  for (int sh = 0; sh < nbits; sh += 8) {
+  for (int sh = 0; sh < nbits; sh += kDigitBits) {
     hipLaunchKernelGGL(k_rs_hist, dim3((unsigned)nb), dim3(kSortThreads), 0,
                        stream, kin, sh, w.hist, nb, w.state);
     hipLaunchKernelGGL(k_rs_rowscan, dim3(kRadix), dim3(kSortThreads), 0,
@@ -504,10 +529,8 @@ static int sort_and_rank(SaWs& w, int64_t nb, int nbits, hipStream_t stream) {
   }
   hipLaunchKernelGGL(k_grp_reduce, dim3((unsigned)nb), dim3(kSortThreads), 0,
                      stream, kin, w.pos, w.blkmax, w.state);
-  hipLaunchKernelGGL(k_grp_carry, dim3(1), dim3(1024), 0, stream, w.blkmax,
-                     w.carry, w.state);
   hipLaunchKernelGGL(k_grp_rank, dim3((unsigned)nb), dim3(kSortThreads), 0,
-                     stream, kin, vin, w.pos, w.carry, w.rank, w.sa, w.grp,
+                     stream, kin, vin, w.pos, w.blkmax, w.rank, w.sa, w.grp,
                      w.state);
   return (int)hipGetLastError();
 }
@@ -568,10 +591,8 @@ extern "C" int sfx_sa_build(const int32_t* text, int64_t m, int64_t n_total,
   for (int64_t h = 1; h < m; h <<= 1) {
     hipLaunchKernelGGL(k_sa_mark, dim3((unsigned)nb), dim3(kSortThreads), 0,
                        stream, w.grp, m, w.tcnt, w.state);
-    hipLaunchKernelGGL(k_sa_tilescan, dim3(1), dim3(1024), 0, stream, w.tcnt,
-                       w.toff, nb, w.state);
     hipLaunchKernelGGL(k_sa_gather, dim3((unsigned)nb), dim3(kSortThreads), 0,
-                       stream, w.sa, w.rank, w.grp, m, h, w.toff, w.keyA,
+                       stream, w.sa, w.rank, w.grp, m, h, nb, w.tcnt, w.keyA,
                        w.valA, w.pos, w.state);
     rc = sort_and_rank(w, nb, nbits, stream);
     if (rc) return rc;
