@@ -31,7 +31,7 @@ extern "C" {
 
 #define SFX_EINVAL (-1)
 #define SFX_MAX_CANDIDATES 32
-#define SFX_ABI_VERSION 4
+#define SFX_ABI_VERSION 5
 
 /* Drafter configuration shared by the local and global paths.
  * Mirrors the constructor arguments of SuffixGPUDrafter
@@ -207,6 +207,28 @@ int sfx_sa_keys(const int32_t* corpus, const int32_t* sa, int64_t n,
 int sfx_sa_build(const int32_t* text, int64_t m, int64_t n_total, void* sa,
                  int32_t sa_is64, void* workspace, size_t workspace_bytes,
                  hipStream_t stream);
+
+/* The same build in steps, for a caller that advances it from a host poll
+ * loop and stops enqueueing rounds once the array is final (no reference
+ * counterpart; global_index.py:201-252 runs the build as one call):
+ *   begin  -- the token round;
+ *   rounds -- doubling rounds first .. first+count-1 (round r doubles
+ *             h = 2^(r-1); rounds past sfx_sa_build_rounds_total(m) are
+ *             skipped; a round after the array is final returns at once);
+ *   finish -- sa[0:m] from the workspace, sa[m:n_total] the identity.
+ * The workspace's u32 state block at sfx_sa_build_flag_offset(m) holds
+ * [0] nonzero once the array is final and [2] the h of the round that
+ * found it final, for an asynchronous copy to the host. */
+int sfx_sa_build_rounds_total(int64_t m);
+int64_t sfx_sa_build_flag_offset(int64_t m);
+int sfx_sa_build_begin(const int32_t* text, int64_t m, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
+int sfx_sa_build_rounds(int64_t m, int32_t first, int32_t count,
+                        void* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+int sfx_sa_build_finish(int64_t m, int64_t n_total, void* sa, int32_t sa_is64,
+                        void* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
 
 /* global_index.py:235-240 _finish_swap: in-place copy of a finished
  * rebuild into the live buffers (corpus, sa: capacity int32 each; sa_key:

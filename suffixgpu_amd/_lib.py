@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsuffixgpu_amd.so"
 MAX_CANDIDATES = 32
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -64,6 +64,13 @@ class SfxGlobalOut(ctypes.Structure):
 # name -> (restype, argtypes)
 SIGNATURES = {
     "sfx_abi_version": (c_i32, []),
+    "sfx_sa_build_rounds_total": (c_i32, [c_i64]),
+    "sfx_sa_build_flag_offset": (c_i64, [c_i64]),
+    "sfx_sa_build_begin": (c_i32, [c_p, c_i64, c_p, ctypes.c_size_t, c_p]),
+    "sfx_sa_build_rounds": (c_i32, [c_i64, c_i32, c_i32, c_p,
+                                    ctypes.c_size_t, c_p]),
+    "sfx_sa_build_finish": (c_i32, [c_i64, c_i64, c_p, c_i32, c_p,
+                                    ctypes.c_size_t, c_p]),
     "sfx_index_swap": (c_i32, [c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64,
                                c_p]),
     "sfx_scatter_append": (c_i32, [ctypes.POINTER(SfxBatch), c_p, c_p]),

@@ -44,7 +44,7 @@ struct SaWs {
   uint32_t* rowsum;  // [256] digit totals
   uint32_t* tcnt;    // [NB] active suffixes per tile
   uint32_t* blkmax;  // [NB] last group start per tile
-  uint32_t* state;   // [0] done, [1] active count
+  uint32_t* state;   // [0] done, [1] active count, [2] h when done
 };
 
 static size_t sa_ws_layout(int64_t n, void* base, SaWs* w) {
@@ -434,7 +434,10 @@ __global__ __launch_bounds__(kSortThreads) void k_sa_gather(
     if (blockIdx.x == 0) {
       if (threadIdx.x == 0) {
         state[1] = tot;
-        if (tot == 0) state[0] = 1;
+        if (tot == 0) {
+          state[0] = 1;
+          state[2] = (uint32_t)h;  // the first h whose round found none
+        }
       }
       if (tot == 0) return;
       ored[0] = 0;  // block 0's own offset (the barrier below publishes it)
@@ -556,6 +559,76 @@ extern "C" size_t sfx_sa_build_workspace_size(int64_t m) {
   return sa_ws_layout(m, nullptr, nullptr);
 }
 
+namespace {
+
+int launch_out(const uint32_t* sa, int64_t m, int64_t n_total, void* sa_out,
+               int32_t sa_is64, hipStream_t stream) {
+  const unsigned out_blocks = (unsigned)((n_total + 255) / 256);
+  if (sa_is64)
+    hipLaunchKernelGGL(k_sa_out<int64_t>, dim3(out_blocks), dim3(256), 0,
+                       stream, sa, m, n_total, (int64_t*)sa_out);
+  else
+    hipLaunchKernelGGL(k_sa_out<int32_t>, dim3(out_blocks), dim3(256), 0,
+                       stream, sa, m, n_total, (int32_t*)sa_out);
+  return (int)hipGetLastError();
+}
+
+bool ws_ok(int64_t m, const void* workspace, size_t bytes) {
+  return m <= 1 || (workspace && bytes >= sa_ws_layout(m, nullptr, nullptr));
+}
+
+// Doubling rounds after the token round: one per h = 1, 2, 4, ... < m.
+int total_rounds(int64_t m) {
+  int r = 0;
+  for (int64_t h = 1; h < m; h <<= 1) ++r;
+  return r;
+}
+
+int build_begin(const int32_t* text, int64_t m, void* workspace,
+                hipStream_t stream) {
+  if (m <= 1) return 0;
+  SaWs w;
+  sa_ws_layout(m, workspace, &w);
+  const int64_t nb = (m + kTile - 1) / kTile;
+  const unsigned eb = (unsigned)((m + 255) / 256);
+  hipLaunchKernelGGL(k_sa_init, dim3(eb), dim3(256), 0, stream, text, m,
+                     w.keyA, w.valA, w.pos, w.state);
+  return sort_and_rank(w, nb, 32, stream);
+}
+
+// Rounds first .. first + count - 1 (round r doubles h = 2^(r-1)).
+int build_rounds(int64_t m, int first, int count, void* workspace,
+                 hipStream_t stream) {
+  if (m <= 1) return 0;
+  SaWs w;
+  sa_ws_layout(m, workspace, &w);
+  const int64_t nb = (m + kTile - 1) / kTile;
+  const uint64_t maxkey = (uint64_t)(m - 1) * (uint64_t)(m + 1) + (uint64_t)m;
+  const int nbits = bits_for(maxkey);
+  const int last = total_rounds(m);
+  for (int r = first < 1 ? 1 : first; r < first + count && r <= last; ++r) {
+    const int64_t h = (int64_t)1 << (r - 1);
+    hipLaunchKernelGGL(k_sa_mark, dim3((unsigned)nb), dim3(kSortThreads), 0,
+                       stream, w.grp, m, w.tcnt, w.state);
+    hipLaunchKernelGGL(k_sa_gather, dim3((unsigned)nb), dim3(kSortThreads), 0,
+                       stream, w.sa, w.rank, w.grp, m, h, nb, w.tcnt, w.keyA,
+                       w.valA, w.pos, w.state);
+    const int rc = sort_and_rank(w, nb, nbits, stream);
+    if (rc) return rc;
+  }
+  return (int)hipGetLastError();
+}
+
+int build_finish(int64_t m, int64_t n_total, void* sa_out, int32_t sa_is64,
+                 void* workspace, hipStream_t stream) {
+  if (m <= 1) return launch_out(nullptr, 0, n_total, sa_out, sa_is64, stream);
+  SaWs w;
+  sa_ws_layout(m, workspace, &w);
+  return launch_out(w.sa, m, n_total, sa_out, sa_is64, stream);
+}
+
+}  // namespace
+
 extern "C" int sfx_sa_build(const int32_t* text, int64_t m, int64_t n_total,
                             void* sa_out, int32_t sa_is64, void* workspace,
                             size_t workspace_bytes, hipStream_t stream) {
@@ -563,47 +636,52 @@ extern "C" int sfx_sa_build(const int32_t* text, int64_t m, int64_t n_total,
     return SFX_EINVAL;
   if (n_total == 0) return 0;
   if (!sa_out || (m > 0 && !text)) return SFX_EINVAL;
-  const size_t need = sa_ws_layout(m, nullptr, nullptr);
-  if (m > 1 && (!workspace || workspace_bytes < need)) return SFX_EINVAL;
-  const unsigned out_blocks = (unsigned)((n_total + 255) / 256);
-  if (m <= 1) {
-    // SA of zero or one symbol is the identity.
-    if (sa_is64)
-      hipLaunchKernelGGL(k_sa_out<int64_t>, dim3(out_blocks), dim3(256), 0,
-                         stream, (const uint32_t*)nullptr, (int64_t)0,
-                         n_total, (int64_t*)sa_out);
-    else
-      hipLaunchKernelGGL(k_sa_out<int32_t>, dim3(out_blocks), dim3(256), 0,
-                         stream, (const uint32_t*)nullptr, (int64_t)0,
-                         n_total, (int32_t*)sa_out);
-    return (int)hipGetLastError();
-  }
-  SaWs w;
-  sa_ws_layout(m, workspace, &w);
-  const int64_t nb = (m + kTile - 1) / kTile;
-  const unsigned eb = (unsigned)((m + 255) / 256);
-  hipLaunchKernelGGL(k_sa_init, dim3(eb), dim3(256), 0, stream, text, m,
-                     w.keyA, w.valA, w.pos, w.state);
-  int rc = sort_and_rank(w, nb, 32, stream);
+  if (!ws_ok(m, workspace, workspace_bytes)) return SFX_EINVAL;
+  int rc = build_begin(text, m, workspace, stream);
   if (rc) return rc;
-  const uint64_t maxkey = (uint64_t)(m - 1) * (uint64_t)(m + 1) + (uint64_t)m;
-  const int nbits = bits_for(maxkey);
-  for (int64_t h = 1; h < m; h <<= 1) {
-    hipLaunchKernelGGL(k_sa_mark, dim3((unsigned)nb), dim3(kSortThreads), 0,
-                       stream, w.grp, m, w.tcnt, w.state);
-    hipLaunchKernelGGL(k_sa_gather, dim3((unsigned)nb), dim3(kSortThreads), 0,
-                       stream, w.sa, w.rank, w.grp, m, h, nb, w.tcnt, w.keyA,
-                       w.valA, w.pos, w.state);
-    rc = sort_and_rank(w, nb, nbits, stream);
-    if (rc) return rc;
-  }
-  if (sa_is64)
-    hipLaunchKernelGGL(k_sa_out<int64_t>, dim3(out_blocks), dim3(256), 0,
-                       stream, (const uint32_t*)w.sa, m, n_total,
-                       (int64_t*)sa_out);
-  else
-    hipLaunchKernelGGL(k_sa_out<int32_t>, dim3(out_blocks), dim3(256), 0,
-                       stream, (const uint32_t*)w.sa, m, n_total,
-                       (int32_t*)sa_out);
-  return (int)hipGetLastError();
+  rc = build_rounds(m, 1, total_rounds(m), workspace, stream);
+  if (rc) return rc;
+  return build_finish(m, n_total, sa_out, sa_is64, workspace, stream);
+}
+
+extern "C" int sfx_sa_build_rounds_total(int64_t m) {
+  return m < 0 ? SFX_EINVAL : total_rounds(m);
+}
+
+extern "C" int64_t sfx_sa_build_flag_offset(int64_t m) {
+  if (m < 0) return SFX_EINVAL;
+  // Lay the workspace out over a stand-in base address to read the state
+  // block's offset; nothing is dereferenced.
+  char* const base = reinterpret_cast<char*>(uintptr_t{1} << 20);
+  SaWs w;
+  sa_ws_layout(m, base, &w);
+  return (int64_t)(reinterpret_cast<char*>(w.state) - base);
+}
+
+extern "C" int sfx_sa_build_begin(const int32_t* text, int64_t m,
+                                  void* workspace, size_t workspace_bytes,
+                                  hipStream_t stream) {
+  if (m < 0 || m > 0x7fffffffLL || (m > 0 && !text)) return SFX_EINVAL;
+  if (!ws_ok(m, workspace, workspace_bytes)) return SFX_EINVAL;
+  return build_begin(text, m, workspace, stream);
+}
+
+extern "C" int sfx_sa_build_rounds(int64_t m, int32_t first, int32_t count,
+                                   void* workspace, size_t workspace_bytes,
+                                   hipStream_t stream) {
+  if (m < 0 || m > 0x7fffffffLL || first < 1 || count < 0) return SFX_EINVAL;
+  if (!ws_ok(m, workspace, workspace_bytes)) return SFX_EINVAL;
+  return build_rounds(m, first, count, workspace, stream);
+}
+
+extern "C" int sfx_sa_build_finish(int64_t m, int64_t n_total, void* sa_out,
+                                   int32_t sa_is64, void* workspace,
+                                   size_t workspace_bytes,
+                                   hipStream_t stream) {
+  if (m < 0 || n_total < m || m > 0x7fffffffLL || n_total > 0x7fffffffLL)
+    return SFX_EINVAL;
+  if (n_total == 0) return 0;
+  if (!sa_out) return SFX_EINVAL;
+  if (!ws_ok(m, workspace, workspace_bytes)) return SFX_EINVAL;
+  return build_finish(m, n_total, sa_out, sa_is64, workspace, stream);
 }

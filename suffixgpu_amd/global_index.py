@@ -85,6 +85,13 @@ class GlobalIndex:
         self.delta_doc_lens: list[int] = []
         self._rebuild_event = None
         self._pending = None
+        # Background rebuilds run their doubling rounds in two chunks: the
+        # first sized from the rounds the previous build needed (plus a
+        # margin), the rest only if the device reports the array is not
+        # final yet (a pinned copy of the build's state block).
+        self.sa_round_hint = 12
+        self._build_state = None  # (m, next_round) while rounds may remain
+        self._flag_host = torch.zeros(4, dtype=torch.int32, pin_memory=True)
 
     # ------------------------------------------------------------------
     # device views
@@ -225,7 +232,7 @@ class GlobalIndex:
             self.rebuild_stream.wait_stream(
                 torch.cuda.current_stream(self.device))
             with torch.cuda.stream(self.rebuild_stream):
-                self._build_staging_sa(dst, m)
+                self._staged_build_begin(dst, m)
             event = torch.cuda.Event()
             event.record(self.rebuild_stream)
             self._pending = (n_new, new_doc_lens)
@@ -234,17 +241,84 @@ class GlobalIndex:
             self._build_staging_sa(dst, m)
             self._finish_swap(n_new, new_doc_lens)
 
-    def _build_staging_sa(self, dst: torch.Tensor, m: int) -> None:
-        """staging_sa[:m] = SA(dst[:m]); staging_sa[m:] = m .. N-1."""
+    def _sa_workspace(self) -> torch.Tensor:
         need = sa_workspace_bytes(self.capacity)
         if self._sa_ws is None or self._sa_ws.numel() < need:
             self._sa_ws = torch.empty(max(need, 1), dtype=torch.uint8,
                                       device=self.device)
+        return self._sa_ws
+
+    def _build_staging_sa(self, dst: torch.Tensor, m: int) -> None:
+        """staging_sa[:m] = SA(dst[:m]); staging_sa[m:] = m .. N-1."""
+        ws = self._sa_workspace()
         check(lib().sfx_sa_build(dst.data_ptr(), m, self.capacity,
                                  self.staging_sa.data_ptr(), 0,
-                                 self._sa_ws.data_ptr(), self._sa_ws.numel(),
+                                 ws.data_ptr(), ws.numel(),
                                  stream_of(self.device)), "SA rebuild")
         self._build_keys(dst, self.staging_sa, self.staging_sa_key)
+
+    # Background builds, enqueued on the current (rebuild) stream.
+    def _staged_build_begin(self, dst: torch.Tensor, m: int) -> None:
+        """Token round + the hinted doubling rounds, a pinned copy of the
+        build state, then (speculatively) the output and key rows."""
+        L = lib()
+        ws = self._sa_workspace()
+        st = stream_of(self.device)
+        total = int(L.sfx_sa_build_rounds_total(m))
+        first = min(self.sa_round_hint, total)
+        check(L.sfx_sa_build_begin(dst.data_ptr(), m, ws.data_ptr(),
+                                   ws.numel(), st), "SA rebuild")
+        check(L.sfx_sa_build_rounds(m, 1, first, ws.data_ptr(), ws.numel(),
+                                    st), "SA rebuild")
+        self._copy_build_state(m)
+        self._staged_build_finish(dst, m)
+        self._build_state = (m, first + 1) if first < total else None
+
+    def _copy_build_state(self, m: int) -> None:
+        if m <= 1:
+            self._flag_host.fill_(1)
+            return
+        off = int(lib().sfx_sa_build_flag_offset(m))
+        state = self._sa_ws[off:off + 16].view(torch.int32)
+        self._flag_host.copy_(state, non_blocking=True)
+
+    def _staged_build_finish(self, dst: torch.Tensor, m: int) -> None:
+        ws = self._sa_ws
+        check(lib().sfx_sa_build_finish(m, self.capacity,
+                                        self.staging_sa.data_ptr(), 0,
+                                        ws.data_ptr(), ws.numel(),
+                                        stream_of(self.device)),
+              "SA rebuild")
+        self._build_keys(dst, self.staging_sa, self.staging_sa_key)
+
+    def _staged_build_check(self) -> bool:
+        """After the build's event: True when the staged output is final;
+        otherwise the remaining rounds, the output and the key rows are
+        enqueued again under a new event."""
+        if self._build_state is None:
+            return True
+        m, nxt = self._build_state
+        self._build_state = None
+        flags = self._flag_host.tolist()
+        if flags[0]:
+            h = max(int(flags[2]), 1)
+            # rounds used: the one that found the array final doubled h
+            self.sa_round_hint = max(1, h.bit_length() - 1) + 2
+            return True
+        L = lib()
+        total = int(L.sfx_sa_build_rounds_total(m))
+        self.sa_round_hint = total
+        self.rebuild_stream.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(self.rebuild_stream):
+            ws = self._sa_ws
+            check(L.sfx_sa_build_rounds(m, nxt, total - nxt + 1,
+                                        ws.data_ptr(), ws.numel(),
+                                        stream_of(self.device)), "SA rebuild")
+            self._staged_build_finish(self.staging_corpus, m)
+        event = torch.cuda.Event()
+        event.record(self.rebuild_stream)
+        self._rebuild_event = event
+        return False
 
     def _count_docs_within(self, tokens: int) -> int:
         acc = 0
@@ -278,9 +352,11 @@ class GlobalIndex:
             done = True
         else:
             done = ev.query()
-        if done:
+        if done and self._staged_build_check():
             n_new, new_doc_lens = self._pending
             self._finish_swap(n_new, new_doc_lens)
+        elif done and self.blocking_poll:
+            self.poll_rebuild()  # the remaining rounds, waited for too
 
     def load_documents(self, docs: list[torch.Tensor]) -> None:
         """Make ``docs`` (oldest first) the active corpus in one rebuild.

@@ -47,3 +47,32 @@ def build_suffix_array(tokens: torch.Tensor) -> torch.Tensor:
         return out
     build_suffix_array_into(tokens, n, out)
     return out
+
+
+def build_suffix_array_rounds(text: torch.Tensor, m: int, out: torch.Tensor,
+                              workspace: torch.Tensor, rounds: int) -> None:
+    """The build with only its first ``rounds`` doubling rounds enqueued
+    (then the output copy): the background rebuild's first chunk.  The
+    result is final iff :func:`build_is_final` says so afterwards."""
+    require_gpu(text, out, workspace)
+    L = lib()
+    st = stream_of(text.device)
+    check(L.sfx_sa_build_begin(text.data_ptr(), m, workspace.data_ptr(),
+                               workspace.numel(), st), "SA build")
+    check(L.sfx_sa_build_rounds(m, 1, max(0, rounds), workspace.data_ptr(),
+                                workspace.numel(), st), "SA build")
+    check(L.sfx_sa_build_finish(m, out.shape[0], out.data_ptr(),
+                                int(out.dtype == torch.int64),
+                                workspace.data_ptr(), workspace.numel(), st),
+          "SA build")
+
+
+def build_state(workspace: torch.Tensor, m: int) -> tuple[bool, int]:
+    """(final, rounds the array needed) from a build's workspace; reads the
+    device (synchronises the current stream)."""
+    if m <= 1:
+        return True, 0
+    off = int(lib().sfx_sa_build_flag_offset(m))
+    st = workspace[off:off + 16].view(torch.int32).cpu().tolist()
+    h = max(int(st[2]), 1)
+    return bool(st[0]), (h.bit_length() - 1 if st[0] else -1)

@@ -345,9 +345,11 @@ def test_split_delta_vs_oracle(gpu, mode):
         np.testing.assert_array_equal(N(got), exp)
 
 
-def test_async_rebuild_blocking_poll(gpu):
+@pytest.mark.parametrize("hint", [12, 1, 3])
+def test_async_rebuild_blocking_poll(gpu, hint):
     """Side-stream rebuilds swapped at deterministic points match the
-    oracle's done-at-next-poll schedule."""
+    oracle's done-at-next-poll schedule.  The build runs its doubling
+    rounds in two chunks; a small first chunk (hint) forces the second."""
     from suffixgpu_amd.global_index import GlobalIndex
     rng = np.random.default_rng(8)
     side = torch.cuda.Stream(gpu)
@@ -355,12 +357,15 @@ def test_async_rebuild_blocking_poll(gpu):
                     max_occurrences=8, rebuild_threshold=150, device=gpu,
                     rebuild_stream=side)
     g.blocking_poll = True
+    g.sa_round_hint = hint
     o = GlobalIndexOracle(capacity=3000, delta_capacity=400, k=4,
                           max_occurrences=8, rebuild_threshold=150,
                           async_rebuild=True)
     for step in range(40):
         docs = [rng.integers(0, 6, size=int(rng.integers(1, 120))).astype(I32)
                 for _ in range(int(rng.integers(1, 4)))]
+        if hint < 12:
+            g.sa_round_hint = hint  # every build starts with a short chunk
         g.append_documents([T(d, gpu) for d in docs])
         o.append_documents(docs)
         if step % 3 == 0:
