@@ -44,12 +44,15 @@ __device__ __forceinline__ int cmp_suffix(const int32_t* __restrict__ sa,
 // The same comparison from the rank's key row: keys[rank * kw + j] holds
 // corpus[sa[rank] + j] (or -1 past the end) for j < kw, so patterns of up
 // to kw tokens are decided by one row load (kw * 4 bytes, one line for
-// kw = 32); longer patterns continue in the corpus.
+// kw = 32); longer patterns continue in the corpus.  pt holds the first
+// min(plen, 32) pattern tokens in registers, so the token loop waits on
+// nothing but the row.
 template <class PatFn>
 __device__ __forceinline__ int cmp_suffix_key(
     const int32_t* __restrict__ keys, int kw,
     const int32_t* __restrict__ sa, const int32_t* __restrict__ corpus,
-    int64_t n, int64_t rank, PatFn pat_at, int plen) {
+    int64_t n, int64_t rank, const int32_t (&pt)[32], PatFn pat_at,
+    int plen) {
   const int4* row = reinterpret_cast<const int4*>(keys + rank * kw);
   const int kn = plen < kw ? plen : kw;
   int4 w[8];
@@ -63,8 +66,7 @@ __device__ __forceinline__ int cmp_suffix_key(
     for (int u = 0; u < 4; ++u) {
       const int j = 4 * q + u;
       if (j >= kn) break;
-      const int32_t pj = pat_at(j);
-      if (t4[u] != pj) return t4[u] < pj ? -1 : 1;
+      if (t4[u] != pt[j]) return t4[u] < pt[j] ? -1 : 1;
     }
   }
   if (plen <= kw) return 0;
@@ -78,22 +80,28 @@ __device__ __forceinline__ int cmp_suffix_key(
   return 0;
 }
 
-__device__ __forceinline__ int64_t kary_probe(int64_t lo, int64_t hi,
-                                              int k, int np) {
-  return lo + ((hi - lo) * (int64_t)(k + 1)) / (np + 1);
+// Probe k of NP (k < NP) splitting [lo, hi]: lo + floor((hi - lo) * f_k)
+// with f_k = floor(2^32 (k + 1) / (NP + 1)) / 2^32, one 32x32->64 multiply
+// (ranges stay below 2^31).  The probes ascend with k and stay below hi,
+// which is all the search needs.
+template <int NP>
+__device__ __forceinline__ int64_t kary_probe(int64_t lo, int64_t hi, int k) {
+  const uint32_t f = (uint32_t)((((uint64_t)(k + 1)) << 32) / (NP + 1));
+  return lo + (int64_t)(((uint64_t)(uint32_t)(hi - lo) * f) >> 32);
 }
 
 // Narrow [lo, hi] (answer inside; ranks < lo false, >= hi true) with the
-// predicate bits of np probes (bit k = probe k true).
+// predicate bits of NP probes (bit k = probe k true).
+template <int NP>
 __device__ __forceinline__ void kary_update(int64_t& lo, int64_t& hi,
-                                            int np, uint32_t bits) {
+                                            uint32_t bits) {
   if (bits == 0) {
-    lo = kary_probe(lo, hi, np - 1, np) + 1;
+    lo = kary_probe<NP>(lo, hi, NP - 1) + 1;
     return;
   }
   const int k = __builtin_ctz(bits);
-  const int64_t nh = kary_probe(lo, hi, k, np);
-  if (k > 0) lo = kary_probe(lo, hi, k - 1, np) + 1;
+  const int64_t nh = kary_probe<NP>(lo, hi, k);
+  if (k > 0) lo = kary_probe<NP>(lo, hi, k - 1) + 1;
   hi = nh;
 }
 
@@ -108,31 +116,32 @@ __device__ __forceinline__ void kary_bounds(
     int64_t n, const int32_t* __restrict__ keys, int kw, PatFn pat_at,
     int plen, int64_t& lower, int64_t& upper) {
   static_assert(G >= 2 && G <= 32 && (64 % G) == 0, "group size");
+  constexpr int H = G / 2;
   const int ln = lane_id();
   const int gl = ln % G;
   const int gbase = ln - gl;
+  int32_t pt[32];
+  if (keys) {
+#pragma unroll
+    for (int j = 0; j < 32; ++j) pt[j] = j < plen ? pat_at(j) : 0;
+  }
   int64_t lo1 = 0, hi1 = n, lo2 = 0, hi2 = n;
   while (lo1 < hi1 || lo2 < hi2) {
     const bool shared = lo1 == lo2 && hi1 == hi2;
     const bool only1 = !shared && lo2 == hi2;
     const bool only2 = !shared && lo1 == hi1;
-    int64_t lo, hi;
-    int np, k;
-    bool upper_half = false;
+    int64_t probe;
     if (shared || only1) {
-      lo = lo1; hi = hi1; np = G; k = gl;
+      probe = kary_probe<G>(lo1, hi1, gl);
     } else if (only2) {
-      lo = lo2; hi = hi2; np = G; k = gl;
+      probe = kary_probe<G>(lo2, hi2, gl);
     } else {
-      np = G / 2;
-      upper_half = gl >= np;
-      k = upper_half ? gl - np : gl;
-      lo = upper_half ? lo2 : lo1;
-      hi = upper_half ? hi2 : hi1;
+      probe = gl >= H ? kary_probe<H>(lo2, hi2, gl - H)
+                      : kary_probe<H>(lo1, hi1, gl);
     }
-    const int64_t probe = kary_probe(lo, hi, k, np);
     const int c =
-        keys ? cmp_suffix_key(keys, kw, sa, corpus, n, probe, pat_at, plen)
+        keys ? cmp_suffix_key(keys, kw, sa, corpus, n, probe, pt, pat_at,
+                              plen)
              : cmp_suffix(sa, corpus, n, probe, pat_at, plen);
     const uint64_t m1 = ballot(c >= 0);
     const uint64_t m2 = ballot(c > 0);
@@ -140,16 +149,16 @@ __device__ __forceinline__ void kary_bounds(
     const uint32_t g1 = (uint32_t)(m1 >> gbase) & full;
     const uint32_t g2 = (uint32_t)(m2 >> gbase) & full;
     if (shared) {
-      kary_update(lo1, hi1, G, g1);
-      kary_update(lo2, hi2, G, g2);
+      kary_update<G>(lo1, hi1, g1);
+      kary_update<G>(lo2, hi2, g2);
     } else if (only1) {
-      kary_update(lo1, hi1, G, g1);
+      kary_update<G>(lo1, hi1, g1);
     } else if (only2) {
-      kary_update(lo2, hi2, G, g2);
+      kary_update<G>(lo2, hi2, g2);
     } else {
-      const uint32_t half = (1u << (G / 2)) - 1u;
-      kary_update(lo1, hi1, G / 2, g1 & half);
-      kary_update(lo2, hi2, G / 2, (g2 >> (G / 2)) & half);
+      const uint32_t half = (1u << H) - 1u;
+      kary_update<H>(lo1, hi1, g1 & half);
+      kary_update<H>(lo2, hi2, (g2 >> H) & half);
     }
   }
   lower = lo1;
