@@ -252,6 +252,45 @@ def _load_pair(gpu, docs, delta_docs, cap, dcap, r, k=16):
     return g, o
 
 
+@pytest.mark.parametrize("kind", ["periodic", "runs"])
+def test_sa_interval_search_long_repeats(gpu, kind):
+    """The key-row k-ary search (32-token rows, probes that skip the tokens
+    both range boundaries already match) on texts whose suffixes share long
+    prefixes: wide intervals at every length, matches past the row."""
+    from suffixgpu_amd.sa_search import suffix_match_backoff
+    from oracle.sa import suffix_match_backoff as o_smb
+    rng = np.random.default_rng(77 if kind == "periodic" else 78)
+    if kind == "periodic":
+        docs = [np.tile(np.array([3, 1, 4, 1, 5], I32), 400)[:int(n)]
+                for n in rng.integers(50, 2000, size=12)]
+        docs += [rng.integers(0, 6, size=300).astype(I32) for _ in range(4)]
+    else:
+        docs = [np.repeat(rng.integers(0, 3, size=60), rng.integers(1, 40,
+                                                              size=60))
+                .astype(I32) for _ in range(16)]
+    cap = sum(len(d) + 1 for d in docs) + 5
+    g, o = _load_pair(gpu, docs, [], cap, 64, 16, k=4)
+    b, p = 64, 32
+    q = np.zeros((b, p), I32)
+    ql = np.zeros(b, np.int64)
+    for i in range(b):
+        src = docs[i % len(docs)]
+        n = int(rng.integers(1, min(len(src), p) + 1))
+        st = int(rng.integers(0, len(src) - n + 1))
+        q[i, :n] = src[st:st + n]
+        ql[i] = n
+        if i % 9 == 0 and n > 2:
+            q[i, n - 1] = 9  # diverges at the last token
+    caps = np.array([32, 16, 8, 4, 2], np.int64)
+    tq, tl, tc_ = T(q, gpu), T(ql, gpu), T(caps, gpu)
+    for got, exp in zip(suffix_match_backoff(g.sa, g.corpus, tq, tl, p, tc_),
+                        o_smb(o.sa, o.corpus, q, ql, p, caps)):
+        np.testing.assert_array_equal(N(got), exp)
+    for got, exp in zip(g._query_backoff(tq, tl, p, tc_),
+                        o._query_backoff(q, ql, p, caps)):
+        np.testing.assert_array_equal(N(got), exp)
+
+
 @pytest.mark.parametrize("vocab", [4, 0])
 def test_queries_vs_oracle(gpu, vocab):
     rng = np.random.default_rng(31 + vocab)
