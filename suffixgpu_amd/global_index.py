@@ -358,6 +358,99 @@ class GlobalIndex:
         elif done and self.blocking_poll:
             self.poll_rebuild()  # the remaining rounds, waited for too
 
+    # ------------------------------------------------------------------
+    # persistence (this library's own format; suffixgpu_amd.persist)
+    # ------------------------------------------------------------------
+    def save(self, path) -> None:
+        """Write the index to ``path``.  An in-flight rebuild is completed
+        (and swapped in) first, so the file holds one consistent state."""
+        from suffixgpu_amd.persist import write_index_file
+        if self._rebuild_event is not None:
+            blocking = self.blocking_poll
+            self.blocking_poll = True
+            try:
+                self.poll_rebuild()
+            finally:
+                self.blocking_poll = blocking
+        m = min(self.active_len + 1, self.capacity) if self.active_len else 0
+        arrays = {
+            "corpus": self.corpus[:m].cpu().numpy(),
+            "sa": self.sa[:m].cpu().numpy(),
+            "delta": self.delta[:self.delta_len].cpu().numpy(),
+        }
+        meta = {
+            "capacity": self.capacity,
+            "delta_capacity": self.delta_capacity,
+            "k": self.k,
+            "max_occurrences": self.max_occurrences,
+            "rebuild_threshold": self.rebuild_threshold,
+            "active_len": self.active_len,
+            "delta_len": self.delta_len,
+            "active_doc_lens": list(self.active_doc_lens),
+            "delta_doc_lens": list(self.delta_doc_lens),
+            "sa_prefix": m,
+            "pad_token": PAD_TOKEN,
+            "sep_token": SEP_TOKEN,
+        }
+        write_index_file(path, meta, arrays)
+
+    def restore(self, path) -> None:
+        """Load a saved index into this one, in place (tensor identities
+        are kept, so captured graphs stay valid).  Capacities must match;
+        any in-flight rebuild is dropped."""
+        from suffixgpu_amd.persist import IndexFormatError, read_index_file
+        meta, arrays = read_index_file(path)
+        if (meta["capacity"] != self.capacity
+                or meta["delta_capacity"] != self.delta_capacity):
+            raise IndexFormatError(
+                f"{path}: capacity {meta['capacity']}/"
+                f"{meta['delta_capacity']} does not match this index "
+                f"({self.capacity}/{self.delta_capacity})")
+        if (meta["pad_token"] != PAD_TOKEN
+                or meta["sep_token"] != SEP_TOKEN):
+            raise IndexFormatError(f"{path}: different sentinel tokens")
+        m = int(meta["sa_prefix"])
+        n_act, n_del = int(meta["active_len"]), int(meta["delta_len"])
+        if (arrays["corpus"].shape != (m,) or arrays["sa"].shape != (m,)
+                or arrays["delta"].shape != (n_del,) or m > self.capacity
+                or n_act > self.capacity or n_del > self.delta_capacity
+                or sum(meta["active_doc_lens"]) != n_act
+                or sum(meta["delta_doc_lens"]) != n_del):
+            raise IndexFormatError(f"{path}: inconsistent index state")
+        if self._rebuild_event is not None:
+            self._rebuild_event.synchronize()
+        self._rebuild_event = None
+        self._pending = None
+        self._build_state = None
+        dev = self.device
+        self.corpus.fill_(PAD_TOKEN)
+        self.corpus[:m].copy_(torch.from_numpy(arrays["corpus"]).to(dev))
+        self.sa.copy_(torch.arange(self.capacity, dtype=torch.int32,
+                                   device=dev))
+        self.sa[:m].copy_(torch.from_numpy(arrays["sa"]).to(dev))
+        self.delta.zero_()
+        self.delta[:n_del].copy_(torch.from_numpy(arrays["delta"]).to(dev))
+        self.delta_len = n_del
+        self.delta_len_t.fill_(n_del)
+        self.active_len = n_act
+        self.active_doc_lens = deque(int(x) for x in meta["active_doc_lens"])
+        self.delta_doc_lens = [int(x) for x in meta["delta_doc_lens"]]
+        self._build_keys(self.corpus, self.sa, self.sa_key)
+
+    @classmethod
+    def from_file(cls, path, device="cuda",
+                  rebuild_stream: torch.cuda.Stream | None = None
+                  ) -> "GlobalIndex":
+        """A new index with the geometry and state saved in ``path``."""
+        from suffixgpu_amd.persist import read_index_file
+        meta, _ = read_index_file(path)
+        gi = cls(meta["capacity"], meta["delta_capacity"], meta["k"],
+                 max_occurrences=meta["max_occurrences"],
+                 rebuild_threshold=meta["rebuild_threshold"], device=device,
+                 rebuild_stream=rebuild_stream)
+        gi.restore(path)
+        return gi
+
     def load_documents(self, docs: list[torch.Tensor]) -> None:
         """Make ``docs`` (oldest first) the active corpus in one rebuild.
 

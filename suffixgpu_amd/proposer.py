@@ -251,5 +251,17 @@ class SuffixGPUDrafter:
         if docs:
             self.global_index.append_documents(docs)
 
+    def save_global_index(self, path) -> None:
+        """Persist the global memory (see GlobalIndex.save)."""
+        if self.global_index is None:
+            raise RuntimeError("save_global_index: global memory is off")
+        self.global_index.save(path)
+
+    def load_global_index(self, path) -> None:
+        """Restore saved global memory into this drafter, in place."""
+        if self.global_index is None:
+            raise RuntimeError("load_global_index: global memory is off")
+        self.global_index.restore(path)
+
     def load_model(self, *args, **kwargs) -> None:
         pass

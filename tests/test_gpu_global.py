@@ -417,3 +417,53 @@ def test_async_rebuild_blocking_poll(gpu, hint):
     o.poll_rebuild()
     torch.cuda.synchronize()
     gpu_state_equal(g, o)
+
+
+def test_save_restore_bit_exact(gpu, tmp_path):
+    """A saved index restores to the same corpus, SA, delta, key rows and
+    host state (into a new index and in place), and answers queries
+    bit-exactly; an in-flight rebuild is completed before saving."""
+    from suffixgpu_amd.global_index import GlobalIndex
+    rng = np.random.default_rng(21)
+    side = torch.cuda.Stream(gpu)
+    g = GlobalIndex(capacity=5000, delta_capacity=600, k=6,
+                    max_occurrences=16, rebuild_threshold=250, device=gpu,
+                    rebuild_stream=side)
+    o = GlobalIndexOracle(capacity=5000, delta_capacity=600, k=6,
+                          max_occurrences=16, rebuild_threshold=250,
+                          async_rebuild=True)
+    for _ in range(12):
+        docs = [rng.integers(0, 9, size=int(rng.integers(5, 150))).astype(I32)
+                for _ in range(3)]
+        g.append_documents([T(d, gpu) for d in docs])
+        o.append_documents(docs)
+    path = tmp_path / "index.sfx"
+    g.save(path)  # completes the pending rebuild, if any
+    o.poll_rebuild()
+    gpu_state_equal(g, o)
+    h = GlobalIndex.from_file(path, device=gpu)
+    gpu_state_equal(h, o)
+    np.testing.assert_array_equal(N(h.sa_key), N(g.sa_key))
+    # in place into an index that holds other data
+    e = GlobalIndex(capacity=5000, delta_capacity=600, k=6,
+                    max_occurrences=16, rebuild_threshold=250, device=gpu)
+    e.append_documents([T(rng.integers(0, 9, size=100).astype(I32), gpu)])
+    ptrs = (e.corpus.data_ptr(), e.sa.data_ptr(), e.sa_key.data_ptr())
+    e.restore(path)
+    assert ptrs == (e.corpus.data_ptr(), e.sa.data_ptr(), e.sa_key.data_ptr())
+    gpu_state_equal(e, o)
+    q = np.zeros((16, 10), I32)
+    ql = np.zeros(16, np.int64)
+    for i in range(16):
+        n = int(rng.integers(1, 11))
+        q[i, :n] = rng.integers(0, 9, size=n)
+        ql[i] = n
+    caps = np.array([10, 5, 2], np.int64)
+    for idx in (h, e):
+        for got, exp in zip(idx._query_backoff(T(q, gpu), T(ql, gpu), 10,
+                                               T(caps, gpu)),
+                            o._query_backoff(q, ql, 10, caps)):
+            np.testing.assert_array_equal(N(got), exp)
+    with pytest.raises(ValueError):
+        GlobalIndex(capacity=4096, delta_capacity=600, k=6,
+                    device=gpu).restore(path)
