@@ -53,7 +53,16 @@ inline size_t one_per_cu_lds(size_t lds, unsigned blocks) {
   return lds;
 }
 
+// Longest row (tokens) the local matcher takes: positions stay int32.
+constexpr int64_t kMaxSeq = int64_t(1) << 30;
+// Rows whose whole-row LDS layout does not fit are streamed in chunks of
+// the largest power of two in [kMinStreamChunk, kMaxStreamChunk] that fits.
+constexpr int kMaxStreamChunk = 16384;
+constexpr int kMinStreamChunk = 1024;
+
 int check_local(const sfx_params& p, const sfx_batch& bt);
+// 0: whole row in LDS; > 0: streamed chunk length; -1: nothing fits.
+int local_chunk(const sfx_params& p, int64_t S);
 size_t local_lds_bytes(const sfx_params& p, int64_t S);
 
 int check_global(const sfx_params& p, const sfx_index& ix, int64_t batch);

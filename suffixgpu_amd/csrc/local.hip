@@ -7,7 +7,8 @@
 // u8), a 33-bin histogram whose suffix sums give every support threshold's
 // candidate length, the ordered ballot/mbcnt compaction of the first R
 // occurrence ends per candidate, and one wave per candidate running the
-// majority-vote expansion straight off the LDS row.
+// majority-vote expansion straight off the LDS row.  Rows too long for
+// LDS stay in HBM and are streamed through it in chunks instead.
 //
 // Follows suffix_gpu/local_matcher.py:83-263 and proposer.py:135-184,
 // 322-327.
@@ -17,17 +18,30 @@
 
 namespace sfx {
 
+template <bool kStream>
 __global__ __launch_bounds__(kLocalThreads) void k_local(LocalArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
-  local_body(a, smem, blockIdx.x);
+  local_body<kStream>(a, smem, blockIdx.x);
 }
 
-
-size_t local_lds_bytes(const sfx_params& p, int64_t S) {
+static size_t layout_bytes(const sfx_params& p, int64_t S, int chunk) {
+  if (chunk == 0 && S > (int64_t)kMaxLds / 4) return (size_t)-1;
   const LocalLayout L =
       local_layout((int)S, p.max_pattern_len, p.num_thresholds,
-                   p.max_occurrences, p.k, kLocalThreads / kWave);
+                   p.max_occurrences, p.k, kLocalThreads / kWave, chunk);
   return (size_t)L.total;
+}
+
+int local_chunk(const sfx_params& p, int64_t S) {
+  if (layout_bytes(p, S, 0) <= kMaxLds) return 0;
+  for (int chunk = kMaxStreamChunk; chunk >= kMinStreamChunk; chunk /= 2)
+    if (layout_bytes(p, S, chunk) <= kMaxLds) return chunk;
+  return -1;
+}
+
+size_t local_lds_bytes(const sfx_params& p, int64_t S) {
+  const int chunk = local_chunk(p, S);
+  return chunk < 0 ? (size_t)-1 : layout_bytes(p, S, chunk);
 }
 
 int check_local(const sfx_params& p, const sfx_batch& bt) {
@@ -39,17 +53,26 @@ int check_local(const sfx_params& p, const sfx_batch& bt) {
       p.num_thresholds > SFX_MAX_CANDIDATES)
     return SFX_EINVAL;
   if (bt.sampled && bt.num_sampled < 0) return SFX_EINVAL;
-  if (local_lds_bytes(p, bt.seq) > kMaxLds) return SFX_EINVAL;
+  if (bt.seq > kMaxSeq) return SFX_EINVAL;
+  if (local_chunk(p, bt.seq) < 0) return SFX_EINVAL;
   return 0;
 }
 
-int launch_local(const LocalArgs& a, hipStream_t stream) {
+int launch_local(LocalArgs a, hipStream_t stream) {
   if (a.bt.batch == 0) return 0;
+  a.chunk = local_chunk(a.p, a.bt.seq);
   const size_t lds = local_lds_bytes(a.p, a.bt.seq);
-  static std::atomic<uint64_t> lds_opt{0};
-  allow_max_lds((const void*)k_local, lds_opt);
-  hipLaunchKernelGGL(k_local, dim3((unsigned)a.bt.batch), dim3(kLocalThreads),
-                     lds, stream, a);
+  if (a.chunk == 0) {
+    static std::atomic<uint64_t> lds_opt{0};
+    allow_max_lds((const void*)k_local<false>, lds_opt);
+    hipLaunchKernelGGL(k_local<false>, dim3((unsigned)a.bt.batch),
+                       dim3(kLocalThreads), lds, stream, a);
+  } else {
+    static std::atomic<uint64_t> lds_opt{0};
+    allow_max_lds((const void*)k_local<true>, lds_opt);
+    hipLaunchKernelGGL(k_local<true>, dim3((unsigned)a.bt.batch),
+                       dim3(kLocalThreads), lds, stream, a);
+  }
   return (int)hipGetLastError();
 }
 

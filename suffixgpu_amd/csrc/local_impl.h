@@ -25,6 +25,7 @@ struct LocalArgs {
   float* score_out;
   int32_t* new_counts;  // step
   StepWs ws;
+  int chunk;  // 0: the whole row is staged in LDS; else streamed in chunks
 };
 
 struct LocalLayout {
@@ -44,14 +45,22 @@ __host__ __device__ inline int mb_bytes(int n, int nthreads) {
   return seg * nthreads;
 }
 
+// Tokens staged ahead of a streamed chunk: the pattern length rounded up
+// to a whole 16-byte word.
+__host__ __device__ inline int stream_halo(int P) { return (P + 3) & ~3; }
+
+// chunk == 0: the row (S tokens) and its match lengths live in LDS.
+// chunk > 0: LDS holds one chunk of positions, its match lengths and the
+// stream_halo(P) tokens before it.
 __host__ __device__ inline LocalLayout local_layout(int S, int P, int C,
-                                                    int R, int K,
-                                                    int nwaves) {
+                                                    int R, int K, int nwaves,
+                                                    int chunk = 0) {
   const int nthreads = nwaves * kWave;
+  const int span = chunk > 0 ? chunk : S;
   LocalLayout L;
   int off = 0;
-  L.row = lds_take(off, S * 4);
-  L.mb = lds_take(off, mb_bytes(S, nthreads));
+  L.row = lds_take(off, (chunk > 0 ? chunk + stream_halo(P) : S) * 4);
+  L.mb = lds_take(off, mb_bytes(span, nthreads));
   L.pat = lds_take(off, P * 4);
   L.hist = lds_take(off, (P + 1) * 4);
   L.cand = lds_take(off, C * 4);
@@ -70,6 +79,12 @@ __host__ __device__ inline LocalLayout local_layout(int S, int P, int C,
 
 constexpr int kLocalThreads = 512;
 
+// kStream: the row stays in HBM.  match_back is computed over chunks of
+// a.chunk positions staged through LDS, once to histogram the match
+// lengths and once more, in order, to compact the first R ends per
+// candidate with the counts carried from chunk to chunk (stopping once
+// every candidate holds R); the expansion reads continuations from HBM.
+template <bool kStream>
 __device__ __forceinline__ void local_body(const LocalArgs& a,
                                            unsigned char* smem, int b) {
   constexpr int NT = kLocalThreads;
@@ -83,8 +98,8 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
   const int C = p.num_thresholds;
   const int R = p.max_occurrences;
   const int K = p.k;
-  const LocalLayout L = local_layout(S, P, C, R, K, NW);
-  int32_t* row = (int32_t*)(smem + L.row);
+  const LocalLayout L = local_layout(S, P, C, R, K, NW, kStream ? a.chunk : 0);
+  int32_t* row = (int32_t*)(smem + L.row);  // the row, or a staged chunk
   uint8_t* mbuf = (uint8_t*)(smem + L.mb);
   int32_t* pat = (int32_t*)(smem + L.pat);
   int32_t* hist = (int32_t*)(smem + L.hist);
@@ -104,21 +119,24 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
 
   // Stage the row, then apply this step's scatter (proposer.py:162-184).
   int32_t* grow = a.bt.tokens + (int64_t)b * S;
-  if ((S & 3) == 0 && (((uintptr_t)grow) & 15) == 0) {
-    const int4* src = reinterpret_cast<const int4*>(grow);
-    int4* dst = reinterpret_cast<int4*>(row);
-    for (int i = tid; i < S / 4; i += NT) dst[i] = src[i];
-  } else {
-    for (int i = tid; i < S; i += NT) row[i] = grow[i];
+  const bool vec4 = (S & 3) == 0 && (((uintptr_t)grow) & 15) == 0;
+  if (!kStream) {
+    if (vec4) {
+      const int4* src = reinterpret_cast<const int4*>(grow);
+      int4* dst = reinterpret_cast<int4*>(row);
+      for (int i = tid; i < S / 4; i += NT) dst[i] = src[i];
+    } else {
+      for (int i = tid; i < S; i += NT) row[i] = grow[i];
+    }
+    __syncthreads();
   }
-  __syncthreads();
   if (a.bt.sampled) {
     const int32_t* sp = a.bt.sampled + (int64_t)b * a.bt.num_sampled;
     for (int64_t j = tid; j < a.bt.num_sampled; j += NT) {
       const int64_t pos = st.base + j;
       const int32_t v = sp[j];
       if (j < st.cnt && v != -1 && pos < S && pos >= 0) {
-        row[pos] = v;
+        if (!kStream) row[pos] = v;
         grow[pos] = v;
       }
     }
@@ -134,28 +152,72 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
 
   SFX_TRACE_POINT(1);
   // Newest-first pattern, -2 fill (local_matcher.py:103-112).
+  const int32_t* src_row = kStream ? grow : row;
   for (int t = tid; t < P; t += NT) {
     const int64_t idx = q - 1 - t;
-    pat[t] = idx >= 0 ? row[idx < S - 1 ? idx : S - 1] : -2;
+    pat[t] = idx >= 0 ? src_row[idx < S - 1 ? idx : S - 1] : -2;
   }
   for (int i = tid; i <= P; i += NT) hist[i] = 0;
   __syncthreads();
 
-  // match_back, zero at i >= q (local_matcher.py:114-132).
-  for (int i = tid; i < S; i += NT) {
-    int m = 0;
-    if ((int64_t)i < q) {
-      for (int t = 0; t < P; ++t) {
-        const int j = i - 1 - t;
-        const int32_t x = j >= 0 ? row[j] : -1;
-        if (x != pat[t]) break;
-        ++m;
+  // Streamed rows: positions 0 .. qe - 1 can match (mb is zero from q on);
+  // chunk [c0, cend) stages x(c0 - halo) .. x(cend - 2), -1 before the row.
+  const int CH = kStream ? a.chunk : S;
+  const int halo = kStream ? stream_halo(P) : 0;
+  const int qe = (int)(q < 0 ? 0 : (q < S ? q : S));
+  auto stage_chunk = [&](int c0, int cend) {
+    const int j0 = c0 - halo;
+    const int nw = (cend - 1 - j0 + 3) / 4;
+    for (int k = tid; k < nw; k += NT) {
+      const int j = j0 + 4 * k;
+      int4 v;
+      if (vec4 && j >= 0 && j + 3 < S) {
+        v = reinterpret_cast<const int4*>(grow)[j >> 2];
+      } else {
+        v.x = j < 0 ? -1 : (j < S ? grow[j] : 0);
+        v.y = j + 1 < 0 ? -1 : (j + 1 < S ? grow[j + 1] : 0);
+        v.z = j + 2 < 0 ? -1 : (j + 2 < S ? grow[j + 2] : 0);
+        v.w = j + 3 < 0 ? -1 : (j + 3 < S ? grow[j + 3] : 0);
       }
+      reinterpret_cast<int4*>(row)[k] = v;
     }
-    mbuf[i] = (uint8_t)m;
-    if (m > 0) atomicAdd(&hist[m], 1);
+  };
+  // match_back of positions c0 .. cend - 1 from the staged chunk.
+  auto chunk_match = [&](int c0, int cend, bool count) {
+    for (int i = c0 + tid; i < cend; i += NT) {
+      const int k = i - 1 - (c0 - halo);  // row index of x(i - 1)
+      int m = 0;
+      while (m < P && row[k - m] == pat[m]) ++m;
+      mbuf[i - c0] = (uint8_t)m;
+      if (count && m > 0) atomicAdd(&hist[m], 1);
+    }
+  };
+
+  // match_back, zero at i >= q (local_matcher.py:114-132).
+  if (kStream) {
+    for (int c0 = 0; c0 < qe; c0 += CH) {
+      const int cend = c0 + CH < qe ? c0 + CH : qe;
+      stage_chunk(c0, cend);
+      __syncthreads();
+      chunk_match(c0, cend, true);
+      __syncthreads();
+    }
+  } else {
+    for (int i = tid; i < S; i += NT) {
+      int m = 0;
+      if ((int64_t)i < q) {
+        for (int t = 0; t < P; ++t) {
+          const int j = i - 1 - t;
+          const int32_t x = j >= 0 ? row[j] : -1;
+          if (x != pat[t]) break;
+          ++m;
+        }
+      }
+      mbuf[i] = (uint8_t)m;
+      if (m > 0) atomicAdd(&hist[m], 1);
+    }
+    __syncthreads();
   }
-  __syncthreads();
 
   SFX_TRACE_POINT(2);
   // Candidates: thr-th largest match_back = largest L with #{mb >= L} >=
@@ -204,10 +266,33 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
   SFX_TRACE_POINT(3);
   // First R ascending ends per candidate (triton_kernels.py:217-243
   // semantics): one ordered pass per group of 8 candidates.
-  for (int g0 = 0; g0 < C; g0 += 8)
-    compact_first_r<NT>(mbuf, S, cand + g0, min(8, C - g0), R, occ + g0 * R,
-                        0, found + g0, scan);
-  __syncthreads();
+  if (!kStream) {
+    for (int g0 = 0; g0 < C; g0 += 8)
+      compact_first_r<NT>(mbuf, S, cand + g0, min(8, C - g0), R,
+                          occ + g0 * R, 0, found + g0, scan);
+    __syncthreads();
+  } else {
+    // Chunks in ascending order; a single chunk's match lengths are still
+    // in LDS from the histogram pass.
+    for (int c = tid; c < C; c += NT) found[c] = 0;
+    __syncthreads();
+    for (int c0 = 0; c0 < qe; c0 += CH) {
+      const int cend = c0 + CH < qe ? c0 + CH : qe;
+      if (qe > CH) {
+        stage_chunk(c0, cend);
+        __syncthreads();
+        chunk_match(c0, cend, false);
+        __syncthreads();
+      }
+      for (int g0 = 0; g0 < C; g0 += 8)
+        compact_first_r<NT, true>(mbuf, cend - c0, cand + g0, min(8, C - g0),
+                                  R, occ + g0 * R, c0, found + g0, scan);
+      __syncthreads();
+      bool open = false;
+      for (int c = 0; c < C; ++c) open |= cand[c] > 0 && found[c] < R;
+      if (!open) break;
+    }
+  }
 
   SFX_TRACE_POINT(4);
   if (a.mode == kLocalGather) {
@@ -225,7 +310,7 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
         int32_t v = -1;
         if (r < min(found[c], R)) {
           const int64_t idx = (int64_t)occ[c * R + r] + j;
-          if (idx < q) v = row[idx < S - 1 ? idx : S - 1];
+          if (idx < q) v = src_row[idx < S - 1 ? idx : S - 1];
         }
         out[e] = v;
       }
@@ -233,7 +318,8 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
     return;
   }
 
-  // One wave per candidate: majority-vote expansion from the LDS row.
+  // One wave per candidate: majority-vote expansion from the LDS row (HBM
+  // when streamed).
   for (int c = wv; c < C; c += NW) {
     const int cv = cand[c];
     const int64_t oc = cv > 0 ? (int64_t)min(found[c], R) : 0;
@@ -241,7 +327,7 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
     const int32_t* oc_list = occ + c * R;
     auto cont_at = [&](int r, int d) -> int32_t {
       const int64_t idx = (int64_t)oc_list[r] + d;
-      return idx < q ? row[idx < S - 1 ? idx : S - 1] : -1;
+      return idx < q ? src_row[idx < S - 1 ? idx : S - 1] : -1;
     };
     const ExpandResult er = expand_wave<false>(
         cont_at, NoWeight(), R, oc, K, cap, p.min_token_prob, p.alpha,

@@ -503,9 +503,11 @@ __device__ __forceinline__ uint4 clear_from(uint4 q, int r) {
 // counts bytes >= thr four at a time (all-zero words skipped), one block
 // scan gives each thread its output offsets, then it writes its hits
 // below R.  out[c * R + slot] = out_base + position; count[c] =
-// min(hits, R).  thr, out and count may be LDS or global.  All threads of
-// the block must call it.
-template <int NT, typename MbPtr>
+// min(hits, R).  With kAcc the call continues an earlier one over the
+// preceding positions: count[c] holds the hits kept so far, new hits take
+// the slots after them and count[c] = min(count[c] + hits, R).  thr, out
+// and count may be LDS or global.  All threads of the block must call it.
+template <int NT, bool kAcc = false, typename MbPtr>
 __device__ __forceinline__ void compact_first_r(MbPtr mb, int64_t n,
                                                 const int* thr, int nthr,
                                                 int R, int32_t* out,
@@ -516,8 +518,12 @@ __device__ __forceinline__ void compact_first_r(MbPtr mb, int64_t n,
   const int64_t beg = (int64_t)threadIdx.x * seg;
   const int64_t end = beg + seg < n ? beg + seg : n;
   ByteGe ge[8];
+  uint32_t kept[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-  for (int c = 0; c < 8; ++c) ge[c] = byte_ge_init(c < nthr ? thr[c] : 0);
+  for (int c = 0; c < 8; ++c) {
+    if (kAcc && c < nthr) kept[c] = (uint32_t)count[c];
+    ge[c] = byte_ge_init(c < nthr && kept[c] < (uint32_t)R ? thr[c] : 0);
+  }
   uint32_t cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   for (int64_t i0 = beg; i0 < end; i0 += 16) {
     uint4 q = *reinterpret_cast<const uint4*>(mb + i0);
@@ -535,6 +541,11 @@ __device__ __forceinline__ void compact_first_r(MbPtr mb, int64_t n,
   SFX_TRACE_POINT(7);
   block_exscan8<NT>(cnt, off, tot, scratch);
   SFX_TRACE_POINT(8);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    off[c] += kept[c];
+    tot[c] += kept[c];
+  }
   bool more = false;
 #pragma unroll
   for (int c = 0; c < 8; ++c) more |= ge[c].on && off[c] < (uint32_t)R;

@@ -24,17 +24,18 @@ struct StepArgs {
   int global_on;
 };
 
+template <bool kStream>
 __global__ __launch_bounds__(kGlobalThreads) void k_step(StepArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   if (!a.global_on) {
-    local_body(a.l, smem, blockIdx.x);
+    local_body<kStream>(a.l, smem, blockIdx.x);
     return;
   }
   const int per = 2 + a.g.dparts;
   const int b = (int)(blockIdx.x / per);
   const int role = (int)(blockIdx.x % per);  // 0: SA, 1..dparts: delta
   if (role == per - 1)
-    local_body(a.l, smem, b);
+    local_body<kStream>(a.l, smem, b);
   else
     global_body(a.g, smem, b, role);
 }
@@ -69,6 +70,7 @@ extern "C" int sfx_propose_step(const sfx_params* p, const sfx_index* ix,
   a.l.draft = draft;
   a.l.num_valid = num_valid;
   a.l.new_counts = new_counts;
+  a.l.chunk = local_chunk(*p, bt->seq);
   size_t lds = local_lds_bytes(*p, bt->seq);
   if (global_on) {
     rc = check_global(*p, *ix, bt->batch);
@@ -94,12 +96,19 @@ extern "C" int sfx_propose_step(const sfx_params* p, const sfx_index* ix,
   }
   if (lds > kMaxLds) return SFX_EINVAL;
   if (bt->batch == 0) return 0;
-  static std::atomic<uint64_t> lds_opt{0};
-  allow_max_lds((const void*)k_step, lds_opt);
   const unsigned blocks =
       (unsigned)(bt->batch * (global_on ? 2 + a.g.dparts : 1));
   lds = one_per_cu_lds(lds, blocks);
-  hipLaunchKernelGGL(k_step, dim3(blocks), dim3(kGlobalThreads), lds, stream,
-                     a);
+  if (a.l.chunk == 0) {
+    static std::atomic<uint64_t> lds_opt{0};
+    allow_max_lds((const void*)k_step<false>, lds_opt);
+    hipLaunchKernelGGL(k_step<false>, dim3(blocks), dim3(kGlobalThreads), lds,
+                       stream, a);
+  } else {
+    static std::atomic<uint64_t> lds_opt{0};
+    allow_max_lds((const void*)k_step<true>, lds_opt);
+    hipLaunchKernelGGL(k_step<true>, dim3(blocks), dim3(kGlobalThreads), lds,
+                       stream, a);
+  }
   return (int)hipGetLastError();
 }

@@ -265,3 +265,37 @@ def test_ingest_then_cross_request_draft(gpu):
                           torch.ones(1, dtype=torch.bool, device=gpu))
     n = int(nv[0])
     assert n > 0 and N(draft)[0, :n].tolist() == (phrase[6:] + phrase)[:n]
+
+
+@pytest.mark.parametrize("enable_global", [False, True])
+def test_step_long_rows_vs_oracle(gpu, enable_global):
+    """Rows of 40000 tokens (streamed local role) in the fused step, with
+    and without the global index: rows are windows of the document stream
+    at committed lengths around the 16384-position chunk boundaries."""
+    from suffixgpu_amd import SuffixGPUDrafter
+    s, t = 40000, 17
+    w, d, o = _global_pair(gpu, seed=9, b=4, s=2048)
+    if not enable_global:
+        kw = dict(GLOBAL_KW, enable_global=False)
+        d, o = SuffixGPUDrafter(device=gpu, **kw), DrafterOracle(**kw)
+    stream = np.concatenate(w.active_docs + w.delta_docs).astype(I32)
+    rng = np.random.default_rng(9)
+    q_list = [0, 3, 16384, 16385, 20000, 39990, s - t, s]
+    b = len(q_list)
+    rows = np.zeros((b, s), dtype=I32)
+    sampled = np.full((b, t), -1, dtype=I32)
+    for i, q in enumerate(q_list):
+        off = int(rng.integers(0, stream.shape[0] - s - t))
+        rows[i] = stream[off:off + s]
+        acc = int(rng.integers(0, t + 1))
+        sampled[i, :acc] = stream[off + q:off + q + acc][:acc]
+    nt = np.array(q_list, dtype=I32)
+    tg = T(rows, gpu)
+    draft, nv, new = d.propose_with_update(T(nt, gpu), tg, T(sampled, gpu))
+    to = rows.copy()
+    ed, env, enew = o.propose_with_update(nt, to, sampled)
+    np.testing.assert_array_equal(N(tg), to)
+    np.testing.assert_array_equal(N(new), enew)
+    np.testing.assert_array_equal(N(draft), ed)
+    np.testing.assert_array_equal(N(nv), env)
+    assert (env > 0).sum() > 0

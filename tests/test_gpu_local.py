@@ -130,3 +130,54 @@ def test_local_drafter_propose_matches_oracle(gpu):
     ed, env = o.propose(enew, to)
     np.testing.assert_array_equal(N(draft), ed)
     np.testing.assert_array_equal(N(nv), env)
+
+
+def _long_rows(seed, s, vocab, q_list, p):
+    """Rows longer than fit in LDS.  Suffixes of each row's last p tokens
+    are planted so that match ends fall on both sides of the 16384- and
+    8192-position chunk boundaries and at the first position, with varied
+    match lengths."""
+    rng = np.random.default_rng(seed)
+    b = len(q_list)
+    tok = rng.integers(0, vocab, size=(b, s)).astype(I32)
+    nt = np.array(q_list, dtype=np.int64)
+    for i in range(b):
+        q = int(min(nt[i], s))
+        if q < 4 * p:
+            continue
+        tail = tok[i, q - p:q].copy()
+        for j, end in enumerate((p, 8192, 8193, 16384, 16385, 16384 + p // 2,
+                                 24575, 32768 - 3, 32768 + 1, q - p - 1)):
+            ln = (p, p // 2, 3, p - 1)[j % 4]
+            if ln <= end <= q - p:
+                tok[i, end - ln:end] = tail[p - ln:]
+    return tok, nt
+
+
+@pytest.mark.parametrize("vocab", [3, 1000])
+@pytest.mark.parametrize("s", [40000, 70001])
+def test_local_long_rows_streamed(gpu, vocab, s):
+    """Rows of 40K-70K tokens take the streamed path (chunks of 16384
+    positions): committed lengths of 0, 1, inside the first chunk, on and
+    just past a chunk boundary, full and past the buffer."""
+    q_list = [0, 1, 5000, 16384, 16385, 16400, 32769, s, s + 7]
+    tok, nt = _long_rows(vocab * 7 + s, s, vocab, q_list, 32)
+    mask = np.ones(len(q_list), bool)
+    mask[2] = False
+    g, o = _pair(gpu, k=16, max_pattern_len=32, max_occurrences=128,
+                 max_spec_factor=2.0, min_token_prob=0.1,
+                 support_thresholds=backoff_thresholds(8))
+    _check(gpu, g, o, nt, tok, mask)
+
+
+def test_local_long_rows_small_chunks(gpu):
+    """k = 2048 with eight thresholds leaves room for 8192-position chunks
+    only: a 20000-token row is streamed in three chunks (five at
+    S = 40000)."""
+    for s in (20000, 40000):
+        q_list = [8191, 8192, 8193, 12000, s]
+        tok, nt = _long_rows(s, s, 50, q_list, 24)
+        g, o = _pair(gpu, k=2048, max_pattern_len=24, max_occurrences=64,
+                     max_spec_factor=None, min_token_prob=0.0,
+                     support_thresholds=(1, 2, 3, 5, 8, 16, 64, 1000))
+        _check(gpu, g, o, nt, tok, np.ones(len(q_list), bool))
