@@ -31,7 +31,7 @@ extern "C" {
 
 #define SFX_EINVAL (-1)
 #define SFX_MAX_CANDIDATES 32
-#define SFX_ABI_VERSION 5
+#define SFX_ABI_VERSION 6
 
 /* Drafter configuration shared by the local and global paths.
  * Mirrors the constructor arguments of SuffixGPUDrafter
@@ -238,6 +238,33 @@ int sfx_index_swap(int32_t* corpus, int32_t* sa, int32_t* sa_key,
                    const int32_t* new_corpus, const int32_t* new_sa,
                    const int32_t* new_sa_key, int64_t capacity,
                    int64_t key_width, hipStream_t stream);
+
+/* ---- delta writes (global_index.py:86-133, 192-199) ------------------- */
+
+/* One document to append: n tokens from src (device) to delta[dst ..
+ * dst + n), followed by SEP (-2) at delta[dst + n]. */
+typedef struct sfx_append_doc {
+  const int32_t* src;
+  int64_t n;
+  int64_t dst;
+} sfx_append_doc;
+
+#define SFX_APPEND_MAX_DOCS 64
+
+/* global_index.py:86-106 append_documents, the device side of it: the
+ * host decides truncation, room and destinations, then appends any number
+ * of documents (host array `docs`, one launch per SFX_APPEND_MAX_DOCS) and
+ * sets *delta_len = new_len (device int64; skipped when NULL).  Every
+ * document must end at or before delta_capacity - 1. */
+int sfx_delta_append(const sfx_append_doc* docs, int32_t ndocs,
+                     int32_t* delta, int64_t delta_capacity,
+                     int64_t* delta_len, int64_t new_len, hipStream_t stream);
+
+/* global_index.py:128-133, 194-199: drop the oldest delta documents or the
+ * snapshot absorbed by a rebuild -- delta[0 .. n) = delta[from ..
+ * from + n) in place -- and set *delta_len = n (skipped when NULL). */
+int sfx_delta_shift(int32_t* delta, int64_t delta_capacity, int64_t from,
+                    int64_t n, int64_t* delta_len, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsuffixgpu_amd.so"
 MAX_CANDIDATES = 32
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -61,6 +61,12 @@ class SfxGlobalOut(ctypes.Structure):
         "draft_score")]
 
 
+class SfxAppendDoc(ctypes.Structure):
+    _fields_ = [("src", c_p), ("n", c_i64), ("dst", c_i64)]
+
+
+APPEND_MAX_DOCS = 64
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "sfx_abi_version": (c_i32, []),
@@ -73,6 +79,9 @@ SIGNATURES = {
                                     ctypes.c_size_t, c_p]),
     "sfx_index_swap": (c_i32, [c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64,
                                c_p]),
+    "sfx_delta_append": (c_i32, [ctypes.POINTER(SfxAppendDoc), c_i32, c_p,
+                                 c_i64, c_p, c_i64, c_p]),
+    "sfx_delta_shift": (c_i32, [c_p, c_i64, c_i64, c_i64, c_p, c_p]),
     "sfx_scatter_append": (c_i32, [ctypes.POINTER(SfxBatch), c_p, c_p]),
     "sfx_match_back": (c_i32, [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p,
                                c_p]),

@@ -38,7 +38,7 @@ int mb_lds_bytes(const sfx_index& ix, int parts) {
 }
 
 int merge_waves_for(const sfx_params& p, const sfx_index& ix, int parts,
-                    size_t* lds) {
+                    size_t* lds, size_t cap) {
   const int NW = kGlobalThreads / kWave;
   const int C = p.num_caps;
   int nmw = C < NW ? C : NW;
@@ -47,7 +47,7 @@ int merge_waves_for(const sfx_params& p, const sfx_index& ix, int parts,
     const GlobalLayout L = global_layout(p.max_pattern_len, C,
                                          p.max_occurrences, p.k, nmw,
                                          mb_lds_bytes(ix, parts));
-    if ((size_t)L.total <= kMaxLds) {
+    if ((size_t)L.total <= cap) {
       *lds = (size_t)L.total;
       return nmw;
     }

@@ -60,14 +60,19 @@ constexpr int64_t kMaxSeq = int64_t(1) << 30;
 constexpr int kMaxStreamChunk = 16384;
 constexpr int kMinStreamChunk = 1024;
 
+// Two workgroups of a kernel share a CU when each takes at most this much
+// LDS (the step kernels' register use allows two 512-thread groups per CU).
+constexpr size_t kHalfLds = kMaxLds / 2;
+
 int check_local(const sfx_params& p, const sfx_batch& bt);
-// 0: whole row in LDS; > 0: streamed chunk length; -1: nothing fits.
-int local_chunk(const sfx_params& p, int64_t S);
-size_t local_lds_bytes(const sfx_params& p, int64_t S);
+// Local layout within `cap` bytes of LDS: 0 = whole row, > 0 = streamed
+// chunk length, -1 = nothing fits.
+int local_chunk(const sfx_params& p, int64_t S, size_t cap = kMaxLds);
+size_t local_lds_bytes(const sfx_params& p, int64_t S, int chunk);
 
 int check_global(const sfx_params& p, const sfx_index& ix, int64_t batch);
 int mb_lds_bytes(const sfx_index& ix, int parts);
 int merge_waves_for(const sfx_params& p, const sfx_index& ix, int parts,
-                    size_t* lds);
+                    size_t* lds, size_t cap = kMaxLds);
 
 }  // namespace sfx

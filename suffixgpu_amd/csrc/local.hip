@@ -32,15 +32,14 @@ static size_t layout_bytes(const sfx_params& p, int64_t S, int chunk) {
   return (size_t)L.total;
 }
 
-int local_chunk(const sfx_params& p, int64_t S) {
-  if (layout_bytes(p, S, 0) <= kMaxLds) return 0;
+int local_chunk(const sfx_params& p, int64_t S, size_t cap) {
+  if (layout_bytes(p, S, 0) <= cap) return 0;
   for (int chunk = kMaxStreamChunk; chunk >= kMinStreamChunk; chunk /= 2)
-    if (layout_bytes(p, S, chunk) <= kMaxLds) return chunk;
+    if (layout_bytes(p, S, chunk) <= cap) return chunk;
   return -1;
 }
 
-size_t local_lds_bytes(const sfx_params& p, int64_t S) {
-  const int chunk = local_chunk(p, S);
+size_t local_lds_bytes(const sfx_params& p, int64_t S, int chunk) {
   return chunk < 0 ? (size_t)-1 : layout_bytes(p, S, chunk);
 }
 
@@ -61,7 +60,7 @@ int check_local(const sfx_params& p, const sfx_batch& bt) {
 int launch_local(LocalArgs a, hipStream_t stream) {
   if (a.bt.batch == 0) return 0;
   a.chunk = local_chunk(a.p, a.bt.seq);
-  const size_t lds = local_lds_bytes(a.p, a.bt.seq);
+  const size_t lds = local_lds_bytes(a.p, a.bt.seq, a.chunk);
   if (a.chunk == 0) {
     static std::atomic<uint64_t> lds_opt{0};
     allow_max_lds((const void*)k_local<false>, lds_opt);

@@ -4,6 +4,8 @@
 // uses the same device building blocks; these entry points expose them one
 // at a time for the index-level API and for parity checks.
 
+#include <algorithm>
+
 #include "launch.h"
 #include "pick.h"
 #include "sa_search.h"
@@ -55,6 +57,56 @@ __global__ __launch_bounds__(256) void k_swap(CopySpan a, CopySpan b,
   copy_span(a, tid, nth);
   copy_span(b, tid, nth);
   copy_span(c, tid, nth);
+}
+
+// ------------------------------------------------------------ delta writes
+// Appends up to SFX_APPEND_MAX_DOCS documents: block (x, d) copies a
+// grid-stride share of document d, block (0, d) also writes its SEP and
+// block (0, 0) the new delta length.
+struct AppendDocs {
+  sfx_append_doc doc[SFX_APPEND_MAX_DOCS];
+};
+
+__global__ __launch_bounds__(256) void k_delta_append(AppendDocs docs,
+                                                      int32_t* delta,
+                                                      int64_t* delta_len,
+                                                      int64_t new_len) {
+  const sfx_append_doc& d = docs.doc[blockIdx.y];
+  int32_t* out = delta + d.dst;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t nth = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = tid; i < d.n; i += nth) out[i] = d.src[i];
+  if (tid == 0) out[d.n] = kSep;
+  if (tid == 0 && blockIdx.y == 0 && delta_len) *delta_len = new_len;
+}
+
+// delta[0 .. n) = delta[from .. from + n) in place (from > 0), by one
+// block in ascending windows: a window's sources are all read before the
+// barrier, and its writes only land on sources of outputs at or below the
+// window, which are read already.
+constexpr int kShiftThreads = 1024;
+constexpr int kShiftPer = 8;
+
+__global__ __launch_bounds__(kShiftThreads) void k_delta_shift(
+    int32_t* delta, int64_t from, int64_t n, int64_t* delta_len,
+    int64_t new_len) {
+  constexpr int64_t W = (int64_t)kShiftThreads * kShiftPer;
+  for (int64_t k = 0; k < n; k += W) {
+    int32_t v[kShiftPer];
+#pragma unroll
+    for (int u = 0; u < kShiftPer; ++u) {
+      const int64_t o = k + u * kShiftThreads + threadIdx.x;
+      v[u] = o < n ? delta[from + o] : 0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kShiftPer; ++u) {
+      const int64_t o = k + u * kShiftThreads + threadIdx.x;
+      if (o < n) delta[o] = v[u];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0 && delta_len) *delta_len = new_len;
 }
 
 // -------------------------------------------------------------- match_back
@@ -250,6 +302,53 @@ extern "C" int sfx_index_swap(int32_t* corpus, int32_t* sa, int32_t* sa_key,
                                                      : 0};
   // enough 256-thread blocks to keep every CU streaming
   hipLaunchKernelGGL(k_swap, dim3(2048), dim3(256), 0, stream, a, b, c);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sfx_delta_append(const sfx_append_doc* docs, int32_t ndocs,
+                                int32_t* delta, int64_t delta_capacity,
+                                int64_t* delta_len, int64_t new_len,
+                                hipStream_t stream) {
+  if (ndocs < 0 || delta_capacity < 0 || new_len < 0 ||
+      new_len > delta_capacity || (ndocs > 0 && (!docs || !delta)))
+    return SFX_EINVAL;
+  int64_t longest = 0;
+  for (int32_t i = 0; i < ndocs; ++i) {
+    const sfx_append_doc& d = docs[i];
+    if (d.n < 0 || d.dst < 0 || d.dst + d.n + 1 > delta_capacity ||
+        (d.n > 0 && !d.src))
+      return SFX_EINVAL;
+    longest = d.n > longest ? d.n : longest;
+  }
+  if (ndocs == 0) {
+    if (!delta_len) return 0;
+    hipLaunchKernelGGL(k_delta_shift, dim3(1), dim3(kShiftThreads), 0,
+                       stream, delta, (int64_t)0, (int64_t)0, delta_len,
+                       new_len);
+    return (int)hipGetLastError();
+  }
+  const unsigned bx = (unsigned)std::min<int64_t>(
+      std::max<int64_t>((longest + 1023) / 1024, 1), 64);
+  for (int32_t g = 0; g < ndocs; g += SFX_APPEND_MAX_DOCS) {
+    const int32_t cnt = std::min<int32_t>(ndocs - g, SFX_APPEND_MAX_DOCS);
+    AppendDocs a = {};
+    for (int32_t i = 0; i < cnt; ++i) a.doc[i] = docs[g + i];
+    hipLaunchKernelGGL(k_delta_append, dim3(bx, (unsigned)cnt), dim3(256), 0,
+                       stream, a, delta, delta_len, new_len);
+    const int rc = (int)hipGetLastError();
+    if (rc) return rc;
+  }
+  return 0;
+}
+
+extern "C" int sfx_delta_shift(int32_t* delta, int64_t delta_capacity,
+                               int64_t from, int64_t n, int64_t* delta_len,
+                               hipStream_t stream) {
+  if (!delta || from < 0 || n < 0 || from + n > delta_capacity)
+    return SFX_EINVAL;
+  if (from == 0 && !delta_len) return 0;
+  hipLaunchKernelGGL(k_delta_shift, dim3(1), dim3(kShiftThreads), 0, stream,
+                     delta, from, from > 0 ? n : 0, delta_len, n);
   return (int)hipGetLastError();
 }
 

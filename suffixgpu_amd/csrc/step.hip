@@ -70,8 +70,24 @@ extern "C" int sfx_propose_step(const sfx_params* p, const sfx_index* ix,
   a.l.draft = draft;
   a.l.num_valid = num_valid;
   a.l.new_counts = new_counts;
-  a.l.chunk = local_chunk(*p, bt->seq);
-  size_t lds = local_lds_bytes(*p, bt->seq);
+  const int dparts =
+      global_on ? delta_parts_for(bt->batch, ix->delta_capacity) : 0;
+  const unsigned blocks =
+      (unsigned)(bt->batch * (global_on ? 2 + dparts : 1));
+  // A grid larger than the CU count runs in waves of workgroups; when every
+  // role fits half a CU's LDS, two groups share each CU and the waves halve.
+  // Otherwise each role takes the LDS layout that suits it best.
+  size_t cap = kMaxLds;
+  if (blocks > (unsigned)device_cus()) {
+    size_t glds = 0;
+    const bool fits =
+        local_chunk(*p, bt->seq, kHalfLds) >= 0 &&
+        (!global_on ||
+         merge_waves_for(*p, *ix, dparts, &glds, kHalfLds) > 0);
+    if (fits) cap = kHalfLds;
+  }
+  a.l.chunk = local_chunk(*p, bt->seq, cap);
+  size_t lds = local_lds_bytes(*p, bt->seq, a.l.chunk);
   if (global_on) {
     rc = check_global(*p, *ix, bt->batch);
     if (rc) return rc;
@@ -89,15 +105,13 @@ extern "C" int sfx_propose_step(const sfx_params* p, const sfx_index* ix,
     a.g.num_valid = num_valid;
     a.g.ws = a.l.ws;
     size_t glds = 0;
-    a.g.dparts = delta_parts_for(bt->batch, ix->delta_capacity);
-    a.g.merge_waves = merge_waves_for(*p, *ix, a.g.dparts, &glds);
-    a.g.mb_lds = mb_lds_bytes(*ix, a.g.dparts);
+    a.g.dparts = dparts;
+    a.g.merge_waves = merge_waves_for(*p, *ix, dparts, &glds, cap);
+    a.g.mb_lds = mb_lds_bytes(*ix, dparts);
     lds = lds > glds ? lds : glds;
   }
   if (lds > kMaxLds) return SFX_EINVAL;
   if (bt->batch == 0) return 0;
-  const unsigned blocks =
-      (unsigned)(bt->batch * (global_on ? 2 + a.g.dparts : 1));
   lds = one_per_cu_lds(lds, blocks);
   if (a.l.chunk == 0) {
     static std::atomic<uint64_t> lds_opt{0};

@@ -12,8 +12,11 @@ their tensor identities.
 
 Host bookkeeping (document lengths, eviction and snapshot arithmetic) is
 plain Python exactly as in the reference; every device operation is a
-stream-ordered copy/fill or a libsuffixgpu_amd kernel.  Queries run the
-fused SA-search + delta-scan + merge kernel (csrc/global.hip).
+stream-ordered copy/fill or a libsuffixgpu_amd kernel.  Appends are
+batched: the documents between two room-making steps go to the delta in
+one launch (copies, separators and the device length), and delta
+compactions are one in-place launch.  Queries run the fused SA-search +
+delta-scan + merge kernel (csrc/global.hip).
 """
 
 from __future__ import annotations
@@ -114,8 +117,12 @@ class GlobalIndex:
     def append_documents(self, docs: list[torch.Tensor]) -> None:
         """Append token tensors to the delta, each followed by SEP_TOKEN.
 
-        Recorded doc lengths include the separator.
+        Recorded doc lengths include the separator.  The host takes every
+        per-document decision of the reference (truncation to the last
+        delta_capacity - 1 tokens, making room); the documents between two
+        room-making steps are written by one sfx_delta_append launch.
         """
+        pending: list[tuple[torch.Tensor, int, int]] = []
         for doc in docs:
             doc = doc.to(self.device).to(torch.int32).reshape(-1)
             n = doc.shape[0]
@@ -125,13 +132,37 @@ class GlobalIndex:
                 doc = doc[-(self.delta_capacity - 1):]
                 n = doc.shape[0]
             if self.delta_len + n + 1 > self.delta_capacity:
+                self._flush_appends(pending)
                 self._make_room(n + 1)
-            self.delta[self.delta_len:self.delta_len + n].copy_(doc)
-            self.delta[self.delta_len + n] = SEP_TOKEN
+            pending.append((doc.contiguous(), n, self.delta_len))
             self.delta_len += n + 1
-            self.delta_len_t.fill_(self.delta_len)
             self.delta_doc_lens.append(n + 1)
+        self._flush_appends(pending)
         self.maybe_rebuild()
+
+    def _flush_appends(self, pending: list) -> None:
+        """Write the pending (doc, n, dst) appends and the delta length."""
+        if not pending:
+            return
+        arr = (_lib.SfxAppendDoc * len(pending))(
+            *[_lib.SfxAppendDoc(d.data_ptr(), n, dst)
+              for d, n, dst in pending])
+        check(lib().sfx_delta_append(arr, len(pending), self.delta.data_ptr(),
+                                     self.delta_capacity,
+                                     self.delta_len_t.data_ptr(),
+                                     self.delta_len, stream_of(self.device)),
+              "delta append")
+        pending.clear()
+
+    def _shift_delta(self, start: int) -> None:
+        """Drop delta[:start]: the rest moves to the front in place and the
+        device length follows (one launch)."""
+        remaining = self.delta_len - start
+        check(lib().sfx_delta_shift(self.delta.data_ptr(),
+                                    self.delta_capacity, start, remaining,
+                                    self.delta_len_t.data_ptr(),
+                                    stream_of(self.device)), "delta shift")
+        self.delta_len = remaining
 
     def _make_room(self, needed: int) -> None:
         self.poll_rebuild()
@@ -151,11 +182,7 @@ class GlobalIndex:
                 break
             acc += ln
             dropped += 1
-        remaining = self.delta_len - acc
-        if remaining > 0:
-            self.delta[:remaining] = self.delta[acc:self.delta_len].clone()
-        self.delta_len = remaining
-        self.delta_len_t.fill_(remaining)
+        self._shift_delta(acc)
         self.delta_doc_lens = self.delta_doc_lens[dropped:]
 
     # ------------------------------------------------------------------
@@ -218,11 +245,7 @@ class GlobalIndex:
         # Staging owns a copy of the snapshot: compact it out of the delta
         # now so appends always see the full capacity.
         absorbed = self._count_docs_within(snap)
-        remaining = self.delta_len - snap
-        if remaining > 0:
-            self.delta[:remaining] = self.delta[snap:self.delta_len].clone()
-        self.delta_len = remaining
-        self.delta_len_t.fill_(remaining)
+        self._shift_delta(snap)
         self.delta_doc_lens = self.delta_doc_lens[absorbed:]
 
         # Real prefix plus one PAD sentinel column, so build-time suffix

@@ -221,6 +221,14 @@ class SuffixGPUDrafter:
     # ------------------------------------------------------------------
     def harvest_finished(self, row_indices: list[int], lengths: list[int],
                          token_ids_gpu: torch.Tensor) -> None:
+        """Append rows[:length] of finished requests to the global memory
+        (proposer.py:329-343).  row_indices and lengths may also be
+        tensors; a device tensor costs one device-to-host copy, since the
+        room-making and rebuild decisions are taken on the host."""
+        if isinstance(row_indices, torch.Tensor):
+            row_indices = row_indices.tolist()
+        if isinstance(lengths, torch.Tensor):
+            lengths = lengths.tolist()
         rows = [token_ids_gpu[r] for r in row_indices]
         self.harvest_rows(rows, lengths)
 

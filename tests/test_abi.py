@@ -83,6 +83,14 @@ def test_argument_errors_are_reported_before_any_launch():
     assert lib.sfx_sa_build(None, -1, 0, None, 0, None, 0, None) == -1
     assert lib.sfx_index_swap(None, None, None, None, None, None, -1, 0,
                               None) == -1
+    # a document that would end past the delta (its SEP at capacity)
+    docs = (_lib.SfxAppendDoc * 2)(_lib.SfxAppendDoc(1, 10, 0),
+                                   _lib.SfxAppendDoc(1, 10, 6))
+    assert lib.sfx_delta_append(docs, 2, 1, 16, None, 17, None) == -1
+    assert lib.sfx_delta_append(docs, 2, 1, 17, None, 18, None) == -1
+    assert lib.sfx_delta_append(docs, -1, 1, 17, None, 0, None) == -1
+    assert lib.sfx_delta_shift(1, 16, 8, 9, None, None) == -1
+    assert lib.sfx_delta_shift(None, 16, 1, 1, None, None) == -1
 
 
 STRUCT_PROBE = r"""
@@ -99,6 +107,8 @@ int main(void) {
   S(sfx_batch); F(sfx_batch, num_tokens_is64); F(sfx_batch, sampled);
   F(sfx_batch, valid_count_is64); F(sfx_batch, mask); F(sfx_batch, limit);
   S(sfx_global_out); F(sfx_global_out, draft_score);
+  S(sfx_append_doc); F(sfx_append_doc, n); F(sfx_append_doc, dst);
+  printf("SFX_APPEND_MAX_DOCS %d\n", SFX_APPEND_MAX_DOCS);
   return 0;
 }
 """
@@ -118,7 +128,9 @@ def test_struct_layouts_match_the_header(tmp_path):
                          text=True).stdout
     c = dict(line.rsplit(" ", 1) for line in out.strip().splitlines())
     mirrors = {"sfx_params": _lib.SfxParams, "sfx_index": _lib.SfxIndex,
-               "sfx_batch": _lib.SfxBatch, "sfx_global_out": _lib.SfxGlobalOut}
+               "sfx_batch": _lib.SfxBatch, "sfx_global_out": _lib.SfxGlobalOut,
+               "sfx_append_doc": _lib.SfxAppendDoc}
+    assert int(c.pop("SFX_APPEND_MAX_DOCS")) == _lib.APPEND_MAX_DOCS
     for key, val in c.items():
         if "." in key:
             t, f = key.split(".")

@@ -299,3 +299,22 @@ def test_step_long_rows_vs_oracle(gpu, enable_global):
     np.testing.assert_array_equal(N(draft), ed)
     np.testing.assert_array_equal(N(nv), env)
     assert (env > 0).sum() > 0
+
+
+@pytest.mark.parametrize("s", [8192, 16384])
+def test_step_dense_grid_vs_oracle(gpu, s):
+    """B=100 rows with global memory on make a grid of 300 workgroups,
+    more than the CUs: the step then sizes every role for two workgroups
+    per CU (at S=16384 the local role streams its row)."""
+    w, d, o = _global_pair(gpu, seed=11, b=100, s=s)
+    bt = w.batch
+    tg = T(bt.tokens, gpu)
+    draft, nv, new = d.propose_with_update(T(bt.num_tokens, gpu), tg,
+                                           T(bt.sampled, gpu))
+    to = bt.tokens.copy()
+    ed, env, enew = o.propose_with_update(bt.num_tokens, to, bt.sampled)
+    np.testing.assert_array_equal(N(tg), to)
+    np.testing.assert_array_equal(N(new), enew)
+    np.testing.assert_array_equal(N(draft), ed)
+    np.testing.assert_array_equal(N(nv), env)
+    assert (env > 0).sum() > 10

@@ -467,3 +467,42 @@ def test_save_restore_bit_exact(gpu, tmp_path):
     with pytest.raises(ValueError):
         GlobalIndex(capacity=4096, delta_capacity=600, k=6,
                     device=gpu).restore(path)
+
+
+def test_batched_appends_match_oracle(gpu):
+    """Harvests of many rows at once: runs of more than 64 documents (two
+    append launches), documents longer than the delta (kept tail), drops of
+    the oldest documents while a rebuild is in flight, compactions at
+    rebuild launch, and lengths given as a device tensor."""
+    from suffixgpu_amd import SuffixGPUDrafter
+    from oracle.drafter import DrafterOracle
+    rng = np.random.default_rng(21)
+    kw = dict(k=4, max_pattern_len=8, max_occurrences=8, num_backoff=3,
+              enable_global=True, global_capacity=20000, delta_capacity=3000,
+              rebuild_threshold=1500)
+    d = SuffixGPUDrafter(device=gpu, **kw)
+    o = DrafterOracle(**kw)
+    s = 4000
+    for rnd in range(6):
+        b = 70 if rnd % 2 == 0 else 9
+        tok = rng.integers(0, 7, size=(b, s)).astype(I32)
+        lengths = rng.integers(0, 60, size=b)
+        lengths[rng.integers(0, b)] = s        # longer than the delta
+        lengths[rng.integers(0, b)] = 0
+        rows = list(range(b))
+        if rnd == 3:
+            d.global_index._rebuild_event = _NeverDone()
+            d.global_index._pending = (d.global_index.active_len,
+                                       d.global_index.active_doc_lens)
+            o.global_index._rebuild_event = _NeverDone()
+            o.global_index._pending = (o.global_index.active_len,
+                                       o.global_index.active_doc_lens)
+        lens = T(lengths, gpu) if rnd % 3 == 1 else lengths.tolist()
+        d.harvest_finished(rows, lens, T(tok, gpu))
+        o.harvest_finished(rows, lengths.tolist(), tok)
+        gpu_state_equal(d.global_index, o.global_index)
+        assert int(d.global_index.delta_len_t.item()) == o.global_index.delta_len
+        if rnd == 3:
+            for gi in (d.global_index, o.global_index):
+                gi._rebuild_event = None
+                gi._pending = None

@@ -207,3 +207,52 @@ def test_expand_division_table(gpu):
                                          np.float32(alpha))
                         for v, n in rows], np.float32)
         np.testing.assert_array_equal(N(score), exp)
+
+
+@pytest.mark.parametrize("start,n", [(1, 39999), (100, 30000), (8191, 8192),
+                                     (20000, 20000), (0, 123), (5, 0)])
+def test_delta_shift_in_place(gpu, start, n):
+    """delta[:n] = delta[start:start + n] in place, overlapping windows
+    included, and the device length set to n; the rest is untouched."""
+    from suffixgpu_amd import _lib
+    rng = np.random.default_rng(start + n)
+    cap = 40000
+    host = rng.integers(0, 1 << 30, size=cap).astype(I32)
+    dl = torch.full((), -7, dtype=torch.int64, device=gpu)
+    d = torch.from_numpy(host).to(gpu)
+    rc = _lib.lib().sfx_delta_shift(d.data_ptr(), cap, start, n,
+                                    dl.data_ptr(),
+                                    torch.cuda.current_stream(gpu).cuda_stream)
+    assert rc == 0
+    want = host.copy()
+    want[:n] = host[start:start + n]
+    np.testing.assert_array_equal(d.cpu().numpy(), want)
+    assert int(dl.item()) == n
+
+
+def test_delta_append_groups(gpu):
+    """150 documents (three launches of at most 64) at host-chosen offsets,
+    a zero-length one among them; each followed by SEP, length set."""
+    from suffixgpu_amd import _lib
+    rng = np.random.default_rng(3)
+    cap = 30000
+    d = torch.full((cap,), 77, dtype=torch.int32, device=gpu)
+    dl = torch.zeros((), dtype=torch.int64, device=gpu)
+    want = np.full(cap, 77, dtype=I32)
+    srcs, descs, off = [], [], 0
+    for i in range(150):
+        n = 0 if i == 17 else int(rng.integers(1, 150))
+        x = rng.integers(0, 1000, size=n).astype(I32)
+        t = torch.from_numpy(x).to(gpu)
+        srcs.append(t)
+        descs.append(_lib.SfxAppendDoc(t.data_ptr(), n, off))
+        want[off:off + n] = x
+        want[off + n] = -2
+        off += n + 1
+    arr = (_lib.SfxAppendDoc * len(descs))(*descs)
+    rc = _lib.lib().sfx_delta_append(arr, len(descs), d.data_ptr(), cap,
+                                     dl.data_ptr(), off,
+                                     torch.cuda.current_stream(gpu).cuda_stream)
+    assert rc == 0
+    np.testing.assert_array_equal(d.cpu().numpy(), want)
+    assert int(dl.item()) == off
