@@ -472,6 +472,12 @@ def e2e_loop(dev, steps: int) -> dict:
     nt = torch.from_numpy(lp.num_tokens).to(dev)
     samp_all = torch.from_numpy(lp.sampled).to(dev)
     samp = samp_all[0].clone()
+    # New requests' rows arrive as an engine stages them: pinned host
+    # buffers copied without blocking the host.
+    fresh = {i: (torch.tensor(rows, dtype=torch.int64, device=dev),
+                 torch.from_numpy(new_rows).pin_memory(),
+                 torch.from_numpy(new_nt).pin_memory())
+             for i, (rows, _, new_rows, new_nt) in lp.harvests.items()}
     for _ in range(3):
         d.propose_with_update(nt, tok, samp)
     torch.cuda.synchronize()
@@ -498,13 +504,13 @@ def e2e_loop(dev, steps: int) -> dict:
         nv_log[i].copy_(out[1])
         hv = lp.harvests.get(i)
         if hv is not None:
-            rows, lengths, new_rows, new_nt = hv
+            rows, lengths, _, _ = hv
             had = gi._rebuild_event is not None
             d.harvest_finished(rows, lengths, tok)
             launches += int(not had and gi._rebuild_event is not None)
-            idx = torch.tensor(rows, dtype=torch.int64, device=dev)
-            tok[idx] = torch.from_numpy(new_rows).to(dev)
-            nt[idx] = torch.from_numpy(new_nt).to(dev)
+            idx, new_rows, new_nt = fresh[i]
+            tok.index_copy_(0, idx, new_rows.to(dev, non_blocking=True))
+            nt.index_copy_(0, idx, new_nt.to(dev, non_blocking=True))
         pending = gi._rebuild_event is not None
         d.poll()
         swaps += int(pending and gi._rebuild_event is None)

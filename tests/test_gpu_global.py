@@ -28,8 +28,19 @@ def N(t):
     return t.cpu().numpy()
 
 
+def key_arrays_equal(gi):
+    """Key rows are the suffixes' first 32 tokens by rank, -1 past the end
+    of the corpus."""
+    corpus, sa = N(gi.corpus), N(gi.sa).astype(np.int64)
+    n, kw = corpus.shape[0], 32
+    pos = sa[:, None] + np.arange(kw)[None, :]
+    want = np.where(pos < n, corpus[np.minimum(pos, n - 1)], -1)
+    np.testing.assert_array_equal(N(gi.sa_key).reshape(n, kw), want)
+
+
 def gpu_state_equal(gi, ref):
     """ref: oracle index or a dict of golden arrays."""
+    key_arrays_equal(gi)
     if isinstance(ref, dict):
         g = ref
         assert gi.active_len == int(g["active_len"])
@@ -506,3 +517,43 @@ def test_batched_appends_match_oracle(gpu):
             for gi in (d.global_index, o.global_index):
                 gi._rebuild_event = None
                 gi._pending = None
+
+
+@pytest.mark.parametrize("keys", [True, False])
+def test_patterns_longer_than_key_rows(gpu, keys):
+    """P = 48 on long-repeat text: interval searches that compare past the
+    32-token key rows (in the corpus), and the same queries on an index
+    passed without key rows (sa[] and corpus compares only)."""
+    from suffixgpu_amd import _lib
+    tc = synth.TemplateCorpus(seed=9, n_templates=6)
+    docs = [tc.sequence(lo=200, hi=900) for _ in range(30)]
+    dd = [tc.sequence(lo=64, hi=300) for _ in range(3)]
+    cap = sum(len(d) + 1 for d in docs) + 11
+    g, o = _load_pair(gpu, docs, dd, cap, 2048, 32, k=16)
+    if not keys:
+        full = g.index_struct()
+        g.index_struct = lambda: _lib.SfxIndex(
+            full.corpus, full.sa, full.capacity, full.delta,
+            full.delta_capacity, full.delta_len, None, 0)
+    rng = np.random.default_rng(10)
+    b, p = 40, 48
+    q = np.zeros((b, p), I32)
+    ql = np.zeros(b, np.int64)
+    for i in range(b):
+        src = docs[i % len(docs)]
+        n = int(rng.integers(1, p + 1))
+        st = int(rng.integers(0, len(src) - n + 1))
+        q[i, :n] = src[st:st + n]
+        ql[i] = n
+    caps = np.array([48, 24, 12, 6, 3, 2], np.int64)
+    tq, tl, tc_ = T(q, gpu), T(ql, gpu), T(caps, gpu)
+    got = g._query_backoff(tq, tl, p, tc_)
+    exp = o._query_backoff(q, ql, p, caps)
+    for a, e in zip(got, exp):
+        np.testing.assert_array_equal(N(a), e)
+    assert (exp[0] > 32).sum() > 5
+    for a, e in zip(g.draft(tq, tl, p, 16, min_token_prob=0.05,
+                            max_spec_factor=1.0, caps=tc_),
+                    o.draft(q, ql, p, 16, min_token_prob=0.05,
+                            max_spec_factor=1.0, caps=caps)):
+        np.testing.assert_array_equal(N(a), e)
