@@ -57,7 +57,8 @@ def parse():
     ap.add_argument("--e2e-steps", type=int, default=1000)
     ap.add_argument("--pmc-workload", action="store_true",
                     help="for rocprofv3 --pmc passes: a copy of known size, "
-                    "then a few step launches; prints no JSON")
+                    "a few step launches, then two SA rebuilds of the "
+                    "corpus as the index runs them; prints no JSON")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR",
                                                          "WRITE_DIR"),
                     help="turn two rocprofv3 --pmc outputs (FETCH_SIZE, "
@@ -334,6 +335,7 @@ def main() -> int:
         "sa_rebuild_hinted_ms": round(sa_reb_ms, 3),
         "sa_rebuild_hinted_rounds": sa_reb_rounds,
         "sa_rebuild_hinted_mtok_s": round(sa_m / (sa_reb_ms * 1e-3) / 1e6, 2),
+        "sa_rebuild_hbm": sa_rebuild_hbm(sa_reb_ms),
         "kernels_us": {"k_step": round(step_us, 3),
                        "k_local_alone": round(k_local_us, 3),
                        "k_global_alone": round(k_global_us, 3)},
@@ -351,6 +353,17 @@ def main() -> int:
 
 def _lib_pad() -> int:
     return 2 ** 31 - 1
+
+
+def sa_rebuild_hbm(rebuild_ms: float):
+    """HBM bytes of one background rebuild of the corpus (rocprofv3 PMC
+    summary) over its measured time, against the 8 TB/s peak."""
+    t = load_traffic("sa_rebuild")
+    if not t:
+        return None
+    gbps = t / (rebuild_ms * 1e-3) / 1e9
+    return {"traffic": t, "achieved_gbps": round(gbps, 1),
+            "peak_gbps": HBM_PEAK_GBPS, "frac": round(gbps / HBM_PEAK_GBPS, 4)}
 
 
 
@@ -555,6 +568,9 @@ def step_kernel_us(d, dev, tokens0, nt, sampled, reps):
 # and writes exactly 256 MiB each.
 PMC_COPY_ELEMS = 1 << 26
 PMC_STEP_LAUNCHES = 10
+PMC_SA_BUILDS = 2
+# kernels of one suffix-array build (csrc/sa_build.hip)
+SA_BUILD_KERNELS = ("k_sa_", "k_rs_", "k_grp_")
 
 
 def pmc_workload(d, w, dev) -> int:
@@ -574,8 +590,26 @@ def pmc_workload(d, w, dev) -> int:
     for _ in range(PMC_STEP_LAUNCHES):
         d.propose_with_update(nt, buf, sampled)
     torch.cuda.synchronize()
+    from suffixgpu_amd.suffix_array import (build_state,
+                                            build_suffix_array_rounds,
+                                            sa_workspace_bytes)
+    flat = np.concatenate([np.append(x, -2) for x in w.active_docs]).astype(
+        np.int32)
+    m = min(flat.shape[0] + 1, CAPACITY)
+    text = torch.full((CAPACITY,), _lib_pad(), dtype=torch.int32, device=dev)
+    text[:flat.shape[0]].copy_(torch.from_numpy(flat))
+    out = torch.empty(CAPACITY, dtype=torch.int32, device=dev)
+    ws = torch.empty(sa_workspace_bytes(CAPACITY), dtype=torch.uint8,
+                     device=dev)
+    build_suffix_array_rounds(text, m, out, ws, 40)
+    torch.cuda.synchronize()
+    final, needed = build_state(ws, m)
+    for _ in range(PMC_SA_BUILDS):
+        build_suffix_array_rounds(text, m, out, ws, needed + 2)
+    torch.cuda.synchronize()
     log(f"pmc workload done: 3 calibration copies of {PMC_COPY_ELEMS * 4} "
-        f"bytes, {PMC_STEP_LAUNCHES} step launches")
+        f"bytes, {PMC_STEP_LAUNCHES} step launches, {PMC_SA_BUILDS} SA "
+        f"rebuilds of m={m} ({needed + 2} rounds)")
     return 0
 
 
@@ -591,8 +625,11 @@ def _pmc_rows(out_dir: str, counter: str):
         with open(f, newline="") as fh:
             for r in csv.DictReader(fh):
                 if r.get("Counter_Name") == counter:
-                    rows.append((r["Kernel_Name"], float(r["Counter_Value"])))
-    return rows
+                    rows.append((int(r.get("Dispatch_Id", len(rows))),
+                                 r["Kernel_Name"],
+                                 float(r["Counter_Value"])))
+    rows.sort()
+    return [(k, v) for _, k, v in rows]
 
 
 def summarize_pmc(fetch_dir: str, write_dir: str) -> dict:
@@ -606,18 +643,31 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> dict:
         rows = _pmc_rows(d_, counter)
         cal = [v for k, v in rows if "bitwise_not" in k]
         step = [v for k, v in rows if "k_step" in k]
-        if not cal or not step:
-            raise SystemExit(f"{counter}: calibration or k_step dispatches "
-                             "missing")
+        # SA builds in dispatch order, each starting with k_sa_init; the
+        # last PMC_SA_BUILDS are the rebuilds as the index runs them
+        builds: list[list[float]] = []
+        for k, v in rows:
+            if "k_sa_init" in k:
+                builds.append([])
+            if builds and any(p in k for p in SA_BUILD_KERNELS):
+                builds[-1].append(v)
+        if not cal or not step or len(builds) < PMC_SA_BUILDS:
+            raise SystemExit(f"{counter}: calibration, k_step or SA build "
+                             "dispatches missing")
         cal_b = statistics.median(cal) * 1024.0
         scale = known / cal_b
         step_b = statistics.mean(step) * 1024.0
+        sa_b = statistics.mean(
+            sum(b) for b in builds[-PMC_SA_BUILDS:]) * 1024.0
         out[name] = {"counter": counter, "calibration_bytes": cal_b,
                      "scale": scale, "step_raw_bytes": step_b,
                      "step_bytes": step_b * scale,
-                     "dispatches": len(step)}
+                     "dispatches": len(step),
+                     "sa_build_bytes": sa_b * scale}
     total = out["fetch"]["step_bytes"] + out["write"]["step_bytes"]
-    return {"k_step": round(total), "detail": out}
+    sa_total = out["fetch"]["sa_build_bytes"] + out["write"]["sa_build_bytes"]
+    return {"k_step": round(total), "sa_rebuild": round(sa_total),
+            "detail": out}
 
 
 def kernel_timings(d, dev, tokens0, nt, sampled, reps):
