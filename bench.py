@@ -269,6 +269,10 @@ def main() -> int:
         f"us/step, drafting rows {(num_valid > 0).sum()}/{B}, "
         f"mean num_valid {num_valid.mean():.2f}")
 
+    adapter_p50 = adapter_step_p50(d, dev, bt, args.steps, args.warmup)
+    log(f"engine adapter step p50 {adapter_p50:.2f} us (step kernel + count "
+        "feedback, captured)")
+
     # ---- the step kernel launched directly (no graph) between HIP events
     # on its stream, then the local and global kernels launched alone.
     step_us = step_kernel_us(d, dev, tokens0, nt, sampled, args.kernel_reps)
@@ -343,6 +347,7 @@ def main() -> int:
         "copy_peak_gbps": round(copy_gbps, 1),
         "roofline_frac_of_copy_peak": round(achieved / copy_gbps, 6),
         "cold_cache_step_p50_us": round(cold_p50, 3),
+        "adapter_step_p50_us": round(adapter_p50, 3),
         "sa_rebuild_concurrent": conc,
         "e2e_decode_loop": e2e,
         "cpu_baseline": cpu,
@@ -353,6 +358,42 @@ def main() -> int:
 
 def _lib_pad() -> int:
     return 2 ** 31 - 1
+
+
+def adapter_step_p50(d, dev, bt, steps: int, warmup: int) -> float:
+    """The engine adapter's captured propose (the step plus the copy of the
+    new counts into its resident counts) on the same 64 rows: p50 of the
+    replays between an event pair; the counts are restored outside it."""
+    import torch
+    from suffixgpu_amd.adapter import SuffixProposerGPU
+    ad = SuffixProposerGPU(k=d.k, max_num_seqs=B, max_model_len=S,
+                           device=dev, drafter=d)
+    for i in range(B):
+        n = int(bt.num_tokens[i])
+        ad.add_request(i, bt.tokens[i, :n])
+    ad.tokens.copy_(torch.from_numpy(bt.tokens).to(dev))
+    counts0 = ad.num_tokens.clone()
+    samp = torch.from_numpy(bt.sampled).to(dev)
+    for _ in range(3):
+        ad.num_tokens.copy_(counts0)
+        ad.propose(samp)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ad.propose(samp)
+    cur = torch.cuda.current_stream(dev)
+    per = []
+    for i in range(warmup + steps):
+        ad.num_tokens.copy_(counts0)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(cur)
+        g.replay()
+        e1.record(cur)
+        if i >= warmup:
+            per.append((e0, e1))
+    torch.cuda.synchronize()
+    return statistics.median(a.elapsed_time(b) * 1e3 for a, b in per)
 
 
 def sa_rebuild_hbm(rebuild_ms: float):
