@@ -265,8 +265,8 @@ def _load_pair(gpu, docs, delta_docs, cap, dcap, r, k=16):
 
 @pytest.mark.parametrize("kind", ["periodic", "runs"])
 def test_sa_interval_search_long_repeats(gpu, kind):
-    """The key-row k-ary search (32-token rows, probes that skip the tokens
-    both range boundaries already match) on texts whose suffixes share long
+    """The key-row k-ary search (32-token rows, lower and upper bounds that
+    share probes until they split) on texts whose suffixes share long
     prefixes: wide intervals at every length, matches past the row."""
     from suffixgpu_amd.sa_search import suffix_match_backoff
     from oracle.sa import suffix_match_backoff as o_smb
