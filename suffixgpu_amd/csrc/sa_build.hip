@@ -1,9 +1,12 @@
 // Suffix-array construction on the GPU: prefix doubling over LSD radix
 // sorts of the still-unsorted suffixes only, with no host synchronisation.
 //
-// Round 0 sorts all positions by token (signed order, 4 passes of 9 bits).
-// Every later round h = 1, 2, 4, ... re-sorts only the suffixes whose
-// group still has more than one member, by the key
+// Round 0 sorts all positions by their first two tokens when the text's
+// tokens span fewer than 2^18 values (every LLM vocabulary; found on the
+// device, so the doubling then starts at h = 2), else by their first token
+// (signed order) -- 4 passes of 9 bits either way.  Every later round
+// h = h0, 2 h0, 4 h0, ... re-sorts only the suffixes whose group still has
+// more than one member, by the key
 // (group head, rank[i+h]+1 or 0) -- a proper prefix sorts first, as in
 // suffix_gpu/suffix_array.py:15-63 -- and writes them back into the SA
 // positions their groups occupy, in order.  rank[i] is the SA position of
@@ -44,7 +47,9 @@ struct SaWs {
   uint32_t* rowsum;  // [256] digit totals
   uint32_t* tcnt;    // [NB] active suffixes per tile
   uint32_t* blkmax;  // [NB] last group start per tile
-  uint32_t* state;   // [0] done, [1] active count, [2] h when done
+  uint32_t* state;   // [0] done, [1] active count, [2] round that found
+                     // none left, [3] / [4] least / largest token other
+                     // than PAD (INT32_MAX), [5] h of round 1
 };
 
 static size_t sa_ws_layout(int64_t n, void* base, SaWs* w) {
@@ -101,17 +106,76 @@ __device__ __forceinline__ uint32_t block_exscan1(uint32_t v, uint32_t* red,
   return before + inc - v;
 }
 
+__global__ __launch_bounds__(64) void k_sa_reset(uint32_t* state) {
+  if (threadIdx.x == 0) {
+    state[3] = (uint32_t)INT32_MAX;
+    state[4] = (uint32_t)INT32_MIN;
+  }
+}
+
+// Least and largest token of the text, PAD (INT32_MAX) left out.
+__global__ __launch_bounds__(256) void k_sa_range(const int32_t* text,
+                                                  int64_t n,
+                                                  uint32_t* state) {
+  __shared__ int32_t red[2][256 / kWave];
+  int32_t lo = INT32_MAX, hi = INT32_MIN;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int32_t t = text[i];
+    if (t != INT32_MAX) {
+      lo = t < lo ? t : lo;
+      hi = t > hi ? t : hi;
+    }
+  }
+  lo = ~wave_max_i32(~lo);  // ~ reverses the signed order, no overflow
+  hi = wave_max_i32(hi);
+  const int wv = threadIdx.x / kWave;
+  if (lane_id() == 0) {
+    red[0][wv] = lo;
+    red[1][wv] = hi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 256 / kWave; ++w) {
+      lo = red[0][w] < lo ? red[0][w] : lo;
+      hi = red[1][w] > hi ? red[1][w] : hi;
+    }
+    if (lo != INT32_MAX) atomicMin((int*)&state[3], lo);
+    if (hi != INT32_MIN) atomicMax((int*)&state[4], hi);
+  }
+}
+
+// Tokens of the pair keys: 1 + t - least, PAD after every other token, 0
+// past the end; pair keys need span + 2 < 2^kPairBits.
+constexpr int kPairBits = 18;
+
 __global__ __launch_bounds__(256) void k_sa_init(const int32_t* text,
                                                  int64_t n, uint64_t* key,
                                                  uint32_t* val, uint32_t* pos,
                                                  uint32_t* state) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int32_t tlo = (int32_t)state[3];
+  const int32_t thi = (int32_t)state[4];
+  // thi < tlo: the text is all PAD
+  const int64_t span = thi < tlo ? 0 : (int64_t)thi - (int64_t)tlo + 1;
+  const bool pairs = span + 2 < ((int64_t)1 << kPairBits);
   if (i == 0) {
     state[0] = 0;
     state[1] = (uint32_t)n;
+    state[5] = pairs ? 2u : 1u;
   }
   if (i >= n) return;
-  key[i] = (uint64_t)((uint32_t)text[i] ^ 0x80000000u);
+  if (pairs) {
+    auto code = [&](int64_t j) -> uint64_t {
+      if (j >= n) return 0;
+      const int32_t t = text[j];
+      return t == INT32_MAX ? (uint64_t)span + 1
+                            : (uint64_t)((int64_t)t - tlo + 1);
+    };
+    key[i] = (code(i) << kPairBits) | code(i + 1);
+  } else {
+    key[i] = (uint64_t)((uint32_t)text[i] ^ 0x80000000u);
+  }
   val[i] = (uint32_t)i;
   pos[i] = (uint32_t)i;
 }
@@ -413,16 +477,18 @@ __global__ __launch_bounds__(kSortThreads) void k_sa_mark(
 }
 
 // Active suffixes of the tile, in SA order, with their sort keys:
-// key = head * (m + 1) + (rank[i + h] + 1, or 0 past the end).
+// key = head * (m + 1) + (rank[i + h] + 1, or 0 past the end), where round
+// r doubles h = state[5] << (r - 1).
 // Each block sums the earlier tiles' counts for its output offset; block 0
 // also sums them all: that is the round's active count, and none left
 // means the array is final (the done flag).
 __global__ __launch_bounds__(kSortThreads) void k_sa_gather(
     const uint32_t* __restrict__ sa, const uint32_t* __restrict__ rank,
-    const uint32_t* __restrict__ grp, int64_t m, int64_t h, int64_t nb,
+    const uint32_t* __restrict__ grp, int64_t m, int round, int64_t nb,
     const uint32_t* __restrict__ tcnt, uint64_t* key, uint32_t* val,
     uint32_t* pos, uint32_t* state) {
   if (state[0]) return;
+  const int64_t h = (int64_t)state[5] << (round - 1);
   __shared__ uint32_t scnt[kSortWaves];
   __shared__ uint32_t ored[kSortWaves];
   {
@@ -436,7 +502,7 @@ __global__ __launch_bounds__(kSortThreads) void k_sa_gather(
         state[1] = tot;
         if (tot == 0) {
           state[0] = 1;
-          state[2] = (uint32_t)h;  // the first h whose round found none
+          state[2] = (uint32_t)round;  // the round that found none
         }
       }
       if (tot == 0) return;
@@ -591,12 +657,16 @@ int build_begin(const int32_t* text, int64_t m, void* workspace,
   sa_ws_layout(m, workspace, &w);
   const int64_t nb = (m + kTile - 1) / kTile;
   const unsigned eb = (unsigned)((m + 255) / 256);
+  hipLaunchKernelGGL(k_sa_reset, dim3(1), dim3(64), 0, stream, w.state);
+  hipLaunchKernelGGL(k_sa_range, dim3((unsigned)(nb < 1024 ? nb : 1024)),
+                     dim3(256), 0, stream, text, m, w.state);
   hipLaunchKernelGGL(k_sa_init, dim3(eb), dim3(256), 0, stream, text, m,
                      w.keyA, w.valA, w.pos, w.state);
-  return sort_and_rank(w, nb, 32, stream);
+  return sort_and_rank(w, nb, 2 * kPairBits, stream);
 }
 
-// Rounds first .. first + count - 1 (round r doubles h = 2^(r-1)).
+// Rounds first .. first + count - 1 (round r doubles h = h0 * 2^(r-1),
+// h0 = 1 or 2 as round 0 decided; with h0 = 2 the last round finds none).
 int build_rounds(int64_t m, int first, int count, void* workspace,
                  hipStream_t stream) {
   if (m <= 1) return 0;
@@ -607,11 +677,10 @@ int build_rounds(int64_t m, int first, int count, void* workspace,
   const int nbits = bits_for(maxkey);
   const int last = total_rounds(m);
   for (int r = first < 1 ? 1 : first; r < first + count && r <= last; ++r) {
-    const int64_t h = (int64_t)1 << (r - 1);
     hipLaunchKernelGGL(k_sa_mark, dim3((unsigned)nb), dim3(kSortThreads), 0,
                        stream, w.grp, m, w.tcnt, w.state);
     hipLaunchKernelGGL(k_sa_gather, dim3((unsigned)nb), dim3(kSortThreads), 0,
-                       stream, w.sa, w.rank, w.grp, m, h, nb, w.tcnt, w.keyA,
+                       stream, w.sa, w.rank, w.grp, m, r, nb, w.tcnt, w.keyA,
                        w.valA, w.pos, w.state);
     const int rc = sort_and_rank(w, nb, nbits, stream);
     if (rc) return rc;

@@ -324,9 +324,8 @@ class GlobalIndex:
         self._build_state = None
         flags = self._flag_host.tolist()
         if flags[0]:
-            h = max(int(flags[2]), 1)
-            # rounds used: the one that found the array final doubled h
-            self.sa_round_hint = max(1, h.bit_length() - 1) + 2
+            # flags[2]: the doubling round that found the array final
+            self.sa_round_hint = max(1, int(flags[2]) - 1) + 2
             return True
         L = lib()
         total = int(L.sfx_sa_build_rounds_total(m))

@@ -74,5 +74,5 @@ def build_state(workspace: torch.Tensor, m: int) -> tuple[bool, int]:
         return True, 0
     off = int(lib().sfx_sa_build_flag_offset(m))
     st = workspace[off:off + 16].view(torch.int32).cpu().tolist()
-    h = max(int(st[2]), 1)
-    return bool(st[0]), (h.bit_length() - 1 if st[0] else -1)
+    # st[2]: the doubling round that found no unsorted group left
+    return bool(st[0]), (max(int(st[2]) - 1, 0) if st[0] else -1)
