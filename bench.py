@@ -684,11 +684,11 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> dict:
         rows = _pmc_rows(d_, counter)
         cal = [v for k, v in rows if "bitwise_not" in k]
         step = [v for k, v in rows if "k_step" in k]
-        # SA builds in dispatch order, each starting with k_sa_init; the
+        # SA builds in dispatch order, each starting with k_sa_range; the
         # last PMC_SA_BUILDS are the rebuilds as the index runs them
         builds: list[list[float]] = []
         for k, v in rows:
-            if "k_sa_init" in k:
+            if "k_sa_range" in k:
                 builds.append([])
             if builds and any(p in k for p in SA_BUILD_KERNELS):
                 builds[-1].append(v)

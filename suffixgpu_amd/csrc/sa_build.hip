@@ -106,17 +106,29 @@ __device__ __forceinline__ uint32_t block_exscan1(uint32_t v, uint32_t* red,
   return before + inc - v;
 }
 
-__global__ __launch_bounds__(64) void k_sa_reset(uint32_t* state) {
-  if (threadIdx.x == 0) {
-    state[3] = (uint32_t)INT32_MAX;
-    state[4] = (uint32_t)INT32_MIN;
+// Block-wide least and largest of one int32 per thread (all threads).
+__device__ __forceinline__ void block_minmax(int32_t& lo, int32_t& hi,
+                                             int32_t (*red)[256 / kWave]) {
+  lo = ~wave_max_i32(~lo);  // ~ reverses the signed order, no overflow
+  hi = wave_max_i32(hi);
+  const int wv = threadIdx.x / kWave;
+  if (lane_id() == 0) {
+    red[0][wv] = lo;
+    red[1][wv] = hi;
+  }
+  __syncthreads();
+  for (int w = 0; w < 256 / kWave; ++w) {
+    lo = red[0][w] < lo ? red[0][w] : lo;
+    hi = red[1][w] > hi ? red[1][w] : hi;
   }
 }
 
-// Least and largest token of the text, PAD (INT32_MAX) left out.
+// Least and largest token of the text, PAD (INT32_MAX) left out, per
+// block (part_lo / part_hi, gridDim.x <= 256 entries each).
 __global__ __launch_bounds__(256) void k_sa_range(const int32_t* text,
                                                   int64_t n,
-                                                  uint32_t* state) {
+                                                  int32_t* part_lo,
+                                                  int32_t* part_hi) {
   __shared__ int32_t red[2][256 / kWave];
   int32_t lo = INT32_MAX, hi = INT32_MIN;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -127,21 +139,10 @@ __global__ __launch_bounds__(256) void k_sa_range(const int32_t* text,
       hi = t > hi ? t : hi;
     }
   }
-  lo = ~wave_max_i32(~lo);  // ~ reverses the signed order, no overflow
-  hi = wave_max_i32(hi);
-  const int wv = threadIdx.x / kWave;
-  if (lane_id() == 0) {
-    red[0][wv] = lo;
-    red[1][wv] = hi;
-  }
-  __syncthreads();
+  block_minmax(lo, hi, red);
   if (threadIdx.x == 0) {
-    for (int w = 1; w < 256 / kWave; ++w) {
-      lo = red[0][w] < lo ? red[0][w] : lo;
-      hi = red[1][w] > hi ? red[1][w] : hi;
-    }
-    if (lo != INT32_MAX) atomicMin((int*)&state[3], lo);
-    if (hi != INT32_MIN) atomicMax((int*)&state[4], hi);
+    part_lo[blockIdx.x] = lo;
+    part_hi[blockIdx.x] = hi;
   }
 }
 
@@ -152,16 +153,23 @@ constexpr int kPairBits = 18;
 __global__ __launch_bounds__(256) void k_sa_init(const int32_t* text,
                                                  int64_t n, uint64_t* key,
                                                  uint32_t* val, uint32_t* pos,
+                                                 const int32_t* part_lo,
+                                                 const int32_t* part_hi,
+                                                 int nparts,
                                                  uint32_t* state) {
+  __shared__ int32_t red[2][256 / kWave];
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int32_t tlo = (int32_t)state[3];
-  const int32_t thi = (int32_t)state[4];
+  int32_t tlo = (int)threadIdx.x < nparts ? part_lo[threadIdx.x] : INT32_MAX;
+  int32_t thi = (int)threadIdx.x < nparts ? part_hi[threadIdx.x] : INT32_MIN;
+  block_minmax(tlo, thi, red);
   // thi < tlo: the text is all PAD
   const int64_t span = thi < tlo ? 0 : (int64_t)thi - (int64_t)tlo + 1;
   const bool pairs = span + 2 < ((int64_t)1 << kPairBits);
   if (i == 0) {
     state[0] = 0;
     state[1] = (uint32_t)n;
+    state[3] = (uint32_t)tlo;
+    state[4] = (uint32_t)thi;
     state[5] = pairs ? 2u : 1u;
   }
   if (i >= n) return;
@@ -657,11 +665,14 @@ int build_begin(const int32_t* text, int64_t m, void* workspace,
   sa_ws_layout(m, workspace, &w);
   const int64_t nb = (m + kTile - 1) / kTile;
   const unsigned eb = (unsigned)((m + 255) / 256);
-  hipLaunchKernelGGL(k_sa_reset, dim3(1), dim3(64), 0, stream, w.state);
-  hipLaunchKernelGGL(k_sa_range, dim3((unsigned)(nb < 1024 ? nb : 1024)),
-                     dim3(256), 0, stream, text, m, w.state);
+  // per-block token ranges in the per-tile arrays, unused until round 1
+  const int parts = (int)(nb < 256 ? nb : 256);
+  int32_t* plo = reinterpret_cast<int32_t*>(w.tcnt);
+  int32_t* phi = reinterpret_cast<int32_t*>(w.blkmax);
+  hipLaunchKernelGGL(k_sa_range, dim3((unsigned)parts), dim3(256), 0, stream,
+                     text, m, plo, phi);
   hipLaunchKernelGGL(k_sa_init, dim3(eb), dim3(256), 0, stream, text, m,
-                     w.keyA, w.valA, w.pos, w.state);
+                     w.keyA, w.valA, w.pos, plo, phi, parts, w.state);
   return sort_and_rank(w, nb, 2 * kPairBits, stream);
 }
 
