@@ -15,9 +15,15 @@
 // flag and every later launch returns at its first instruction, so the
 // fixed launch sequence (capturable, no host reads) is safe for any input.
 //
+// A round works on its active list: the still-unsorted suffixes in SA
+// order, (key, suffix, SA position) per entry.  The round's last kernel
+// marks every entry whose new group is a singleton and counts the others
+// per tile; the next round's gather compacts the rest of the list into the
+// next list, so no round rescans the m SA positions.
+//
 // Each LSD pass is histogram (per 4096-element tile) -> per-digit row scan
 // across tiles -> stable scatter.  The scatter ranks equal digits inside a
-// wave with eight ballots (wave64 match) and across waves by per-wave digit
+// wave with nine ballots (wave64 match) and across waves by per-wave digit
 // counts, so tile order and element order are kept.
 
 #include "launch.h"
@@ -25,31 +31,35 @@
 
 namespace sfx {
 
-constexpr int kSortThreads = 256;
-constexpr int kSortItems = 16;
-constexpr int kTile = kSortThreads * kSortItems;  // 4096
+constexpr int kTile = 4096;  // list entries per tile (one block per tile)
 constexpr int kDigitBits = 9;
 constexpr int kRadix = 1 << kDigitBits;                 // 512
-constexpr int kDigitsPerThread = kRadix / kSortThreads;  // 2
-constexpr int kSortWaves = kSortThreads / kWave;  // 4
-constexpr int kWaveSpan = kTile / kSortWaves;     // 1024 per wave
+constexpr uint32_t kFinished = 0xffffffffu;  // hd[] of a singleton entry
+// state[] words: [0] done, [1] / [6] list length of even / odd rounds,
+// [2] round that found none left, [3] / [4] least / largest token other
+// than PAD (INT32_MAX), [5] h of round 1.
+constexpr int kDone = 0, kLenEven = 1, kFoundNone = 2, kTokLo = 3,
+              kTokHi = 4, kH0 = 5, kLenOdd = 6;
+__host__ __device__ constexpr int len_slot(int round) {
+  return (round & 1) ? kLenOdd : kLenEven;
+}
 
 struct SaWs {
   uint64_t* keyA;
   uint64_t* keyB;
   uint32_t* valA;
   uint32_t* valB;
-  uint32_t* pos;     // SA positions of the active suffixes, ascending
+  uint32_t* pos[2];  // SA positions of the list entries (ascending) of
+                     // even / odd rounds
   uint32_t* rank;    // [m] group head of text position i
   uint32_t* sa;      // [m] current suffix order
-  uint32_t* grp;     // [m] group head of SA position j
-  uint32_t* hist;    // [256][NB] digit counts per tile, then offsets
-  uint32_t* rowsum;  // [256] digit totals
-  uint32_t* tcnt;    // [NB] active suffixes per tile
+  uint32_t* hd;      // [list] group head of a sorted entry, kFinished for a
+                     // singleton
+  uint32_t* hist;    // [512][NB] digit counts per tile, then offsets
+  uint32_t* rowsum;  // [512] digit totals
+  uint32_t* tcnt;    // [NB] unfinished entries per tile of the sorted list
   uint32_t* blkmax;  // [NB] last group start per tile
-  uint32_t* state;   // [0] done, [1] active count, [2] round that found
-                     // none left, [3] / [4] least / largest token other
-                     // than PAD (INT32_MAX), [5] h of round 1
+  uint32_t* state;   // the state[] words above
 };
 
 static size_t sa_ws_layout(int64_t n, void* base, SaWs* w) {
@@ -67,10 +77,11 @@ static size_t sa_ws_layout(int64_t n, void* base, SaWs* w) {
   s.keyB = (uint64_t*)take(N * 8);
   s.valA = (uint32_t*)take(N * 4);
   s.valB = (uint32_t*)take(N * 4);
-  s.pos = (uint32_t*)take(N * 4);
+  s.pos[0] = (uint32_t*)take(N * 4);
+  s.pos[1] = (uint32_t*)take(N * 4);
   s.rank = (uint32_t*)take(N * 4);
   s.sa = (uint32_t*)take(N * 4);
-  s.grp = (uint32_t*)take(N * 4);
+  s.hd = (uint32_t*)take(N * 4);
   s.hist = (uint32_t*)take((size_t)kRadix * NB * 4);
   s.rowsum = (uint32_t*)take(kRadix * 4);
   s.tcnt = (uint32_t*)take(NB * 4);
@@ -130,14 +141,23 @@ __global__ __launch_bounds__(256) void k_sa_range(const int32_t* text,
                                                   int32_t* part_lo,
                                                   int32_t* part_hi) {
   __shared__ int32_t red[2][256 / kWave];
+  constexpr int kUnroll = 8;
   int32_t lo = INT32_MAX, hi = INT32_MIN;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int32_t t = text[i];
-    if (t != INT32_MAX) {
-      lo = t < lo ? t : lo;
-      hi = t > hi ? t : hi;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i0 < n;
+       i0 += kUnroll * stride) {
+    int32_t t[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = i0 + u * stride;
+      t[u] = i < n ? text[i] : INT32_MAX;
     }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      if (t[u] != INT32_MAX) {
+        lo = t[u] < lo ? t[u] : lo;
+        hi = t[u] > hi ? t[u] : hi;
+      }
   }
   block_minmax(lo, hi, red);
   if (threadIdx.x == 0) {
@@ -166,11 +186,11 @@ __global__ __launch_bounds__(256) void k_sa_init(const int32_t* text,
   const int64_t span = thi < tlo ? 0 : (int64_t)thi - (int64_t)tlo + 1;
   const bool pairs = span + 2 < ((int64_t)1 << kPairBits);
   if (i == 0) {
-    state[0] = 0;
-    state[1] = (uint32_t)n;
-    state[3] = (uint32_t)tlo;
-    state[4] = (uint32_t)thi;
-    state[5] = pairs ? 2u : 1u;
+    state[kDone] = 0;
+    state[len_slot(0)] = (uint32_t)n;
+    state[kTokLo] = (uint32_t)tlo;
+    state[kTokHi] = (uint32_t)thi;
+    state[kH0] = pairs ? 2u : 1u;
   }
   if (i >= n) return;
   if (pairs) {
@@ -204,105 +224,98 @@ __device__ __forceinline__ uint32_t digit_of(uint64_t k, int sh) {
   return (uint32_t)(k >> sh) & (kRadix - 1u);
 }
 
-// Block-wide exclusive scan of the kRadix digit counts held
-// kDigitsPerThread per thread (digits tid * kDigitsPerThread + j).
-__device__ __forceinline__ void digit_exscan(const uint32_t (&c)[kDigitsPerThread],
-                                             uint32_t (&ex)[kDigitsPerThread],
-                                             uint32_t* red) {
-  uint32_t sum = 0;
-#pragma unroll
-  for (int j = 0; j < kDigitsPerThread; ++j) sum += c[j];
-  uint32_t tot;
-  uint32_t run = block_exscan1<kSortThreads>(sum, red, &tot);
-#pragma unroll
-  for (int j = 0; j < kDigitsPerThread; ++j) {
-    ex[j] = run;
-    run += c[j];
-  }
-}
-
 // ---------------------------------------------------------------- radix
+// The passes run NT threads per 4096-element tile.  With about one active
+// tile per CU, 1024 threads (16 waves) keep four times more loads and LDS
+// operations in flight per CU than 256 threads would.
 
-__global__ __launch_bounds__(kSortThreads) void k_rs_hist(
+constexpr int kRsThreads = 1024;
+constexpr int kRsHists = 4;  // LDS sub-histograms of the histogram pass
+
+template <int NT>
+__global__ __launch_bounds__(NT) void k_rs_hist(
     const uint64_t* __restrict__ key, int sh, uint32_t* hist, int64_t nb,
-    const uint32_t* state) {
-  if (state[0]) return;
-  const int64_t A = state[1];
+    const uint32_t* state, int slot) {
+  static_assert(kTile % NT == 0 && NT >= kRadix, "tile shape");
+  constexpr int kItems = kTile / NT;
+  if (state[kDone]) return;
+  const int64_t A = state[slot];
   const int64_t base = (int64_t)blockIdx.x * kTile;
   if (base >= A) return;
-  // One histogram per wave (LDS atomics of a wave only collide on equal
-  // digits), summed at the end.
-  __shared__ uint32_t h[kSortWaves][kRadix];
+  // Waves w, w + kRsHists, ... share a histogram (LDS atomics collide only
+  // on equal digits); the sub-histograms are summed at the end.
+  __shared__ uint32_t h[kRsHists][kRadix];
   const int tid = threadIdx.x;
-  const int wv = tid / kWave;
+  const int hw = (tid / kWave) % kRsHists;
+  for (int e = tid; e < kRsHists * kRadix; e += NT) (&h[0][0])[e] = 0;
+  uint32_t d[kItems];
 #pragma unroll
-  for (int w = 0; w < kSortWaves; ++w)
-#pragma unroll
-    for (int j = 0; j < kDigitsPerThread; ++j)
-      h[w][tid * kDigitsPerThread + j] = 0;
-  uint32_t d[kSortItems];
-#pragma unroll
-  for (int r = 0; r < kSortItems; ++r) {
-    const int64_t idx = base + (int64_t)r * kSortThreads + tid;
+  for (int r = 0; r < kItems; ++r) {
+    const int64_t idx = base + (int64_t)r * NT + tid;
     d[r] = idx < A ? digit_of(key[idx], sh) : kRadix;
   }
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < kSortItems; ++r)
-    if (d[r] < kRadix) atomicAdd(&h[wv][d[r]], 1u);
+  for (int r = 0; r < kItems; ++r)
+    if (d[r] < kRadix) atomicAdd(&h[hw][d[r]], 1u);
   __syncthreads();
-#pragma unroll
-  for (int j = 0; j < kDigitsPerThread; ++j) {
-    const int dg = tid * kDigitsPerThread + j;
+  if (tid < kRadix) {
     uint32_t sum = 0;
 #pragma unroll
-    for (int w = 0; w < kSortWaves; ++w) sum += h[w][dg];
-    hist[(int64_t)dg * nb + blockIdx.x] = sum;
+    for (int w = 0; w < kRsHists; ++w) sum += h[w][tid];
+    hist[(int64_t)tid * nb + blockIdx.x] = sum;
   }
 }
 
 // Row d of the histogram (tiles 0 .. ceil(A/4096)) becomes its exclusive
 // prefix; rowsum[d] the digit total.  One block per digit.
-__global__ __launch_bounds__(kSortThreads) void k_rs_rowscan(
-    uint32_t* hist, int64_t nb, uint32_t* rowsum, const uint32_t* state) {
-  if (state[0]) return;
-  __shared__ uint32_t red[kSortWaves];
-  const int64_t nbA = tiles_of(state[1]);
+template <int NT>
+__global__ __launch_bounds__(NT) void k_rs_rowscan(
+    uint32_t* hist, int64_t nb, uint32_t* rowsum, const uint32_t* state,
+    int slot) {
+  if (state[kDone]) return;
+  __shared__ uint32_t red[NT / kWave];
+  const int64_t nbA = tiles_of(state[slot]);
   uint32_t* row = hist + (int64_t)blockIdx.x * nb;
   uint32_t carry = 0;
-  for (int64_t c0 = 0; c0 < nbA; c0 += kSortThreads) {
+  for (int64_t c0 = 0; c0 < nbA; c0 += NT) {
     const int64_t t = c0 + threadIdx.x;
     const uint32_t v = t < nbA ? row[t] : 0u;
     uint32_t tot;
-    const uint32_t ex = block_exscan1<kSortThreads>(v, red, &tot);
+    const uint32_t ex = block_exscan1<NT>(v, red, &tot);
     if (t < nbA) row[t] = carry + ex;
     carry += tot;
   }
   if (threadIdx.x == 0) rowsum[blockIdx.x] = carry;
 }
 
-// Stable scatter of one tile.  Wave w owns the tile's elements
-// base + w*1024 + s*64 + lane (s < 16), i.e. a contiguous quarter, so the
-// element order is (wave, step, lane).  The waves first count their digits
-// (LDS atomics), one scan gives every (wave, digit) its output offset, and
-// then each wave places its elements step by step with an eight-ballot
-// digit match, advancing only its own offsets: three barriers per tile.
-__global__ __launch_bounds__(kSortThreads) void k_rs_scatter(
+// Stable scatter of one tile.  Wave w owns the tile's contiguous span
+// base + w * kTile / NW .. + kTile / NW, 64 consecutive elements per step,
+// so the element order is (wave, step, lane).  The waves first count their
+// digits (LDS atomics), one scan gives every (wave, digit) its output
+// offset, and then each wave places its elements step by step with a
+// nine-ballot digit match, advancing only its own offsets: three barriers
+// per tile.
+template <int NT>
+__global__ __launch_bounds__(NT) void k_rs_scatter(
     const uint64_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint64_t* __restrict__ kout, uint32_t* __restrict__ vout, int sh,
     const uint32_t* __restrict__ hist, int64_t nb,
-    const uint32_t* __restrict__ rowsum, const uint32_t* state) {
-  if (state[0]) return;
-  const int64_t A = state[1];
+    const uint32_t* __restrict__ rowsum, const uint32_t* state, int slot) {
+  constexpr int NW = NT / kWave;
+  constexpr int kSpan = kTile / NW;
+  constexpr int kSteps = kSpan / kWave;
+  static_assert(kTile % NT == 0 && NT >= kRadix, "tile shape");
+  if (state[kDone]) return;
+  const int64_t A = state[slot];
   const int64_t base = (int64_t)blockIdx.x * kTile;
   if (base >= A) return;
-  __shared__ uint32_t woff[kSortWaves][kRadix];
-  __shared__ uint32_t red[kSortWaves];
+  __shared__ uint32_t woff[NW][kRadix];
+  __shared__ uint32_t red[NW];
   const int tid = threadIdx.x;
   const int wv = tid / kWave;
   const int ln = lane_id();
-  constexpr int kSteps = kWaveSpan / kWave;  // 16
-  const int64_t wbase = base + (int64_t)wv * kWaveSpan;
+  const int64_t wbase = base + (int64_t)wv * kSpan;
   uint64_t k[kSteps];
   uint32_t v[kSteps];
 #pragma unroll
@@ -311,30 +324,24 @@ __global__ __launch_bounds__(kSortThreads) void k_rs_scatter(
     k[s] = idx < A ? kin[idx] : 0;
     v[s] = idx < A ? vin[idx] : 0;
   }
-#pragma unroll
-  for (int w = 0; w < kSortWaves; ++w)
-#pragma unroll
-    for (int j = 0; j < kDigitsPerThread; ++j)
-      woff[w][tid * kDigitsPerThread + j] = 0;
-  uint32_t rs[kDigitsPerThread], dbase[kDigitsPerThread];
-#pragma unroll
-  for (int j = 0; j < kDigitsPerThread; ++j)
-    rs[j] = rowsum[tid * kDigitsPerThread + j];
-  digit_exscan(rs, dbase, red);  // ends with a barrier: counters zeroed
+  for (int e = tid; e < NW * kRadix; e += NT) (&woff[0][0])[e] = 0;
+  // Digit d's first output slot: the totals of the digits below it.
+  uint32_t tot;
+  const uint32_t dbase =
+      block_exscan1<NT>(tid < kRadix ? rowsum[tid] : 0u, red, &tot);
+  // block_exscan1 ends with a barrier: the counters are zeroed.
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
     if (wbase + s * kWave + ln < A)
       atomicAdd(&woff[wv][digit_of(k[s], sh)], 1u);
   }
   __syncthreads();
+  if (tid < kRadix) {
+    uint32_t run = dbase + hist[(int64_t)tid * nb + blockIdx.x];
 #pragma unroll
-  for (int j = 0; j < kDigitsPerThread; ++j) {
-    const int dg = tid * kDigitsPerThread + j;
-    uint32_t run = dbase[j] + hist[(int64_t)dg * nb + blockIdx.x];
-#pragma unroll
-    for (int w = 0; w < kSortWaves; ++w) {
-      const uint32_t c = woff[w][dg];
-      woff[w][dg] = run;
+    for (int w = 0; w < NW; ++w) {
+      const uint32_t c = woff[w][tid];
+      woff[w][tid] = run;
       run += c;
     }
   }
@@ -367,20 +374,23 @@ __device__ __forceinline__ bool starts_group(const uint64_t* key, int64_t t,
   return t == 0 || key[t - 1] != kt;
 }
 
-__global__ __launch_bounds__(kSortThreads) void k_grp_reduce(
+template <int NT>
+__global__ __launch_bounds__(NT) void k_grp_reduce(
     const uint64_t* __restrict__ key, const uint32_t* __restrict__ pos,
-    uint32_t* blkmax, const uint32_t* state) {
-  if (state[0]) return;
-  const int64_t A = state[1];
+    uint32_t* blkmax, const uint32_t* state, int slot) {
+  constexpr int NW = NT / kWave;
+  constexpr int kSpan = kTile / NW;
+  if (state[kDone]) return;
+  const int64_t A = state[slot];
   const int64_t base = (int64_t)blockIdx.x * kTile;
   if (base >= A) return;
-  __shared__ uint32_t smax[kSortWaves];
+  __shared__ uint32_t smax[NW];
   const int wv = threadIdx.x / kWave;
   const int ln = lane_id();
-  const int64_t wbase = base + (int64_t)wv * kWaveSpan;
+  const int64_t wbase = base + (int64_t)wv * kSpan;
   uint32_t mx = 0;
-#pragma unroll 4
-  for (int s = 0; s < kWaveSpan / kWave; ++s) {
+#pragma unroll
+  for (int s = 0; s < kSpan / kWave; ++s) {
     const int64_t t = wbase + s * kWave + ln;
     if (t < A) {
       const uint64_t kt = key[t];
@@ -392,34 +402,43 @@ __global__ __launch_bounds__(kSortThreads) void k_grp_reduce(
   __syncthreads();
   if (threadIdx.x == 0) {
     uint32_t m = 0;
-    for (int w = 0; w < kSortWaves; ++w) m = max(m, smax[w]);
+    for (int w = 0; w < NW; ++w) m = max(m, smax[w]);
     blkmax[blockIdx.x] = m;
   }
 }
 
-// rank[val[t]] = head, sa[pos[t]] = val[t], grp[pos[t]] = head.
-// The group start carried into a tile is the largest start of all earlier
-// tiles: each block reduces blkmax[0 .. tile) itself.
-__global__ __launch_bounds__(kSortThreads) void k_grp_rank(
+// rank[val[t]] = head, sa[pos[t]] = val[t]; hd[t] = head, or kFinished
+// when t's group is the singleton {t}; tcnt[tile] = the tile's entries
+// that are not finished.  The group start carried into a tile is the
+// largest start of all earlier tiles: each block reduces blkmax[0 .. tile)
+// itself.
+template <int NT>
+__global__ __launch_bounds__(NT) void k_grp_rank(
     const uint64_t* __restrict__ key, const uint32_t* __restrict__ val,
     const uint32_t* __restrict__ pos, const uint32_t* __restrict__ blkmax,
-    uint32_t* rank, uint32_t* sa, uint32_t* grp, const uint32_t* state) {
-  if (state[0]) return;
-  const int64_t A = state[1];
+    uint32_t* __restrict__ rank, uint32_t* __restrict__ sa,
+    uint32_t* __restrict__ hd, uint32_t* __restrict__ tcnt,
+    const uint32_t* state, int slot) {
+  constexpr int NW = NT / kWave;
+  constexpr int kSpan = kTile / NW;
+  constexpr int kSteps = kSpan / kWave;
+  if (state[kDone]) return;
+  const int64_t A = state[slot];
   const int64_t base = (int64_t)blockIdx.x * kTile;
   if (base >= A) return;
-  __shared__ uint32_t smax[kSortWaves];
-  __shared__ uint32_t cred[kSortWaves];
+  __shared__ uint32_t smax[NW];
+  __shared__ uint32_t cred[NW];
+  __shared__ uint32_t ucnt[NW];
   uint32_t cm = 0;
-  for (int t = threadIdx.x; t < (int)blockIdx.x; t += kSortThreads)
+  for (int t = threadIdx.x; t < (int)blockIdx.x; t += NT)
     cm = max(cm, blkmax[t]);
   cm = (uint32_t)wave_max_i32((int)cm);
   if (lane_id() == 0) cred[threadIdx.x / kWave] = cm;
   const int wv = threadIdx.x / kWave;
   const int ln = lane_id();
-  const int64_t wbase = base + (int64_t)wv * kWaveSpan;
-  constexpr int kSteps = kWaveSpan / kWave;  // 16
+  const int64_t wbase = base + (int64_t)wv * kSpan;
   uint32_t st[kSteps];  // start position of a group beginning here, or 0
+  uint32_t single = 0;  // bit s: entry s is a group of its own
   uint32_t mx = 0;
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
@@ -427,7 +446,10 @@ __global__ __launch_bounds__(kSortThreads) void k_grp_rank(
     st[s] = 0;
     if (t < A) {
       const uint64_t kt = key[t];
-      if (starts_group(key, t, kt)) st[s] = pos[t];
+      const bool first = starts_group(key, t, kt);
+      const bool last = t + 1 == A || key[t + 1] != kt;
+      if (first) st[s] = pos[t];
+      single |= (uint32_t)(first && last) << s;
     }
     mx = max(mx, st[s]);
   }
@@ -435,82 +457,69 @@ __global__ __launch_bounds__(kSortThreads) void k_grp_rank(
   if (ln == 0) smax[wv] = mx;
   __syncthreads();
   uint32_t run = 0;
-  for (int w = 0; w < kSortWaves; ++w) run = max(run, cred[w]);
+  for (int w = 0; w < NW; ++w) run = max(run, cred[w]);
   for (int w = 0; w < wv; ++w) run = max(run, smax[w]);
+  uint32_t open = 0;
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
     const int64_t t = wbase + s * kWave + ln;
     const uint32_t head = max(run, wave_incl_max(st[s]));
     run = max(run, (uint32_t)__builtin_amdgcn_readlane((int)head, kWave - 1));
+    const bool fin = (single >> s) & 1u;
+    open += (uint32_t)popc(ballot(t < A && !fin));
     if (t < A) {
       const uint32_t i = val[t];
-      const uint32_t j = pos[t];
       rank[i] = head;
-      sa[j] = i;
-      grp[j] = head;
+      sa[pos[t]] = i;
+      hd[t] = fin ? kFinished : head;
     }
   }
-}
-
-// ------------------------------------------------------ active suffixes
-// SA position j is finished when its group is the singleton {j}.
-__device__ __forceinline__ bool unfinished(const uint32_t* grp, int64_t j,
-                                           int64_t m) {
-  const bool single =
-      grp[j] == (uint32_t)j && (j + 1 == m || grp[j + 1] == (uint32_t)(j + 1));
-  return !single;
-}
-
-__global__ __launch_bounds__(kSortThreads) void k_sa_mark(
-    const uint32_t* __restrict__ grp, int64_t m, uint32_t* tcnt,
-    const uint32_t* state) {
-  if (state[0]) return;
-  __shared__ uint32_t scnt[kSortWaves];
-  const int wv = threadIdx.x / kWave;
-  const int ln = lane_id();
-  const int64_t wbase = (int64_t)blockIdx.x * kTile + (int64_t)wv * kWaveSpan;
-  uint32_t cnt = 0;
-#pragma unroll 4
-  for (int s = 0; s < kWaveSpan / kWave; ++s) {
-    const int64_t j = wbase + s * kWave + ln;
-    cnt += (uint32_t)popc(ballot(j < m && unfinished(grp, j, m)));
-  }
-  if (ln == 0) scnt[wv] = cnt;
+  if (ln == 0) ucnt[wv] = open;
   __syncthreads();
   if (threadIdx.x == 0) {
     uint32_t c = 0;
-    for (int w = 0; w < kSortWaves; ++w) c += scnt[w];
+    for (int w = 0; w < NW; ++w) c += ucnt[w];
     tcnt[blockIdx.x] = c;
   }
 }
 
-// Active suffixes of the tile, in SA order, with their sort keys:
-// key = head * (m + 1) + (rank[i + h] + 1, or 0 past the end), where round
-// r doubles h = state[5] << (r - 1).
-// Each block sums the earlier tiles' counts for its output offset; block 0
-// also sums them all: that is the round's active count, and none left
-// means the array is final (the done flag).
-__global__ __launch_bounds__(kSortThreads) void k_sa_gather(
-    const uint32_t* __restrict__ sa, const uint32_t* __restrict__ rank,
-    const uint32_t* __restrict__ grp, int64_t m, int round, int64_t nb,
-    const uint32_t* __restrict__ tcnt, uint64_t* key, uint32_t* val,
-    uint32_t* pos, uint32_t* state) {
-  if (state[0]) return;
-  const int64_t h = (int64_t)state[5] << (round - 1);
-  __shared__ uint32_t scnt[kSortWaves];
-  __shared__ uint32_t ored[kSortWaves];
+// ------------------------------------------------------ active suffixes
+// Round r's list: the unfinished entries of round r-1's sorted list (hd,
+// vold, pold; length in state[cin]) in the same SA order, keyed
+// head * (m + 1) + (rank[i + h] + 1, or 0 past the end), where round r
+// doubles h = state[kH0] << (r - 1).  Each block sums the earlier tiles'
+// counts for its output offset; block 0 also sums them all: that is the
+// new length (state[cout]), and none left means the array is final (the
+// done flag).
+template <int NT>
+__global__ __launch_bounds__(NT) void k_sa_gather(
+    const uint32_t* __restrict__ hd, const uint32_t* __restrict__ vold,
+    const uint32_t* __restrict__ pold, const uint32_t* __restrict__ rank,
+    const uint32_t* __restrict__ tcnt, int64_t m, int round,
+    uint64_t* __restrict__ key, uint32_t* __restrict__ val,
+    uint32_t* __restrict__ pos, uint32_t* state, int cin, int cout) {
+  constexpr int NW = NT / kWave;
+  constexpr int kSpan = kTile / NW;
+  constexpr int kSteps = kSpan / kWave;
+  if (state[kDone]) return;
+  const int64_t Aold = state[cin];
+  const int64_t base = (int64_t)blockIdx.x * kTile;
+  if (blockIdx.x > 0 && base >= Aold) return;  // block 0 writes the length
+  const int64_t h = (int64_t)state[kH0] << (round - 1);
+  __shared__ uint32_t scnt[NW];
+  __shared__ uint32_t ored[NW];
   {
-    const int64_t upto = blockIdx.x == 0 ? nb : (int64_t)blockIdx.x;
+    const int64_t upto = blockIdx.x == 0 ? tiles_of(Aold) : (int64_t)blockIdx.x;
     uint32_t c = 0;
-    for (int64_t t = threadIdx.x; t < upto; t += kSortThreads) c += tcnt[t];
+    for (int64_t t = threadIdx.x; t < upto; t += NT) c += tcnt[t];
     uint32_t tot;
-    block_exscan1<kSortThreads>(c, ored, &tot);
+    block_exscan1<NT>(c, ored, &tot);
     if (blockIdx.x == 0) {
       if (threadIdx.x == 0) {
-        state[1] = tot;
+        state[cout] = tot;
         if (tot == 0) {
-          state[0] = 1;
-          state[2] = (uint32_t)round;  // the round that found none
+          state[kDone] = 1;
+          state[kFoundNone] = (uint32_t)round;
         }
       }
       if (tot == 0) return;
@@ -521,16 +530,14 @@ __global__ __launch_bounds__(kSortThreads) void k_sa_gather(
   }
   const int wv = threadIdx.x / kWave;
   const int ln = lane_id();
-  const int64_t wbase = (int64_t)blockIdx.x * kTile + (int64_t)wv * kWaveSpan;
-  constexpr int kSteps = kWaveSpan / kWave;
-  uint32_t flags = 0;
+  const int64_t wbase = base + (int64_t)wv * kSpan;
+  uint32_t hv[kSteps];
   uint32_t cnt = 0;
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
-    const int64_t j = wbase + s * kWave + ln;
-    const bool a = j < m && unfinished(grp, j, m);
-    flags |= (uint32_t)a << s;
-    cnt += (uint32_t)popc(ballot(a));
+    const int64_t t = wbase + s * kWave + ln;
+    hv[s] = t < Aold ? hd[t] : kFinished;
+    cnt += (uint32_t)popc(ballot(hv[s] != kFinished));
   }
   if (ln == 0) scnt[wv] = cnt;
   __syncthreads();
@@ -539,17 +546,17 @@ __global__ __launch_bounds__(kSortThreads) void k_sa_gather(
   const uint64_t M1 = (uint64_t)m + 1;
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
-    const int64_t j = wbase + s * kWave + ln;
-    const bool a = (flags >> s) & 1u;
+    const int64_t t = wbase + s * kWave + ln;
+    const bool a = hv[s] != kFinished;
     const uint64_t bm = ballot(a);
     if (a) {
       const uint32_t o = out + (uint32_t)rank_lt(bm);
-      const uint32_t i = sa[j];
+      const uint32_t i = vold[t];
       const uint64_t k2 =
           (int64_t)i + h < m ? (uint64_t)rank[i + h] + 1 : 0;
-      key[o] = (uint64_t)grp[j] * M1 + k2;
+      key[o] = (uint64_t)hv[s] * M1 + k2;
       val[o] = i;
-      pos[o] = (uint32_t)j;
+      pos[o] = pold[t];
     }
     out += (uint32_t)popc(bm);
   }
@@ -582,33 +589,62 @@ static int bits_for(uint64_t maxval) {
   return b;
 }
 
-// LSD radix sort of the active (key, val) pairs by the low `nbits` bits,
+static int passes_of(int nbits) {
+  return (nbits + kDigitBits - 1) / kDigitBits;
+}
+
+// Key bits of a doubling round: head * (m + 1) + k2 with head < m, k2 <= m.
+static int round_bits(int64_t m) {
+  return bits_for((uint64_t)(m - 1) * (uint64_t)(m + 1) + (uint64_t)m);
+}
+
+// Key buffer (0: A, 1: B) holding round r's list before its sort: round 0
+// starts in A, and each round's gather writes the buffer its predecessor's
+// sorted list is not in.
+static int list_buf(int64_t m, int round) {
+  const int p0 = passes_of(2 * kPairBits);
+  const int p = passes_of(round_bits(m));
+  int x = 0;
+  for (int q = 0; q < round; ++q) x = (x ^ ((q == 0 ? p0 : p) & 1)) ^ 1;
+  return x;
+}
+
+// Buffer holding round r's sorted list.
+static int sorted_buf(int64_t m, int round) {
+  const int p = round == 0 ? passes_of(2 * kPairBits)
+                           : passes_of(round_bits(m));
+  return list_buf(m, round) ^ (p & 1);
+}
+
+// LSD radix sort of round r's list by the low `nbits` bits of its keys,
 // then the group heads of the sorted order.
-static int sort_and_rank(SaWs& w, int64_t nb, int nbits, hipStream_t stream) {
-  uint64_t* kin = w.keyA;
-  uint32_t* vin = w.valA;
-  uint64_t* kout = w.keyB;
-  uint32_t* vout = w.valB;
+static int sort_and_rank(SaWs& w, int64_t nb, int64_t m, int round,
+                         hipStream_t stream) {
+  const int nbits = round == 0 ? 2 * kPairBits : round_bits(m);
+  const int slot = len_slot(round);
+  uint64_t* keys[2] = {w.keyA, w.keyB};
+  uint32_t* vals[2] = {w.valA, w.valB};
+  int x = list_buf(m, round);
   for (int sh = 0; sh < nbits; sh += kDigitBits) {
-    hipLaunchKernelGGL(k_rs_hist, dim3((unsigned)nb), dim3(kSortThreads), 0,
-                       stream, kin, sh, w.hist, nb, w.state);
-    hipLaunchKernelGGL(k_rs_rowscan, dim3(kRadix), dim3(kSortThreads), 0,
-                       stream, w.hist, nb, w.rowsum, w.state);
-    hipLaunchKernelGGL(k_rs_scatter, dim3((unsigned)nb), dim3(kSortThreads),
-                       0, stream, kin, vin, kout, vout, sh, w.hist, nb,
-                       w.rowsum, w.state);
-    uint64_t* tk = kin;
-    kin = kout;
-    kout = tk;
-    uint32_t* tv = vin;
-    vin = vout;
-    vout = tv;
+    hipLaunchKernelGGL(k_rs_hist<kRsThreads>, dim3((unsigned)nb),
+                       dim3(kRsThreads), 0, stream, keys[x], sh, w.hist, nb,
+                       w.state, slot);
+    hipLaunchKernelGGL(k_rs_rowscan<kRsThreads>, dim3(kRadix),
+                       dim3(kRsThreads), 0, stream, w.hist, nb, w.rowsum,
+                       w.state, slot);
+    hipLaunchKernelGGL(k_rs_scatter<kRsThreads>, dim3((unsigned)nb),
+                       dim3(kRsThreads), 0, stream, keys[x], vals[x],
+                       keys[x ^ 1], vals[x ^ 1], sh, w.hist, nb, w.rowsum,
+                       w.state, slot);
+    x ^= 1;
   }
-  hipLaunchKernelGGL(k_grp_reduce, dim3((unsigned)nb), dim3(kSortThreads), 0,
-                     stream, kin, w.pos, w.blkmax, w.state);
-  hipLaunchKernelGGL(k_grp_rank, dim3((unsigned)nb), dim3(kSortThreads), 0,
-                     stream, kin, vin, w.pos, w.blkmax, w.rank, w.sa, w.grp,
-                     w.state);
+  uint32_t* pos = w.pos[round & 1];
+  hipLaunchKernelGGL(k_grp_reduce<kRsThreads>, dim3((unsigned)nb),
+                     dim3(kRsThreads), 0, stream, keys[x], pos, w.blkmax,
+                     w.state, slot);
+  hipLaunchKernelGGL(k_grp_rank<kRsThreads>, dim3((unsigned)nb),
+                     dim3(kRsThreads), 0, stream, keys[x], vals[x], pos,
+                     w.blkmax, w.rank, w.sa, w.hd, w.tcnt, w.state, slot);
   return (int)hipGetLastError();
 }
 
@@ -672,8 +708,8 @@ int build_begin(const int32_t* text, int64_t m, void* workspace,
   hipLaunchKernelGGL(k_sa_range, dim3((unsigned)parts), dim3(256), 0, stream,
                      text, m, plo, phi);
   hipLaunchKernelGGL(k_sa_init, dim3(eb), dim3(256), 0, stream, text, m,
-                     w.keyA, w.valA, w.pos, plo, phi, parts, w.state);
-  return sort_and_rank(w, nb, 2 * kPairBits, stream);
+                     w.keyA, w.valA, w.pos[0], plo, phi, parts, w.state);
+  return sort_and_rank(w, nb, m, 0, stream);
 }
 
 // Rounds first .. first + count - 1 (round r doubles h = h0 * 2^(r-1),
@@ -684,16 +720,18 @@ int build_rounds(int64_t m, int first, int count, void* workspace,
   SaWs w;
   sa_ws_layout(m, workspace, &w);
   const int64_t nb = (m + kTile - 1) / kTile;
-  const uint64_t maxkey = (uint64_t)(m - 1) * (uint64_t)(m + 1) + (uint64_t)m;
-  const int nbits = bits_for(maxkey);
   const int last = total_rounds(m);
+  uint64_t* keys[2] = {w.keyA, w.keyB};
+  uint32_t* vals[2] = {w.valA, w.valB};
   for (int r = first < 1 ? 1 : first; r < first + count && r <= last; ++r) {
-    hipLaunchKernelGGL(k_sa_mark, dim3((unsigned)nb), dim3(kSortThreads), 0,
-                       stream, w.grp, m, w.tcnt, w.state);
-    hipLaunchKernelGGL(k_sa_gather, dim3((unsigned)nb), dim3(kSortThreads), 0,
-                       stream, w.sa, w.rank, w.grp, m, r, nb, w.tcnt, w.keyA,
-                       w.valA, w.pos, w.state);
-    const int rc = sort_and_rank(w, nb, nbits, stream);
+    const int src = sorted_buf(m, r - 1);
+    const int dst = list_buf(m, r);
+    hipLaunchKernelGGL(k_sa_gather<kRsThreads>, dim3((unsigned)nb),
+                       dim3(kRsThreads), 0, stream, w.hd, vals[src],
+                       w.pos[(r - 1) & 1], w.rank, w.tcnt, m, r, keys[dst],
+                       vals[dst], w.pos[r & 1], w.state, len_slot(r - 1),
+                       len_slot(r));
+    const int rc = sort_and_rank(w, nb, m, r, stream);
     if (rc) return rc;
   }
   return (int)hipGetLastError();
