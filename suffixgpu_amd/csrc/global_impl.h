@@ -265,6 +265,17 @@ __device__ __forceinline__ int32_t delta_end_at(const GlobalArgs& a, int b,
   return a.ws.d_end[(slot * C + c) * R + r];
 }
 
+// Position of the r-th SA sample of the interval [s, s + ilen): stride
+// ilen / R when it is longer than R (global_index.py:339-352).
+__device__ __forceinline__ int32_t sa_sample(const GlobalArgs& a, int64_t s,
+                                             int64_t ilen, int r) {
+  const int R = a.p.max_occurrences;
+  const int64_t N = a.ix.capacity;
+  int64_t idx = ilen > R ? s + ((int64_t)r * ilen) / R : s + r;
+  idx = idx < 0 ? 0 : (idx > N - 1 ? N - 1 : idx);
+  return a.ix.sa[idx];
+}
+
 // One wave: the continuation block of one candidate (src 1: the SA
 // interval [sa_s, sa_s + ilen), sampled with stride ilen / R when longer
 // than R (global_index.py:339-352); src 2: the row's delta ends minus len)
@@ -288,9 +299,7 @@ __device__ __forceinline__ ExpandResult gather_expand(
   for (int r = ln; r < occ; r += kWave) {
     int32_t pos;
     if (src == 1) {
-      int64_t idx = ilen > R ? sa_s + ((int64_t)r * ilen) / R : sa_s + r;
-      idx = idx < 0 ? 0 : (idx > N - 1 ? N - 1 : idx);
-      pos = a.ix.sa[idx];
+      pos = sa_sample(a, sa_s, ilen, r);
     } else {
       const int64_t e = (int64_t)delta_end_at(a, b, c, r, dpc) - len;
       pos = (int32_t)(e < 0 ? 0 : e);

@@ -78,6 +78,8 @@ struct RowState {
   bool mask;
 };
 
+// Called by every lane of the wave (the accepted count is a ballot over
+// the row's sampled ids, one id per lane).
 __device__ __forceinline__ RowState row_state(const sfx_batch& bt, int b) {
   RowState st;
   st.base = load_count(bt.num_tokens, bt.num_tokens_is64, b);
@@ -87,7 +89,10 @@ __device__ __forceinline__ RowState row_state(const sfx_batch& bt, int b) {
       st.cnt = load_count(bt.valid_count, bt.valid_count_is64, b);
     } else {
       const int32_t* sp = bt.sampled + (int64_t)b * bt.num_sampled;
-      for (int64_t j = 0; j < bt.num_sampled; ++j) st.cnt += sp[j] != -1;
+      for (int64_t j0 = 0; j0 < bt.num_sampled; j0 += kWave) {
+        const int64_t j = j0 + lane_id();
+        st.cnt += popc(ballot(j < bt.num_sampled && sp[j] != -1));
+      }
     }
     st.q = st.base + st.cnt;
     st.mask = st.cnt > 0 && st.q < bt.limit;
