@@ -64,7 +64,8 @@ typedef struct sfx_index {
     const int32_t* delta;     /* [delta_capacity] append-only delta       */
     int64_t delta_capacity;   /* D                                        */
     const int64_t* delta_len; /* device scalar: committed delta length    */
-    const int32_t* sa_key;    /* [capacity, key_width] or NULL            */
+    const int32_t* sa_key;    /* [capacity, key_width] or NULL; 16-byte
+                                 aligned                                 */
     int64_t key_width;        /* 4..32, a multiple of 4                   */
 } sfx_index;
 

@@ -66,7 +66,8 @@ int check_global(const sfx_params& p, const sfx_index& ix, int64_t batch) {
   if (ix.delta_capacity < 1 || ix.delta_capacity > 0x7fffffffLL)
     return SFX_EINVAL;
   if (ix.sa_key &&
-      (ix.key_width < 4 || ix.key_width > 32 || (ix.key_width & 3)))
+      (ix.key_width < 4 || ix.key_width > 32 || (ix.key_width & 3) ||
+       ((uintptr_t)ix.sa_key & 15)))
     return SFX_EINVAL;
   size_t lds = 0;
   const int parts = delta_parts_for(batch, ix.delta_capacity);

@@ -481,34 +481,32 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
     __syncthreads();
     SFX_TRACE_POINT(2);
     // Each cap takes its longest non-empty interval (sa_search.py:
-    // 137-163).
+    // 137-163); wave w selects caps w, w + NW, ...
     int32_t* sal = (int32_t*)(smem + L.sal);
     int32_t* sas = (int32_t*)(smem + L.sas);
     int32_t* sae = (int32_t*)(smem + L.sae);
-    if (wv == 0) {
-      for (int c = 0; c < C; ++c) {
-        const int cap = p.caps[c];
-        int best = 0;
-        for (int base = 1; base <= P; base += kWave) {
-          const int l = base + ln;
-          const bool f = l <= P && l <= cap && l <= plen &&
-                         ubs[l - 1] > lbs[l - 1];
-          const uint64_t m = ballot(f);
-          if (m) best = base + 63 - __builtin_clzll(m);
-        }
-        if (ln == 0) {
-          const int64_t s0 = best ? lbs[best - 1] : 0;
-          const int64_t e0 = best ? ubs[best - 1] : 0;
-          sal[c] = best;
-          sas[c] = (int32_t)s0;
-          sae[c] = (int32_t)e0;
-          a.ws.sa_len[(int64_t)b * C + c] = best;
-          a.ws.sa_s[(int64_t)b * C + c] = (int32_t)s0;
-          a.ws.sa_e[(int64_t)b * C + c] = (int32_t)e0;
-          if (a.out.sa_len) a.out.sa_len[(int64_t)b * C + c] = best;
-          if (a.out.sa_start) a.out.sa_start[(int64_t)b * C + c] = s0;
-          if (a.out.sa_end) a.out.sa_end[(int64_t)b * C + c] = e0;
-        }
+    for (int c = wv; c < C; c += NW) {
+      const int cap = p.caps[c];
+      int best = 0;
+      for (int base = 1; base <= P; base += kWave) {
+        const int l = base + ln;
+        const bool f = l <= P && l <= cap && l <= plen &&
+                       ubs[l - 1] > lbs[l - 1];
+        const uint64_t m = ballot(f);
+        if (m) best = base + 63 - __builtin_clzll(m);
+      }
+      if (ln == 0) {
+        const int64_t s0 = best ? lbs[best - 1] : 0;
+        const int64_t e0 = best ? ubs[best - 1] : 0;
+        sal[c] = best;
+        sas[c] = (int32_t)s0;
+        sae[c] = (int32_t)e0;
+        a.ws.sa_len[(int64_t)b * C + c] = best;
+        a.ws.sa_s[(int64_t)b * C + c] = (int32_t)s0;
+        a.ws.sa_e[(int64_t)b * C + c] = (int32_t)e0;
+        if (a.out.sa_len) a.out.sa_len[(int64_t)b * C + c] = best;
+        if (a.out.sa_start) a.out.sa_start[(int64_t)b * C + c] = s0;
+        if (a.out.sa_end) a.out.sa_end[(int64_t)b * C + c] = e0;
       }
     }
     if (a.step) {

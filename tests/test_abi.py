@@ -91,6 +91,17 @@ def test_argument_errors_are_reported_before_any_launch():
     assert lib.sfx_delta_append(docs, -1, 1, 17, None, 0, None) == -1
     assert lib.sfx_delta_shift(1, 16, 8, 9, None, None) == -1
     assert lib.sfx_delta_shift(None, 16, 1, 1, None, None) == -1
+    # key rows must be 16-byte aligned (they are read as 16-byte words).
+    # An empty batch with a stand-in workspace runs every host check and
+    # launches nothing, so the addresses are never dereferenced.
+    p = _lib.make_params(4, 8, 16, 1, [1], [8, 4, 2], None, 0.0, 0.0, 0.0)
+    out = _lib.SfxGlobalOut()
+    for key, rc in ((0x100008, -1), (0x100010, 0)):
+        ix = _lib.SfxIndex(0x200000, 0x300000, 1 << 10, 0x400000, 1 << 10,
+                           0x500000, key, 32)
+        assert lib.sfx_global_query(ctypes.byref(p), ctypes.byref(ix), None,
+                                    0, 1, None, ctypes.byref(out), 0x600000,
+                                    1 << 40, None) == rc
 
 
 STRUCT_PROBE = r"""
