@@ -22,40 +22,56 @@ __device__ __forceinline__ void final_pick(const sfx_params& p,
                                            int* misc) {
   const int C = p.num_caps;
   const int K = p.k;
-  if (threadIdx.x == 0) {
-    int plen = 0, psrc = 0;
-    int best = 0, bnv = 0, blen = 0, bsrc = 0;
-    float bscore = 0.0f;
-    for (int c = 0; c < C; ++c) {
-      const int64_t i = (int64_t)b * C + c;
-      const int sl = ws.sa_len[i];
-      const int dl = ws.dl_c[i];
-      const bool use_sa = sl >= dl && sl > 0;
-      const bool use_d = dl > sl && dl > 0;
-      const int len = use_sa ? sl : (use_d ? dl : 0);
-      const int src = (use_sa ? 1 : 0) + (use_d ? 2 : 0);
-      int esrc = src, elen = len;
-      if (c > 0 && len == plen && src == psrc && len > 0) esrc = elen = 0;
-      plen = len;
-      psrc = src;
-      const float sc =
-          esrc == 1 ? ws.sa_score[i] : (esrc == 2 ? ws.dn_score[i] : 0.0f);
-      const int nv = esrc == 1 ? ws.sa_nv[i] : (esrc == 2 ? ws.dn_nv[i] : 0);
-      if (c == 0 || sc > bscore) {
-        best = c;
-        bscore = sc;
-        bnv = nv;
-        blen = elen;
-        bsrc = esrc;
-      }
+  SFX_TRACE_POINT(13);
+  if (threadIdx.x < kWave) {
+    // Lane c holds cap c's global candidate; every load is issued at once.
+    const int c = threadIdx.x;
+    const bool on = c < C;
+    const int64_t i = (int64_t)b * C + (on ? c : 0);
+    int sl = 0, dl = 0, snv = 0, dnv = 0;
+    float ssc = 0.0f, dsc = 0.0f;
+    if (on) {
+      sl = ws.sa_len[i];
+      dl = ws.dl_c[i];
+      ssc = ws.sa_score[i];
+      dsc = ws.dn_score[i];
+      snv = ws.sa_nv[i];
+      dnv = ws.dn_nv[i];
     }
-    const int64_t cap = spec_cap(p, blen);
-    const int64_t cap0 = cap > 0 ? cap : 0;
-    const int gemit = (int)((int64_t)bnv < cap0 ? bnv : cap0);
-    const bool g = bscore > ws.l_score[b];
-    misc[0] = g ? gemit : ws.l_emit[b];
-    misc[1] = g ? bsrc : 0;
-    misc[2] = best;
+    const float lscore = ws.l_score[b];
+    const int lemit = ws.l_emit[b];
+    const bool use_sa = sl >= dl && sl > 0;
+    const bool use_d = dl > sl && dl > 0;
+    const int len = use_sa ? sl : (use_d ? dl : 0);
+    const int src = (use_sa ? 1 : 0) + (use_d ? 2 : 0);
+    const int plen = __shfl_up(len, 1);
+    const int psrc = __shfl_up(src, 1);
+    const bool dup = c > 0 && len == plen && src == psrc && len > 0;
+    const int esrc = dup ? 0 : src;
+    const int elen = dup ? 0 : len;
+    const float sc = esrc == 1 ? ssc : (esrc == 2 ? dsc : 0.0f);
+    const int nv = esrc == 1 ? snv : (esrc == 2 ? dnv : 0);
+    // First argmax: scores are sums of probabilities (>= 0), so their bit
+    // patterns order like the values; lanes past C (0) lose every tie to
+    // a lower cap.
+    const uint32_t key = on ? __float_as_uint(sc) : 0u;
+    const uint32_t top = wave_all_max(key);
+    const int best = __builtin_amdgcn_readfirstlane(
+        __builtin_ctzll(ballot(on && key == top)));
+    const float bscore = __uint_as_float(
+        (uint32_t)__builtin_amdgcn_readlane((int)key, best));
+    const int bnv = __builtin_amdgcn_readlane(nv, best);
+    const int blen = __builtin_amdgcn_readlane(elen, best);
+    const int bsrc = __builtin_amdgcn_readlane(esrc, best);
+    if (c == 0) {
+      const int64_t cap = spec_cap(p, blen);
+      const int64_t cap0 = cap > 0 ? cap : 0;
+      const int gemit = (int)((int64_t)bnv < cap0 ? bnv : cap0);
+      const bool g = bscore > lscore;
+      misc[0] = g ? gemit : lemit;
+      misc[1] = g ? bsrc : 0;
+      misc[2] = best;
+    }
   }
   __syncthreads();
   const int nv = misc[0];
@@ -67,6 +83,7 @@ __device__ __forceinline__ void final_pick(const sfx_params& p,
   for (int j = threadIdx.x; j < K; j += blockDim.x)
     draft[(int64_t)b * K + j] = j < nv ? chain[j] : -1;
   if (threadIdx.x == 0) num_valid[b] = nv;
+  SFX_TRACE_POINT(14);
 }
 
 // Row state of a decode step: committed count q after the update and
