@@ -244,15 +244,29 @@ __device__ __forceinline__ void hash_vote(int32_t v0, int32_t v1,
   wave_lds_sync();  // the table is rewritten by the next depth
 }
 
+// Depths the unit vote settles by counting alone (the fast path below).
+constexpr int kFastDepths = 32;
+
 // Wave-cooperative depth-wise majority vote of one candidate
 // (suffix_gpu/expand.py:59-147 == triton_kernels.py:139-215).
 //
 // Occurrence r (< R) is row r of the candidate's continuation block;
-// cont_at(r, d) returns its token at depth d and is only called for rows
-// still on the chain (r < occ and every earlier depth voted for them).
-// chain_out[0..K) receives the chain (-1 past the first invalid depth).
+// cont_at(r, d) returns its token at depth d (any d < K) and is only
+// called for rows r < occ.  chain_out[0..K) receives the chain (-1 past
+// the first invalid depth).
 //
-// Unit votes with R <= 128 (two rows per lane): up to kQuickVotes distinct
+// Unit votes with R <= 128 (two rows per lane) first take the fast path:
+// with r* the first active row, P the lane masks of the rows on the chain
+// (they agreed with every winner so far) and E those holding r*'s token at
+// depth d, |P & E| rows vote for r*'s token and |P & ~E| rows with a
+// token split among other values.  When the former is the larger count
+// r*'s token wins outright whatever the others hold, so such a depth costs
+// two ballots and the fp32 update of a full vote (the factor g / (g + 0)
+// is exactly 1 and skipped).  The first depth without that majority
+// continues in the full vote below with the rows still on the chain.  Most
+// candidates' rows agree, so most chains end on the fast path.
+//
+// The full vote: up to kQuickVotes distinct
 // values are counted one at a time with two ballots (the first remaining
 // row's value is broadcast, its matches counted and retired), stopping as
 // soon as the remaining rows cannot outvote the best -- which settles most
@@ -281,7 +295,66 @@ __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
     bool ok1 = r1 < R && (int64_t)r1 < occ;
     int v0 = ok0 && K > 0 ? cont_at(r0, 0) : -1;
     int v1 = ok1 && K > 0 ? cont_at(r1, 0) : -1;
-    for (; d < K; ++d) {
+    bool ended = false;
+    {
+      const uint64_t s0 = ballot(v0 != -1);
+      const uint64_t s1 = ballot(v1 != -1);
+      const int kf = K < kFastDepths ? K : kFastDepths;
+      if (s0 | s1) {
+        const int rs = s0 ? __builtin_ctzll(s0) : kWave + __builtin_ctzll(s1);
+        // rows past occ read row rs (their results are masked off)
+        const int q0 = ok0 ? r0 : rs;
+        const int q1 = ok1 ? r1 : rs;
+        // rows on the chain; depth d's tokens (a: row rs's, made scalar so
+        // that every test on it is uniform), depth d + 1's loaded ahead
+        uint64_t P0 = ballot(ok0), P1 = ballot(ok1);
+        int na = cont_at(rs, 0), t0 = v0, t1 = v1;
+        int n0 = -1, n1 = -1;
+        for (; d < kf; ++d) {
+          const int a = __builtin_amdgcn_readfirstlane(na);
+          if (d + 1 < kf) {
+            na = cont_at(rs, d + 1);
+            n0 = cont_at(q0, d + 1);
+            n1 = cont_at(q1, d + 1);
+          }
+          const uint64_t E0 = a != -1 ? ballot(t0 == a) : 0;
+          const uint64_t E1 = a != -1 ? ballot(t1 == a) : 0;
+          const uint64_t A0 = P0 & E0, A1 = P1 & E1;  // votes for a
+          const int g = popc(A0) + popc(A1);
+          const int x = popc(P0 & ~E0 & ballot(t0 != -1)) +
+                        popc(P1 & ~E1 & ballot(t1 != -1));
+          if (g <= x) break;  // no outright winner: full vote from here
+          // g / (g + 0) is exactly 1: the division is skipped then
+          float f = 1.0f;
+          if (x != 0 || alpha != 0.0f)
+            f = __fdiv_rn((float)g, __fadd_rn((float)(g + x), alpha));
+          prob = __fmul_rn(prob, f);
+          if (!(prob >= min_prob)) {
+            ended = true;
+            break;
+          }
+          if ((int64_t)d < cap) score = __fadd_rn(score, prob);
+          P0 = A0;
+          P1 = A1;
+          t0 = n0;
+          t1 = n1;
+        }
+        for (int dd = ln; dd < d; dd += kWave) chain_out[dd] = cont_at(rs, dd);
+        nv = d;
+        if (!ended && d > 0) {
+          // the full vote continues with the rows still on the chain
+          ok0 = (P0 >> ln) & 1;
+          ok1 = (P1 >> ln) & 1;
+          if (d == kf && d < K) {  // not loaded ahead
+            t0 = ok0 ? cont_at(r0, d) : -1;
+            t1 = ok1 ? cont_at(r1, d) : -1;
+          }
+          v0 = ok0 ? t0 : -1;
+          v1 = ok1 ? t1 : -1;
+        }
+      }
+    }
+    for (; !ended && d < K; ++d) {
       const bool a0 = ok0 && v0 != -1;
       const bool a1 = ok1 && v1 != -1;
       // next depth's tokens for every row still on the chain (a superset
