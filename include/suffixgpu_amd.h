@@ -114,7 +114,8 @@ int sfx_first_occurrences(const int32_t* mb, int64_t n_cols,
 
 /* triton_kernels.py:284-302 sa_search / sa_search.py:66-107: exact lower
  * and upper bounds of each pattern (row-major [B, M], plen[b] valid) among
- * the suffixes listed by sa; a corpus read at or past n compares as -1. */
+ * the suffixes listed by sa; a corpus read at or past n compares as -1.
+ * 1 <= n < 2^31. */
 int sfx_sa_search(const int32_t* sa, const int32_t* corpus, int64_t n,
                   const int32_t* pattern, int64_t batch, int64_t width,
                   const int64_t* plen, int64_t* lower, int64_t* upper,

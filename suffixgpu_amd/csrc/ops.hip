@@ -398,7 +398,7 @@ extern "C" int sfx_sa_search(const int32_t* sa, const int32_t* corpus,
                              int64_t batch, int64_t width,
                              const int64_t* plen, int64_t* lower,
                              int64_t* upper, hipStream_t stream) {
-  if (batch < 0 || n < 1 || width < 0) return SFX_EINVAL;
+  if (batch < 0 || n < 1 || n > 0x7fffffffLL || width < 0) return SFX_EINVAL;
   if (batch == 0) return 0;
   if (!sa || !corpus || !plen || !lower || !upper ||
       (width > 0 && !pattern))

@@ -80,36 +80,37 @@ __device__ __forceinline__ int cmp_suffix_key(
   return 0;
 }
 
-// Probe k of NP (k < NP) splitting [lo, hi]: lo + floor((hi - lo) * f_k)
-// with f_k = floor(2^32 (k + 1) / (NP + 1)) / 2^32, one 32x32->64 multiply
-// (ranges stay below 2^31).  The probes ascend with k and stay below hi,
-// which is all the search needs.
-template <int NP>
-__device__ __forceinline__ int64_t kary_probe(int64_t lo, int64_t hi, int k) {
-  const uint32_t f = (uint32_t)((((uint64_t)(k + 1)) << 32) / (NP + 1));
-  return lo + (int64_t)(((uint64_t)(uint32_t)(hi - lo) * f) >> 32);
+// Probe k of a range [lo, hi) cut by NP probes: lo + floor((hi - lo) *
+// (k + 1) c / 2^32) with c = floor(2^32 / (NP + 1)), one 32x32->64
+// multiply (ranks stay below 2^31).  kc = (k + 1) c < 2^32, so the probes
+// ascend with k and stay below hi, which is all the search needs.
+__device__ __forceinline__ uint32_t kary_at(uint32_t lo, uint32_t hi,
+                                            uint32_t kc) {
+  return lo + (uint32_t)(((uint64_t)(hi - lo) * kc) >> 32);
 }
 
 // Narrow [lo, hi] (answer inside; ranks < lo false, >= hi true) with the
-// predicate bits of NP probes (bit k = probe k true).
-template <int NP>
-__device__ __forceinline__ void kary_update(int64_t& lo, int64_t& hi,
-                                            uint32_t bits) {
-  if (bits == 0) {
-    lo = kary_probe<NP>(lo, hi, NP - 1) + 1;
-    return;
-  }
-  const int k = __builtin_ctz(bits);
-  const int64_t nh = kary_probe<NP>(lo, hi, k);
-  if (k > 0) lo = kary_probe<NP>(lo, hi, k - 1) + 1;
-  hi = nh;
+// predicate bits of np probes of scale c (bit k = probe k true).
+__device__ __forceinline__ void kary_narrow(uint32_t& lo, uint32_t& hi,
+                                            uint32_t bits, int np,
+                                            uint32_t c) {
+  const int k = bits ? __builtin_ctz(bits) : np;  // first true probe
+  const uint32_t nlo = k > 0 ? kary_at(lo, hi, (uint32_t)k * c) + 1 : lo;
+  const uint32_t nhi = bits ? kary_at(lo, hi, (uint32_t)(k + 1) * c) : hi;
+  lo = nlo;
+  hi = nhi;
 }
 
 // Exact lower bound (first rank with cmp >= 0) and upper bound (first rank
 // with cmp > 0) of one pattern.  Called by all G lanes of an aligned group
 // with identical arguments; returns the bounds on every lane of the group.
 // keys (kw = key width, 4 <= kw <= 32, kw % 4 == 0) may be NULL: then the
-// comparison reads sa and the corpus.
+// comparison reads sa and the corpus.  n < 2^31.
+//
+// The groups of a wave are in different phases (both bounds on one range,
+// one bound left, or the bounds split), so each lane's probe and both
+// bounds' updates are computed for every phase with selects: no phase
+// branches for the wave to run one after another.
 template <int G, class PatFn>
 __device__ __forceinline__ void kary_bounds(
     const int32_t* __restrict__ sa, const int32_t* __restrict__ corpus,
@@ -117,6 +118,8 @@ __device__ __forceinline__ void kary_bounds(
     int plen, int64_t& lower, int64_t& upper) {
   static_assert(G >= 2 && G <= 32 && (64 % G) == 0, "group size");
   constexpr int H = G / 2;
+  constexpr uint32_t cG = (uint32_t)((1ull << 32) / (G + 1));
+  constexpr uint32_t cH = (uint32_t)((1ull << 32) / (H + 1));
   const int ln = lane_id();
   const int gl = ln % G;
   const int gbase = ln - gl;
@@ -125,40 +128,40 @@ __device__ __forceinline__ void kary_bounds(
 #pragma unroll
     for (int j = 0; j < 32; ++j) pt[j] = j < plen ? pat_at(j) : 0;
   }
-  int64_t lo1 = 0, hi1 = n, lo2 = 0, hi2 = n;
+  uint32_t lo1 = 0, hi1 = (uint32_t)n, lo2 = 0, hi2 = (uint32_t)n;
   while (lo1 < hi1 || lo2 < hi2) {
     const bool shared = lo1 == lo2 && hi1 == hi2;
     const bool only1 = !shared && lo2 == hi2;
     const bool only2 = !shared && lo1 == hi1;
-    int64_t probe;
-    if (shared || only1) {
-      probe = kary_probe<G>(lo1, hi1, gl);
-    } else if (only2) {
-      probe = kary_probe<G>(lo2, hi2, gl);
-    } else {
-      probe = gl >= H ? kary_probe<H>(lo2, hi2, gl - H)
-                      : kary_probe<H>(lo1, hi1, gl);
-    }
-    const int c =
+    const bool split = !shared && !only1 && !only2;
+    // G probes over the one live range, or G/2 per bound once they split
+    const bool upper_half = split && gl >= H;
+    const bool use2 = only2 || upper_half;
+    const uint32_t c = split ? cH : cG;
+    const int np = split ? H : G;
+    const int k = upper_half ? gl - H : gl;
+    const int64_t probe = (int64_t)kary_at(use2 ? lo2 : lo1, use2 ? hi2 : hi1,
+                                           (uint32_t)(k + 1) * c);
+    const int cv =
         keys ? cmp_suffix_key(keys, kw, sa, corpus, n, probe, pt, pat_at,
                               plen)
              : cmp_suffix(sa, corpus, n, probe, pat_at, plen);
-    const uint64_t m1 = ballot(c >= 0);
-    const uint64_t m2 = ballot(c > 0);
+    const uint64_t m1 = ballot(cv >= 0);
+    const uint64_t m2 = ballot(cv > 0);
     const uint32_t full = G == 32 ? 0xffffffffu : ((1u << G) - 1u);
+    const uint32_t half = (1u << H) - 1u;
     const uint32_t g1 = (uint32_t)(m1 >> gbase) & full;
     const uint32_t g2 = (uint32_t)(m2 >> gbase) & full;
-    if (shared) {
-      kary_update<G>(lo1, hi1, g1);
-      kary_update<G>(lo2, hi2, g2);
-    } else if (only1) {
-      kary_update<G>(lo1, hi1, g1);
-    } else if (only2) {
-      kary_update<G>(lo2, hi2, g2);
-    } else {
-      const uint32_t half = (1u << H) - 1u;
-      kary_update<H>(lo1, hi1, g1 & half);
-      kary_update<H>(lo2, hi2, (g2 >> H) & half);
+    uint32_t l1 = lo1, h1 = hi1, l2 = lo2, h2 = hi2;
+    kary_narrow(l1, h1, split ? (g1 & half) : g1, np, c);
+    kary_narrow(l2, h2, split ? ((g2 >> H) & half) : g2, np, c);
+    if (!only2) {
+      lo1 = l1;
+      hi1 = h1;
+    }
+    if (!only1) {
+      lo2 = l2;
+      hi2 = h2;
     }
   }
   lower = lo1;
