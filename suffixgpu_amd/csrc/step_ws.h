@@ -39,11 +39,13 @@ struct StepWs {
 // The delta scan of a row is split over up to kMaxDeltaParts workgroups,
 // each taking an equal share of the live delta (a device value).  The
 // split stops where the step's grid would exceed kGridSlots workgroups:
-// one per CU of an MI355X (256 CUs), since two co-resident workgroups of
-// these latency-bound roles slow each other down more than a split gains.
+// 1.25 per CU of an MI355X (256 CUs).  At B = 64 that is three parts (320
+// workgroups, a quarter of the CUs holding two, in half-CU LDS layouts):
+// step p50 49.2 -> 47.5 us against two parts at one workgroup per CU;
+// four parts (384) measured 50.4 us.
 constexpr int kMaxDeltaParts = 4;
 constexpr int64_t kDeltaPartSpan = 16384;
-constexpr int64_t kGridSlots = 256;
+constexpr int64_t kGridSlots = 320;
 
 __host__ __device__ inline int delta_parts_for(int64_t B,
                                                int64_t delta_capacity) {
