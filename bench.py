@@ -59,6 +59,17 @@ def parse():
                     help="for rocprofv3 --pmc passes: a copy of known size, "
                     "a few step launches, then two SA rebuilds of the "
                     "corpus as the index runs them; prints no JSON")
+    ap.add_argument("--sync-check", action="store_true",
+                    help="for rocprofv3 --hip-trace: 20 eager "
+                    "propose_with_update calls, then 20 graph replays, each "
+                    "section between device synchronisations; prints no "
+                    "JSON")
+    ap.add_argument("--summarize-api", metavar="TRACE_DIR",
+                    help="HIP API calls per section of a --sync-check "
+                    "trace (rocprofv3 --hip-trace CSV output)")
+    ap.add_argument("--summarize-counters", metavar="PMC_DIR",
+                    help="mean of every counter per dispatch, per kernel, "
+                    "from one rocprofv3 --pmc output of --pmc-workload")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR",
                                                          "WRITE_DIR"),
                     help="turn two rocprofv3 --pmc outputs (FETCH_SIZE, "
@@ -199,6 +210,13 @@ def main() -> int:
     if args.summarize_pmc:
         print(json.dumps(summarize_pmc(*args.summarize_pmc), indent=1))
         return 0
+    if args.summarize_counters:
+        print(json.dumps(summarize_counters(args.summarize_counters),
+                         indent=1))
+        return 0
+    if args.summarize_api:
+        print(json.dumps(summarize_api(args.summarize_api), indent=1))
+        return 0
     if args.gpus != 1:
         print(json.dumps({"error": "this drafter benchmark runs on exactly "
                           "one GPU (the workload is one GPU's rows); "
@@ -234,6 +252,8 @@ def main() -> int:
     log(f"index: active_len={gi.active_len} delta_len={gi.delta_len}")
     if args.pmc_workload:
         return pmc_workload(d, w, dev)
+    if args.sync_check:
+        return sync_check(d, w, dev)
 
     bt = w.batch
     tokens0 = torch.from_numpy(bt.tokens).to(dev)
@@ -665,6 +685,115 @@ def pmc_workload(d, w, dev) -> int:
         f"bytes, {PMC_STEP_LAUNCHES} step launches, {PMC_SA_BUILDS} SA "
         f"rebuilds of m={m} ({needed + 2} rounds)")
     return 0
+
+
+SYNC_CHECK_STEPS = 20
+
+
+def sync_check(d, w, dev) -> int:
+    """Host-side API calls of the step, for a HIP API trace: eager
+    propose_with_update calls, then replays of one captured step, each
+    section bracketed by device synchronisations.  The step itself must
+    make no synchronising call and no device-to-host copy."""
+    import torch
+    bt = w.batch
+    buf = torch.from_numpy(bt.tokens).to(dev)
+    nt = torch.from_numpy(bt.num_tokens).to(dev)
+    sampled = torch.from_numpy(bt.sampled).to(dev)
+    for _ in range(3):
+        d.propose_with_update(nt, buf, sampled)
+    torch.cuda.synchronize()
+    for _ in range(SYNC_CHECK_STEPS):
+        d.propose_with_update(nt, buf, sampled)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        d.propose_with_update(nt, buf, sampled)
+    graph.replay()
+    torch.cuda.synchronize()
+    for _ in range(SYNC_CHECK_STEPS):
+        graph.replay()
+    torch.cuda.synchronize()
+    log(f"sync check done: {SYNC_CHECK_STEPS} eager steps, "
+        f"{SYNC_CHECK_STEPS} graph replays")
+    return 0
+
+
+# HIP API calls that block the host on the device or copy to the host.
+_BLOCKING = ("Synchronize", "hipMemcpy", "hipEventQuery", "hipStreamQuery",
+             "hipMallocHost", "hipHostMalloc", "hipMalloc", "hipFree")
+
+
+def summarize_api(trace_dir: str) -> dict:
+    """Per section of a --sync-check run (the spans between consecutive
+    hipDeviceSynchronize calls of the main thread), the HIP API calls made,
+    and which of them would block or allocate."""
+    import csv
+    from collections import Counter
+    files = sorted(Path(trace_dir).rglob("*hip_api_trace.csv"))
+    if not files:
+        raise SystemExit(f"no hip_api_trace.csv under {trace_dir}")
+    calls = []
+    for f in files:
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                calls.append((int(r["Start_Timestamp"]), r["Thread_Id"],
+                              r["Function"]))
+    calls.sort()
+    syncs = [c for c in calls if c[2] == "hipDeviceSynchronize"]
+    main_tid = Counter(c[1] for c in syncs).most_common(1)[0][0]
+    seq = [c for c in calls if c[1] == main_tid]
+    marks = [i for i, c in enumerate(seq) if c[2] == "hipDeviceSynchronize"]
+    sections = []
+    for a, b in zip(marks, marks[1:]):
+        hist = Counter(c[2] for c in seq[a + 1:b])
+        if not hist:
+            continue
+        sections.append({
+            "calls": dict(hist.most_common()),
+            "blocking_or_allocating": sorted(
+                n for n in hist if any(x in n for x in _BLOCKING))})
+    # The last two sections are the timed eager calls and the replays
+    # (capture and its first replay sit between them).
+    eager = [s for s in sections
+             if s["calls"].get("hipExtLaunchKernel", 0)
+             + s["calls"].get("hipLaunchKernel", 0)
+             + s["calls"].get("hipModuleLaunchKernel", 0)
+             >= SYNC_CHECK_STEPS]
+    replay = [s for s in sections
+              if s["calls"].get("hipGraphLaunch", 0) == SYNC_CHECK_STEPS]
+    return {"steps_per_section": SYNC_CHECK_STEPS,
+            "eager_steps": eager[-1] if eager else None,
+            "graph_replays": replay[-1] if replay else None,
+            "sections": len(sections)}
+
+
+def summarize_counters(out_dir: str) -> dict:
+    """{kernel: {"dispatches": n, counter: mean per dispatch}} over every
+    counter in one rocprofv3 --pmc CSV output directory (values summed over
+    the counter's instances within a dispatch)."""
+    import csv
+    from collections import defaultdict
+    files = sorted(Path(out_dir).rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {out_dir}")
+    per = defaultdict(float)            # (dispatch, kernel, counter) -> sum
+    for f in files:
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                name = r["Kernel_Name"].split("(")[0].replace("void ", "")
+                per[(int(r["Dispatch_Id"]), name, r["Counter_Name"])] += \
+                    float(r["Counter_Value"])
+    agg = defaultdict(lambda: defaultdict(list))
+    for (disp, name, ctr), v in per.items():
+        agg[name][ctr].append(v)
+    out = {}
+    for name, ctrs in sorted(agg.items()):
+        n = max(len(v) for v in ctrs.values())
+        out[name] = {"dispatches": n}
+        out[name].update({c: round(sum(v) / len(v), 1)
+                          for c, v in sorted(ctrs.items())})
+    return out
 
 
 def _pmc_rows(out_dir: str, counter: str):
