@@ -242,10 +242,15 @@ __global__ __launch_bounds__(NT) void k_rs_hist(
   const int64_t A = state[slot];
   const int64_t base = (int64_t)blockIdx.x * kTile;
   if (base >= A) return;
-  // Waves w, w + kRsHists, ... share a histogram (LDS atomics collide only
-  // on equal digits); the sub-histograms are summed at the end.
+  // Waves w, w + kRsHists, ... share a histogram; the sub-histograms are
+  // summed at the end.  A wave's lanes hold consecutive entries, and equal
+  // keys sit next to each other in every pass (suffixes inside repeated
+  // text share their key until h outgrows the repeat), so each run of
+  // equal digits adds its length with one atomic from its first lane:
+  // same-address LDS atomics within a wave would serialise.
   __shared__ uint32_t h[kRsHists][kRadix];
   const int tid = threadIdx.x;
+  const int ln = lane_id();
   const int hw = (tid / kWave) % kRsHists;
   for (int e = tid; e < kRsHists * kRadix; e += NT) (&h[0][0])[e] = 0;
   uint32_t d[kItems];
@@ -256,8 +261,15 @@ __global__ __launch_bounds__(NT) void k_rs_hist(
   }
   __syncthreads();
 #pragma unroll
-  for (int r = 0; r < kItems; ++r)
-    if (d[r] < kRadix) atomicAdd(&h[hw][d[r]], 1u);
+  for (int r = 0; r < kItems; ++r) {
+    const uint32_t prev = __shfl_up(d[r], 1);
+    const bool start = ln == 0 || prev != d[r];
+    const uint64_t starts = ballot(start);
+    const uint64_t after = ln == kWave - 1 ? 0ull : starts >> (ln + 1);
+    const uint32_t len =
+        after ? (uint32_t)__builtin_ctzll(after) + 1u : (uint32_t)(kWave - ln);
+    if (start && d[r] < kRadix) atomicAdd(&h[hw][d[r]], len);
+  }
   __syncthreads();
   if (tid < kRadix) {
     uint32_t sum = 0;
@@ -318,6 +330,7 @@ __global__ __launch_bounds__(NT) void k_rs_scatter(
   const int64_t wbase = base + (int64_t)wv * kSpan;
   uint64_t k[kSteps];
   uint32_t v[kSteps];
+  uint64_t peers[kSteps];  // lanes of the same step holding the same digit
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
     const int64_t idx = wbase + s * kWave + ln;
@@ -329,11 +342,16 @@ __global__ __launch_bounds__(NT) void k_rs_scatter(
   uint32_t tot;
   const uint32_t dbase =
       block_exscan1<NT>(tid < kRadix ? rowsum[tid] : 0u, red, &tot);
-  // block_exscan1 ends with a barrier: the counters are zeroed.
+  // block_exscan1 ends with a barrier: the counters are zeroed.  Each
+  // digit's count of a step is added once, by its lowest lane (equal
+  // digits would otherwise serialise on one LDS address).
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
-    if (wbase + s * kWave + ln < A)
-      atomicAdd(&woff[wv][digit_of(k[s], sh)], 1u);
+    const bool act = wbase + s * kWave + ln < A;
+    const uint32_t d = digit_of(k[s], sh);
+    peers[s] = match_digit(act, d);
+    if (act && rank_lt(peers[s]) == 0)
+      atomicAdd(&woff[wv][d], (uint32_t)popc(peers[s]));
   }
   __syncthreads();
   if (tid < kRadix) {
@@ -350,15 +368,14 @@ __global__ __launch_bounds__(NT) void k_rs_scatter(
   for (int s = 0; s < kSteps; ++s) {
     const bool act = wbase + s * kWave + ln < A;
     const uint32_t d = digit_of(k[s], sh);
-    const uint64_t peers = match_digit(act, d);
-    const int rk = rank_lt(peers);
+    const int rk = rank_lt(peers[s]);
     if (act) {
       const uint32_t p = woff[wv][d] + (uint32_t)rk;
       kout[p] = k[s];
       vout[p] = v[s];
     }
     wave_lds_sync();  // every lane has read its offset
-    if (act && rk == 0) woff[wv][d] += (uint32_t)popc(peers);
+    if (act && rk == 0) woff[wv][d] += (uint32_t)popc(peers[s]);
     wave_lds_sync();
   }
 }
