@@ -78,12 +78,15 @@ def parse():
 
 
 # --------------------------------------------------------------- roofline
-def local_algorithmic_bytes(new_counts, accepted, k) -> int:
+def local_algorithmic_bytes(new_counts, accepted, k, b=None,
+                            s=None) -> int:
     """Rows scanned once + sampled block read + scatter writes + draft,
-    num_valid and counts (in/out)."""
-    n_eff = np.minimum(new_counts.astype(np.int64), S)
-    return int(4 * n_eff.sum() + 4 * B * T_SAMPLED + 4 * accepted.sum()
-               + 4 * B * (k + 3))
+    num_valid and counts (in/out), for b rows of s tokens."""
+    b = B if b is None else b
+    s = S if s is None else s
+    n_eff = np.minimum(new_counts.astype(np.int64), s)
+    return int(4 * n_eff.sum() + 4 * b * T_SAMPLED + 4 * accepted.sum()
+               + 4 * b * (k + 3))
 
 
 def reference_probe_footprint(sa, corpus, rpat, plen, P):
@@ -319,6 +322,8 @@ def main() -> int:
     conc = concurrent_rebuild(graph, w, dev, build_ms["corpus_hinted"][1])
     log(f"copy peak {copy_gbps:.0f} GB/s; cold-cache step p50 "
         f"{cold_p50:.2f} us; rebuild during replays: {conc}")
+    c5 = c5_local_step(dev, args.kernel_reps)
+    log(f"local step at B={C5_B} S={C5_S}: {c5}")
     e2e = None
     if not args.no_e2e:
         e2e = e2e_loop(dev, args.e2e_steps)
@@ -369,6 +374,7 @@ def main() -> int:
         "cold_cache_step_p50_us": round(cold_p50, 3),
         "adapter_step_p50_us": round(adapter_p50, 3),
         "sa_rebuild_concurrent": conc,
+        "c5_local_step": c5,
         "e2e_decode_loop": e2e,
         "cpu_baseline": cpu,
     }
@@ -638,6 +644,43 @@ def step_kernel_us(d, dev, tokens0, nt, sampled, reps):
     return statistics.mean(e0.elapsed_time(e1) * 1e3 for e0, e1 in evs)
 
 
+# The local step at the decode-loop shape (B=256 rows of S=16384 tokens,
+# num_tokens uniform in [4096, 16384], global memory off): the shape where
+# the token rows alone are 16 MiB, for a per-kernel bandwidth fraction.
+C5_B, C5_S, C5_LO = 256, 16384, 4096
+
+
+def c5_local(dev):
+    """(drafter, tokens, counts, sampled) of the local-only B=256 S=16384
+    step."""
+    import torch
+    from suffixgpu_amd import SuffixGPUDrafter, synth
+    bt = synth.local_zipf(seed=5, b=C5_B, s=C5_S, lo=C5_LO, t=T_SAMPLED)
+    d = SuffixGPUDrafter(device=dev, enable_global=False, **CFG)
+    return (d, torch.from_numpy(bt.tokens).to(dev),
+            torch.from_numpy(bt.num_tokens).to(dev),
+            torch.from_numpy(bt.sampled).to(dev))
+
+
+def c5_local_step(dev, reps: int) -> dict:
+    """Kernel time (HIP events, direct launches), algorithmic bytes and
+    the HBM roofline fraction of the local step at B=256, S=16384."""
+    d, tok, nt, sampled = c5_local(dev)
+    us = step_kernel_us(d, dev, tok, nt, sampled, reps)
+    buf = tok.clone()
+    _, _, new = d.propose_with_update(nt, buf, sampled)
+    acc = (sampled.cpu().numpy() != -1).sum(1)
+    nbytes = local_algorithmic_bytes(new.cpu().numpy(), acc, CFG["k"],
+                                     C5_B, C5_S)
+    gbps = nbytes / (us * 1e-6) / 1e9
+    return {"workload": f"local-only propose_with_update, B={C5_B} "
+                        f"S={C5_S}, num_tokens U[{C5_LO},{C5_S}]",
+            "kernel_us": round(us, 3), "algorithmic_bytes": nbytes,
+            "achieved_gbps": round(gbps, 1),
+            "frac": round(gbps / HBM_PEAK_GBPS, 5),
+            "traffic": load_traffic("k_step_c5_local")}
+
+
 # Calibration copy for the PMC passes: bitwise_not over 2^26 int32 reads
 # and writes exactly 256 MiB each.
 PMC_COPY_ELEMS = 1 << 26
@@ -680,6 +723,10 @@ def pmc_workload(d, w, dev) -> int:
     final, needed = build_state(ws, m)
     for _ in range(PMC_SA_BUILDS):
         build_suffix_array_rounds(text, m, out, ws, needed + 2)
+    torch.cuda.synchronize()
+    c5d, c5t, c5n, c5s = c5_local(dev)
+    for _ in range(PMC_STEP_LAUNCHES):
+        c5d.propose_with_update(c5n, c5t, c5s)
     torch.cuda.synchronize()
     log(f"pmc workload done: 3 calibration copies of {PMC_COPY_ELEMS * 4} "
         f"bytes, {PMC_STEP_LAUNCHES} step launches, {PMC_SA_BUILDS} SA "
@@ -769,9 +816,9 @@ def summarize_api(trace_dir: str) -> dict:
 
 
 def summarize_counters(out_dir: str) -> dict:
-    """{kernel: {"dispatches": n, counter: mean per dispatch}} over every
-    counter in one rocprofv3 --pmc CSV output directory (values summed over
-    the counter's instances within a dispatch)."""
+    """{"kernel grid=G": {"dispatches": n, counter: mean per dispatch}}
+    over every counter in one rocprofv3 --pmc CSV output directory (values
+    summed over the counter's instances within a dispatch)."""
     import csv
     from collections import defaultdict
     files = sorted(Path(out_dir).rglob("*counter_collection.csv"))
@@ -782,6 +829,7 @@ def summarize_counters(out_dir: str) -> dict:
         with open(f, newline="") as fh:
             for r in csv.DictReader(fh):
                 name = r["Kernel_Name"].split("(")[0].replace("void ", "")
+                name += f" grid={r.get('Grid_Size', '?')}"
                 per[(int(r["Dispatch_Id"]), name, r["Counter_Name"])] += \
                     float(r["Counter_Value"])
     agg = defaultdict(lambda: defaultdict(list))
@@ -825,7 +873,10 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> dict:
                               ("write", write_dir, "WRITE_SIZE")):
         rows = _pmc_rows(d_, counter)
         cal = [v for k, v in rows if "bitwise_not" in k]
-        step = [v for k, v in rows if "k_step" in k]
+        # the first PMC_STEP_LAUNCHES step launches are the B=64 global-on
+        # step; the ones after them the B=256 S=16384 local step
+        steps = [v for k, v in rows if "k_step" in k]
+        step, c5 = steps[:PMC_STEP_LAUNCHES], steps[PMC_STEP_LAUNCHES:]
         # SA builds in dispatch order, each starting with k_sa_range; the
         # last PMC_SA_BUILDS are the rebuilds as the index runs them
         builds: list[list[float]] = []
@@ -842,15 +893,19 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> dict:
         step_b = statistics.mean(step) * 1024.0
         sa_b = statistics.mean(
             sum(b) for b in builds[-PMC_SA_BUILDS:]) * 1024.0
+        c5_b = statistics.mean(c5) * 1024.0 if c5 else 0.0
         out[name] = {"counter": counter, "calibration_bytes": cal_b,
                      "scale": scale, "step_raw_bytes": step_b,
                      "step_bytes": step_b * scale,
                      "dispatches": len(step),
-                     "sa_build_bytes": sa_b * scale}
+                     "sa_build_bytes": sa_b * scale,
+                     "c5_local_dispatches": len(c5),
+                     "c5_local_bytes": c5_b * scale}
     total = out["fetch"]["step_bytes"] + out["write"]["step_bytes"]
     sa_total = out["fetch"]["sa_build_bytes"] + out["write"]["sa_build_bytes"]
+    c5_total = out["fetch"]["c5_local_bytes"] + out["write"]["c5_local_bytes"]
     return {"k_step": round(total), "sa_rebuild": round(sa_total),
-            "detail": out}
+            "k_step_c5_local": round(c5_total) or None, "detail": out}
 
 
 def kernel_timings(d, dev, tokens0, nt, sampled, reps):

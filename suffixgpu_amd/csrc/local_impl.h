@@ -118,15 +118,18 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
   const int64_t q = st.q;
 
   // Stage the row, then apply this step's scatter (proposer.py:162-184).
+  // Only positions below min(q, S) are ever read (match_back, pattern and
+  // continuations all stop at q), so the rest of the row stays in HBM.
   int32_t* grow = a.bt.tokens + (int64_t)b * S;
   const bool vec4 = (S & 3) == 0 && (((uintptr_t)grow) & 15) == 0;
   if (!kStream) {
+    const int qs = (int)(q < 0 ? 0 : (q < S ? q : S));
     if (vec4) {
       const int4* src = reinterpret_cast<const int4*>(grow);
       int4* dst = reinterpret_cast<int4*>(row);
-      for (int i = tid; i < S / 4; i += NT) dst[i] = src[i];
+      for (int i = tid; i < (qs + 3) / 4; i += NT) dst[i] = src[i];
     } else {
-      for (int i = tid; i < S; i += NT) row[i] = grow[i];
+      for (int i = tid; i < qs; i += NT) row[i] = grow[i];
     }
     __syncthreads();
   }
