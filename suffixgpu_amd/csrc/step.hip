@@ -1,8 +1,9 @@
 // Fused decode step (suffix_gpu/proposer.py:186-327) in one launch.
 //
 // With global memory each request row gets 2 + dparts 512-thread
-// workgroups, interleaved: SA interval search, dparts delta-scan parts,
-// local match.  The SA and delta workgroups hand over through the
+// workgroups: SA interval search, dparts delta-scan parts, local match,
+// interleaved by row (or ordered by role when the grid exceeds two
+// workgroups per CU).  The SA and delta workgroups hand over through the
 // workspace and the last of them merges the row's global candidates;
 // local and global results meet the same way and the later one writes the
 // row's draft.  Nothing waits on another workgroup,
@@ -22,6 +23,7 @@ struct StepArgs {
   LocalArgs l;
   GlobalArgs g;
   int global_on;
+  int role_major;  // blocks ordered by role (local, SA, delta parts), not row
 };
 
 template <bool kStream>
@@ -32,8 +34,19 @@ __global__ __launch_bounds__(kGlobalThreads) void k_step(StepArgs a) {
     return;
   }
   const int per = 2 + a.g.dparts;
-  const int b = (int)(blockIdx.x / per);
-  const int role = (int)(blockIdx.x % per);  // 0: SA, 1..dparts: delta
+  int b, role;  // role 0: SA, 1..dparts: delta parts, per - 1: local
+  if (a.role_major) {
+    // A grid beyond the workgroups that run at once finishes in waves:
+    // dispatched first, the longest roles (local, then SA) start at once
+    // and the shorter delta parts fill the slots they free.
+    const int B = (int)a.g.B;
+    const int slot = (int)(blockIdx.x / B);
+    b = (int)(blockIdx.x % B);
+    role = slot == 0 ? per - 1 : slot - 1;
+  } else {
+    b = (int)(blockIdx.x / per);
+    role = (int)(blockIdx.x % per);
+  }
   if (role == per - 1)
     local_body<kStream>(a.l, smem, b);
   else
@@ -113,6 +126,8 @@ extern "C" int sfx_propose_step(const sfx_params* p, const sfx_index* ix,
   if (lds > kMaxLds) return SFX_EINVAL;
   if (bt->batch == 0) return 0;
   lds = one_per_cu_lds(lds, blocks);
+  a.role_major =
+      global_on && blocks > 2u * (unsigned)device_cus() ? 1 : 0;
   if (a.l.chunk == 0) {
     static std::atomic<uint64_t> lds_opt{0};
     allow_max_lds((const void*)k_step<false>, lds_opt);

@@ -43,16 +43,24 @@ struct StepWs {
 // workgroups, a quarter of the CUs holding two, in half-CU LDS layouts):
 // step p50 49.2 -> 47.5 us against two parts at one workgroup per CU;
 // four parts (384) measured 50.4 us.
+// A batch whose grid exceeds two workgroups per CU even with one part
+// (3 B > 512) runs in waves of workgroups anyway; its split stops at
+// kWaveGridSlots (four per CU) instead.  At B = 256, D = 2^16 with a full
+// delta that is two parts: step 123 -> 97 us against one part; three
+// parts measured 103 us, four 107 us.
 constexpr int kMaxDeltaParts = 4;
 constexpr int64_t kDeltaPartSpan = 16384;
+constexpr int64_t kCus = 256;
 constexpr int64_t kGridSlots = 320;
+constexpr int64_t kWaveGridSlots = 4 * kCus;
 
 __host__ __device__ inline int delta_parts_for(int64_t B,
                                                int64_t delta_capacity) {
   const int64_t n = (delta_capacity > 0 ? delta_capacity : 0) + 1;
   int64_t parts = (n + kDeltaPartSpan - 1) / kDeltaPartSpan;
   parts = parts < 1 ? 1 : (parts > kMaxDeltaParts ? kMaxDeltaParts : parts);
-  while (parts > 1 && B * (2 + parts) > kGridSlots) --parts;
+  const int64_t slots = 3 * B > 2 * kCus ? kWaveGridSlots : kGridSlots;
+  while (parts > 1 && B * (2 + parts) > slots) --parts;
   return (int)parts;
 }
 
