@@ -2,8 +2,7 @@
 //
 // With global memory each request row gets 2 + dparts 512-thread
 // workgroups: SA interval search, dparts delta-scan parts, local match,
-// interleaved by row (or ordered by role when the grid exceeds two
-// workgroups per CU).  The SA and delta workgroups hand over through the
+// ordered by role.  The SA and delta workgroups hand over through the
 // workspace and the last of them merges the row's global candidates;
 // local and global results meet the same way and the later one writes the
 // row's draft.  Nothing waits on another workgroup,
@@ -23,7 +22,6 @@ struct StepArgs {
   LocalArgs l;
   GlobalArgs g;
   int global_on;
-  int role_major;  // blocks ordered by role (local, SA, delta parts), not row
 };
 
 template <bool kStream>
@@ -33,21 +31,18 @@ __global__ __launch_bounds__(kGlobalThreads) void k_step(StepArgs a) {
     local_body<kStream>(a.l, smem, blockIdx.x);
     return;
   }
+  // Blocks are ordered by role, longest first: local, SA, then the delta
+  // parts (role 0: SA, 1..dparts: delta parts, per - 1: local).  A grid
+  // beyond the workgroups that run at once finishes in waves, and so the
+  // longest roles start at once while the shorter delta parts fill the
+  // slots they free: B = 256, S = 16384 with two delta parts measured
+  // 112-115 us with blocks ordered row by row, 94-97 us so.  At B = 64
+  // (one wave) the two orders measured the same within 0.3 us.
   const int per = 2 + a.g.dparts;
-  int b, role;  // role 0: SA, 1..dparts: delta parts, per - 1: local
-  if (a.role_major) {
-    // A grid beyond the workgroups that run at once finishes in waves:
-    // dispatched first, the longest roles (local, then SA) start at once
-    // and the shorter delta parts fill the slots they free (B = 256,
-    // S = 16384, two delta parts: 112-115 us row by row, 94-97 us so).
-    const int B = (int)a.g.B;
-    const int slot = (int)(blockIdx.x / B);
-    b = (int)(blockIdx.x % B);
-    role = slot == 0 ? per - 1 : slot - 1;
-  } else {
-    b = (int)(blockIdx.x / per);
-    role = (int)(blockIdx.x % per);
-  }
+  const int B = (int)a.g.B;
+  const int slot = (int)(blockIdx.x / B);
+  const int b = (int)(blockIdx.x % B);
+  const int role = slot == 0 ? per - 1 : slot - 1;
   if (role == per - 1)
     local_body<kStream>(a.l, smem, b);
   else
@@ -127,8 +122,6 @@ extern "C" int sfx_propose_step(const sfx_params* p, const sfx_index* ix,
   if (lds > kMaxLds) return SFX_EINVAL;
   if (bt->batch == 0) return 0;
   lds = one_per_cu_lds(lds, blocks);
-  a.role_major =
-      global_on && blocks > 2u * (unsigned)device_cus() ? 1 : 0;
   if (a.l.chunk == 0) {
     static std::atomic<uint64_t> lds_opt{0};
     allow_max_lds((const void*)k_step<false>, lds_opt);
