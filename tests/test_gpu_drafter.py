@@ -318,3 +318,24 @@ def test_step_dense_grid_vs_oracle(gpu, s):
     np.testing.assert_array_equal(N(draft), ed)
     np.testing.assert_array_equal(N(nv), env)
     assert (env > 0).sum() > 10
+
+
+@pytest.mark.parametrize("b", [180, 256])
+def test_step_wave_grid_split_delta_vs_oracle(gpu, b):
+    """Batches whose grid runs in waves (3 B > 512) split a 2^16-capacity
+    delta over several parts within 1024 workgroups (B=180: 3 parts, 900
+    workgroups; B=256: 2 parts, 1024), dispatched by role."""
+    w, d, o = _global_pair(gpu, seed=12, b=b, s=2048,
+                           delta_capacity=1 << 16)
+    assert d.global_index.delta_len > 30000
+    bt = w.batch
+    tg = T(bt.tokens, gpu)
+    draft, nv, new = d.propose_with_update(T(bt.num_tokens, gpu), tg,
+                                           T(bt.sampled, gpu))
+    to = bt.tokens.copy()
+    ed, env, enew = o.propose_with_update(bt.num_tokens, to, bt.sampled)
+    np.testing.assert_array_equal(N(tg), to)
+    np.testing.assert_array_equal(N(new), enew)
+    np.testing.assert_array_equal(N(draft), ed)
+    np.testing.assert_array_equal(N(nv), env)
+    assert (env > 0).sum() > b // 2
