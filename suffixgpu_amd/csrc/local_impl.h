@@ -229,8 +229,16 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
   // histogram, then one ballot per threshold (#{mb >= L} is monotone in L,
   // so the largest qualifying L is the number of qualifying L).
   if (wv == 0) {
+    // P <= 64: lane ln holds #{mb >= P - ln} in a register (one DPP scan);
+    // longer patterns keep the suffix counts in hist[].
+    const bool in_reg = P <= kWave;
+    int sfx = 0;
+    if (in_reg) {
+      const int Lv = P - ln;
+      sfx = (int)wave_incl_scan(Lv >= 1 ? (uint32_t)hist[Lv] : 0u);
+    }
     int carry = 0;
-    for (int top = P; top >= 1; top -= kWave) {
+    for (int top = in_reg ? 0 : P; top >= 1; top -= kWave) {
       const int Lv = top - ln;
       int x = Lv >= 1 ? hist[Lv] : 0;
 #pragma unroll
@@ -252,9 +260,13 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
       int v = 0;
       if (thr <= w) {
         const int t = thr < 1 ? 1 : thr;
-        for (int base = 1; base <= P; base += kWave) {
-          const int Lv = base + ln;
-          v += popc(ballot(Lv <= P && hist[Lv] >= t));
+        if (in_reg) {
+          v = popc(ballot(ln < P && sfx >= t));
+        } else {
+          for (int base = 1; base <= P; base += kWave) {
+            const int Lv = base + ln;
+            v += popc(ballot(Lv <= P && hist[Lv] >= t));
+          }
         }
       }
       if (!(v >= p.min_match_len && st.mask)) v = 0;
