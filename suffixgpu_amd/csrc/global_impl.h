@@ -198,16 +198,12 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
     }
     __syncthreads();
   }
-  mx = wave_max_i32(mx);
+  // match lengths are >= 0: the unsigned DPP max is the signed one
+  mx = (int)wave_all_max((uint32_t)mx);
   if (ln == 0) red[wv] = mx;
   __syncthreads();
-  if (tid == 0) {
-    int m = 0;
-    for (int w = 0; w < NW; ++w) m = max(m, red[w]);
-    misc[0] = m;
-  }
-  __syncthreads();
-  const int part_max = misc[0];
+  int part_max = 0;
+  for (int w = 0; w < NW; ++w) part_max = max(part_max, red[w]);
   SFX_TRACE_POINT(2);
   for (int c = tid; c < C; c += NT) lo_lds[c] = min(part_max, p.caps[c]);
   __syncthreads();
