@@ -17,9 +17,24 @@ def sa_workspace_bytes(n: int) -> int:
     return int(lib().sfx_sa_build_workspace_size(int(n)))
 
 
+# Doubling rounds enqueued between two reads of the build's done flag in
+# the adaptive build.
+SA_CHECK_ROUNDS = 3
+
+
 def build_suffix_array_into(text: torch.Tensor, m: int, out: torch.Tensor,
-                            workspace: torch.Tensor | None = None) -> None:
-    """out[:m] = SA(text[:m]); out[m:] = m .. len(out)-1 (int32 or int64)."""
+                            workspace: torch.Tensor | None = None,
+                            adaptive: bool = True) -> None:
+    """out[:m] = SA(text[:m]); out[m:] = m .. len(out)-1 (int32 or int64).
+
+    adaptive (the default): the doubling rounds are enqueued
+    SA_CHECK_ROUNDS at a time, and the host reads the device's done flag
+    (one synchronisation of the current stream) before enqueuing more, so
+    a build stops within a few launches of the round that finished it.
+    The reference's build synchronises too (suffix_gpu/suffix_array.py:
+    torch.unique).  adaptive=False enqueues the fixed launch sequence for
+    every round the length allows, with no host read: the form to capture
+    in a graph or to run in the background."""
     require_gpu(text, out)
     if text.dtype != torch.int32 or not text.is_contiguous():
         raise ValueError("text must be a contiguous int32 tensor")
@@ -31,10 +46,41 @@ def build_suffix_array_into(text: torch.Tensor, m: int, out: torch.Tensor,
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8,
                                 device=text.device)
+    if adaptive and m > 1:
+        _build_adaptive(text, m, out, workspace)
+        return
     check(lib().sfx_sa_build(text.data_ptr(), m, out.shape[0],
                              out.data_ptr(), int(out.dtype == torch.int64),
                              workspace.data_ptr(), workspace.numel(),
                              stream_of(text.device)), "build_suffix_array")
+
+
+def _build_adaptive(text: torch.Tensor, m: int, out: torch.Tensor,
+                    workspace: torch.Tensor) -> None:
+    L = lib()
+    st = stream_of(text.device)
+    ws, nbytes = workspace.data_ptr(), workspace.numel()
+    total = int(L.sfx_sa_build_rounds_total(m))
+    off = int(L.sfx_sa_build_flag_offset(m))
+    state = workspace[off:off + 16].view(torch.int32)
+    flag = torch.empty(4, dtype=torch.int32, pin_memory=True)
+    check(L.sfx_sa_build_begin(text.data_ptr(), m, ws, nbytes, st),
+          "build_suffix_array")
+    first = 1
+    while first <= total:
+        n = min(SA_CHECK_ROUNDS, total - first + 1)
+        check(L.sfx_sa_build_rounds(m, first, n, ws, nbytes, st),
+              "build_suffix_array")
+        first += n
+        flag.copy_(state, non_blocking=True)
+        done = torch.cuda.Event()
+        done.record(torch.cuda.current_stream(text.device))
+        done.synchronize()
+        if int(flag[0]):
+            break
+    check(L.sfx_sa_build_finish(m, out.shape[0], out.data_ptr(),
+                                int(out.dtype == torch.int64), ws, nbytes,
+                                st), "build_suffix_array")
 
 
 def build_suffix_array(tokens: torch.Tensor) -> torch.Tensor:
