@@ -174,7 +174,7 @@ def time_sa_builds(w, dev, side):
             e1 = torch.cuda.Event(enable_timing=True)
             with torch.cuda.stream(side):
                 e0.record(side)
-                build_suffix_array_into(text, mm, out, ws)
+                build_suffix_array_into(text, mm, out, ws, adaptive=True)
                 e1.record(side)
             e1.synchronize()
             times.append(e0.elapsed_time(e1))
@@ -908,6 +908,21 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> dict:
             "k_step_c5_local": round(c5_total) or None, "detail": out}
 
 
+def row_tails(counts, rows, P):
+    """Each row's last min(count, P) tokens, left-aligned in a [B, P]
+    int32 tensor (zero after them), and those lengths as int64: the query
+    form of the global kernel, for timing it and counting its bytes."""
+    import torch
+    q = counts.to(torch.int64)
+    n = q.clamp(max=P)
+    j = torch.arange(P, device=rows.device, dtype=torch.int64)
+    src = (q - n).unsqueeze(1) + j.unsqueeze(0)
+    keep = j.unsqueeze(0) < n.unsqueeze(1)
+    vals = rows.gather(1, src.clamp(0, rows.shape[1] - 1))
+    return (torch.where(keep, vals, torch.zeros_like(vals)).to(torch.int32)
+            .contiguous(), n.contiguous())
+
+
 def kernel_timings(d, dev, tokens0, nt, sampled, reps):
     """Average duration of the local and the global kernel, each launched
     alone on the current stream between HIP events."""
@@ -938,8 +953,7 @@ def kernel_timings(d, dev, tokens0, nt, sampled, reps):
     # the global kernel, query form: tails of the updated rows
     upd = tokens0.clone()
     new = d.update_state(nt, upd, sampled)
-    tails, tail_len = d._gather_tails(new, upd)
-    tails = tails.to(torch.int32).contiguous()
+    tails, tail_len = row_tails(new, upd, d.max_pattern_len)
     gi = d.global_index
     caps = [int(x) for x in d._global_caps.tolist()]
     pg = _lib.make_params(d.k, d.max_pattern_len, gi.max_occurrences, 1,
@@ -988,8 +1002,7 @@ def global_algorithmic_bytes(d, dev, buf, new_counts):
     gi = d.global_index
     P = d.max_pattern_len
     q = torch.from_numpy(new_counts.astype(np.int64)).to(dev)
-    tails, tail_len = d._gather_tails(q, buf)
-    tails = tails.to(torch.int32)
+    tails, tail_len = row_tails(q, buf, P)
     res = gi._run_query(tails, tail_len, P, d._global_caps,
                         want=("len", "occ", "sa_start", "sa_end", "sa_len",
                               "d_len"))

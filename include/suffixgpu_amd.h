@@ -31,7 +31,7 @@ extern "C" {
 
 #define SFX_EINVAL (-1)
 #define SFX_MAX_CANDIDATES 32
-#define SFX_ABI_VERSION 6
+#define SFX_ABI_VERSION 7
 
 /* Drafter configuration shared by the local and global paths.
  * Mirrors the constructor arguments of SuffixGPUDrafter
@@ -56,7 +56,13 @@ typedef struct sfx_params {
 /* Global index buffers (suffix_gpu/global_index.py:63-74), plus the key
  * array of the suffix array (no reference counterpart): row r holds the
  * first key_width tokens of the suffix at sa[r] (-1 past the end), built
- * by sfx_sa_keys() with every suffix array; NULL disables it. */
+ * by sfx_sa_keys() with every suffix array; NULL disables it.
+ *
+ * The key rows may be double-buffered: with key_select != NULL the kernels
+ * read the device word *key_select when they run and take sa_key_alt when
+ * it is nonzero, sa_key otherwise.  A rebuild writes the idle buffer and
+ * sfx_index_swap() flips the word, so a swap copies no key rows and graphs
+ * captured over this struct follow the live buffer. */
 typedef struct sfx_index {
     const int32_t* corpus;    /* [capacity] PAD-filled ring               */
     const int32_t* sa;        /* [capacity] suffix array of corpus        */
@@ -67,6 +73,10 @@ typedef struct sfx_index {
     const int32_t* sa_key;    /* [capacity, key_width] or NULL; 16-byte
                                  aligned                                 */
     int64_t key_width;        /* 4..32, a multiple of 4                   */
+    const int32_t* sa_key_alt; /* second key-row buffer (same layout) or
+                                  NULL                                   */
+    const int32_t* key_select; /* device int32 selecting sa_key_alt when
+                                  nonzero, or NULL (sa_key is live)      */
 } sfx_index;
 
 /* One decode step's batch (suffix_gpu/proposer.py:135-214).
@@ -233,13 +243,15 @@ int sfx_sa_build_finish(int64_t m, int64_t n_total, void* sa, int32_t sa_is64,
                         hipStream_t stream);
 
 /* global_index.py:235-240 _finish_swap: in-place copy of a finished
- * rebuild into the live buffers (corpus, sa: capacity int32 each; sa_key:
- * capacity * key_width int32, skipped when key_width is 0), one launch, so
- * graphs captured over the live buffers keep their pointers. */
-int sfx_index_swap(int32_t* corpus, int32_t* sa, int32_t* sa_key,
-                   const int32_t* new_corpus, const int32_t* new_sa,
-                   const int32_t* new_sa_key, int64_t capacity,
-                   int64_t key_width, hipStream_t stream);
+ * rebuild into the live buffers (corpus, sa: capacity int32 each), one
+ * launch, so graphs captured over the live buffers keep their pointers.
+ * The key rows are not copied: when key_select is not NULL the same launch
+ * stores key_select_value there (sfx_index.key_select picks the buffer the
+ * rebuild wrote). */
+int sfx_index_swap(int32_t* corpus, int32_t* sa, const int32_t* new_corpus,
+                   const int32_t* new_sa, int64_t capacity,
+                   int32_t* key_select, int32_t key_select_value,
+                   hipStream_t stream);
 
 /* ---- delta writes (global_index.py:86-133, 192-199) ------------------- */
 

@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsuffixgpu_amd.so"
 MAX_CANDIDATES = 32
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -41,6 +41,7 @@ class SfxIndex(ctypes.Structure):
         ("corpus", c_p), ("sa", c_p), ("capacity", c_i64),
         ("delta", c_p), ("delta_capacity", c_i64), ("delta_len", c_p),
         ("sa_key", c_p), ("key_width", c_i64),
+        ("sa_key_alt", c_p), ("key_select", c_p),
     ]
 
 
@@ -77,8 +78,7 @@ SIGNATURES = {
                                     ctypes.c_size_t, c_p]),
     "sfx_sa_build_finish": (c_i32, [c_i64, c_i64, c_p, c_i32, c_p,
                                     ctypes.c_size_t, c_p]),
-    "sfx_index_swap": (c_i32, [c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64,
-                               c_p]),
+    "sfx_index_swap": (c_i32, [c_p, c_p, c_p, c_p, c_i64, c_p, c_i32, c_p]),
     "sfx_delta_append": (c_i32, [ctypes.POINTER(SfxAppendDoc), c_i32, c_p,
                                  c_i64, c_p, c_i64, c_p]),
     "sfx_delta_shift": (c_i32, [c_p, c_i64, c_i64, c_i64, c_p, c_p]),
@@ -160,9 +160,13 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+# Error code of the C ABI besides hipError_t values.
+EINVAL = -1
+
+
 def check(rc: int, what: str) -> None:
     if rc != 0:
-        if rc == -1:
+        if rc == EINVAL:
             raise SuffixGPUError(f"{what}: invalid argument")
         raise SuffixGPUError(f"{what}: HIP error {rc}")
 

@@ -69,6 +69,10 @@ int check_global(const sfx_params& p, const sfx_index& ix, int64_t batch) {
       (ix.key_width < 4 || ix.key_width > 32 || (ix.key_width & 3) ||
        ((uintptr_t)ix.sa_key & 15)))
     return SFX_EINVAL;
+  // A selector needs both key buffers, with the same alignment rule.
+  if (ix.key_select &&
+      (!ix.sa_key || !ix.sa_key_alt || ((uintptr_t)ix.sa_key_alt & 15)))
+    return SFX_EINVAL;
   size_t lds = 0;
   const int parts = delta_parts_for(batch, ix.delta_capacity);
   if (merge_waves_for(p, ix, parts, &lds) < 1) return SFX_EINVAL;

@@ -399,6 +399,13 @@ __device__ __forceinline__ void source_expand(
   }
 }
 
+// The key rows the index's selector word names (sfx_index.key_select).
+__device__ __forceinline__ const int32_t* live_keys(const sfx_index& ix) {
+  if (ix.key_select && ix.sa_key_alt && *ix.key_select != 0)
+    return ix.sa_key_alt;
+  return ix.sa_key;
+}
+
 // role 0: SA search; role 1 .. dparts: delta part role - 1.
 __device__ __forceinline__ void global_body(const GlobalArgs& a,
                                             unsigned char* smem, int b,
@@ -462,12 +469,13 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
     constexpr int G = kSearchGroup;
     const int ngroups = NT / G;
     const int g = tid / G;
+    const int32_t* keys = live_keys(a.ix);
     for (int l = g + 1; l <= P; l += ngroups) {
       int64_t lo = 0, hi = 0;
       if (l <= plen) {
         auto pat_at = [&](int j) -> int32_t { return rpat[l - 1 - j]; };
-        kary_bounds<G>(a.ix.sa, a.ix.corpus, N, a.ix.sa_key,
-                       (int)a.ix.key_width, pat_at, l, lo, hi);
+        kary_bounds<G>(a.ix.sa, a.ix.corpus, N, keys, (int)a.ix.key_width,
+                       pat_at, l, lo, hi);
       }
       if (tid % G == 0) {
         lbs[l - 1] = lo;

@@ -50,13 +50,16 @@ __device__ __forceinline__ void copy_span(const CopySpan& c, int64_t tid,
   for (int64_t i = 4 * n4 + tid; i < c.n; i += nthreads) c.dst[i] = c.src[i];
 }
 
+// The swap's in-place copies of corpus and SA; block 0 also stores the
+// key-row selector word (a vector store from one lane).
 __global__ __launch_bounds__(256) void k_swap(CopySpan a, CopySpan b,
-                                              CopySpan c) {
+                                              int32_t* key_select,
+                                              int32_t key_select_value) {
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t nth = (int64_t)gridDim.x * blockDim.x;
   copy_span(a, tid, nth);
   copy_span(b, tid, nth);
-  copy_span(c, tid, nth);
+  if (key_select && tid == 0) *key_select = key_select_value;
 }
 
 // ------------------------------------------------------------ delta writes
@@ -286,22 +289,24 @@ extern "C" int sfx_trace_set(uint64_t* buf) {
 
 extern "C" int sfx_abi_version(void) { return SFX_ABI_VERSION; }
 
-extern "C" int sfx_index_swap(int32_t* corpus, int32_t* sa, int32_t* sa_key,
+extern "C" int sfx_index_swap(int32_t* corpus, int32_t* sa,
                               const int32_t* new_corpus,
-                              const int32_t* new_sa,
-                              const int32_t* new_sa_key, int64_t capacity,
-                              int64_t key_width, hipStream_t stream) {
-  if (capacity < 0 || key_width < 0 || (key_width > 0 && !sa_key) ||
-      (key_width > 0 && !new_sa_key))
+                              const int32_t* new_sa, int64_t capacity,
+                              int32_t* key_select, int32_t key_select_value,
+                              hipStream_t stream) {
+  if (capacity < 0) return SFX_EINVAL;
+  if (capacity == 0 && !key_select) return 0;
+  if (capacity > 0 && (!corpus || !sa || !new_corpus || !new_sa))
     return SFX_EINVAL;
-  if (capacity == 0) return 0;
-  if (!corpus || !sa || !new_corpus || !new_sa) return SFX_EINVAL;
   const CopySpan a{corpus, new_corpus, capacity};
   const CopySpan b{sa, new_sa, capacity};
-  const CopySpan c{sa_key, new_sa_key, key_width > 0 ? capacity * key_width
-                                                     : 0};
-  // enough 256-thread blocks to keep every CU streaming
-  hipLaunchKernelGGL(k_swap, dim3(2048), dim3(256), 0, stream, a, b, c);
+  // Up to eight 256-thread blocks per CU keep every CU streaming (32 MiB
+  // of copies at N = 2^22).
+  const int64_t want = (capacity / 4 + 255) / 256;
+  const unsigned blocks =
+      (unsigned)(want < 1 ? 1 : (want > 2048 ? 2048 : want));
+  hipLaunchKernelGGL(k_swap, dim3(blocks), dim3(256), 0, stream, a, b,
+                     key_select, key_select_value);
   return (int)hipGetLastError();
 }
 

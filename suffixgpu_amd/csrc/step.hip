@@ -60,11 +60,14 @@ extern "C" size_t sfx_step_workspace_size(const sfx_params* p,
   return step_ws_layout(*p, batch, delta_capacity, nullptr, nullptr);
 }
 
-extern "C" int sfx_propose_step(const sfx_params* p, const sfx_index* ix,
-                                const sfx_batch* bt, int32_t* draft,
-                                int32_t* num_valid, int32_t* new_counts,
-                                void* workspace, size_t workspace_bytes,
-                                hipStream_t stream) {
+namespace {
+
+// The fused step over `workspace` laid out with counter arrays of
+// `counter_rows` rows (-1: the batch size).
+int launch_step(const sfx_params* p, const sfx_index* ix, const sfx_batch* bt,
+                int32_t* draft, int32_t* num_valid, int32_t* new_counts,
+                void* workspace, size_t workspace_bytes, int64_t counter_rows,
+                hipStream_t stream) {
   if (!p || !bt || !draft || !num_valid) return SFX_EINVAL;
   int rc = check_local(*p, *bt);
   if (rc) return rc;
@@ -100,10 +103,11 @@ extern "C" int sfx_propose_step(const sfx_params* p, const sfx_index* ix,
   if (global_on) {
     rc = check_global(*p, *ix, bt->batch);
     if (rc) return rc;
-    const size_t need =
-        step_ws_layout(*p, bt->batch, ix->delta_capacity, nullptr, nullptr);
+    const size_t need = step_ws_layout(*p, bt->batch, ix->delta_capacity,
+                                       nullptr, nullptr, counter_rows);
     if (!workspace || workspace_bytes < need) return SFX_EINVAL;
-    step_ws_layout(*p, bt->batch, ix->delta_capacity, workspace, &a.l.ws);
+    step_ws_layout(*p, bt->batch, ix->delta_capacity, workspace, &a.l.ws,
+                   counter_rows);
     a.g.p = *p;
     a.g.ix = *ix;
     a.g.B = bt->batch;
@@ -134,4 +138,15 @@ extern "C" int sfx_propose_step(const sfx_params* p, const sfx_index* ix,
                        stream, a);
   }
   return (int)hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" int sfx_propose_step(const sfx_params* p, const sfx_index* ix,
+                                const sfx_batch* bt, int32_t* draft,
+                                int32_t* num_valid, int32_t* new_counts,
+                                void* workspace, size_t workspace_bytes,
+                                hipStream_t stream) {
+  return launch_step(p, ix, bt, draft, num_valid, new_counts, workspace,
+                     workspace_bytes, -1, stream);
 }

@@ -91,10 +91,13 @@ __host__ __device__ inline int64_t delta_mb_stride(int64_t part_cap) {
 
 inline size_t ws_align(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Returns the byte size; fills `ws` when base != nullptr.
+// Returns the byte size; fills `ws` when base != nullptr.  The three
+// handover counter arrays come first, each sized for `counter_rows` rows
+// (B when negative), so a caller that fixes counter_rows keeps them at the
+// same offsets for every batch size.
 inline size_t step_ws_layout(const sfx_params& p, int64_t B,
                              int64_t delta_capacity, void* base,
-                             StepWs* ws) {
+                             StepWs* ws, int64_t counter_rows = -1) {
   const size_t C = p.num_caps > 0 ? (size_t)p.num_caps : 1;
   const size_t K = (size_t)p.k;
   const size_t R = (size_t)p.max_occurrences;
@@ -106,10 +109,11 @@ inline size_t step_ws_layout(const sfx_params& p, int64_t B,
     off += ws_align(bytes);
     return ptr;
   };
+  const size_t cr = counter_rows < 0 ? b : (size_t)counter_rows;
   StepWs w;
-  w.join = (unsigned*)take(b * 4);
-  w.djoin = (unsigned*)take(b * 4);
-  w.pick = (unsigned*)take(b * 4);
+  w.join = (unsigned*)take(cr * 4);
+  w.djoin = (unsigned*)take(cr * 4);
+  w.pick = (unsigned*)take(cr * 4);
   w.l_chain = (int32_t*)take(b * K * 4);
   w.l_emit = (int32_t*)take(b * 4);
   w.l_score = (float*)take(b * 4);

@@ -1,14 +1,17 @@
-"""Cross-request global memory: suffix array over finished responses.
+"""The drafter's memory of earlier responses, held on the GPU.
 
-Mirrors suffix_gpu/global_index.py:34-553: a PAD-filled corpus ring of
-``capacity`` int32 tokens with its suffix array (immutable between
-rebuilds), an append-only delta of ``delta_capacity`` tokens whose
-documents end with SEP, and a double-buffered rebuild: eviction-trimmed
-active corpus + whole-document delta snapshot go to the staging buffers,
-the delta is compacted at launch, the staging suffix array is built on the
-rebuild stream (csrc/sa_build.hip, no host synchronisation), and
-``poll_rebuild`` swaps it in with in-place copies so captured graphs keep
-their tensor identities.
+Follows suffix_gpu/global_index.py:34-553.  Finished responses live in two
+places: a ring of ``capacity`` int32 tokens (whole documents, PAD after
+the last one) indexed by a suffix array that only a rebuild changes, and a
+small append-only ``delta`` of the most recent documents (each closed by
+SEP) that queries scan directly.  A rebuild assembles the next ring in
+staging buffers -- the oldest whole documents dropped until the kept ones
+plus the delta's whole documents fit -- removes the absorbed documents
+from the delta at once, sorts the staging suffixes on the rebuild stream
+(csrc/sa_build.hip, no host synchronisation) and writes the staging key
+rows.  ``poll_rebuild`` then copies ring and suffix array into the live
+tensors in place, so captured graphs keep their pointers, and flips a
+device selector word to the freshly written key rows (no key-row copy).
 
 Host bookkeeping (document lengths, eviction and snapshot arithmetic) is
 plain Python exactly as in the reference; every device operation is a
@@ -40,7 +43,8 @@ SEP_TOKEN = -2
 
 
 class GlobalIndex:
-    """GPU-resident global suffix index with periodic rebuilds."""
+    """Suffix-array memory of finished responses on one GPU: a sorted
+    ring rebuilt in the background plus a directly scanned delta."""
 
     def __init__(self, capacity: int, delta_capacity: int, k: int,
                  max_occurrences: int = 32,
@@ -75,9 +79,12 @@ class GlobalIndex:
         self.delta = torch.zeros(delta_capacity, dtype=torch.int32,
                                  device=dev)
         self.delta_len_t = torch.zeros((), dtype=torch.int64, device=dev)
-        self.sa_key = torch.empty(capacity * KEY_WIDTH, dtype=torch.int32,
-                                  device=dev)
-        self.staging_sa_key = torch.empty_like(self.sa_key)
+        # Two key-row buffers; the device word key_select names the live
+        # one (the step reads it), a rebuild writes the other.
+        self._keys = [torch.empty(capacity * KEY_WIDTH, dtype=torch.int32,
+                                  device=dev) for _ in range(2)]
+        self._key_live = 0
+        self.key_select = torch.zeros(1, dtype=torch.int32, device=dev)
         self._build_keys(self.corpus, self.sa, self.sa_key)
         self._sa_ws: torch.Tensor | None = None
         self._query_ws: dict = {}
@@ -99,12 +106,36 @@ class GlobalIndex:
     # ------------------------------------------------------------------
     # device views
     # ------------------------------------------------------------------
+    @property
+    def sa_key(self) -> torch.Tensor:
+        """Key rows of the live suffix array ([capacity * 32] int32)."""
+        return self._keys[self._key_live]
+
+    @property
+    def staging_sa_key(self) -> torch.Tensor:
+        """Key rows a rebuild writes (the idle buffer)."""
+        return self._keys[1 - self._key_live]
+
     def index_struct(self) -> _lib.SfxIndex:
         return _lib.SfxIndex(self.corpus.data_ptr(), self.sa.data_ptr(),
                              self.capacity, self.delta.data_ptr(),
                              self.delta_capacity,
                              self.delta_len_t.data_ptr(),
-                             self.sa_key.data_ptr(), KEY_WIDTH)
+                             self._keys[0].data_ptr(), KEY_WIDTH,
+                             self._keys[1].data_ptr(),
+                             self.key_select.data_ptr())
+
+    def device_bytes(self) -> dict:
+        """Device memory held by the index, by role (bytes)."""
+        ws = self._sa_ws.numel() if self._sa_ws is not None else 0
+        qws = sum(t.numel() for t in self._query_ws.values())
+        return {
+            "corpus_sa": 4 * 4 * self.capacity,  # live + staging, int32
+            "key_rows": 2 * 4 * KEY_WIDTH * self.capacity,
+            "delta": 4 * self.delta_capacity + 8,
+            "sa_build_workspace": ws,
+            "query_workspace": qws,
+        }
 
     def _build_keys(self, corpus, sa, keys) -> None:
         check(lib().sfx_sa_keys(corpus.data_ptr(), sa.data_ptr(),
@@ -170,7 +201,8 @@ class GlobalIndex:
             self._launch_rebuild()
         if self.delta_len + needed <= self.delta_capacity:
             return
-        # A rebuild is in flight (staging buffers busy): drop oldest docs.
+        # The staging buffers still belong to the running rebuild, so the
+        # delta can only make room by forgetting its earliest documents.
         self._drop_oldest_docs(
             self.delta_len + needed - self.delta_capacity)
 
@@ -189,7 +221,8 @@ class GlobalIndex:
     # rebuild (global_index.py:138-252)
     # ------------------------------------------------------------------
     def maybe_rebuild(self) -> None:
-        """Kick off a rebuild when the delta grew past the threshold."""
+        """Start a background rebuild once the delta holds at least
+        rebuild_threshold tokens and none is running."""
         self.poll_rebuild()
         if self._rebuild_event is not None or self.delta_len == 0:
             return
@@ -295,7 +328,9 @@ class GlobalIndex:
                                     st), "SA rebuild")
         self._copy_build_state(m)
         self._staged_build_finish(dst, m)
-        self._build_state = (m, first + 1) if first < total else None
+        # Kept even when every round was enqueued: the state copy then
+        # still tells how many rounds this text needed (the next hint).
+        self._build_state = (m, first + 1)
 
     def _copy_build_state(self, m: int) -> None:
         if m <= 1:
@@ -317,26 +352,36 @@ class GlobalIndex:
     def _staged_build_check(self) -> bool:
         """After the build's event: True when the staged output is final;
         otherwise the remaining rounds, the output and the key rows are
-        enqueued again under a new event."""
+        enqueued again under a new event.  Every state copy that comes back
+        sets the round hint to the rounds this text needed plus 2, so a
+        long-repeat text raises it only until a shorter one follows."""
         if self._build_state is None:
             return True
         m, nxt = self._build_state
         self._build_state = None
+        if m <= 1:
+            return True  # nothing to sort; the hint stays as it is
         flags = self._flag_host.tolist()
-        if flags[0]:
-            # flags[2]: the doubling round that found the array final
-            self.sa_round_hint = max(1, int(flags[2]) - 1) + 2
-            return True
         L = lib()
         total = int(L.sfx_sa_build_rounds_total(m))
-        self.sa_round_hint = total
+        if flags[0]:
+            # flags[2]: the doubling round that found no unsorted group
+            self.sa_round_hint = max(1, int(flags[2]) - 1) + 2
+            return True
+        if nxt > total:
+            # Every round ran; only the round after the last one could
+            # have raised the flag, so the array is final as it stands.
+            self.sa_round_hint = total
+            return True
         self.rebuild_stream.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(self.rebuild_stream):
             ws = self._sa_ws
             check(L.sfx_sa_build_rounds(m, nxt, total - nxt + 1,
                                         ws.data_ptr(), ws.numel(),
                                         stream_of(self.device)), "SA rebuild")
+            self._copy_build_state(m)
             self._staged_build_finish(self.staging_corpus, m)
+        self._build_state = (m, total + 1)
         event = torch.cuda.Event()
         event.record(self.rebuild_stream)
         self._rebuild_event = event
@@ -353,12 +398,16 @@ class GlobalIndex:
         return count
 
     def _finish_swap(self, n_new: int, new_doc_lens: deque[int]) -> None:
-        # In-place copies: captured graphs bind the active tensors' storage.
+        # Ring and suffix array are copied into the live tensors (captured
+        # graphs hold their pointers); the key rows switch buffers by the
+        # selector word, in the same launch.
+        live = 1 - self._key_live
         check(lib().sfx_index_swap(
             self.corpus.data_ptr(), self.sa.data_ptr(),
-            self.sa_key.data_ptr(), self.staging_corpus.data_ptr(),
-            self.staging_sa.data_ptr(), self.staging_sa_key.data_ptr(),
-            self.capacity, KEY_WIDTH, stream_of(self.device)), "swap")
+            self.staging_corpus.data_ptr(), self.staging_sa.data_ptr(),
+            self.capacity, self.key_select.data_ptr(), live,
+            stream_of(self.device)), "swap")
+        self._key_live = live
         self.active_len = n_new
         self.active_doc_lens = new_doc_lens
         self._rebuild_event = None

@@ -131,7 +131,8 @@ def expand_chain(cont: torch.Tensor, num_occ: torch.Tensor, k: int,
 
 def scatter_append(token_ids_gpu: torch.Tensor, base: torch.Tensor,
                    cnt: torch.Tensor, sampled: torch.Tensor) -> None:
-    """Append each row's valid sampled tokens at its base offset."""
+    """Writes row b's first cnt[b] sampled ids (skipping -1) at
+    positions base[b], base[b] + 1, ... of its token row, below S."""
     bt, keep = _lib.make_batch(token_ids_gpu, base, sampled=sampled,
                                valid_count=cnt)
     check(lib().sfx_scatter_append(bt, None,

@@ -20,7 +20,8 @@ from suffixgpu_amd._lib import check, lib, require_gpu, stream_of
 
 
 class LocalMatchKernel(nn.Module):
-    """Multi-length local suffix matcher with score-ranked expansion."""
+    """Matches each row's newest tokens against the row itself at
+    several support thresholds and drafts from the best-scored match."""
 
     def __init__(self, k: int, max_pattern_len: int = 32,
                  min_match_len: int = 1, max_occurrences: int = 32,
@@ -49,14 +50,6 @@ class LocalMatchKernel(nn.Module):
             k, max_pattern_len, max_occurrences, self.min_match_len,
             self.support_thresholds, (), max_spec_factor, max_spec_offset,
             min_token_prob, vote_smoothing_alpha)
-
-    def _spec_cap(self, match_len: torch.Tensor) -> torch.Tensor:
-        """max(0, floor(f * L + off)) in fp32 (local_matcher.py:76-81)."""
-        if self.max_spec_factor is None:
-            return torch.full_like(match_len, self.k)
-        cap = (self.max_spec_factor * match_len.to(torch.float32)
-               + self.max_spec_offset).floor().to(torch.int64)
-        return cap.clamp(min=0)
 
     def gather_candidates(self, num_tokens_no_spec: torch.Tensor,
                           token_ids: torch.Tensor,
@@ -103,17 +96,3 @@ class LocalMatchKernel(nn.Module):
         del keep
         return draft, nv, mlen, occ, score
 
-
-def select_local_best(cand: torch.Tensor, chain: torch.Tensor,
-                      num_emit: torch.Tensor, occ: torch.Tensor,
-                      score: torch.Tensor):
-    """Best-scored candidate per row; exact ties prefer the longer match.
-
-    local_matcher.py:245-263: first argmax of fp32 score + fl32(len)*1e-6.
-    """
-    b = cand.shape[0]
-    tie = cand.to(torch.float32) * 1e-6
-    best = (score + tie).argmax(dim=1)
-    bidx = torch.arange(b, device=cand.device)
-    return (chain[bidx, best], num_emit[bidx, best], cand[bidx, best],
-            occ[bidx, best], score[bidx, best])

@@ -95,7 +95,7 @@ class SuffixGPUDrafter:
             self.vote_smoothing_alpha)
         self.global_index: GlobalIndex | None = None
         self._ingested: dict = {}
-        self._ws: dict[int, torch.Tensor] = {}
+        self._ws: dict[tuple, torch.Tensor] = {}
         if enable_global:
             self.global_index = GlobalIndex(
                 capacity=global_capacity, delta_capacity=delta_capacity,
@@ -104,22 +104,9 @@ class SuffixGPUDrafter:
                 rebuild_stream=rebuild_stream)
 
     # ------------------------------------------------------------------
-    def _gather_tails(self, num_tokens_no_spec: torch.Tensor,
-                      token_ids_gpu: torch.Tensor):
-        """Padded [B, P] tails (last P tokens) and lengths (:110-125)."""
-        b, s = token_ids_gpu.shape
-        p = self.max_pattern_len
-        q_len = num_tokens_no_spec.to(torch.int64)
-        tail_len = torch.minimum(q_len, torch.full_like(q_len, p))
-        offs = torch.arange(p, dtype=torch.int64, device=self.device)
-        idx = q_len.unsqueeze(1) - tail_len.unsqueeze(1) + offs.unsqueeze(0)
-        valid = offs.unsqueeze(0) < tail_len.unsqueeze(1)
-        tails = torch.where(
-            valid, token_ids_gpu.gather(1, idx.clamp(0, s - 1)), 0)
-        return tails, tail_len
-
     def poll(self) -> None:
-        """Host-side: swap in a finished background rebuild, if any."""
+        """Called by the host between steps: a background rebuild whose
+        event has completed becomes the live index."""
         if self.global_index is not None:
             self.global_index.poll_rebuild()
 
@@ -171,17 +158,36 @@ class SuffixGPUDrafter:
                                   None, combined_mask, 0)
         return draft, nv
 
-    def _workspace(self, b: int) -> torch.Tensor:
-        ws = self._ws.get(b)
+    def _workspace(self, b: int, stream: int) -> torch.Tensor:
+        """The fused step's workspace for `b` rows.
+
+        Its handover counters must be zero when a call starts, and every
+        call leaves them zero, so two calls that share a workspace must
+        not run at the same time.  Eager calls therefore get one per
+        (batch size, stream): two streams driving one drafter never share.
+        Calls recorded into a HIP graph get one per batch size of their
+        own ("graph"), so a replay never shares with an eager call on any
+        stream.  It is made (and zeroed) outside the capture at the first
+        eager call of that batch size -- a capture records no fill -- or,
+        when a capture comes first, inside it (the replay then re-zeroes
+        it, which is harmless).  Replays of graphs captured for one batch
+        size share that workspace and must not overlap each other."""
+        capturing = torch.cuda.is_current_stream_capturing()
+        key = (b, "graph") if capturing else (b, stream)
+        ws = self._ws.get(key)
         if ws is None:
-            dcap = (self.global_index.delta_capacity
-                    if self.global_index is not None else 0)
-            nbytes = int(lib().sfx_step_workspace_size(self._params, b,
-                                                       dcap))
-            ws = torch.zeros(max(1, nbytes), dtype=torch.uint8,
-                             device=self.device)
-            self._ws[b] = ws
+            ws = self._new_workspace(b)
+            self._ws[key] = ws
+        if not capturing and (b, "graph") not in self._ws:
+            self._ws[(b, "graph")] = self._new_workspace(b)
         return ws
+
+    def _new_workspace(self, b: int) -> torch.Tensor:
+        dcap = (self.global_index.delta_capacity
+                if self.global_index is not None else 0)
+        nbytes = int(lib().sfx_step_workspace_size(self._params, b, dcap))
+        return torch.zeros(max(1, nbytes), dtype=torch.uint8,
+                           device=self.device)
 
     def _step(self, num_tokens, tokens, sampled, valid_cnt, mask, limit):
         bt, keep = _lib.make_batch(tokens, num_tokens, sampled=sampled,
@@ -204,7 +210,7 @@ class SuffixGPUDrafter:
                   "propose")
             del keep
             return draft, num_valid, new
-        ws = self._workspace(b)
+        ws = self._workspace(b, cur)
         rc = L.sfx_propose_step(self._params,
                                 self.global_index.index_struct(), bt,
                                 draft.data_ptr(), num_valid.data_ptr(),

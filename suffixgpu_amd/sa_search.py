@@ -19,7 +19,8 @@ from suffixgpu_amd._lib import check, lib, require_gpu, stream_of
 def search_interval(sa: torch.Tensor, corpus: torch.Tensor,
                     pattern: torch.Tensor, pattern_len: torch.Tensor
                     ) -> tuple[torch.Tensor, torch.Tensor]:
-    """SA interval [start, end) of suffixes starting with each pattern."""
+    """Per pattern, the ranks [start, end) of the suffixes that begin
+    with its first pattern_len tokens (start == end: none)."""
     return kernels.sa_search(sa, corpus, pattern, pattern_len)
 
 

@@ -22,19 +22,36 @@ def sa_workspace_bytes(n: int) -> int:
 SA_CHECK_ROUNDS = 3
 
 
+def _workspace_ok(workspace: torch.Tensor | None, text: torch.Tensor,
+                  need: int) -> torch.Tensor:
+    """The caller's byte workspace, or a new one when it is None or short.
+    A workspace must be a contiguous uint8 tensor on the text's device:
+    its numel() is the byte count and the state block is sliced by byte
+    offset."""
+    if workspace is not None:
+        if (workspace.dtype != torch.uint8 or not workspace.is_contiguous()
+                or workspace.device != text.device):
+            raise ValueError("workspace must be a contiguous uint8 tensor on "
+                             f"{text.device}")
+        if workspace.numel() >= need:
+            return workspace
+    return torch.empty(max(need, 1), dtype=torch.uint8, device=text.device)
+
+
 def build_suffix_array_into(text: torch.Tensor, m: int, out: torch.Tensor,
                             workspace: torch.Tensor | None = None,
-                            adaptive: bool = True) -> None:
+                            adaptive: bool = False) -> None:
     """out[:m] = SA(text[:m]); out[m:] = m .. len(out)-1 (int32 or int64).
 
-    adaptive (the default): the doubling rounds are enqueued
-    SA_CHECK_ROUNDS at a time, and the host reads the device's done flag
-    (one synchronisation of the current stream) before enqueuing more, so
-    a build stops within a few launches of the round that finished it.
-    The reference's build synchronises too (suffix_gpu/suffix_array.py:
-    torch.unique).  adaptive=False enqueues the fixed launch sequence for
-    every round the length allows, with no host read: the form to capture
-    in a graph or to run in the background."""
+    adaptive=False (the default) enqueues the fixed launch sequence for
+    every doubling round the length allows, with no host read: launches
+    after the finishing round return at their first instruction, and the
+    call can be captured in a graph or run in the background.
+    adaptive=True enqueues the rounds SA_CHECK_ROUNDS at a time and reads
+    the device's done flag (one synchronisation of the current stream)
+    before enqueuing more, so the build stops within a few launches of the
+    round that finished it (the reference's build synchronises too, on
+    torch.unique in suffix_gpu/suffix_array.py)."""
     require_gpu(text, out)
     if text.dtype != torch.int32 or not text.is_contiguous():
         raise ValueError("text must be a contiguous int32 tensor")
@@ -42,10 +59,7 @@ def build_suffix_array_into(text: torch.Tensor, m: int, out: torch.Tensor,
         raise ValueError("out must be a contiguous int32/int64 tensor")
     if m > text.shape[0] or m > out.shape[0]:
         raise ValueError("m exceeds the text or output length")
-    need = sa_workspace_bytes(m)
-    if workspace is None or workspace.numel() < need:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8,
-                                device=text.device)
+    workspace = _workspace_ok(workspace, text, sa_workspace_bytes(m))
     if adaptive and m > 1:
         _build_adaptive(text, m, out, workspace)
         return
@@ -91,7 +105,7 @@ def build_suffix_array(tokens: torch.Tensor) -> torch.Tensor:
     out = torch.empty(n, dtype=torch.int64, device=tokens.device)
     if n == 0:
         return out
-    build_suffix_array_into(tokens, n, out)
+    build_suffix_array_into(tokens, n, out, adaptive=True)
     return out
 
 
@@ -101,6 +115,7 @@ def build_suffix_array_rounds(text: torch.Tensor, m: int, out: torch.Tensor,
     (then the output copy): the background rebuild's first chunk.  The
     result is final iff :func:`build_is_final` says so afterwards."""
     require_gpu(text, out, workspace)
+    workspace = _workspace_ok(workspace, text, sa_workspace_bytes(m))
     L = lib()
     st = stream_of(text.device)
     check(L.sfx_sa_build_begin(text.data_ptr(), m, workspace.data_ptr(),

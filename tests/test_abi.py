@@ -64,6 +64,8 @@ def test_abi_version_and_constants(so):
     assert so.sfx_abi_version() == header_define("SFX_ABI_VERSION")
     assert _lib.ABI_VERSION == header_define("SFX_ABI_VERSION")
     assert _lib.MAX_CANDIDATES == header_define("SFX_MAX_CANDIDATES")
+    assert _lib.EINVAL == header_define("SFX_EINVAL")
+
 
 
 def test_workspace_sizes_are_host_only(so):
@@ -81,7 +83,9 @@ def test_argument_errors_are_reported_before_any_launch():
     # invalid sizes are rejected on the host: nothing is enqueued
     assert lib.sfx_sa_keys(None, None, 16, 3, None, None) == -1
     assert lib.sfx_sa_build(None, -1, 0, None, 0, None, 0, None) == -1
-    assert lib.sfx_index_swap(None, None, None, None, None, None, -1, 0,
+    assert lib.sfx_index_swap(None, None, None, None, -1, None, 0,
+                              None) == -1
+    assert lib.sfx_index_swap(None, None, None, None, 16, None, 0,
                               None) == -1
     # a document that would end past the delta (its SEP at capacity)
     docs = (_lib.SfxAppendDoc * 2)(_lib.SfxAppendDoc(1, 10, 0),
@@ -102,6 +106,13 @@ def test_argument_errors_are_reported_before_any_launch():
         assert lib.sfx_global_query(ctypes.byref(p), ctypes.byref(ix), None,
                                     0, 1, None, ctypes.byref(out), 0x600000,
                                     1 << 40, None) == rc
+    # a key-row selector needs both buffers, each 16-byte aligned
+    for alt, rc in ((0, -1), (0x700008, -1), (0x700010, 0)):
+        ix = _lib.SfxIndex(0x200000, 0x300000, 1 << 10, 0x400000, 1 << 10,
+                           0x500000, 0x100010, 32, alt, 0x800000)
+        assert lib.sfx_global_query(ctypes.byref(p), ctypes.byref(ix), None,
+                                    0, 1, None, ctypes.byref(out), 0x600000,
+                                    1 << 40, None) == rc
 
 
 STRUCT_PROBE = r"""
@@ -114,7 +125,8 @@ int main(void) {
   S(sfx_params); F(sfx_params, k); F(sfx_params, spec_factor);
   F(sfx_params, alpha); F(sfx_params, thresholds); F(sfx_params, caps);
   S(sfx_index); F(sfx_index, delta_len); F(sfx_index, sa_key);
-  F(sfx_index, key_width);
+  F(sfx_index, key_width); F(sfx_index, sa_key_alt);
+  F(sfx_index, key_select);
   S(sfx_batch); F(sfx_batch, num_tokens_is64); F(sfx_batch, sampled);
   F(sfx_batch, valid_count_is64); F(sfx_batch, mask); F(sfx_batch, limit);
   S(sfx_global_out); F(sfx_global_out, draft_score);

@@ -1,0 +1,319 @@
+"""The drafter at the full sizes of its benchmark workloads, against the
+oracle (which sorts its own suffix arrays; nothing the GPU built is handed
+to it):
+
+* a 2^22-token template corpus with a half-full 2^16 delta, B=64, S=8192
+  (the measured step): index, key rows, one propose_with_update, the
+  global query of the same tails, and graph replays of the step;
+* suffix-array builds of that 4,193,511-token corpus and of 2^22 uniform
+  tokens (V=128256), adaptive and fixed-sequence, plus the corpus
+  snapshot rebuilt in the background while local-only B=64 S=8192 steps
+  run on the main stream, swapped in, and stepped again;
+* the B=256, S=16384 decode loop: 70 captured steps with the step-63
+  harvest of 16 rows, background rebuilds and swaps (blocking poll), the
+  oracle stepping every update and the full step on chosen steps.
+"""
+
+from __future__ import annotations
+
+import copy
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sa as osa
+from oracle.drafter import DrafterOracle
+from suffixgpu_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+I32 = np.int32
+CFG = dict(k=16, max_pattern_len=32, max_occurrences=128, num_backoff=8,
+           max_spec_factor=2.0, min_token_prob=0.1)
+N22 = 1 << 22
+D16 = 1 << 16
+
+
+def T(a, dev, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return t if dtype is None else t.to(dtype)
+
+
+def N(t):
+    return t.cpu().numpy()
+
+
+def keys_by_definition(corpus: torch.Tensor, sa: torch.Tensor,
+                       keys: torch.Tensor, width: int = 32,
+                       rows: int = 1 << 18) -> None:
+    """Key row r holds corpus[sa[r] + j] for j < width, -1 at or past the
+    end: checked with torch gathers on the device, in slices of ranks."""
+    n = corpus.shape[0]
+    kv = keys.view(n, width)
+    j = torch.arange(width, device=corpus.device, dtype=torch.int64)
+    for r0 in range(0, n, rows):
+        pos = sa[r0:r0 + rows].to(torch.int64).unsqueeze(1) + j
+        want = torch.where(pos < n, corpus[pos.clamp(max=n - 1)],
+                           torch.full_like(pos, -1, dtype=torch.int32))
+        bad = (kv[r0:r0 + rows] != want).any(dim=1)
+        if bool(bad.any()):
+            r = r0 + int(bad.nonzero()[0, 0])
+            raise AssertionError(f"key row {r} differs from its definition")
+
+
+def index_equal(gi, og) -> None:
+    assert gi.active_len == og.active_len
+    assert gi.delta_len == og.delta_len
+    assert list(gi.active_doc_lens) == list(og.active_doc_lens)
+    assert list(gi.delta_doc_lens) == list(og.delta_doc_lens)
+    np.testing.assert_array_equal(N(gi.corpus), og.corpus)
+    np.testing.assert_array_equal(N(gi.sa), og.sa)
+    np.testing.assert_array_equal(N(gi.delta)[:gi.delta_len],
+                                  og.delta[:og.delta_len])
+    assert int(gi.delta_len_t.item()) == gi.delta_len
+    keys_by_definition(gi.corpus, gi.sa, gi.sa_key)
+
+
+# ------------------------------------------------------------ 2^22 corpus
+@pytest.fixture(scope="module")
+def c3(gpu):
+    """The template workload, the oracle's index over it, and the GPU
+    drafter loaded with the same documents (rebuild stream attached,
+    rebuilds held off until a test asks for one)."""
+    from suffixgpu_amd import SuffixGPUDrafter
+    w = synth.global_corpus(seed=3, capacity=N22, delta_fill=1 << 15,
+                            n_docs=1024, b=64, s=8192)
+    kw = dict(enable_global=True, global_capacity=N22, delta_capacity=D16,
+              rebuild_threshold=1 << 30, **CFG)
+    o = DrafterOracle(**kw)
+    o.global_index.load_documents(w.active_docs)
+    o.global_index.append_documents(w.delta_docs)
+    side = torch.cuda.Stream(gpu)
+    d = SuffixGPUDrafter(device=gpu, rebuild_stream=side, **kw)
+    d.global_index.blocking_poll = True
+    d.global_index.load_documents([T(x, gpu) for x in w.active_docs])
+    d.global_index.append_documents([T(x, gpu) for x in w.delta_docs])
+    torch.cuda.synchronize()
+    return w, o, d
+
+
+def test_c3_index_matches_oracle(c3):
+    """Corpus, suffix array (4,193,511 sorted positions + identity tail),
+    delta and key rows of the 2^22 index."""
+    w, o, d = c3
+    gi, og = d.global_index, o.global_index
+    assert gi.active_len == sum(len(x) + 1 for x in w.active_docs)
+    assert gi.active_len + 1 == 4_193_511
+    index_equal(gi, og)
+
+
+def _c3_step_check(w, o, d, gpu):
+    bt = w.batch
+    tg = T(bt.tokens, gpu)
+    draft, nv, new = d.propose_with_update(T(bt.num_tokens, gpu), tg,
+                                           T(bt.sampled, gpu))
+    to = bt.tokens.copy()
+    ed, env, enew = o.propose_with_update(bt.num_tokens, to, bt.sampled)
+    np.testing.assert_array_equal(N(tg), to)
+    np.testing.assert_array_equal(N(new), enew)
+    np.testing.assert_array_equal(N(draft), ed)
+    np.testing.assert_array_equal(N(nv), env)
+    return tg, to, enew, env
+
+
+def test_c3_step_matches_oracle(c3, gpu):
+    """One B=64, S=8192 propose_with_update with global memory on, the
+    query of the same tails (SA + delta lengths, continuations and
+    occurrence counts per cap), and three graph replays of the step."""
+    from oracle.local import gather_tails
+    w, o, d = c3
+    tg, to, enew, env = _c3_step_check(w, o, d, gpu)
+    assert (env > 0).sum() >= 48
+    tails, tl = gather_tails(enew, to, 32)
+    caps = np.asarray(o._global_caps)
+    got = d.global_index._query_backoff(T(tails.astype(I32), gpu),
+                                        T(tl.astype(np.int64), gpu), 32,
+                                        T(caps, gpu))
+    exp = o.global_index._query_backoff(tails.astype(I32), tl, 32, caps)
+    for a, e in zip(got, exp):
+        np.testing.assert_array_equal(N(a), e)
+    # the step as the benchmark replays it
+    bt = w.batch
+    tok = T(bt.tokens, gpu)
+    nt = T(bt.num_tokens, gpu)
+    samp = T(bt.sampled, gpu)
+    for _ in range(2):
+        d.propose_with_update(nt, tok, samp)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = d.propose_with_update(nt, tok, samp)
+    for _ in range(3):
+        tok.copy_(T(bt.tokens, gpu))
+        graph.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(N(out[0]), N(d.propose_with_update(
+            nt, T(bt.tokens, gpu), samp)[0]))
+        np.testing.assert_array_equal(N(out[1]), env)
+        np.testing.assert_array_equal(N(tok), to)
+
+
+# ------------------------------------------------------------ SA builds
+def test_c4_from_scratch_builds(c3, gpu):
+    """The 4,193,511-token corpus and 2^22 uniform tokens, built from
+    scratch by the adaptive and the fixed-sequence form, against the
+    oracle's own builds; key rows of the uniform build by definition."""
+    from suffixgpu_amd.suffix_array import build_suffix_array_into
+    from suffixgpu_amd.global_index import PAD_TOKEN
+    w, o, d = c3
+    og = o.global_index
+    m = og.active_len + 1
+    text = torch.full((N22,), PAD_TOKEN, dtype=torch.int32, device=gpu)
+    text[:og.active_len].copy_(T(og.corpus[:og.active_len], gpu))
+    out = torch.empty(N22, dtype=torch.int32, device=gpu)
+    for adaptive in (True, False):
+        out.fill_(-7)
+        build_suffix_array_into(text, m, out, adaptive=adaptive)
+        np.testing.assert_array_equal(N(out), og.sa)
+    rng = np.random.default_rng(4)
+    uni = rng.integers(0, synth.VOCAB_LARGE, size=N22).astype(I32)
+    exp = osa.build_suffix_array(uni).astype(I32)
+    tu = T(uni, gpu)
+    for adaptive in (True, False):
+        out.fill_(-7)
+        build_suffix_array_into(tu, N22, out, adaptive=adaptive)
+        np.testing.assert_array_equal(N(out), exp)
+    from suffixgpu_amd import _lib
+    keys = torch.empty(N22 * 32, dtype=torch.int32, device=gpu)
+    _lib.check(_lib.lib().sfx_sa_keys(tu.data_ptr(), out.data_ptr(), N22, 32,
+                                      keys.data_ptr(),
+                                      _lib.stream_of(gpu)), "keys")
+    keys_by_definition(tu, out, keys)
+
+
+def test_c2_b64_local_matches_oracle(gpu):
+    """Local-only propose_with_update and propose at B=64, S=8192."""
+    from suffixgpu_amd import SuffixGPUDrafter
+    w = synth.local_zipf(seed=2, b=64, s=8192)
+    d = SuffixGPUDrafter(device=gpu, **CFG)
+    o = DrafterOracle(**CFG)
+    tg = T(w.tokens, gpu)
+    draft, nv, new = d.propose_with_update(T(w.num_tokens, gpu), tg,
+                                           T(w.sampled, gpu))
+    to = w.tokens.copy()
+    ed, env, enew = o.propose_with_update(w.num_tokens, to, w.sampled)
+    np.testing.assert_array_equal(N(tg), to)
+    np.testing.assert_array_equal(N(new), enew)
+    np.testing.assert_array_equal(N(draft), ed)
+    np.testing.assert_array_equal(N(nv), env)
+    draft, nv = d.propose(new, tg)
+    ed, env = o.propose(enew, to)
+    np.testing.assert_array_equal(N(draft), ed)
+    np.testing.assert_array_equal(N(nv), env)
+
+
+def test_c4_background_rebuild_and_swap(c3, gpu):
+    """The snapshot rebuild of the 2^22 index (oldest documents evicted so
+    that the corpus and the delta's whole documents fit) on the rebuild
+    stream while local-only B=64 steps run on the main stream; then the
+    swap, the index against the oracle's, and a global step on it.  Runs
+    last on the shared index: it changes it."""
+    from suffixgpu_amd import SuffixGPUDrafter
+    w, o, d = c3
+    o = copy.deepcopy(o)
+    gi, og = d.global_index, o.global_index
+    lw = synth.local_zipf(seed=2, b=64, s=8192)
+    dl = SuffixGPUDrafter(device=gpu, **CFG)
+    nt, samp = T(lw.num_tokens, gpu), T(lw.sampled, gpu)
+    ref = dl.propose_with_update(nt, T(lw.tokens, gpu), samp)
+    torch.cuda.synchronize()
+    gi.rebuild_threshold = og.rebuild_threshold = 1
+    gi.blocking_poll = False
+    gi.maybe_rebuild()
+    assert gi._rebuild_event is not None
+    outs = [dl.propose_with_update(nt, T(lw.tokens, gpu), samp)
+            for _ in range(8)]
+    gi.blocking_poll = True
+    gi.poll_rebuild()
+    og.maybe_rebuild()  # the oracle builds and swaps at once
+    torch.cuda.synchronize()
+    assert gi._rebuild_event is None
+    for got in outs:
+        for a, e in zip(got, ref):
+            np.testing.assert_array_equal(N(a), N(e))
+    index_equal(gi, og)
+    assert gi.active_len + gi.delta_len > 0 and gi.delta_len == 0
+    gi.rebuild_threshold = og.rebuild_threshold = 1 << 30
+    _c3_step_check(w, o, d, gpu)
+
+
+# ------------------------------------------------------------ decode loop
+C5_CHECK = (0, 1, 2, 3, 62, 63, 64, 65, 69)
+
+
+def test_c5_decode_loop_matches_oracle(gpu):
+    """B=256, S=16384: 70 replays of a captured propose_with_update with
+    the sampled block and counts fed back on the device, the step-63
+    harvest of the 16 longest rows into global memory (background
+    rebuilds at delta_capacity/2, blocking poll every step) and the rows
+    reset; new counts every step, the full step and token rows on the
+    chosen steps, and the index after the harvest."""
+    from suffixgpu_amd import SuffixGPUDrafter
+    steps = 70
+    lp = synth.decode_loop(seed=5, b=256, s=16384, steps=steps)
+    assert 63 in lp.harvests
+    kw = dict(enable_global=True, global_capacity=N22, delta_capacity=D16,
+              rebuild_threshold=D16 // 2, **CFG)
+    side = torch.cuda.Stream(gpu)
+    d = SuffixGPUDrafter(device=gpu, rebuild_stream=side, **kw)
+    gi = d.global_index
+    gi.blocking_poll = True
+    o = DrafterOracle(async_rebuild=True, **kw)
+    tok = T(lp.tokens, gpu)
+    nt = T(lp.num_tokens, gpu)
+    samp_all = T(lp.sampled, gpu)
+    samp = samp_all[0].clone()
+    for _ in range(3):
+        d.propose_with_update(nt, tok, samp)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = d.propose_with_update(nt, tok, samp)
+    torch.cuda.synchronize()
+    to = lp.tokens.copy()
+    ont = lp.num_tokens.copy()
+    swaps = 0
+    for i in range(steps):
+        samp.copy_(samp_all[i])
+        graph.replay()
+        nt.copy_(out[2])
+        if i in C5_CHECK:
+            ed, env, enew = o.propose_with_update(ont, to, lp.sampled[i])
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(N(out[0]), ed, err_msg=f"step {i}")
+            np.testing.assert_array_equal(N(out[1]), env, err_msg=f"step {i}")
+            np.testing.assert_array_equal(N(tok), to, err_msg=f"step {i}")
+        else:
+            enew = o.update_state(ont, to, lp.sampled[i])
+        np.testing.assert_array_equal(N(out[2]), enew, err_msg=f"step {i}")
+        ont = enew
+        hv = lp.harvests.get(i)
+        if hv is not None:
+            rows, lengths, new_rows, new_q = hv
+            before = gi.active_len
+            d.harvest_finished(rows, lengths, tok)
+            o.harvest_finished(rows, lengths, to)
+            idx = torch.tensor(rows, dtype=torch.int64, device=gpu)
+            tok.index_copy_(0, idx, T(new_rows, gpu))
+            nt.index_copy_(0, idx, T(new_q, gpu))
+            to[rows] = new_rows
+            ont = ont.copy()
+            ont[rows] = new_q
+            swaps += int(gi.active_len != before)
+        d.poll()
+        o.poll()
+        if hv is not None:
+            torch.cuda.synchronize()
+            index_equal(gi, o.global_index)
+    assert swaps >= 1 and gi.active_len > 0

@@ -430,6 +430,39 @@ def test_async_rebuild_blocking_poll(gpu, hint):
     gpu_state_equal(g, o)
 
 
+def test_round_hint_follows_the_last_build(gpu):
+    """The background rebuild's first chunk of doubling rounds is sized
+    from the rounds the previous build needed: a long exact repeat (one
+    token 6000 times) raises the hint past the default; once that document
+    is evicted, a build over short-repeat documents lowers it again (the
+    state copy is read even when the first chunk held every round)."""
+    from suffixgpu_amd.global_index import GlobalIndex
+    rng = np.random.default_rng(31)
+    side = torch.cuda.Stream(gpu)
+    kw = dict(capacity=8000, delta_capacity=7000, k=4, max_occurrences=8,
+              rebuild_threshold=4000)
+    g = GlobalIndex(device=gpu, rebuild_stream=side, **kw)
+    g.blocking_poll = True
+    o = GlobalIndexOracle(async_rebuild=True, **kw)
+    rep = np.full(6000, 3, I32)
+    g.append_documents([T(rep, gpu)])
+    o.append_documents([rep])
+    g.poll_rebuild()
+    o.poll_rebuild()
+    gpu_state_equal(g, o)
+    high = g.sa_round_hint
+    assert high > 12
+    docs = [rng.integers(0, 1000, size=900).astype(I32) for _ in range(5)]
+    g.append_documents([T(d, gpu) for d in docs])
+    o.append_documents(docs)
+    g.poll_rebuild()
+    o.poll_rebuild()
+    torch.cuda.synchronize()
+    gpu_state_equal(g, o)
+    assert list(g.active_doc_lens) == [901] * 5
+    assert g.sa_round_hint < 8 < high
+
+
 def test_save_restore_bit_exact(gpu, tmp_path):
     """A saved index restores to the same corpus, SA, delta, key rows and
     host state (into a new index and in place), and answers queries

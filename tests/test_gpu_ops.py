@@ -256,3 +256,25 @@ def test_delta_append_groups(gpu):
     assert rc == 0
     np.testing.assert_array_equal(d.cpu().numpy(), want)
     assert int(dl.item()) == off
+
+
+@pytest.mark.parametrize("weighted", [False, True])
+def test_majority_token_vs_oracle(gpu, weighted):
+    """expand._majority_token (a one-depth expansion) against the oracle's
+    pairwise vote.  Weights are multiples of 1/8, so every weight sum is
+    exact in fp32 whatever the summation order, and tokens and counts
+    compare exactly."""
+    from oracle.expand import majority_token as o_major
+    from suffixgpu_amd.expand import _majority_token
+    rng = np.random.default_rng(17)
+    b, r = 96, 40
+    vals = rng.integers(0, 6, size=(b, r)).astype(np.int64)
+    act = rng.random((b, r)) < 0.7
+    act[:4] = False  # rows with no active entry
+    w = ((rng.integers(1, 9, size=(b, r)) / 8).astype(np.float32)
+         if weighted else None)
+    tok, cnt = _majority_token(T(vals, gpu), T(act, gpu), -5,
+                               None if w is None else T(w, gpu))
+    etok, ecnt = o_major(vals, act, -5, w)
+    np.testing.assert_array_equal(N(tok), etok)
+    np.testing.assert_array_equal(N(cnt), ecnt)
