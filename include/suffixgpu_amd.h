@@ -3,11 +3,12 @@
  *
  * Every entry point takes device pointers, plain integer sizes and a
  * hipStream_t, enqueues work on that stream and returns without waiting.
- * None of them allocates device or host memory, synchronises, or keeps
- * state between calls: scratch memory is a caller-provided workspace whose
- * size the matching *_workspace_size() function reports.  Workspaces of the
- * fused step must be zero-filled once when allocated; the kernels leave
- * them zeroed again at the end of every call.
+ * None of them allocates device or host memory or synchronises.  Scratch
+ * memory is a caller-provided workspace whose size the matching
+ * *_workspace_size() function reports; the one exception,
+ * sfx_propose_step_noalloc, keeps its scratch in a static device array.
+ * Workspaces of the fused step must be zero-filled once when allocated;
+ * the kernels leave them zeroed again at the end of every call.
  *
  * Return value: 0 on success, SFX_EINVAL (-1) for an argument the kernels
  * cannot accept (reported before anything is enqueued), otherwise the
@@ -201,6 +202,26 @@ int sfx_propose_step(const sfx_params* p, const sfx_index* index,
                      int32_t* num_valid, int32_t* new_counts,
                      void* workspace, size_t workspace_bytes,
                      hipStream_t stream);
+
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): sfx_propose_step with no workspace argument.  The
+ * step's scratch is a static device array of SFX_NOALLOC_SCRATCH_BYTES
+ * bytes that every GPU the library runs on holds until the process ends;
+ * the call allocates nothing.  A batch of more than SFX_NOALLOC_MAX_ROWS
+ * rows, or one whose step needs more scratch than the array holds (large
+ * delta capacities with many rows), returns SFX_ENOSCRATCH before anything
+ * is enqueued.  Every call on one GPU shares that GPU's array: calls that
+ * overlap on a GPU (from two streams, or concurrent replays of graphs that
+ * hold this call) race and corrupt each other's drafts.  `stream` must
+ * belong to the device current on the calling thread. */
+#define SFX_ENOSCRATCH (-2)
+#define SFX_NOALLOC_SCRATCH_BYTES 16777216 /* 16 MiB */
+#define SFX_NOALLOC_MAX_ROWS 4096
+int sfx_propose_step_noalloc(const sfx_params* p, const sfx_index* index,
+                             const sfx_batch* batch, int32_t* draft,
+                             int32_t* num_valid, int32_t* new_counts,
+                             hipStream_t stream);
 
 /* ---- suffix-array rebuild (suffix_gpu/suffix_array.py:15-63,
  *      global_index.py:217-223) ------------------------------------------ */

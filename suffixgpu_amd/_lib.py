@@ -111,6 +111,10 @@ SIGNATURES = {
                                  ctypes.POINTER(SfxIndex),
                                  ctypes.POINTER(SfxBatch), c_p, c_p, c_p,
                                  c_p, ctypes.c_size_t, c_p]),
+    "sfx_propose_step_noalloc": (c_i32, [ctypes.POINTER(SfxParams),
+                                         ctypes.POINTER(SfxIndex),
+                                         ctypes.POINTER(SfxBatch), c_p, c_p,
+                                         c_p, c_p]),
     "sfx_sa_build_workspace_size": (ctypes.c_size_t, [c_i64]),
     "sfx_sa_keys": (c_i32, [c_p, c_p, c_i64, c_i64, c_p, c_p]),
     "sfx_sa_build": (c_i32, [c_p, c_i64, c_i64, c_p, c_i32, c_p,
@@ -160,14 +164,23 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
-# Error code of the C ABI besides hipError_t values.
+# Error codes of the C ABI besides hipError_t values.
 EINVAL = -1
+ENOSCRATCH = -2
+NOALLOC_SCRATCH_BYTES = 16 << 20
+NOALLOC_MAX_ROWS = 4096
 
 
 def check(rc: int, what: str) -> None:
     if rc != 0:
         if rc == EINVAL:
             raise SuffixGPUError(f"{what}: invalid argument")
+        if rc == ENOSCRATCH:
+            raise SuffixGPUError(
+                f"{what}: the batch needs more than the "
+                f"{NOALLOC_SCRATCH_BYTES >> 20} MiB static step scratch "
+                f"(or more than {NOALLOC_MAX_ROWS} rows); use the "
+                "workspace form")
         raise SuffixGPUError(f"{what}: HIP error {rc}")
 
 

@@ -9,6 +9,8 @@
 // so any scheduling order completes.  Local-only drafting is one workgroup
 // per row.  One kernel node per step keeps a captured HIP graph minimal.
 
+#include <mutex>
+
 #include "global_impl.h"
 #include "launch.h"
 #include "local_impl.h"
@@ -58,6 +60,23 @@ extern "C" size_t sfx_step_workspace_size(const sfx_params* p,
                                           int64_t delta_capacity) {
   if (!p || batch < 0) return 0;
   return step_ws_layout(*p, batch, delta_capacity, nullptr, nullptr);
+}
+
+// ------------------------------------------------- allocation-free form
+// The step's workspace as a file-scope device array: each GPU the library
+// runs on holds one copy until the process ends, and every call on that
+// GPU shares it.  Its handover counters sit at fixed offsets (arrays of
+// SFX_NOALLOC_MAX_ROWS rows), are cleared once per device at set-up and are
+// left zero by every step, so calls of any batch size can follow each
+// other; calls that overlap on one GPU race on them.
+static __device__ __align__(256) unsigned char
+    scratch[(size_t)SFX_NOALLOC_SCRATCH_BYTES];
+
+static __global__ __launch_bounds__(256) void k_zero_words(uint32_t* w,
+                                                           int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    w[i] = 0u;
 }
 
 namespace {
@@ -140,6 +159,38 @@ int launch_step(const sfx_params* p, const sfx_index* ix, const sfx_batch* bt,
   return (int)hipGetLastError();
 }
 
+constexpr int64_t kScratchRows = SFX_NOALLOC_MAX_ROWS;
+constexpr int kMaxDevices = 64;
+
+std::mutex scratch_mu;
+void* scratch_ptr[kMaxDevices] = {};
+
+// This device's copy of `scratch` (the device current on this host
+// thread).  The first call on a device resolves the address with
+// hipGetSymbolAddress -- in host code the array's name is not a device
+// address -- and clears the counter arrays with a fill kernel on `stream`.
+int scratch_of_current_device(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return SFX_EINVAL;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!ptr) return SFX_EINVAL;
+    const int64_t words = 3 * kScratchRows;  // join, djoin, pick
+    hipLaunchKernelGGL(k_zero_words, dim3(64), dim3(256), 0, stream,
+                       (uint32_t*)ptr, words);
+    e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    scratch_ptr[dev] = ptr;
+  }
+  *out = scratch_ptr[dev];
+  return 0;
+}
+
 }  // namespace
 
 extern "C" int sfx_propose_step(const sfx_params* p, const sfx_index* ix,
@@ -149,4 +200,26 @@ extern "C" int sfx_propose_step(const sfx_params* p, const sfx_index* ix,
                                 hipStream_t stream) {
   return launch_step(p, ix, bt, draft, num_valid, new_counts, workspace,
                      workspace_bytes, -1, stream);
+}
+
+extern "C" int sfx_propose_step_noalloc(const sfx_params* p,
+                                        const sfx_index* ix,
+                                        const sfx_batch* bt, int32_t* draft,
+                                        int32_t* num_valid,
+                                        int32_t* new_counts,
+                                        hipStream_t stream) {
+  if (!p || !bt) return SFX_EINVAL;
+  if (!ix)  // local-only steps use no workspace
+    return launch_step(p, nullptr, bt, draft, num_valid, new_counts, nullptr,
+                       0, -1, stream);
+  if (bt->batch < 0) return SFX_EINVAL;
+  if (bt->batch > kScratchRows ||
+      step_ws_layout(*p, bt->batch, ix->delta_capacity, nullptr, nullptr,
+                     kScratchRows) > (size_t)SFX_NOALLOC_SCRATCH_BYTES)
+    return SFX_ENOSCRATCH;
+  void* ws = nullptr;
+  const int rc = scratch_of_current_device(stream, &ws);
+  if (rc) return rc;
+  return launch_step(p, ix, bt, draft, num_valid, new_counts, ws,
+                     (size_t)SFX_NOALLOC_SCRATCH_BYTES, kScratchRows, stream);
 }

@@ -65,7 +65,10 @@ def test_abi_version_and_constants(so):
     assert _lib.ABI_VERSION == header_define("SFX_ABI_VERSION")
     assert _lib.MAX_CANDIDATES == header_define("SFX_MAX_CANDIDATES")
     assert _lib.EINVAL == header_define("SFX_EINVAL")
-
+    assert _lib.ENOSCRATCH == header_define("SFX_ENOSCRATCH")
+    assert (_lib.NOALLOC_SCRATCH_BYTES
+            == header_define("SFX_NOALLOC_SCRATCH_BYTES"))
+    assert _lib.NOALLOC_MAX_ROWS == header_define("SFX_NOALLOC_MAX_ROWS")
 
 
 def test_workspace_sizes_are_host_only(so):
