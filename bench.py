@@ -49,7 +49,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--cpu-steps", type=int, default=40)
+    ap.add_argument("--cpu-steps", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=50)
     ap.add_argument("--no-e2e", action="store_true",
@@ -329,9 +329,12 @@ def main() -> int:
         e2e = e2e_loop(dev, args.e2e_steps)
         log(f"e2e decode loop: {e2e}")
 
+    local_cfgs = local_configs(dev, 200, not args.no_cpu)
+    sweep = latency_sweep(dev, 50)
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(d, w, args.cpu_steps)
+        cpu = cpu_baseline(d, w, args.cpu_steps,
+                           (draft, num_valid, new_counts))
 
     sa_corpus_ms, sa_m = build_ms["corpus"]
     sa_uni_ms, _ = build_ms["uniform"]
@@ -376,6 +379,9 @@ def main() -> int:
         "sa_rebuild_concurrent": conc,
         "c5_local_step": c5,
         "e2e_decode_loop": e2e,
+        "local_configs": local_cfgs,
+        "latency_sweep": sweep,
+        "vram": drafter_device_bytes(d, B, S),
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
@@ -531,6 +537,183 @@ def concurrent_rebuild(graph, w, dev, rounds: int) -> dict:
                 round(statistics.median(during), 3) if during else None}
 
 
+def replay_p50(fn, reps: int, warmup: int = 5, before=None):
+    """Capture fn() once as a HIP graph; p50 µs of `reps` replays between
+    event pairs (``before`` runs outside each timed pair), and the wall µs
+    per replay of `reps` replays queued back to back."""
+    import torch
+    for _ in range(3):
+        if before:
+            before()
+        fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn()
+    cur = torch.cuda.current_stream()
+    per = []
+    for i in range(warmup + reps):
+        if before:
+            before()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(cur)
+        g.replay()
+        e1.record(cur)
+        if i >= warmup:
+            per.append((e0, e1))
+    torch.cuda.synchronize()
+    p50 = statistics.median(a.elapsed_time(b) * 1e3 for a, b in per)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g.replay()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e6 / reps
+    return p50, wall, out, g
+
+
+def cpu_times(fn, reps: int, warmup: int) -> float:
+    """p50 µs of fn() over `reps` calls after `warmup` calls."""
+    for _ in range(warmup):
+        fn()
+    per = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        per.append(time.perf_counter() - t0)
+    return statistics.median(per) * 1e6
+
+
+# The reference's two local-only workloads: propose on B=8 rows of S=2048
+# uniform tokens with one support threshold, and propose_with_update on
+# B=64 rows of S=8192 Zipf tokens with eight.
+CFG1 = dict(k=16, max_pattern_len=32, max_occurrences=128, num_backoff=1,
+            max_spec_factor=None, min_token_prob=0.0)
+
+
+def local_configs(dev, reps: int, cpu: bool) -> dict:
+    """GPU graph-replay p50 and the oracle's CPU time (one thread, and all
+    cores by row slices) for the two local-only workloads; the GPU output
+    of each is compared with the oracle's."""
+    import torch
+    from oracle.drafter import DrafterOracle
+    from oracle.pool import RowPool, default_workers
+    from suffixgpu_amd import SuffixGPUDrafter, synth
+    res = {}
+    for name, w, kw, upd in (
+            ("config1", synth.local_uniform(seed=1), CFG1, False),
+            ("config2", synth.local_zipf(seed=2), CFG, True)):
+        d = SuffixGPUDrafter(device=dev, **kw)
+        tok = torch.from_numpy(w.tokens).to(dev)
+        nt = torch.from_numpy(w.num_tokens).to(dev)
+        if upd:
+            samp = torch.from_numpy(w.sampled).to(dev)
+            fn = lambda: d.propose_with_update(nt, tok, samp)  # noqa: E731
+        else:
+            fn = lambda: d.propose(nt, tok)  # noqa: E731
+        p50, wall, out, _ = replay_p50(fn, reps)
+        o = DrafterOracle(**kw)
+        tok_o = w.tokens.copy()
+        if upd:
+            exp = o.propose_with_update(w.num_tokens, tok_o, w.sampled)
+        else:
+            exp = o.propose(w.num_tokens, tok_o)
+        same = all(np.array_equal(a.cpu().numpy(), e)
+                   for a, e in zip(out, exp))
+        r = {"b": int(w.tokens.shape[0]), "s": int(w.tokens.shape[1]),
+             "op": "propose_with_update" if upd else "propose",
+             "gpu_graph_p50_us": round(p50, 3),
+             "gpu_graph_wall_us": round(wall, 3),
+             "matches_oracle": bool(same)}
+        if cpu:
+            def one():
+                t = w.tokens.copy()
+                if upd:
+                    o.propose_with_update(w.num_tokens, t, w.sampled)
+                else:
+                    o.propose(w.num_tokens, t)
+            r["cpu_1thread_us"] = round(cpu_times(one, 5 if upd else 20,
+                                                  1 if upd else 3), 1)
+            with RowPool(kw) as pool:
+                def many():
+                    t = w.tokens.copy()
+                    if upd:
+                        pool.propose_with_update(w.num_tokens, t, w.sampled)
+                    else:
+                        pool.propose(w.num_tokens, t)
+                r["cpu_all_cores_us"] = round(cpu_times(many, 20, 3), 1)
+                r["cpu_cores"] = pool.workers
+        res[name] = r
+        log(f"{name}: {r}")
+        del d, tok
+    return res
+
+
+# The reference's standalone latency sweep (bench_vs_cpu.py --mode
+# latency): propose() on uniform-random rows (vocab 32000, num_tokens in
+# [S/2, S)), k=16, max_pattern_len=24, spec_factor 2.0, min_prob 0.1, and
+# with global memory a 2^20 corpus / 2^15 delta fed 96 documents of 4096
+# tokens.  Its published L20 graph-mode ms/step (RESULTS.md §4):
+REF_SWEEP_GRAPH_MS = {
+    (False, 4096): (0.10, 0.11, 0.13, 0.16),
+    (False, 16384): (0.14, 0.15, 0.15, 0.23),
+    (True, 4096): (0.34, 0.38, 0.44, 0.65),
+    (True, 16384): (0.38, 0.42, 0.46, 0.74),
+}
+SWEEP_B = (1, 8, 32, 128)
+
+
+def latency_sweep(dev, reps: int) -> list:
+    import torch
+    from suffixgpu_amd import SuffixGPUDrafter
+    rng = np.random.default_rng(0)
+    kw = dict(k=16, max_pattern_len=24, max_spec_factor=2.0,
+              min_token_prob=0.1, global_capacity=1 << 20,
+              delta_capacity=1 << 15)
+    rows = []
+    for glob in (False, True):
+        d = SuffixGPUDrafter(device=dev, enable_global=glob,
+                             rebuild_stream=torch.cuda.Stream(dev), **kw)
+        if glob:
+            gi = d.global_index
+            gi.blocking_poll = True
+            docs = [torch.from_numpy(rng.integers(0, 32000, size=4096)).to(
+                dev, torch.int32) for _ in range(96)]
+            d.harvest_rows(docs, [4096] * len(docs))
+            d.poll()
+            torch.cuda.synchronize()
+        for s in (4096, 16384):
+            for i, b in enumerate(SWEEP_B):
+                buf = torch.from_numpy(rng.integers(0, 32000, size=(b, s))).to(
+                    dev, torch.int32)
+                nt = torch.from_numpy(rng.integers(
+                    s // 2, s, size=b).astype(np.int32)).to(dev)
+                p50, wall, _, _ = replay_p50(lambda: d.propose(nt, buf), reps)
+                rows.append({"global": glob, "s": s, "b": b,
+                             "graph_p50_us": round(p50, 2),
+                             "graph_wall_us": round(wall, 2),
+                             "reference_l20_graph_us":
+                                 REF_SWEEP_GRAPH_MS[(glob, s)][i] * 1e3})
+        del d
+    log("latency sweep: " + "; ".join(
+        f"{'g' if r['global'] else 'l'} S={r['s']} B={r['b']}: "
+        f"{r['graph_p50_us']}" for r in rows))
+    return rows
+
+
+def drafter_device_bytes(d, b: int, s: int) -> dict:
+    """Device memory the drafter holds (exact tensor sizes), next to the
+    caller's [B, S] token buffer."""
+    ws = sum(t.numel() for t in d._ws.values())
+    out = {"step_workspaces": ws}
+    if d.global_index is not None:
+        out.update(d.global_index.device_bytes())
+    total = sum(out.values())
+    return {"persistent_mb": round(total / 1e6, 1),
+            "by_role_mb": {k: round(v / 1e6, 2) for k, v in out.items()},
+            "token_buffer_mb": round(b * s * 4 / 1e6, 1)}
+
+
 def e2e_loop(dev, steps: int) -> dict:
     """Scripted decode loop (B=256, S=16384): captured propose_with_update
     per step with the sampled block and counts fed back on the device,
@@ -620,7 +803,10 @@ def e2e_loop(dev, steps: int) -> dict:
                 round(float(nv_log.sum().item()) / steps, 2),
             "harvests": len(lp.harvests), "rebuilds_launched": launches,
             "swaps": swaps, "active_len": gi.active_len,
-            "generate_s": round(gen_s, 2)}
+            "generate_s": round(gen_s, 2),
+            "vram": dict(drafter_device_bytes(d, lp.tokens.shape[0],
+                                              lp.tokens.shape[1]),
+                         reference_l20_persistent_mb=96.3)}
 
 
 def step_kernel_us(d, dev, tokens0, nt, sampled, reps):
@@ -1053,34 +1239,52 @@ def load_traffic(kernel: str):
         return None
 
 
-def cpu_baseline(d, w, steps):
+def cpu_baseline(d, w, steps, gpu_out):
     """The oracle (numpy restatement of the reference's CPU path) timed on
-    this host on `steps` steps of the same batch and index state."""
+    this host on the same batch and index state: every host core (row
+    slices in worker processes, `steps` steps after 3) and one thread (a
+    few steps).  The index arrays are the GPU-built ones, loaded into the
+    oracle (its own builds are checked by the config parity tests); the
+    first CPU step is compared with the GPU step."""
     from oracle.drafter import DrafterOracle
+    from oracle.pool import RowPool
     gi = d.global_index
-    o = DrafterOracle(enable_global=True, global_capacity=CAPACITY,
-                      delta_capacity=DELTA_CAP, rebuild_threshold=1 << 30,
-                      **CFG)
+    kw = dict(enable_global=True, global_capacity=CAPACITY,
+              delta_capacity=DELTA_CAP, rebuild_threshold=1 << 30, **CFG)
+    index = {"corpus": gi.corpus.cpu().numpy(), "sa": gi.sa.cpu().numpy(),
+             "delta": gi.delta[:gi.delta_len].cpu().numpy(),
+             "active_len": gi.active_len, "delta_len": gi.delta_len}
+    o = DrafterOracle(**kw)
     og = o.global_index
-    og.corpus[:] = gi.corpus.cpu().numpy()
-    og.sa[:] = gi.sa.cpu().numpy()
-    og.delta[:] = gi.delta.cpu().numpy()
+    og.corpus[:] = index["corpus"]
+    og.sa[:] = index["sa"]
+    og.delta[:gi.delta_len] = index["delta"]
     og.active_len = gi.active_len
     og.delta_len = gi.delta_len
     bt = w.batch
-    times = []
-    for _ in range(steps):
-        tok = bt.tokens.copy()
-        t0 = time.perf_counter()
-        o.propose_with_update(bt.num_tokens, tok, bt.sampled)
-        times.append(time.perf_counter() - t0)
-    us = statistics.median(times) * 1e6
-    log(f"cpu baseline: {us / 1e3:.1f} ms/step")
-    return {"value": round(us, 1), "unit": "us/step", "cores": 1,
+    tok = bt.tokens.copy()
+    first = o.propose_with_update(bt.num_tokens, tok, bt.sampled)
+    same = all(np.array_equal(a, b) for a, b in zip(first, gpu_out))
+
+    def one():
+        o.propose_with_update(bt.num_tokens, bt.tokens.copy(), bt.sampled)
+    one_us = cpu_times(one, 3, 0)
+    with RowPool(kw, index=index) as pool:
+        def many():
+            pool.propose_with_update(bt.num_tokens, bt.tokens.copy(),
+                                     bt.sampled)
+        us = cpu_times(many, steps, 3)
+        cores = pool.workers
+    log(f"cpu baseline: {us / 1e3:.1f} ms/step on {cores} cores, "
+        f"{one_us / 1e3:.1f} ms/step on one thread; matches GPU: {same}")
+    return {"value": round(us, 1), "unit": "us/step", "cores": cores,
             "kind": "port",
             "sample": f"{steps} propose_with_update steps of the same B=64 "
-                      "batch and index (numpy oracle, one thread); "
-                      f"host has {os.cpu_count()} logical CPUs"}
+                      "batch and index (the numpy oracle, rows split over "
+                      f"{cores} worker processes), after 3 warm-up steps; "
+                      f"host has {os.cpu_count()} logical CPUs",
+            "one_thread_us": round(one_us, 1),
+            "matches_gpu_step": bool(same)}
 
 
 if __name__ == "__main__":

@@ -504,3 +504,45 @@ def test_proposer_global_harvest():
     exp_chain, _ = naive.global_chain([done], [9, 8, 7, 6], 4, 8, 8)
     assert nv[1] == len(exp_chain) and draft[1, :nv[1]].tolist() == exp_chain
     assert nv[0] == 0
+
+
+def test_row_pool_matches_single_process():
+    """The row-parallel oracle (the benchmark's multi-core CPU baseline)
+    returns exactly the single-process step, local-only and with a global
+    index, and updates the token rows the same way."""
+    from oracle.pool import RowPool
+    from suffixgpu_amd import synth
+    kw = dict(k=8, max_pattern_len=16, max_occurrences=32, num_backoff=6,
+              max_spec_factor=2.0, min_token_prob=0.05)
+    w = synth.local_zipf(seed=9, b=13, s=600, lo=100)
+    o = DrafterOracle(**kw)
+    tok = w.tokens.copy()
+    exp = o.propose_with_update(w.num_tokens, tok, w.sampled)
+    with RowPool(kw, workers=3) as pool:
+        tp = w.tokens.copy()
+        got = pool.propose_with_update(w.num_tokens, tp, w.sampled)
+        np.testing.assert_array_equal(tp, tok)
+        for a, e in zip(got, exp):
+            np.testing.assert_array_equal(a, e)
+        for a, e in zip(pool.propose(exp[2], tp), o.propose(exp[2], tok)):
+            np.testing.assert_array_equal(a, e)
+    gkw = dict(kw, enable_global=True, global_capacity=1 << 14,
+               delta_capacity=1 << 12, rebuild_threshold=1 << 20)
+    gw = synth.global_corpus(seed=4, capacity=1 << 14, delta_fill=2100,
+                             n_docs=12, b=11, s=1600, seq_hi=1300)
+    o = DrafterOracle(**gkw)
+    o.global_index.load_documents(gw.active_docs)
+    o.global_index.append_documents(gw.delta_docs)
+    g = o.global_index
+    index = {"corpus": g.corpus, "sa": g.sa, "delta": g.delta[:g.delta_len],
+             "active_len": g.active_len, "delta_len": g.delta_len}
+    tok = gw.batch.tokens.copy()
+    exp = o.propose_with_update(gw.batch.num_tokens, tok, gw.batch.sampled)
+    assert (exp[1] > 0).any()
+    with RowPool(gkw, index=index, workers=4) as pool:
+        tp = gw.batch.tokens.copy()
+        got = pool.propose_with_update(gw.batch.num_tokens, tp,
+                                       gw.batch.sampled)
+    np.testing.assert_array_equal(tp, tok)
+    for a, e in zip(got, exp):
+        np.testing.assert_array_equal(a, e)
