@@ -32,7 +32,7 @@ extern "C" {
 
 #define SFX_EINVAL (-1)
 #define SFX_MAX_CANDIDATES 32
-#define SFX_ABI_VERSION 7
+#define SFX_ABI_VERSION 8
 
 /* Drafter configuration shared by the local and global paths.
  * Mirrors the constructor arguments of SuffixGPUDrafter
@@ -78,6 +78,10 @@ typedef struct sfx_index {
                                   NULL                                   */
     const int32_t* key_select; /* device int32 selecting sa_key_alt when
                                   nonzero, or NULL (sa_key is live)      */
+    const void* gram;          /* n-gram range table of sa_key's suffix
+                                  array (sfx_gram_build), or NULL         */
+    const void* gram_alt;      /* the table of sa_key_alt's, or NULL      */
+    int64_t gram_slots;        /* slots per table, a power of two         */
 } sfx_index;
 
 /* One decode step's batch (suffix_gpu/proposer.py:135-214).
@@ -240,6 +244,19 @@ int sfx_sa_keys(const int32_t* corpus, const int32_t* sa, int64_t n,
 int sfx_sa_build(const int32_t* text, int64_t m, int64_t n_total, void* sa,
                  int32_t sa_is64, void* workspace, size_t workspace_bytes,
                  hipStream_t stream);
+
+/* No reference counterpart.  The n-gram range table of a suffix array:
+ * for every distinct run of the first k tokens (k = 1..4, real tokens
+ * only) among the sorted suffixes, the rank range of the suffixes that
+ * start with it, so that an interval search starts inside the range of its
+ * pattern's first tokens.  `table` (256-byte aligned, sfx_gram_table_bytes
+ * bytes, zero-filled once when allocated) is rebuilt in place from the key
+ * rows (key_width 4..32, 16-byte aligned) of ranks 0..m-1; enqueued on
+ * `stream` with no host read.  A table whose slots run out marks itself
+ * unusable and searches then ignore it. */
+size_t sfx_gram_table_bytes(int64_t slots);
+int sfx_gram_build(const int32_t* keys, int64_t key_width, int64_t m,
+                   void* table, int64_t slots, hipStream_t stream);
 
 /* The same build in steps, for a caller that advances it from a host poll
  * loop and stops enqueueing rounds once the array is final (no reference

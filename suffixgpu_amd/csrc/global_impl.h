@@ -3,6 +3,7 @@
 // Included by global.hip (standalone kernel) and step.hip (fused step).
 #pragma once
 
+#include "gram.h"
 #include "pick.h"
 #include "sa_search.h"
 #include "sfx_common.h"
@@ -34,8 +35,8 @@ struct GlobalArgs {
 
 struct GlobalLayout {
   int rpat, lb, ub, found, scan, red, misc, lo, dlen, dcnt, dpc, sal, sas,
-      sae, dtok, dmb, mpos, mcache, mA, mH, chain, nv, score, rlen, rocc,
-      total;
+      sae, caps, dtok, dmb, mpos, mcache, mA, mH, chain, nv, score, rlen,
+      rocc, total;
 };
 
 // Delta tokens staged per chunk (after a halo of P rounded up to 4
@@ -73,6 +74,7 @@ __host__ __device__ inline GlobalLayout global_layout(int P, int C, int R,
   L.sal = g_take(off, C * 4);
   L.sas = g_take(off, C * 4);
   L.sae = g_take(off, C * 4);
+  L.caps = g_take(off, C * 4);
   L.chain = g_take(off, C * K * 4);
   L.nv = g_take(off, C * 4);
   L.score = g_take(off, C * 4);
@@ -205,7 +207,8 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
   int part_max = 0;
   for (int w = 0; w < NW; ++w) part_max = max(part_max, red[w]);
   SFX_TRACE_POINT(2);
-  for (int c = tid; c < C; c += NT) lo_lds[c] = min(part_max, p.caps[c]);
+  const int32_t* caps = (const int32_t*)(smem + L.caps);
+  for (int c = tid; c < C; c += NT) lo_lds[c] = min(part_max, caps[c]);
   __syncthreads();
   for (int g0 = 0; g0 < C; g0 += 8)
     compact_first_r<NT>(mb, phi - plo, lo_lds + g0, min(8, C - g0), R,
@@ -222,13 +225,14 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
 // workgroup): dlen[c] = min(max mb, cap), dpc[c][k] = part k's kept hits,
 // dcnt[c] = min(sum, R).
 __device__ __forceinline__ void delta_combine(const GlobalArgs& a, int b,
+                                              const int32_t* caps,
                                               int32_t* dlen, int32_t* dcnt,
                                               int32_t* dpc) {
   const int C = a.p.num_caps;
   const int R = a.p.max_occurrences;
   const int KD = a.dparts;
   for (int c = threadIdx.x; c < C; c += blockDim.x) {
-    const int cap = a.p.caps[c];
+    const int cap = caps[c];
     int mx = 0;
     for (int k = 0; k < KD; ++k) mx = max(mx, a.ws.d_mx[(int64_t)b * KD + k]);
     const int lo = min(mx, cap);
@@ -406,6 +410,12 @@ __device__ __forceinline__ const int32_t* live_keys(const sfx_index& ix) {
   return ix.sa_key;
 }
 
+// The n-gram range table of the live suffix array, or NULL.
+__device__ __forceinline__ const void* live_gram(const sfx_index& ix) {
+  if (ix.key_select && ix.gram_alt && *ix.key_select != 0) return ix.gram_alt;
+  return ix.gram;
+}
+
 // role 0: SA search; role 1 .. dparts: delta part role - 1.
 __device__ __forceinline__ void global_body(const GlobalArgs& a,
                                             unsigned char* smem, int b,
@@ -432,6 +442,10 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
   const int64_t N = a.ix.capacity;
   const int64_t D = a.ix.delta_capacity;
   SFX_TRACE_POINT(0);
+  // The caps, read by thread index later (delta thresholds, combine): a
+  // varying index into the kernel arguments is a vector load from device
+  // memory, so it is issued once here, ahead of the first barrier.
+  if (tid < C) ((int32_t*)(smem + L.caps))[tid] = p.caps[tid];
 
   // Query tail, newest first: rpat[t] = tail token t back from the end;
   // -3 past the start (global_index.py:493-501).
@@ -470,12 +484,48 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
     const int ngroups = NT / G;
     const int g = tid / G;
     const int32_t* keys = live_keys(a.ix);
+    // The n-gram table narrows each search to the ranks that share its
+    // pattern's first min(l, kGramMax) tokens (the whole answer for
+    // l <= kGramMax); without a usable table every search spans [0, N).
+    const void* gram = live_gram(a.ix);
+    uint32_t gram_epoch = 0;
+    if (gram) {
+      const GramHeader* gh = reinterpret_cast<const GramHeader*>(gram);
+      if (gh->ok && a.ix.gram_slots > 0) gram_epoch = gh->epoch;
+    }
+    const uint32_t gram_mask = (uint32_t)(a.ix.gram_slots - 1);
     for (int l = g + 1; l <= P; l += ngroups) {
       int64_t lo = 0, hi = 0;
       if (l <= plen) {
         auto pat_at = [&](int j) -> int32_t { return rpat[l - 1 - j]; };
-        kary_bounds<G>(a.ix.sa, a.ix.corpus, N, keys, (int)a.ix.key_width,
-                       pat_at, l, lo, hi);
+        uint32_t r0 = 0, r1 = (uint32_t)N;
+        int found = -1;
+        const int k = l < kGramMax ? l : kGramMax;
+        int32_t t[4] = {0, 0, 0, 0};
+        bool real = true;
+#pragma unroll
+        for (int j = 0; j < kGramMax; ++j) {
+          if (j < k) {
+            t[j] = pat_at(j);
+            real = real && gram_real(t[j]);
+          }
+        }
+        if (gram_epoch && real)
+          found = gram_lookup<G>(gram, gram_mask, gram_epoch, t[0], t[1],
+                                 t[2], t[3], k, r0, r1);
+        if (found == 0) {
+          lo = hi = 0;  // no suffix starts with the first k tokens
+        } else if (found == 1 && l == k) {
+          lo = r0;
+          hi = r1;
+        } else {
+          if (found != 1) {
+            r0 = 0;
+            r1 = (uint32_t)N;
+          }
+          kary_bounds<G>(a.ix.sa, a.ix.corpus, N, keys, (int)a.ix.key_width,
+                         pat_at, l, lo, hi, r0, r1);
+        }
       }
       if (tid % G == 0) {
         lbs[l - 1] = lo;
@@ -542,7 +592,7 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
       int32_t* dlen = (int32_t*)(smem + L.dlen);
       int32_t* dcnt = (int32_t*)(smem + L.dcnt);
       int32_t* dpc = (int32_t*)(smem + L.dpc);
-      delta_combine(a, b, dlen, dcnt, dpc);
+      delta_combine(a, b, (const int32_t*)(smem + L.caps), dlen, dcnt, dpc);
       __syncthreads();
       for (int c = tid; c < C; c += NT) a.ws.dl_c[(int64_t)b * C + c] = dlen[c];
       SFX_TRACE_POINT(5);
@@ -563,7 +613,7 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
   int32_t* dlen = (int32_t*)(smem + L.dlen);
   int32_t* dcnt = (int32_t*)(smem + L.dcnt);
   int32_t* dpc = (int32_t*)(smem + L.dpc);
-  delta_combine(a, b, dlen, dcnt, dpc);
+  delta_combine(a, b, (const int32_t*)(smem + L.caps), dlen, dcnt, dpc);
   __syncthreads();
   if (a.out.d_len || a.out.d_cnt)
     for (int c = tid; c < C; c += NT) {

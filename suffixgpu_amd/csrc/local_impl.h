@@ -29,8 +29,8 @@ struct LocalArgs {
 };
 
 struct LocalLayout {
-  int row, mb, pat, hist, cand, found, scan, occ, A, H, chain, nv, score,
-      misc, total;
+  int row, mb, pat, hist, cand, found, thr, scan, occ, A, H, chain, nv,
+      score, misc, total;
 };
 
 __host__ __device__ inline int lds_take(int& off, int bytes) {
@@ -65,6 +65,7 @@ __host__ __device__ inline LocalLayout local_layout(int S, int P, int C,
   L.hist = lds_take(off, (P + 1) * 4);
   L.cand = lds_take(off, C * 4);
   L.found = lds_take(off, C * 4);
+  L.thr = lds_take(off, C * 4);
   L.scan = lds_take(off, 4 * nwaves * 8);
   L.occ = lds_take(off, C * R * 4);
   L.A = lds_take(off, nwaves * ((R + 3) & ~3) * 4);
@@ -105,6 +106,7 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
   int32_t* hist = (int32_t*)(smem + L.hist);
   int32_t* cand = (int32_t*)(smem + L.cand);
   int32_t* found = (int32_t*)(smem + L.found);
+  int32_t* thr_lds = (int32_t*)(smem + L.thr);
   uint32_t* scan = (uint32_t*)(smem + L.scan);
   int32_t* occ = (int32_t*)(smem + L.occ);
   int32_t* Abuf = (int32_t*)(smem + L.A);
@@ -114,6 +116,7 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
   int* misc = (int*)(smem + L.misc);
 
   SFX_TRACE_POINT(0);
+  if (tid < C) thr_lds[tid] = p.thresholds[tid];
   const RowState st = row_state(a.bt, b);
   const int64_t q = st.q;
 
@@ -125,9 +128,22 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
   if (!kStream) {
     const int qs = (int)(q < 0 ? 0 : (q < S ? q : S));
     if (vec4) {
+      // Four 16-byte loads in flight per thread before their LDS stores.
       const int4* src = reinterpret_cast<const int4*>(grow);
       int4* dst = reinterpret_cast<int4*>(row);
-      for (int i = tid; i < (qs + 3) / 4; i += NT) dst[i] = src[i];
+      const int n4 = (qs + 3) / 4;
+      int i = tid;
+      for (; i + 3 * NT < n4; i += 4 * NT) {
+        const int4 v0 = src[i];
+        const int4 v1 = src[i + NT];
+        const int4 v2 = src[i + 2 * NT];
+        const int4 v3 = src[i + 3 * NT];
+        dst[i] = v0;
+        dst[i + NT] = v1;
+        dst[i + 2 * NT] = v2;
+        dst[i + 3 * NT] = v3;
+      }
+      for (; i < n4; i += NT) dst[i] = src[i];
     } else {
       for (int i = tid; i < qs; i += NT) row[i] = grow[i];
     }
@@ -206,18 +222,76 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
       __syncthreads();
     }
   } else {
-    for (int i = tid; i < S; i += NT) {
-      int m = 0;
-      if ((int64_t)i < q) {
-        for (int t = 0; t < P; ++t) {
-          const int j = i - 1 - t;
-          const int32_t x = j >= 0 ? row[j] : -1;
-          if (x != pat[t]) break;
-          ++m;
+    // Four ends i0 .. i0 + 3 per thread from two 16-byte LDS reads: x(i - 1)
+    // is tested against the newest pattern token first and only ends that
+    // pass walk further back.  Match lengths are stored as one u32 of four
+    // bytes; positions from qe on are never read (the compaction stops
+    // there).  Each wave adds equal lengths to the histogram with one LDS
+    // atomic (matches pile onto hist[1] and hist[2] on repetitive rows).
+    // The first four pattern tokens are tested at every end without a
+    // branch (two 16-byte reads give x(i0 - 4) .. x(i0 + 3)); only ends
+    // matching all four walk further back.  On rows whose newest token is
+    // frequent most ends match one token, so the walk's setup would run in
+    // most waves' iterations.
+    const int32_t p0 = pat[0];
+    const int32_t p1 = P > 1 ? pat[1] : 0;
+    const int32_t p2 = P > 2 ? pat[2] : 0;
+    const int32_t p3 = P > 3 ? pat[3] : 0;
+    const int4* row4 = reinterpret_cast<const int4*>(row);
+    const int ng = (qe + 3) / 4;
+    for (int g = tid; g - tid < ng; g += NT) {
+      uint32_t word = 0;
+      if (g < ng) {
+        const int i0 = 4 * g;
+        const int4 lo4 = g > 0 ? row4[g - 1] : make_int4(-1, -1, -1, -1);
+        const int4 hi4 = row4[g];
+        // w[k] = x(i0 - 4 + k); end i0 + u reads x(i0 + u - 1 - t) =
+        // w[3 + u - t] for pattern token t
+        const int32_t w[8] = {lo4.x, lo4.y, lo4.z, lo4.w,
+                              hi4.x, hi4.y, hi4.z, hi4.w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const bool e0 = i0 + u < qe && w[3 + u] == p0;
+          const bool e1 = e0 && P > 1 && w[2 + u] == p1;
+          const bool e2 = e1 && P > 2 && w[1 + u] == p2;
+          const bool e3 = e2 && P > 3 && w[u] == p3;
+          int m = (int)e0 + (int)e1 + (int)e2 + (int)e3;
+          if (e3 && P > 4) {
+            // Walk back four tokens per step: the four row tokens and
+            // pattern tokens of a step are independent LDS reads.
+            const int base = i0 + u - 1;  // row index of x(i - 1)
+            while (m < P) {
+              int32_t x4[4], p4[4];
+#pragma unroll
+              for (int k = 0; k < 4; ++k) {
+                const int j = base - m - k;
+                x4[k] = j >= 0 ? row[j] : -1;
+                p4[k] = pat[m + k < P ? m + k : P - 1];
+              }
+              int k = 0;
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                k += (k == e && m + e < P && x4[e] == p4[e]) ? 1 : 0;
+              m += k;
+              if (k < 4) break;
+            }
+          }
+          word |= (uint32_t)m << (8 * u);
+        }
+        *reinterpret_cast<uint32_t*>(mbuf + i0) = word;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int m = (int)((word >> (8 * u)) & 0xffu);
+        uint64_t pend = ballot(m > 0);
+        while (pend) {
+          const int lead = __builtin_ctzll(pend);
+          const int mv = __builtin_amdgcn_readlane(m, lead);
+          const uint64_t same = ballot(m == mv) & pend;
+          if (ln == lead) atomicAdd(&hist[mv], popc(same));
+          pend &= ~same;
         }
       }
-      mbuf[i] = (uint8_t)m;
-      if (m > 0) atomicAdd(&hist[m], 1);
     }
     __syncthreads();
   }
@@ -251,12 +325,21 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
       carry = __shfl(x, kWave - 1);
     }
     wave_lds_sync();
-    int maxthr = p.thresholds[0];
-    for (int c = 1; c < C; ++c) maxthr = max(maxthr, p.thresholds[c]);
+    // Both loops run unrolled over the largest candidate count, so every
+    // threshold is a kernel argument at a fixed offset (a scalar load issued
+    // at the start); a varying index would turn each read into a vector
+    // load from the argument segment in device memory.
+    // Lane c holds threshold c, copied to LDS at the start of the block
+    // (a varying index into the kernel arguments is a vector load from the
+    // argument segment in device memory; issued there, its latency hides
+    // behind the row staging).
+    const int thr_l = ln < C ? thr_lds[ln] : (int)0x80000000;
+    const int maxthr = (int)(wave_all_max((uint32_t)thr_l ^ 0x80000000u) ^
+                             0x80000000u);
     const int w = min(maxthr, S);
     int prev_raw = -1;
     for (int c = 0; c < C; ++c) {
-      const int thr = p.thresholds[c];
+      const int thr = __builtin_amdgcn_readlane(thr_l, c);
       int v = 0;
       if (thr <= w) {
         const int t = thr < 1 ? 1 : thr;
@@ -283,7 +366,7 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
   // semantics): one ordered pass per group of 8 candidates.
   if (!kStream) {
     for (int g0 = 0; g0 < C; g0 += 8)
-      compact_first_r<NT>(mbuf, S, cand + g0, min(8, C - g0), R,
+      compact_first_r<NT>(mbuf, qe, cand + g0, min(8, C - g0), R,
                           occ + g0 * R, 0, found + g0, scan);
     __syncthreads();
   } else {
@@ -352,6 +435,7 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
       res_nv[c] = er.nv;
       res_score[c] = er.score;
     }
+    if (c < 6) SFX_TRACE_WAVE(10 + c);
   }
   __syncthreads();
 

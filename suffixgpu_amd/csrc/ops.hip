@@ -196,7 +196,8 @@ __global__ __launch_bounds__(kSearchThreads) void k_sa_search(
   pl = pl < 0 ? 0 : (pl > width ? width : pl);
   auto pat_at = [&](int j) -> int32_t { return pr[j]; };
   int64_t lo, hi;
-  kary_bounds<kOpGroup>(sa, corpus, n, nullptr, 0, pat_at, (int)pl, lo, hi);
+  kary_bounds<kOpGroup>(sa, corpus, n, nullptr, 0, pat_at, (int)pl, lo, hi,
+                        0u, (uint32_t)n);
   if (threadIdx.x % kOpGroup == 0) {
     lower[row] = lo;
     upper[row] = hi;

@@ -105,7 +105,9 @@ __device__ __forceinline__ void kary_narrow(uint32_t& lo, uint32_t& hi,
 // with cmp > 0) of one pattern.  Called by all G lanes of an aligned group
 // with identical arguments; returns the bounds on every lane of the group.
 // keys (kw = key width, 4 <= kw <= 32, kw % 4 == 0) may be NULL: then the
-// comparison reads sa and the corpus.  n < 2^31.
+// comparison reads sa and the corpus.  n < 2^31.  The search runs inside
+// [r0, r1], which must hold both bounds (every rank below r0 compares
+// below the pattern, every rank from r1 on above it); [0, n] always does.
 //
 // The groups of a wave are in different phases (both bounds on one range,
 // one bound left, or the bounds split), so each lane's probe and both
@@ -115,7 +117,7 @@ template <int G, class PatFn>
 __device__ __forceinline__ void kary_bounds(
     const int32_t* __restrict__ sa, const int32_t* __restrict__ corpus,
     int64_t n, const int32_t* __restrict__ keys, int kw, PatFn pat_at,
-    int plen, int64_t& lower, int64_t& upper) {
+    int plen, int64_t& lower, int64_t& upper, uint32_t r0, uint32_t r1) {
   static_assert(G >= 2 && G <= 32 && (64 % G) == 0, "group size");
   constexpr int H = G / 2;
   constexpr uint32_t cG = (uint32_t)((1ull << 32) / (G + 1));
@@ -128,7 +130,7 @@ __device__ __forceinline__ void kary_bounds(
 #pragma unroll
     for (int j = 0; j < 32; ++j) pt[j] = j < plen ? pat_at(j) : 0;
   }
-  uint32_t lo1 = 0, hi1 = (uint32_t)n, lo2 = 0, hi2 = (uint32_t)n;
+  uint32_t lo1 = r0, hi1 = r1, lo2 = r0, hi2 = r1;
   while (lo1 < hi1 || lo2 < hi2) {
     const bool shared = lo1 == lo2 && hi1 == hi2;
     const bool only1 = !shared && lo2 == hi2;

@@ -17,9 +17,18 @@ extern __device__ uint64_t* sfx_trace_buf;
     if (threadIdx.x == 0 && sfx_trace_buf)                             \
       sfx_trace_buf[(uint64_t)blockIdx.x * 16 + (slot)] = wall_clock64(); \
   } while (0)
+// Lane 0 of the calling wave stores instead (per-wave phase ends).
+#define SFX_TRACE_WAVE(slot)                                           \
+  do {                                                                 \
+    if (__lane_id() == 0 && sfx_trace_buf)                             \
+      sfx_trace_buf[(uint64_t)blockIdx.x * 16 + (slot)] = wall_clock64(); \
+  } while (0)
 #else
 #define SFX_TRACE_POINT(slot) \
   do {                        \
+  } while (0)
+#define SFX_TRACE_WAVE(slot) \
+  do {                       \
   } while (0)
 #endif
 

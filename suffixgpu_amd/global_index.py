@@ -37,6 +37,15 @@ PAD_TOKEN = torch.iinfo(torch.int32).max
 # Tokens of every suffix kept next to the suffix array (one 128-byte row
 # per rank) so an interval-search probe is a single row load.
 KEY_WIDTH = 32
+# Slots of the n-gram range table per corpus position (a power of two in
+# all): a corpus of real text holds about 1.6 distinct runs of 1-4 tokens
+# per position, so the table stays about 40% full.
+GRAM_SLOTS_PER_TOKEN = 4
+
+
+def gram_slots_for(capacity: int) -> int:
+    n = max(1024, GRAM_SLOTS_PER_TOKEN * capacity)
+    return 1 << (n - 1).bit_length()
 # Written between documents; negative, so no query token (>= 0) can match
 # it and neither matches nor continuations cross document boundaries.
 SEP_TOKEN = -2
@@ -50,7 +59,8 @@ class GlobalIndex:
                  max_occurrences: int = 32,
                  rebuild_threshold: int | None = None,
                  device: torch.device | str = "cuda",
-                 rebuild_stream: torch.cuda.Stream | None = None):
+                 rebuild_stream: torch.cuda.Stream | None = None,
+                 gram_slots: int | None = None):
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise _lib.SuffixGPUError(
@@ -79,13 +89,21 @@ class GlobalIndex:
         self.delta = torch.zeros(delta_capacity, dtype=torch.int32,
                                  device=dev)
         self.delta_len_t = torch.zeros((), dtype=torch.int64, device=dev)
-        # Two key-row buffers; the device word key_select names the live
-        # one (the step reads it), a rebuild writes the other.
+        # Two key-row buffers and n-gram range tables; the device word
+        # key_select names the live pair (the step reads it), a rebuild
+        # writes the other.
         self._keys = [torch.empty(capacity * KEY_WIDTH, dtype=torch.int32,
                                   device=dev) for _ in range(2)]
+        # gram_slots (a power of two) overrides the table size; a table
+        # too small for the corpus marks itself unusable and searches span
+        # the whole suffix array instead.
+        self.gram_slots = gram_slots or gram_slots_for(capacity)
+        gbytes = int(lib().sfx_gram_table_bytes(self.gram_slots))
+        self._grams = [torch.zeros(gbytes, dtype=torch.uint8, device=dev)
+                       for _ in range(2)]
         self._key_live = 0
         self.key_select = torch.zeros(1, dtype=torch.int32, device=dev)
-        self._build_keys(self.corpus, self.sa, self.sa_key)
+        self._build_keys(self.corpus, self.sa, self._key_live)
         self._sa_ws: torch.Tensor | None = None
         self._query_ws: dict = {}
 
@@ -123,7 +141,9 @@ class GlobalIndex:
                              self.delta_len_t.data_ptr(),
                              self._keys[0].data_ptr(), KEY_WIDTH,
                              self._keys[1].data_ptr(),
-                             self.key_select.data_ptr())
+                             self.key_select.data_ptr(),
+                             self._grams[0].data_ptr(),
+                             self._grams[1].data_ptr(), self.gram_slots)
 
     def device_bytes(self) -> dict:
         """Device memory held by the index, by role (bytes)."""
@@ -132,15 +152,23 @@ class GlobalIndex:
         return {
             "corpus_sa": 4 * 4 * self.capacity,  # live + staging, int32
             "key_rows": 2 * 4 * KEY_WIDTH * self.capacity,
+            "gram_tables": sum(t.numel() for t in self._grams),
             "delta": 4 * self.delta_capacity + 8,
             "sa_build_workspace": ws,
             "query_workspace": qws,
         }
 
-    def _build_keys(self, corpus, sa, keys) -> None:
+    def _build_keys(self, corpus, sa, slot: int) -> None:
+        """Key rows and n-gram range table of (corpus, sa) into buffer
+        pair `slot` (0 or 1), on the current stream."""
+        keys, gram = self._keys[slot], self._grams[slot]
+        st = stream_of(self.device)
         check(lib().sfx_sa_keys(corpus.data_ptr(), sa.data_ptr(),
                                 self.capacity, KEY_WIDTH, keys.data_ptr(),
-                                stream_of(self.device)), "SA key rows")
+                                st), "SA key rows")
+        check(lib().sfx_gram_build(keys.data_ptr(), KEY_WIDTH, self.capacity,
+                                   gram.data_ptr(), self.gram_slots, st),
+              "n-gram table")
 
     # ------------------------------------------------------------------
     # writes (global_index.py:86-133)
@@ -311,7 +339,7 @@ class GlobalIndex:
                                  self.staging_sa.data_ptr(), 0,
                                  ws.data_ptr(), ws.numel(),
                                  stream_of(self.device)), "SA rebuild")
-        self._build_keys(dst, self.staging_sa, self.staging_sa_key)
+        self._build_keys(dst, self.staging_sa, 1 - self._key_live)
 
     # Background builds, enqueued on the current (rebuild) stream.
     def _staged_build_begin(self, dst: torch.Tensor, m: int) -> None:
@@ -347,7 +375,7 @@ class GlobalIndex:
                                         ws.data_ptr(), ws.numel(),
                                         stream_of(self.device)),
               "SA rebuild")
-        self._build_keys(dst, self.staging_sa, self.staging_sa_key)
+        self._build_keys(dst, self.staging_sa, 1 - self._key_live)
 
     def _staged_build_check(self) -> bool:
         """After the build's event: True when the staged output is final;
@@ -506,7 +534,7 @@ class GlobalIndex:
         self.active_len = n_act
         self.active_doc_lens = deque(int(x) for x in meta["active_doc_lens"])
         self.delta_doc_lens = [int(x) for x in meta["delta_doc_lens"]]
-        self._build_keys(self.corpus, self.sa, self.sa_key)
+        self._build_keys(self.corpus, self.sa, self._key_live)
 
     @classmethod
     def from_file(cls, path, device="cuda",

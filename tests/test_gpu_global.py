@@ -590,3 +590,112 @@ def test_patterns_longer_than_key_rows(gpu, keys):
                     o.draft(q, ql, p, 16, min_token_prob=0.05,
                             max_spec_factor=1.0, caps=caps)):
         np.testing.assert_array_equal(N(a), e)
+
+
+PAD = np.iinfo(np.int32).max
+
+
+def gram_runs(corpus, sa):
+    """{(k, t0, t1, t2, t3): (lo, hi)}: every maximal run of ranks whose
+    suffixes start with the same k real tokens (k = 1..4; tokens past k
+    are 0), from the suffix array by its definition."""
+    n = corpus.shape[0]
+    pos = sa.astype(np.int64)
+    idx = pos[:, None] + np.arange(4)[None, :]
+    tok = np.where(idx < n, corpus[np.minimum(idx, n - 1)], -1).astype(
+        np.int64)
+    real = (tok >= 0) & (tok != PAD)
+    out = {}
+    for k in range(1, 5):
+        key = np.where(np.arange(4)[None, :] < k, tok, 0)
+        ok = real[:, :k].all(axis=1)
+        new = np.ones(n, bool)
+        new[1:] = (key[1:] != key[:-1]).any(axis=1) | (ok[1:] != ok[:-1])
+        starts = np.flatnonzero(new)
+        ends = np.append(starts[1:], n)
+        for a, z in zip(starts, ends):
+            if ok[a]:
+                out[(k, *key[a].tolist())] = (int(a), int(z))
+    return out
+
+
+def gpu_gram_table(g):
+    """The live table's entries of its current build."""
+    raw = N(g._grams[g._key_live])
+    head = raw[:256].view(np.uint32)
+    slots = raw[256:].view(np.int32).reshape(-1, 8)
+    live = slots[slots[:, 4].view(np.uint32) == head[0]]
+    tab = {}
+    for row in live:
+        key = (int(row[7]), int(row[0]), int(row[1]), int(row[2]),
+               int(row[3]))
+        assert key not in tab, key
+        tab[key] = (int(row[5]), int(row[6]))
+    return int(head[1]), tab
+
+
+def test_gram_table_matches_runs(gpu):
+    """The n-gram range table after a rebuild holds exactly the runs of
+    1..4 real tokens of the sorted suffixes with their rank ranges, also
+    after a second rebuild reuses it (epochs, no clearing)."""
+    from suffixgpu_amd.global_index import GlobalIndex
+    tc = synth.TemplateCorpus(seed=13, n_templates=5)
+    g = GlobalIndex(capacity=1 << 14, delta_capacity=1 << 12, k=8,
+                    max_occurrences=16, rebuild_threshold=1 << 30,
+                    device=gpu)
+    for rep in range(2):
+        docs = [tc.sequence(lo=100 + 50 * rep, hi=700)
+                for _ in range(12 + 5 * rep)]
+        g.load_documents([T(d, gpu) for d in docs])
+        torch.cuda.synchronize()
+        ok, tab = gpu_gram_table(g)
+        assert ok == 1
+        exp = gram_runs(N(g.corpus), N(g.sa))
+        assert len(exp) > 1000
+        assert tab == exp
+
+
+@pytest.mark.parametrize("slots", [None, 1024])
+def test_queries_with_and_without_gram_table(gpu, slots):
+    """Capped SA + delta queries, drafts and the fused step agree with the
+    oracle with the table in use and with a table too small for the corpus
+    (it marks itself unusable; every search spans the whole array);
+    queries holding separator, padding or -1 tokens skip the table."""
+    from suffixgpu_amd.global_index import GlobalIndex
+    from oracle.global_index import GlobalIndexOracle
+    tc = synth.TemplateCorpus(seed=14, n_templates=6)
+    docs = [tc.sequence(lo=200, hi=900) for _ in range(30)]
+    kw = dict(capacity=1 << 15, delta_capacity=1 << 12, k=12,
+              max_occurrences=32, rebuild_threshold=1 << 30)
+    g = GlobalIndex(device=gpu, gram_slots=slots, **kw)
+    o = GlobalIndexOracle(**kw)
+    g.load_documents([T(d, gpu) for d in docs])
+    o.load_documents(docs)
+    dd = [tc.sequence(lo=64, hi=300) for _ in range(4)]
+    g.append_documents([T(d, gpu) for d in dd])
+    o.append_documents(dd)
+    torch.cuda.synchronize()
+    ok, _ = gpu_gram_table(g)
+    assert ok == (1 if slots is None else 0)
+    rng = np.random.default_rng(15)
+    b, p = 48, 40
+    q = np.zeros((b, p), I32)
+    ql = np.zeros(b, np.int64)
+    for i in range(b):
+        src = docs[i % len(docs)]
+        n = int(rng.integers(1, p + 1))
+        st = int(rng.integers(0, len(src) - n + 1))
+        q[i, :n] = src[st:st + n]
+        ql[i] = n
+        if i % 8 == 7:  # tokens a query never holds by contract
+            q[i, int(rng.integers(0, n))] = (-2, PAD, -1)[i % 3]
+    caps = np.array([40, 20, 10, 5, 3, 2, 1], np.int64)
+    tq, tl, tc_ = T(q, gpu), T(ql, gpu), T(caps, gpu)
+    for got, exp in zip(g._query_backoff(tq, tl, p, tc_),
+                        o._query_backoff(q, ql, p, caps)):
+        np.testing.assert_array_equal(N(got), exp)
+    for got, exp in zip(g.draft(tq, tl, p, 12, min_token_prob=0.05,
+                                caps=tc_),
+                        o.draft(q, ql, p, 12, min_token_prob=0.05,
+                                caps=caps)):
+        np.testing.assert_array_equal(N(got), exp)
