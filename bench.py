@@ -203,8 +203,49 @@ def time_sa_builds(w, dev, side):
         build_ms[name + "_hinted"] = (min(times), rounds)
         log(f"SA rebuild {name} ({rounds} rounds, as the index runs it): "
             f"{min(times):.2f} ms")
+        if name == "corpus":
+            build_ms["tables"] = index_tables_ms(text, out, dev, side)
+            log(f"key rows + n-gram table of the corpus: "
+                f"{build_ms['tables']}")
     del ws
     return build_ms
+
+
+def index_tables_ms(text, sa, dev, side) -> dict:
+    """What a rebuild adds after the suffix array, on the rebuild stream:
+    the key rows and the n-gram range table (best of 3, HIP events)."""
+    import torch
+    from suffixgpu_amd import _lib
+    from suffixgpu_amd.global_index import KEY_WIDTH, gram_slots_for
+    L = _lib.lib()
+    n = text.shape[0]
+    keys = torch.empty(n * KEY_WIDTH, dtype=torch.int32, device=dev)
+    slots = gram_slots_for(n)
+    gram = torch.zeros(int(L.sfx_gram_table_bytes(slots)), dtype=torch.uint8,
+                       device=dev)
+    res = {"keys": [], "gram": []}
+    for _ in range(3):
+        torch.cuda.synchronize()
+        side.wait_stream(torch.cuda.current_stream(dev))
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        with torch.cuda.stream(side):
+            ev[0].record(side)
+            _lib.check(L.sfx_sa_keys(text.data_ptr(), sa.data_ptr(), n,
+                                     KEY_WIDTH, keys.data_ptr(),
+                                     side.cuda_stream), "keys")
+            ev[1].record(side)
+            _lib.check(L.sfx_gram_build(keys.data_ptr(), KEY_WIDTH, n,
+                                        gram.data_ptr(), slots,
+                                        side.cuda_stream), "gram")
+            ev[2].record(side)
+        ev[2].synchronize()
+        res["keys"].append(ev[0].elapsed_time(ev[1]))
+        res["gram"].append(ev[1].elapsed_time(ev[2]))
+    ok = int(gram[4:8].view(torch.int32).item())
+    del keys, gram
+    return {"key_rows_ms": round(min(res["keys"]), 3),
+            "gram_table_ms": round(min(res["gram"]), 3),
+            "gram_slots": slots, "gram_table_usable": bool(ok)}
 
 
 # ------------------------------------------------------------------ main
@@ -368,6 +409,7 @@ def main() -> int:
         "sa_rebuild_hinted_rounds": sa_reb_rounds,
         "sa_rebuild_hinted_mtok_s": round(sa_m / (sa_reb_ms * 1e-3) / 1e6, 2),
         "sa_rebuild_hbm": sa_rebuild_hbm(sa_reb_ms),
+        "rebuild_tables": build_ms["tables"],
         "kernels_us": {"k_step": round(step_us, 3),
                        "k_local_alone": round(k_local_us, 3),
                        "k_global_alone": round(k_global_us, 3)},

@@ -279,6 +279,13 @@ using namespace sfx;
 
 #ifdef SFX_TRACE
 __device__ uint64_t* sfx_trace_buf = nullptr;
+__device__ uint64_t* sfx_trace_stats = nullptr;
+
+// Profiling builds only: per-wave expansion counters (8 u64 per wave).
+extern "C" int sfx_trace_stats_set(uint64_t* buf) {
+  return (int)hipMemcpyToSymbol(HIP_SYMBOL(sfx_trace_stats), &buf,
+                                sizeof(buf));
+}
 
 // Profiling builds only: point the phase-timestamp buffer (device memory,
 // 16 u64 per block) at `buf`, or disable with NULL.

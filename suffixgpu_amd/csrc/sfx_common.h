@@ -23,12 +23,23 @@ extern __device__ uint64_t* sfx_trace_buf;
     if (__lane_id() == 0 && sfx_trace_buf)                             \
       sfx_trace_buf[(uint64_t)blockIdx.x * 16 + (slot)] = wall_clock64(); \
   } while (0)
+// Per-wave counters of the last expansion (8 u64 per wave of 8).
+extern __device__ uint64_t* sfx_trace_stats;
+#define SFX_TRACE_STAT(idx, val)                                       \
+  do {                                                                 \
+    if (__lane_id() == 0 && sfx_trace_stats)                           \
+      sfx_trace_stats[((uint64_t)blockIdx.x * 8 + threadIdx.x / 64) * 8 + \
+                      (idx)] = (uint64_t)(val);                        \
+  } while (0)
 #else
 #define SFX_TRACE_POINT(slot) \
   do {                        \
   } while (0)
 #define SFX_TRACE_WAVE(slot) \
   do {                       \
+  } while (0)
+#define SFX_TRACE_STAT(idx, val) \
+  do {                           \
   } while (0)
 #endif
 
@@ -297,6 +308,10 @@ __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
   float score = 0.0f;
   int nv = 0;
   int d = 0;
+#ifdef SFX_TRACE
+  const uint64_t t_start = wall_clock64();
+  int st_quick = 0, st_hash = 0, st_full = 0, st_fast = 0;
+#endif
   if (!kWeighted && R <= 2 * kWave) {
     const int r0 = ln;
     const int r1 = ln + kWave;
@@ -350,6 +365,10 @@ __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
         }
         for (int dd = ln; dd < d; dd += kWave) chain_out[dd] = cont_at(rs, dd);
         nv = d;
+#ifdef SFX_TRACE
+        st_fast = d;
+        SFX_TRACE_STAT(5, wall_clock64() - t_start);
+#endif
         if (!ended && d > 0) {
           // the full vote continues with the rows still on the chain
           ok0 = (P0 >> ln) & 1;
@@ -378,7 +397,13 @@ __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
       int bcnt = 0;
       int btok = 0x7fffffff;
       int left = nact;
+#ifdef SFX_TRACE
+      ++st_full;
+#endif
       for (int it = 0; it < kQuickVotes && left > 0 && left >= bcnt; ++it) {
+#ifdef SFX_TRACE
+        ++st_quick;
+#endif
         int x;
         if (rem0)
           x = __builtin_amdgcn_readlane(v0, __builtin_ctzll(rem0));
@@ -401,6 +426,9 @@ __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
         // the chain ends here whichever token wins.
         const int vmin = min_votes(prob, denom, min_prob, nact);
         if (vmin > nact || (left < vmin && bcnt < vmin)) break;
+#ifdef SFX_TRACE
+        ++st_hash;
+#endif
         hash_vote(v0, v1, rem0, rem1, H, bcnt, btok);
       }
       const float vf = (float)bcnt;
@@ -494,6 +522,15 @@ __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
     }
   }
   for (int dd = d + ln; dd < K; dd += kWave) chain_out[dd] = -1;
+#ifdef SFX_TRACE
+  SFX_TRACE_STAT(0, occ);
+  SFX_TRACE_STAT(1, st_fast);
+  SFX_TRACE_STAT(2, st_full);
+  SFX_TRACE_STAT(3, st_quick);
+  SFX_TRACE_STAT(4, st_hash);
+  SFX_TRACE_STAT(6, wall_clock64() - t_start);
+  SFX_TRACE_STAT(7, nv);
+#endif
   ExpandResult res;
   res.nv = nv;
   res.score = score;
