@@ -230,7 +230,7 @@ def index_tables_ms(text, sa, dev, side) -> dict:
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         with torch.cuda.stream(side):
             ev[0].record(side)
-            _lib.check(L.sfx_sa_keys(text.data_ptr(), sa.data_ptr(), n,
+            _lib.check(L.sfx_sa_keys(text.data_ptr(), sa.data_ptr(), n, n,
                                      KEY_WIDTH, keys.data_ptr(),
                                      side.cuda_stream), "keys")
             ev[1].record(side)
@@ -241,7 +241,7 @@ def index_tables_ms(text, sa, dev, side) -> dict:
         ev[2].synchronize()
         res["keys"].append(ev[0].elapsed_time(ev[1]))
         res["gram"].append(ev[1].elapsed_time(ev[2]))
-    ok = int(gram[4:8].view(torch.int32).item())
+    ok = int(gram[0:4].view(torch.int32).item())  # header word 0: ok
     del keys, gram
     return {"key_rows_ms": round(min(res["keys"]), 3),
             "gram_table_ms": round(min(res["gram"]), 3),

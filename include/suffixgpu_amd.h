@@ -32,7 +32,7 @@ extern "C" {
 
 #define SFX_EINVAL (-1)
 #define SFX_MAX_CANDIDATES 32
-#define SFX_ABI_VERSION 8
+#define SFX_ABI_VERSION 9
 
 /* Drafter configuration shared by the local and global paths.
  * Mirrors the constructor arguments of SuffixGPUDrafter
@@ -81,7 +81,7 @@ typedef struct sfx_index {
     const void* gram;          /* n-gram range table of sa_key's suffix
                                   array (sfx_gram_build), or NULL         */
     const void* gram_alt;      /* the table of sa_key_alt's, or NULL      */
-    int64_t gram_slots;        /* slots per table, a power of two         */
+    int64_t gram_slots;        /* slots per table, a power of two >= 16   */
 } sfx_index;
 
 /* One decode step's batch (suffix_gpu/proposer.py:135-214).
@@ -238,9 +238,12 @@ int sfx_propose_step_noalloc(const sfx_params* p, const sfx_index* index,
 size_t sfx_sa_build_workspace_size(int64_t m);
 
 /* keys[r * width + j] = j-th token of the suffix at sa[r] (corpus reads at
- * or past n give -1), for r < n and j < width (4..32, multiple of 4). */
+ * or past n give -1), for r < rows <= n and j < width (4..32, multiple of
+ * 4).  A rebuild whose ranks from some r on are the padding suffixes of
+ * the previous build in the same buffer rewrites only the rows below. */
 int sfx_sa_keys(const int32_t* corpus, const int32_t* sa, int64_t n,
-                int64_t width, int32_t* keys, hipStream_t stream);
+                int64_t rows, int64_t width, int32_t* keys,
+                hipStream_t stream);
 int sfx_sa_build(const int32_t* text, int64_t m, int64_t n_total, void* sa,
                  int32_t sa_is64, void* workspace, size_t workspace_bytes,
                  hipStream_t stream);
@@ -250,10 +253,12 @@ int sfx_sa_build(const int32_t* text, int64_t m, int64_t n_total, void* sa,
  * only) among the sorted suffixes, the rank range of the suffixes that
  * start with it, so that an interval search starts inside the range of its
  * pattern's first tokens.  `table` (256-byte aligned, sfx_gram_table_bytes
- * bytes, zero-filled once when allocated) is rebuilt in place from the key
- * rows (key_width 4..32, 16-byte aligned) of ranks 0..m-1; enqueued on
- * `stream` with no host read.  A table whose slots run out marks itself
- * unusable and searches then ignore it. */
+ * bytes for `slots` slots, a power of two >= 16, in buckets of 16) is
+ * rebuilt in place from the key rows (key_width 4..32, 16-byte aligned) of
+ * ranks 0..m-1, enqueued on `stream` with no host read; it needs no
+ * initial contents (a zero-filled table reads as unusable).  A build whose
+ * runs overflow the buckets marks the table unusable and searches then
+ * ignore it. */
 size_t sfx_gram_table_bytes(int64_t slots);
 int sfx_gram_build(const int32_t* keys, int64_t key_width, int64_t m,
                    void* table, int64_t slots, hipStream_t stream);

@@ -488,12 +488,8 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
     // pattern's first min(l, kGramMax) tokens (the whole answer for
     // l <= kGramMax); without a usable table every search spans [0, N).
     const void* gram = live_gram(a.ix);
-    uint32_t gram_epoch = 0;
-    if (gram) {
-      const GramHeader* gh = reinterpret_cast<const GramHeader*>(gram);
-      if (gh->ok && a.ix.gram_slots > 0) gram_epoch = gh->epoch;
-    }
-    const uint32_t gram_mask = (uint32_t)(a.ix.gram_slots - 1);
+    if (gram && !reinterpret_cast<const GramHeader*>(gram)->ok)
+      gram = nullptr;
     for (int l = g + 1; l <= P; l += ngroups) {
       int64_t lo = 0, hi = 0;
       if (l <= plen) {
@@ -510,9 +506,9 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
             real = real && gram_real(t[j]);
           }
         }
-        if (gram_epoch && real)
-          found = gram_lookup<G>(gram, gram_mask, gram_epoch, t[0], t[1],
-                                 t[2], t[3], k, r0, r1);
+        if (gram && real)
+          found = gram_lookup<G>(gram, a.ix.gram_slots, t[0], t[1], t[2],
+                                 t[3], k, r0, r1);
         if (found == 0) {
           lo = hi = 0;  // no suffix starts with the first k tokens
         } else if (found == 1 && l == k) {

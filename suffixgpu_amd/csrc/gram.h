@@ -7,13 +7,18 @@
 // 2^22-token template corpus this cuts the slowest of a row's 32 searches
 // from 6 dependent rounds to at most 3 (one lookup plus two rounds).
 //
-// Layout: a 256-byte header {epoch, ok} and `slots` (a power of two)
-// 32-byte slots {t[4], epoch, lo, hi, k}, open addressing with linear
-// probing.  A slot belongs to the table built with header epoch e iff its
-// own epoch equals e, so a rebuild never clears the table: it bumps the
-// epoch and claims slots with a compare-and-swap on their epoch word.  A
-// build that runs out of probes sets ok = 0, and searches then ignore the
-// table (exact, only slower).
+// Layout: a 256-byte header {ok}, then one u32 fill count per bucket
+// (padded to 256 bytes), then the buckets: kGramBucket consecutive 32-byte
+// slots {t[4], lo, hi, k, pad} each (512 bytes, aligned).  A run hashes to
+// bucket b; an insert takes position atomicAdd(&count[b], 1) and, when b
+// is full, moves on to b + 1, b + 2, ... (at most kGramSpill buckets).
+// The counts keep counting past kGramBucket, so count[b] > kGramBucket
+// tells a lookup that runs hashed to b (or before) may sit further on.
+// The counts live in a 4 MiB array for 2^24 slots, so the inserts' atomics
+// stay in cache while the slot stores stream out; a lookup is one round of
+// loads (the bucket's slots and its count together) unless its bucket
+// overflowed.  An insert that finds no room sets ok = 0 and searches then
+// ignore the table (exact, only slower).
 //
 // Only runs of real tokens are stored (0 <= t < INT32_MAX): query patterns
 // hold real tokens, and the separator, the corpus padding and the -1 read
@@ -26,35 +31,56 @@
 namespace sfx {
 
 constexpr int kGramMax = 4;
-constexpr int kGramProbes = 64;  // longest probe sequence of an insert
+constexpr int kGramBucket = 16;  // slots per bucket
+constexpr int kGramSpill = 8;    // buckets an insert or lookup may visit
 
 struct GramSlot {
-  int32_t t[4];    // the run's tokens, zero past k
-  uint32_t epoch;  // the build that wrote the slot
-  uint32_t lo;     // first rank
-  uint32_t hi;     // one past the last rank
-  uint32_t k;      // run length in tokens
+  int32_t t[4];  // the run's tokens, zero past k
+  uint32_t lo;   // first rank
+  uint32_t hi;   // one past the last rank
+  uint32_t k;    // run length in tokens
+  uint32_t pad;
 };
 static_assert(sizeof(GramSlot) == 32, "one slot is two 16-byte words");
 
 struct GramHeader {
-  uint32_t epoch;  // the current build (0: never built)
-  uint32_t ok;     // every run of the current build was stored
-  uint32_t pad[62];
+  uint32_t ok;  // every run of the last build was stored
+  uint32_t pad[63];
 };
-static_assert(sizeof(GramHeader) == 256, "slots start 256-byte aligned");
+static_assert(sizeof(GramHeader) == 256, "counts start 256-byte aligned");
+
+// Buckets of a table of `slots` slots (a power of two >= kGramBucket).
+__host__ __device__ inline int64_t gram_buckets(int64_t slots) {
+  return slots / kGramBucket;
+}
+
+__host__ __device__ inline size_t gram_counts_bytes(int64_t slots) {
+  return ((size_t)gram_buckets(slots) * 4 + 255) & ~(size_t)255;
+}
 
 __host__ __device__ inline size_t gram_table_bytes(int64_t slots) {
-  return sizeof(GramHeader) + (size_t)slots * sizeof(GramSlot);
+  return sizeof(GramHeader) + gram_counts_bytes(slots) +
+         (size_t)slots * sizeof(GramSlot);
 }
 
-__device__ __forceinline__ GramSlot* gram_slots(void* table) {
-  return reinterpret_cast<GramSlot*>((char*)table + sizeof(GramHeader));
+__device__ __forceinline__ uint32_t* gram_counts(void* table) {
+  return reinterpret_cast<uint32_t*>((char*)table + sizeof(GramHeader));
 }
 
-__device__ __forceinline__ const GramSlot* gram_slots(const void* table) {
-  return reinterpret_cast<const GramSlot*>((const char*)table +
+__device__ __forceinline__ const uint32_t* gram_counts(const void* table) {
+  return reinterpret_cast<const uint32_t*>((const char*)table +
                                            sizeof(GramHeader));
+}
+
+__device__ __forceinline__ GramSlot* gram_slots(void* table, int64_t slots) {
+  return reinterpret_cast<GramSlot*>((char*)table + sizeof(GramHeader) +
+                                     gram_counts_bytes(slots));
+}
+
+__device__ __forceinline__ const GramSlot* gram_slots(const void* table,
+                                                      int64_t slots) {
+  return reinterpret_cast<const GramSlot*>(
+      (const char*)table + sizeof(GramHeader) + gram_counts_bytes(slots));
 }
 
 __device__ __forceinline__ bool gram_real(int32_t t) {
@@ -80,38 +106,55 @@ __device__ __forceinline__ uint32_t gram_hash(int32_t t0, int32_t t1,
   return h;
 }
 
-// One group of G lanes looks the run (t0..t3, k) up in G consecutive
-// slots per step.  Returns 1 (found, [lo, hi) set), 0 (absent) or -1 (no
-// answer within the probe limit: search the whole array).  Every lane of
-// the group gets the same result.
+// One group of G lanes looks the run (t0..t3, k) up, kGramBucket / G
+// slots of a bucket per lane.  Returns 1 (found, [lo, hi) set), 0 (absent)
+// or -1 (no answer within kGramSpill buckets: search the whole array).
+// Every lane of the group gets the same result.
 template <int G>
-__device__ __forceinline__ int gram_lookup(const void* table,
-                                           uint32_t mask, uint32_t epoch,
+__device__ __forceinline__ int gram_lookup(const void* table, int64_t slots,
                                            int32_t t0, int32_t t1,
                                            int32_t t2, int32_t t3, int k,
                                            uint32_t& lo, uint32_t& hi) {
-  const GramSlot* slots = gram_slots(table);
+  static_assert(kGramBucket % G == 0, "lanes split a bucket evenly");
+  constexpr int PL = kGramBucket / G;  // slots per lane
+  const uint32_t* counts = gram_counts(table);
+  const GramSlot* sl = gram_slots(table, slots);
+  const uint32_t bmask = (uint32_t)(gram_buckets(slots) - 1);
   const int ln = lane_id();
   const int gl = ln % G;
   const int gbase = ln - gl;
   const uint32_t full = G == 32 ? 0xffffffffu : ((1u << G) - 1u);
   const uint32_t h = gram_hash(t0, t1, t2, t3, k);
-  for (int base = 0; base < kGramProbes + G; base += G) {
-    const uint32_t s = (h + (uint32_t)(base + gl)) & mask;
-    const int4 a = *reinterpret_cast<const int4*>(&slots[s].t[0]);
-    const uint4 b = *reinterpret_cast<const uint4*>(&slots[s].epoch);
-    const bool live = b.x == epoch;
-    const bool hit = live && (int)b.w == k && a.x == t0 && a.y == t1 &&
-                     a.z == t2 && a.w == t3;
+  for (int s = 0; s < kGramSpill; ++s) {
+    const uint32_t bk = (h + (uint32_t)s) & bmask;
+    const uint32_t cnt = counts[bk];
+    int4 a[PL];
+    uint4 w[PL];
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const GramSlot* q = sl + (size_t)bk * kGramBucket + gl * PL + i;
+      a[i] = *reinterpret_cast<const int4*>(&q->t[0]);
+      w[i] = *reinterpret_cast<const uint4*>(&q->lo);
+    }
+    bool hit = false;
+    uint32_t hl = 0, hh = 0;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const uint32_t pos = (uint32_t)(gl * PL + i);
+      const bool h1 = pos < cnt && (int)w[i].z == k && a[i].x == t0 &&
+                      a[i].y == t1 && a[i].z == t2 && a[i].w == t3;
+      hl = h1 ? w[i].x : hl;
+      hh = h1 ? w[i].y : hh;
+      hit = hit || h1;
+    }
     const uint32_t mh = (uint32_t)(ballot(hit) >> gbase) & full;
-    const uint32_t me = (uint32_t)(ballot(!live) >> gbase) & full;
-    if (mh && (!me || __builtin_ctz(mh) < __builtin_ctz(me))) {
+    if (mh) {
       const int src = gbase + __builtin_ctz(mh);
-      lo = (uint32_t)__shfl((int)b.y, src);
-      hi = (uint32_t)__shfl((int)b.z, src);
+      lo = (uint32_t)__shfl((int)hl, src);
+      hi = (uint32_t)__shfl((int)hh, src);
       return 1;
     }
-    if (me) return 0;
+    if (cnt <= (uint32_t)kGramBucket) return 0;
   }
   return -1;
 }

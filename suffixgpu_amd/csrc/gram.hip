@@ -1,23 +1,28 @@
 // Building the n-gram range table (gram.h) of a suffix array from its key
-// rows, on the caller's stream with no host synchronisation: a new epoch,
-// then one pass in which every rank that starts a run inserts it with
-// hi = lo + 1, then one pass in which every rank that ends a run stores
-// hi.  Rank r starts the run of its first k tokens for every k above the
-// common prefix (capped at kGramMax) of suffixes r - 1 and r, and ends it
-// for every k above that of r and r + 1; both come from the first 16 bytes
-// of adjacent key rows.
+// rows, on the caller's stream with no host synchronisation: the bucket
+// counts are cleared, then one pass inserts every run at the rank that
+// starts it, and one pass stores hi for the runs longer than one rank.
+// Rank r starts the run of its first k tokens for every k above the common
+// prefix (capped at kGramMax) of suffixes r - 1 and r, and ends it for
+// every k above that of r and r + 1; all three come from the first 16
+// bytes of adjacent key rows.  A run that starts and ends at r (most runs
+// of three and four tokens) is stored whole by the insert pass, so the
+// second pass looks up only the runs that span several ranks.
 
 #include "gram.h"
 #include "launch.h"
 
 namespace sfx {
 
-__global__ void k_gram_epoch(GramHeader* h) {
-  if (threadIdx.x == 0) {
-    const uint32_t e = h->epoch + 1;
-    h->epoch = e == 0 ? 1 : e;  // 0 marks a table never built
-    h->ok = 1;
-  }
+__global__ __launch_bounds__(256) void k_gram_clear(void* table,
+                                                    int64_t buckets) {
+  uint32_t* counts = gram_counts(table);
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+       i < buckets; i += stride)
+    counts[i] = 0;
+  if (blockIdx.x == 0 && threadIdx.x == 0)
+    reinterpret_cast<GramHeader*>(table)->ok = 1;
 }
 
 // Leading tokens two runs share (0 .. kGramMax).
@@ -40,64 +45,90 @@ __device__ __forceinline__ int4 first4(const int4& a, int k) {
   return make_int4(a.x, k > 1 ? a.y : 0, k > 2 ? a.z : 0, k > 3 ? a.w : 0);
 }
 
+// The rank's leading tokens and its common prefixes with both neighbours.
+struct RankRuns {
+  int4 cur;
+  int lcp_prev, lcp_next, nreal;
+};
+
+__device__ __forceinline__ RankRuns rank_runs(const int32_t* __restrict__ keys,
+                                              int kw, int64_t m, int64_t r) {
+  RankRuns q;
+  q.cur = *reinterpret_cast<const int4*>(keys + r * kw);
+  q.lcp_prev =
+      r > 0 ? common4(*reinterpret_cast<const int4*>(keys + (r - 1) * kw),
+                      q.cur)
+            : 0;
+  q.lcp_next =
+      r + 1 < m
+          ? common4(q.cur, *reinterpret_cast<const int4*>(keys + (r + 1) * kw))
+          : 0;
+  q.nreal = real4(q.cur);
+  return q;
+}
+
 __global__ __launch_bounds__(256) void k_gram_insert(
     const int32_t* __restrict__ keys, int kw, int64_t m, void* table,
-    uint32_t mask) {
+    int64_t slots) {
   const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= m) return;
-  GramHeader* hdr = reinterpret_cast<GramHeader*>(table);
-  GramSlot* slots = gram_slots(table);
-  const uint32_t ep = hdr->epoch;
-  const int4 cur = *reinterpret_cast<const int4*>(keys + r * kw);
-  const int lcp =
-      r > 0 ? common4(*reinterpret_cast<const int4*>(keys + (r - 1) * kw),
-                      cur)
-            : 0;
-  const int nreal = real4(cur);
-  for (int k = lcp + 1; k <= nreal; ++k) {
-    const int4 t = first4(cur, k);
+  const RankRuns q = rank_runs(keys, kw, m, r);
+  if (q.nreal <= q.lcp_prev) return;  // every run here started earlier
+  uint32_t* counts = gram_counts(table);
+  GramSlot* sl = gram_slots(table, slots);
+  const uint32_t bmask = (uint32_t)(gram_buckets(slots) - 1);
+  for (int k = q.lcp_prev + 1; k <= q.nreal; ++k) {
+    const int4 t = first4(q.cur, k);
     const uint32_t h = gram_hash(t.x, t.y, t.z, t.w, k);
+    // hi is known now when the run ends here; else the close pass sets it
+    const uint32_t hi = k > q.lcp_next ? (uint32_t)r + 1 : 0u;
     bool placed = false;
-    for (int p = 0; p < kGramProbes && !placed; ++p) {
-      GramSlot& s = slots[(h + (uint32_t)p) & mask];
-      const uint32_t e = s.epoch;
-      if (e == ep) continue;
-      if (atomicCAS(&s.epoch, e, ep) != e) continue;  // taken meanwhile
-      *reinterpret_cast<int4*>(&s.t[0]) = t;
-      s.lo = (uint32_t)r;
-      s.hi = (uint32_t)r + 1;
-      s.k = (uint32_t)k;
-      placed = true;
+    for (int s = 0; s < kGramSpill && !placed; ++s) {
+      const uint32_t bk = (h + (uint32_t)s) & bmask;
+      const uint32_t pos = atomicAdd(&counts[bk], 1u);
+      if (pos < (uint32_t)kGramBucket) {
+        GramSlot* d = sl + (size_t)bk * kGramBucket + pos;
+        *reinterpret_cast<int4*>(&d->t[0]) = t;
+        *reinterpret_cast<uint4*>(&d->lo) =
+            make_uint4((uint32_t)r, hi, (uint32_t)k, 0u);
+        placed = true;
+      }
     }
-    if (!placed) hdr->ok = 0;
+    if (!placed) reinterpret_cast<GramHeader*>(table)->ok = 0;
   }
 }
 
 __global__ __launch_bounds__(256) void k_gram_close(
     const int32_t* __restrict__ keys, int kw, int64_t m, void* table,
-    uint32_t mask) {
+    int64_t slots) {
   const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= m) return;
-  GramHeader* hdr = reinterpret_cast<GramHeader*>(table);
-  GramSlot* slots = gram_slots(table);
-  const uint32_t ep = hdr->epoch;
-  const int4 cur = *reinterpret_cast<const int4*>(keys + r * kw);
-  const int lcp =
-      r + 1 < m
-          ? common4(cur, *reinterpret_cast<const int4*>(keys + (r + 1) * kw))
-          : 0;
-  const int nreal = real4(cur);
-  for (int k = lcp + 1; k <= nreal; ++k) {
-    const int4 t = first4(cur, k);
+  const RankRuns q = rank_runs(keys, kw, m, r);
+  // runs ending at r that started before r: lcp_next < k <= lcp_prev
+  const int kmax = q.lcp_prev < q.nreal ? q.lcp_prev : q.nreal;
+  if (kmax <= q.lcp_next) return;
+  const uint32_t* counts = gram_counts(table);
+  GramSlot* sl = gram_slots(table, slots);
+  const uint32_t bmask = (uint32_t)(gram_buckets(slots) - 1);
+  for (int k = q.lcp_next + 1; k <= kmax; ++k) {
+    const int4 t = first4(q.cur, k);
     const uint32_t h = gram_hash(t.x, t.y, t.z, t.w, k);
-    for (int p = 0; p < kGramProbes; ++p) {
-      GramSlot& s = slots[(h + (uint32_t)p) & mask];
-      if (s.epoch != ep) break;  // not stored: the insert pass failed
-      if ((int)s.k == k && s.t[0] == t.x && s.t[1] == t.y &&
-          s.t[2] == t.z && s.t[3] == t.w) {
-        s.hi = (uint32_t)r + 1;
-        break;
+    bool done = false;
+    for (int s = 0; s < kGramSpill && !done; ++s) {
+      const uint32_t bk = (h + (uint32_t)s) & bmask;
+      const uint32_t cnt = counts[bk];
+      const uint32_t n = cnt < (uint32_t)kGramBucket ? cnt : kGramBucket;
+      GramSlot* b = sl + (size_t)bk * kGramBucket;
+      for (uint32_t i = 0; i < n; ++i) {
+        const int4 a = *reinterpret_cast<const int4*>(&b[i].t[0]);
+        if ((int)b[i].k == k && a.x == t.x && a.y == t.y && a.z == t.z &&
+            a.w == t.w) {
+          b[i].hi = (uint32_t)r + 1;
+          done = true;
+          break;
+        }
       }
+      if (cnt <= (uint32_t)kGramBucket) break;  // absent: the insert failed
     }
   }
 }
@@ -106,28 +137,35 @@ __global__ __launch_bounds__(256) void k_gram_close(
 
 using namespace sfx;
 
+static bool gram_slots_ok(int64_t slots) {
+  return slots >= kGramBucket && !(slots & (slots - 1)) &&
+         slots <= (1ll << 31);
+}
+
 extern "C" size_t sfx_gram_table_bytes(int64_t slots) {
-  if (slots < 1 || (slots & (slots - 1))) return 0;
+  if (!gram_slots_ok(slots)) return 0;
   return gram_table_bytes(slots);
 }
 
 extern "C" int sfx_gram_build(const int32_t* keys, int64_t key_width,
                               int64_t m, void* table, int64_t slots,
                               hipStream_t stream) {
-  if (!table || slots < 1 || (slots & (slots - 1)) || slots > (1ll << 31) ||
-      m < 0 || m > 0x7fffffffLL || key_width < 4 || key_width > 32 ||
-      (key_width & 3) || (m > 0 && !keys) ||
-      ((uintptr_t)table & 255) || ((uintptr_t)keys & 15))
+  if (!table || !gram_slots_ok(slots) || m < 0 || m > 0x7fffffffLL ||
+      key_width < 4 || key_width > 32 || (key_width & 3) ||
+      (m > 0 && !keys) || ((uintptr_t)table & 255) ||
+      ((uintptr_t)keys & 15))
     return SFX_EINVAL;
-  hipLaunchKernelGGL(k_gram_epoch, dim3(1), dim3(64), 0, stream,
-                     reinterpret_cast<GramHeader*>(table));
+  const int64_t nb = gram_buckets(slots);
+  const unsigned cblocks =
+      (unsigned)(nb / 256 < 1024 ? (nb + 255) / 256 : 1024);
+  hipLaunchKernelGGL(k_gram_clear, dim3(cblocks), dim3(256), 0, stream,
+                     table, nb);
   if (m > 0) {
     const unsigned blocks = (unsigned)((m + 255) / 256);
-    const uint32_t mask = (uint32_t)(slots - 1);
     hipLaunchKernelGGL(k_gram_insert, dim3(blocks), dim3(256), 0, stream,
-                       keys, (int)key_width, m, table, mask);
+                       keys, (int)key_width, m, table, slots);
     hipLaunchKernelGGL(k_gram_close, dim3(blocks), dim3(256), 0, stream,
-                       keys, (int)key_width, m, table, mask);
+                       keys, (int)key_width, m, table, slots);
   }
   return (int)hipGetLastError();
 }

@@ -580,12 +580,13 @@ __global__ __launch_bounds__(NT) void k_sa_gather(
 }
 
 // ------------------------------------------------------------ outputs
-// keys[r * W + j] = corpus[sa[r] + j] (-1 at or past n).
+// keys[r * W + j] = corpus[sa[r] + j] (-1 at or past n), ranks r < rows.
 __global__ __launch_bounds__(256) void k_rank_keys(const int32_t* corpus,
                                                  const int32_t* sa, int64_t n,
-                                                 int W, int32_t* keys) {
+                                                 int64_t rows, int W,
+                                                 int32_t* keys) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (e >= n * W) return;
+  if (e >= rows * W) return;
   const int64_t r = e / W;
   const int j = (int)(e - r * W);
   const int64_t p = (int64_t)sa[r] + j;
@@ -597,10 +598,11 @@ __global__ __launch_bounds__(256) void k_rank_keys(const int32_t* corpus,
 // instructions for the 128 B-per-rank write that bounds the kernel.
 __global__ __launch_bounds__(256) void k_rank_keys4(const int32_t* corpus,
                                                   const int32_t* sa, int64_t n,
-                                                  int W, int32_t* keys) {
+                                                  int64_t rows, int W,
+                                                  int32_t* keys) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int W4 = W >> 2;
-  if (e >= n * W4) return;
+  if (e >= rows * W4) return;
   const int64_t r = e / W4;
   const int64_t p = (int64_t)sa[r] + 4 * (e - r * W4);
   int4 v;
@@ -689,19 +691,23 @@ static int sort_and_rank(SaWs& w, int64_t nb, int64_t m, int round,
 using namespace sfx;
 
 extern "C" int sfx_sa_keys(const int32_t* corpus, const int32_t* sa,
-                           int64_t n, int64_t width, int32_t* keys,
-                           hipStream_t stream) {
-  if (n < 0 || width < 4 || width > 32 || (width & 3)) return SFX_EINVAL;
-  if (n == 0) return 0;
+                           int64_t n, int64_t rows, int64_t width,
+                           int32_t* keys, hipStream_t stream) {
+  if (n < 0 || rows < 0 || rows > n || n > 0x7fffffffLL || width < 4 ||
+      width > 32 || (width & 3))
+    return SFX_EINVAL;
+  if (rows == 0) return 0;
   if (!corpus || !sa || !keys) return SFX_EINVAL;
-  const int64_t total = n * width;
+  const int64_t total = rows * width;
   if ((((uintptr_t)keys) & 15) == 0) {
     const int64_t total4 = total / 4;
     hipLaunchKernelGGL(k_rank_keys4, dim3((unsigned)((total4 + 255) / 256)),
-                       dim3(256), 0, stream, corpus, sa, n, (int)width, keys);
+                       dim3(256), 0, stream, corpus, sa, n, rows, (int)width,
+                       keys);
   } else {
     hipLaunchKernelGGL(k_rank_keys, dim3((unsigned)((total + 255) / 256)),
-                       dim3(256), 0, stream, corpus, sa, n, (int)width, keys);
+                       dim3(256), 0, stream, corpus, sa, n, rows, (int)width,
+                       keys);
   }
   return (int)hipGetLastError();
 }

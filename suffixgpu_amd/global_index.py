@@ -38,8 +38,9 @@ PAD_TOKEN = torch.iinfo(torch.int32).max
 # per rank) so an interval-search probe is a single row load.
 KEY_WIDTH = 32
 # Slots of the n-gram range table per corpus position (a power of two in
-# all): a corpus of real text holds about 1.6 distinct runs of 1-4 tokens
-# per position, so the table stays about 40% full.
+# all, in buckets of 16): a corpus of real text holds about 1.6 distinct
+# runs of 1-4 tokens per position, so the buckets stay about 40% full and
+# almost never overflow.
 GRAM_SLOTS_PER_TOKEN = 4
 
 
@@ -103,7 +104,11 @@ class GlobalIndex:
                        for _ in range(2)]
         self._key_live = 0
         self.key_select = torch.zeros(1, dtype=torch.int32, device=dev)
-        self._build_keys(self.corpus, self.sa, self._key_live)
+        # Per buffer: ranks from this one on hold padding-suffix rows (the
+        # suffix array is the identity there and the corpus PAD), so the
+        # next build into it rewrites only the rows below max(m, this).
+        self._key_rows = [capacity, capacity]
+        self._build_keys(self.corpus, self.sa, self._key_live, 0)
         self._sa_ws: torch.Tensor | None = None
         self._query_ws: dict = {}
 
@@ -158,17 +163,22 @@ class GlobalIndex:
             "query_workspace": qws,
         }
 
-    def _build_keys(self, corpus, sa, slot: int) -> None:
+    def _build_keys(self, corpus, sa, slot: int, m: int) -> None:
         """Key rows and n-gram range table of (corpus, sa) into buffer
-        pair `slot` (0 or 1), on the current stream."""
+        pair `slot` (0 or 1), on the current stream.  Ranks from m on are
+        the padding suffixes (sa the identity, corpus PAD): their rows are
+        rewritten only where the buffer's previous build had real ones,
+        and they hold no run of real tokens for the table."""
         keys, gram = self._keys[slot], self._grams[slot]
         st = stream_of(self.device)
+        rows = max(m, self._key_rows[slot])
         check(lib().sfx_sa_keys(corpus.data_ptr(), sa.data_ptr(),
-                                self.capacity, KEY_WIDTH, keys.data_ptr(),
-                                st), "SA key rows")
-        check(lib().sfx_gram_build(keys.data_ptr(), KEY_WIDTH, self.capacity,
+                                self.capacity, rows, KEY_WIDTH,
+                                keys.data_ptr(), st), "SA key rows")
+        check(lib().sfx_gram_build(keys.data_ptr(), KEY_WIDTH, m,
                                    gram.data_ptr(), self.gram_slots, st),
               "n-gram table")
+        self._key_rows[slot] = m
 
     # ------------------------------------------------------------------
     # writes (global_index.py:86-133)
@@ -339,7 +349,7 @@ class GlobalIndex:
                                  self.staging_sa.data_ptr(), 0,
                                  ws.data_ptr(), ws.numel(),
                                  stream_of(self.device)), "SA rebuild")
-        self._build_keys(dst, self.staging_sa, 1 - self._key_live)
+        self._build_keys(dst, self.staging_sa, 1 - self._key_live, m)
 
     # Background builds, enqueued on the current (rebuild) stream.
     def _staged_build_begin(self, dst: torch.Tensor, m: int) -> None:
@@ -375,7 +385,7 @@ class GlobalIndex:
                                         ws.data_ptr(), ws.numel(),
                                         stream_of(self.device)),
               "SA rebuild")
-        self._build_keys(dst, self.staging_sa, 1 - self._key_live)
+        self._build_keys(dst, self.staging_sa, 1 - self._key_live, m)
 
     def _staged_build_check(self) -> bool:
         """After the build's event: True when the staged output is final;
@@ -534,7 +544,7 @@ class GlobalIndex:
         self.active_len = n_act
         self.active_doc_lens = deque(int(x) for x in meta["active_doc_lens"])
         self.delta_doc_lens = [int(x) for x in meta["delta_doc_lens"]]
-        self._build_keys(self.corpus, self.sa, self._key_live)
+        self._build_keys(self.corpus, self.sa, self._key_live, m)
 
     @classmethod
     def from_file(cls, path, device="cuda",

@@ -39,3 +39,22 @@ def gpu():
     from suffixgpu_amd import _lib
     _lib.lib()
     return torch.device("cuda", 0)
+
+
+def keys_by_definition(corpus: torch.Tensor, sa: torch.Tensor,
+                       keys: torch.Tensor, width: int = 32,
+                       rows: int = 1 << 18) -> None:
+    """Key row r holds corpus[sa[r] + j] for j < width, -1 at or past the
+    end: checked with torch gathers on the device, in slices of ranks."""
+    import torch
+    n = corpus.shape[0]
+    kv = keys.view(n, width)
+    j = torch.arange(width, device=corpus.device, dtype=torch.int64)
+    for r0 in range(0, n, rows):
+        pos = sa[r0:r0 + rows].to(torch.int64).unsqueeze(1) + j
+        want = torch.where(pos < n, corpus[pos.clamp(max=n - 1)],
+                           torch.full_like(pos, -1, dtype=torch.int32))
+        bad = (kv[r0:r0 + rows] != want).any(dim=1)
+        if bool(bad.any()):
+            r = r0 + int(bad.nonzero()[0, 0])
+            raise AssertionError(f"key row {r} differs from its definition")

@@ -25,6 +25,7 @@ import torch
 from oracle import sa as osa
 from oracle.drafter import DrafterOracle
 from suffixgpu_amd import synth
+from tests.conftest import keys_by_definition
 
 pytestmark = pytest.mark.gpu
 
@@ -42,24 +43,6 @@ def T(a, dev, dtype=None):
 
 def N(t):
     return t.cpu().numpy()
-
-
-def keys_by_definition(corpus: torch.Tensor, sa: torch.Tensor,
-                       keys: torch.Tensor, width: int = 32,
-                       rows: int = 1 << 18) -> None:
-    """Key row r holds corpus[sa[r] + j] for j < width, -1 at or past the
-    end: checked with torch gathers on the device, in slices of ranks."""
-    n = corpus.shape[0]
-    kv = keys.view(n, width)
-    j = torch.arange(width, device=corpus.device, dtype=torch.int64)
-    for r0 in range(0, n, rows):
-        pos = sa[r0:r0 + rows].to(torch.int64).unsqueeze(1) + j
-        want = torch.where(pos < n, corpus[pos.clamp(max=n - 1)],
-                           torch.full_like(pos, -1, dtype=torch.int32))
-        bad = (kv[r0:r0 + rows] != want).any(dim=1)
-        if bool(bad.any()):
-            r = r0 + int(bad.nonzero()[0, 0])
-            raise AssertionError(f"key row {r} differs from its definition")
 
 
 def index_equal(gi, og) -> None:
@@ -186,8 +169,8 @@ def test_c4_from_scratch_builds(c3, gpu):
         np.testing.assert_array_equal(N(out), exp)
     from suffixgpu_amd import _lib
     keys = torch.empty(N22 * 32, dtype=torch.int32, device=gpu)
-    _lib.check(_lib.lib().sfx_sa_keys(tu.data_ptr(), out.data_ptr(), N22, 32,
-                                      keys.data_ptr(),
+    _lib.check(_lib.lib().sfx_sa_keys(tu.data_ptr(), out.data_ptr(), N22,
+                                      N22, 32, keys.data_ptr(),
                                       _lib.stream_of(gpu)), "keys")
     keys_by_definition(tu, out, keys)
 

@@ -11,7 +11,7 @@ import torch
 from oracle import naive
 from oracle.global_index import GlobalIndexOracle
 from suffixgpu_amd import synth
-from tests.conftest import golden
+from tests.conftest import golden, keys_by_definition
 from tests.test_oracle_golden import _docs, trace_ops
 
 pytestmark = pytest.mark.gpu
@@ -620,39 +620,48 @@ def gram_runs(corpus, sa):
 
 
 def gpu_gram_table(g):
-    """The live table's entries of its current build."""
+    """(ok, entries) of the live table: a 256-byte header {ok}, one u32
+    fill count per bucket of 16 slots (padded to 256 bytes), then the
+    32-byte slots {t0..t3, lo, hi, k, pad}; a bucket's first
+    min(count, 16) slots are filled."""
     raw = N(g._grams[g._key_live])
-    head = raw[:256].view(np.uint32)
-    slots = raw[256:].view(np.int32).reshape(-1, 8)
-    live = slots[slots[:, 4].view(np.uint32) == head[0]]
+    slots_n = g.gram_slots
+    nb = slots_n // 16
+    cbytes = (nb * 4 + 255) // 256 * 256
+    ok = int(raw[:4].view(np.uint32)[0])
+    counts = raw[256:256 + nb * 4].view(np.uint32)
+    slots = raw[256 + cbytes:].view(np.int32).reshape(nb, 16, 8)
     tab = {}
-    for row in live:
-        key = (int(row[7]), int(row[0]), int(row[1]), int(row[2]),
-               int(row[3]))
-        assert key not in tab, key
-        tab[key] = (int(row[5]), int(row[6]))
-    return int(head[1]), tab
+    for b in np.flatnonzero(counts):
+        for row in slots[b, :min(int(counts[b]), 16)]:
+            key = (int(row[6]), int(row[0]), int(row[1]), int(row[2]),
+                   int(row[3]))
+            assert key not in tab, key
+            tab[key] = (int(row[4]), int(row[5]))
+    return ok, tab
 
 
 def test_gram_table_matches_runs(gpu):
     """The n-gram range table after a rebuild holds exactly the runs of
     1..4 real tokens of the sorted suffixes with their rank ranges, also
-    after a second rebuild reuses it (epochs, no clearing)."""
+    after later rebuilds reuse both buffers (a shorter corpus after a
+    longer one, so stale rows and slots are left behind)."""
     from suffixgpu_amd.global_index import GlobalIndex
     tc = synth.TemplateCorpus(seed=13, n_templates=5)
     g = GlobalIndex(capacity=1 << 14, delta_capacity=1 << 12, k=8,
                     max_occurrences=16, rebuild_threshold=1 << 30,
                     device=gpu)
-    for rep in range(2):
-        docs = [tc.sequence(lo=100 + 50 * rep, hi=700)
-                for _ in range(12 + 5 * rep)]
+    for rep, nd in enumerate((12, 17, 4, 3, 15)):
+        docs = [tc.sequence(lo=100 + 50 * (rep % 2), hi=700)
+                for _ in range(nd)]
         g.load_documents([T(d, gpu) for d in docs])
         torch.cuda.synchronize()
         ok, tab = gpu_gram_table(g)
         assert ok == 1
         exp = gram_runs(N(g.corpus), N(g.sa))
-        assert len(exp) > 1000
+        assert len(exp) > 200
         assert tab == exp
+        keys_by_definition(g.corpus, g.sa, g.sa_key)
 
 
 @pytest.mark.parametrize("slots", [None, 1024])
