@@ -34,9 +34,9 @@ struct GlobalArgs {
 };
 
 struct GlobalLayout {
-  int rpat, lb, ub, found, scan, red, misc, lo, dlen, dcnt, dpc, sal, sas,
-      sae, caps, dtok, dmb, mpos, mcache, mA, mH, chain, nv, score, rlen,
-      rocc, total;
+  int rpat, lb, ub, found, scan, red, misc, lo, ulo, umap, dlen, dcnt, dpc,
+      sal, sas, sae, caps, dtok, dmb, mpos, mcache, mA, mH, chain, nv, score,
+      rlen, rocc, total;
 };
 
 // Delta tokens staged per chunk (after a halo of P rounded up to 4
@@ -68,6 +68,8 @@ __host__ __device__ inline GlobalLayout global_layout(int P, int C, int R,
   L.red = g_take(off, NW * 4);
   L.misc = g_take(off, 64);
   L.lo = g_take(off, C * 4);
+  L.ulo = g_take(off, (C + 1) * 4);
+  L.umap = g_take(off, C * 4);
   L.dlen = g_take(off, C * 4);
   L.dcnt = g_take(off, C * 4);
   L.dpc = g_take(off, C * kMaxDeltaParts * 4);
@@ -98,9 +100,12 @@ __host__ __device__ inline GlobalLayout global_layout(int P, int C, int R,
 // words (chunks of kDeltaChunk positions after a halo of P rounded up to
 // 4), kept as u8 in LDS (kMbLds) or the workspace; then one ordered pass
 // extracts the part's first R ends per cap with mb >= min(part max, cap).
-// The merge keeps a part's list only where that threshold equals the
-// row's min(max mb, cap) -- any other part has no end that reaches it --
-// and concatenates the kept lists in part order (global_index.py:465-546).
+// Caps whose thresholds are equal (every cap at or above the part's
+// longest match, and the repeated smallest caps) share one list, so the
+// pass runs once per distinct threshold.  The merge keeps a part's list
+// only where that threshold equals the row's min(max mb, cap) -- any other
+// part has no end that reaches it -- and concatenates the kept lists in
+// part order (global_index.py:465-546).
 template <bool kMbLds>
 __device__ __forceinline__ void delta_role(const GlobalArgs& a,
                                            const GlobalLayout& L,
@@ -161,6 +166,9 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
     }
   };
   const int32_t r0 = rpat[0];
+  const int32_t r1 = P > 1 ? rpat[1] : 0;
+  const int32_t r2 = P > 2 ? rpat[2] : 0;
+  const int32_t r3 = P > 3 ? rpat[3] : 0;
   int4 stage[kStage4];
   if (plo < phi) load_chunk(plo, stage);
   int mx = 0;
@@ -176,25 +184,48 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
     }
     __syncthreads();
     if (c0 + kDeltaChunk < phi) load_chunk(c0 + kDeltaChunk, stage);
-    // Ends i0 .. i0 + 3 (i0 = c0 + 4g) test x(i - 1) against the newest
-    // pattern token first; only ends that pass walk further back.
+    // Ends i0 .. i0 + 3 (i0 = c0 + 4g) from two 16-byte LDS reads, which
+    // give x(i0 - 4) .. x(i0 + 3) (the halo is at least 4): the four
+    // newest pattern tokens are tested at every end without a branch, and
+    // only ends matching all four walk further back, four tokens a step.
     const int ng = (int)((cend - c0 + 3) / 4);
     for (int g = tid; g < ng; g += NT) {
       const int k = 4 * g + halo;  // dtok index of x(i0)
       const int4 lo4 = reinterpret_cast<const int4*>(dtok)[(k >> 2) - 1];
       const int4 hi4 = reinterpret_cast<const int4*>(dtok)[k >> 2];
-      const int32_t prev[4] = {lo4.w, hi4.x, hi4.y, hi4.z};  // x(i - 1)
+      // w[j] = x(i0 - 4 + j); end i0 + u reads x(i0 + u - 1 - t) =
+      // w[3 + u - t] for pattern token t
+      const int32_t w[8] = {lo4.x, lo4.y, lo4.z, lo4.w,
+                            hi4.x, hi4.y, hi4.z, hi4.w};
       const int64_t i0 = c0 + 4 * (int64_t)g;
       uint32_t word = 0;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (prev[q] == r0 && i0 + q < cend) {
-          int m = 1;
-          const int base = k - 1 + q;
-          while (m < P && dtok[base - m] == rpat[m]) ++m;
-          word |= (uint32_t)m << (8 * q);
-          mx = max(mx, m);
+      for (int u = 0; u < 4; ++u) {
+        const bool e0 = i0 + u < cend && w[3 + u] == r0;
+        const bool e1 = e0 && P > 1 && w[2 + u] == r1;
+        const bool e2 = e1 && P > 2 && w[1 + u] == r2;
+        const bool e3 = e2 && P > 3 && w[u] == r3;
+        int m = (int)e0 + (int)e1 + (int)e2 + (int)e3;
+        if (e3 && P > 4) {
+          const int base = k - 1 + u;  // dtok index of x(i - 1)
+          while (m < P) {
+            int32_t x4[4], p4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int j = base - m - e;
+              x4[e] = j >= 0 ? dtok[j] : -1;
+              p4[e] = rpat[m + e < P ? m + e : P - 1];
+            }
+            int n4 = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              n4 += (n4 == e && m + e < P && x4[e] == p4[e]) ? 1 : 0;
+            m += n4;
+            if (n4 < 4) break;
+          }
         }
+        word |= (uint32_t)m << (8 * u);
+        mx = max(mx, m);
       }
       *reinterpret_cast<uint32_t*>(mb + (i0 - plo)) = word;
     }
@@ -208,16 +239,33 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
   for (int w = 0; w < NW; ++w) part_max = max(part_max, red[w]);
   SFX_TRACE_POINT(2);
   const int32_t* caps = (const int32_t*)(smem + L.caps);
-  for (int c = tid; c < C; c += NT) lo_lds[c] = min(part_max, caps[c]);
+  int32_t* ulo = (int32_t*)(smem + L.ulo);
+  int32_t* umap = (int32_t*)(smem + L.umap);
+  if (tid == 0) {
+    // distinct thresholds in cap order; list u serves every cap mapped to u
+    int nu = 0;
+    for (int c = 0; c < C; ++c) {
+      const int t = min(part_max, caps[c]);
+      lo_lds[c] = t;
+      int u = 0;
+      while (u < nu && ulo[u] != t) ++u;
+      if (u == nu) ulo[nu++] = t;
+      umap[c] = u;
+    }
+    ulo[C] = nu;
+  }
   __syncthreads();
-  for (int g0 = 0; g0 < C; g0 += 8)
-    compact_first_r<NT>(mb, phi - plo, lo_lds + g0, min(8, C - g0), R,
+  const int nu = ulo[C];
+  for (int g0 = 0; g0 < nu; g0 += 8)
+    compact_first_r<NT>(mb, phi - plo, ulo + g0, min(8, nu - g0), R,
                         a.ws.d_end + (slot * C + g0) * R, (int32_t)plo,
                         found + g0, scan);
   __syncthreads();
   SFX_TRACE_POINT(3);
-  for (int c = tid; c < C; c += NT)
-    a.ws.d_cnt[slot * C + c] = lo_lds[c] > 0 ? found[c] : 0;
+  for (int c = tid; c < C; c += NT) {
+    a.ws.d_cnt[slot * C + c] = lo_lds[c] > 0 ? found[umap[c]] : 0;
+    a.ws.d_map[slot * C + c] = umap[c];
+  }
   if (tid == 0) a.ws.d_mx[slot] = part_max;
 }
 
@@ -262,7 +310,7 @@ __device__ __forceinline__ int32_t delta_end_at(const GlobalArgs& a, int b,
     ++k;
   }
   const int64_t slot = (int64_t)b * KD + k;
-  return a.ws.d_end[(slot * C + c) * R + r];
+  return a.ws.d_end[(slot * C + a.ws.d_map[slot * C + c]) * R + r];
 }
 
 // Position of the r-th SA sample of the interval [s, s + ilen): stride

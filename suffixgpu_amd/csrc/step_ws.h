@@ -32,6 +32,8 @@ struct StepWs {
   int32_t* dn_chain;  // [B,C,K]
   int32_t* d_mx;      // [B,KD] largest match length in each delta part
   int32_t* d_cnt;     // [B,KD,C] hits (<= R) at the part's own threshold
+  int32_t* d_map;     // [B,KD,C] the part's list of cap c (caps with equal
+                      // thresholds share one)
   int32_t* d_end;     // [B,KD,C,R] ascending end positions in the delta
   uint8_t* d_mb;      // [B*KD, stride] match lengths when LDS is too small
 };
@@ -130,6 +132,7 @@ inline size_t step_ws_layout(const sfx_params& p, int64_t B,
   const int KD = delta_parts_for(B, delta_capacity);
   w.d_mx = (int32_t*)take(b * KD * 4);
   w.d_cnt = (int32_t*)take(b * KD * C * 4);
+  w.d_map = (int32_t*)take(b * KD * C * 4);
   w.d_end = (int32_t*)take(b * KD * C * R * 4);
   const int64_t pcap = delta_part_cap(delta_capacity, KD);
   w.d_mb = (uint8_t*)take(pcap > kDeltaMbLdsMax
