@@ -88,7 +88,7 @@ __host__ __device__ inline GlobalLayout global_layout(int P, int C, int R,
   const int delta_end = off;
   off = ubase;
   L.mpos = g_take(off, nmw * Rp * 4);
-  L.mcache = g_take(off, nmw * R * K * 4);
+  L.mcache = g_take(off, nmw * R * (K + 1) * 4);
   L.mA = g_take(off, nmw * Rp * 4);
   L.mH = g_take(off, nmw * 2 * kHashSlots * 4);
   L.total = off > delta_end ? off : delta_end;
@@ -343,7 +343,7 @@ __device__ __forceinline__ ExpandResult gather_expand(
   const int64_t N = a.ix.capacity;
   const int64_t D = a.ix.delta_capacity;
   int32_t* mpos = (int32_t*)(smem + L.mpos) + wv * Rp;
-  int32_t* mcache = (int32_t*)(smem + L.mcache) + (int64_t)wv * R * K;
+  int32_t* mcache = (int32_t*)(smem + L.mcache) + (int64_t)wv * R * (K + 1);
   for (int r = ln; r < occ; r += kWave) {
     int32_t pos;
     if (src == 1) {
@@ -363,10 +363,13 @@ __device__ __forceinline__ ExpandResult gather_expand(
     slen = *a.ix.delta_len;
     slen = slen < 0 ? 0 : (slen > D ? D : slen);
   }
-  // One occurrence row per lane: its K tokens are independent loads.
+  // One occurrence row per lane: its K tokens are independent loads.  Rows
+  // are K + 1 words apart in LDS (an odd stride), so the lanes' reads and
+  // writes of one depth fall in distinct banks.
+  const int Kp = K + 1;
   for (int r = ln; r < occ; r += kWave) {
     const int64_t base = (int64_t)mpos[r] + len;
-    int32_t* dst = mcache + r * K;
+    int32_t* dst = mcache + r * Kp;
     for (int j0 = 0; j0 < K; j0 += 16) {
       int32_t v[16];
 #pragma unroll
@@ -385,11 +388,11 @@ __device__ __forceinline__ ExpandResult gather_expand(
   SFX_TRACE_POINT(11);
   if (cont_out)
     for (int e = ln; e < R * K; e += kWave)
-      cont_out[e] = e < occ * K ? mcache[e] : -1;
+      cont_out[e] = e < occ * K ? mcache[(e / K) * Kp + e % K] : -1;
   ExpandResult er{0, 0.0f};
   if (expand) {
     const int64_t cap = spec_cap(p, len);
-    auto cont_at = [&](int r, int d) -> int32_t { return mcache[r * K + d]; };
+    auto cont_at = [&](int r, int d) -> int32_t { return mcache[r * Kp + d]; };
     er = expand_wave<false>(cont_at, NoWeight(), R, occ, K, cap,
                             p.min_token_prob, p.alpha,
                             (int32_t*)(smem + L.mA) + wv * Rp, nullptr,

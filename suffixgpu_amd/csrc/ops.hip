@@ -224,10 +224,11 @@ struct ExpandArgs {
 
 __host__ __device__ inline int round16(int x) { return (x + 15) & ~15; }
 
-// Per-wave LDS: continuation cache [R*K], vote buffer A [R], weights W [R],
+// Per-wave LDS: continuation cache [R, K + 1], vote buffer A [R],
+// weights W [R],
 // chain [K]; every region 16-byte aligned.
 __host__ __device__ inline int expand_wave_bytes(int R, int K) {
-  return round16(R * K * 4) + 2 * round16(R * 4) + round16(K * 4) +
+  return round16(R * (K + 1) * 4) + 2 * round16(R * 4) + round16(K * 4) +
          2 * kHashSlots * 4;
 }
 
@@ -241,19 +242,21 @@ __global__ __launch_bounds__(256) void k_expand(ExpandArgs a) {
   const int R = a.R;
   const int K = a.K;
   unsigned char* base = smem + (size_t)wv * expand_wave_bytes(R, K);
+  const int cb = round16(R * (K + 1) * 4);
   int32_t* cache = (int32_t*)base;
-  int32_t* A = (int32_t*)(base + round16(R * K * 4));
-  float* W = (float*)(base + round16(R * K * 4) + round16(R * 4));
-  int32_t* chain =
-      (int32_t*)(base + round16(R * K * 4) + 2 * round16(R * 4));
-  int32_t* H = (int32_t*)(base + round16(R * K * 4) + 2 * round16(R * 4) +
-                          round16(K * 4));
+  int32_t* A = (int32_t*)(base + cb);
+  float* W = (float*)(base + cb + round16(R * 4));
+  int32_t* chain = (int32_t*)(base + cb + 2 * round16(R * 4));
+  int32_t* H = (int32_t*)(base + cb + 2 * round16(R * 4) + round16(K * 4));
   const int32_t* src = a.cont + row * R * K;
-  for (int e = ln; e < R * K; e += kWave) cache[e] = src[e];
+  // rows K + 1 words apart (an odd stride): one depth's rows fall in
+  // distinct LDS banks for the expansion's per-lane reads
+  for (int e = ln; e < R * K; e += kWave)
+    cache[(e / K) * (K + 1) + e % K] = src[e];
   wave_lds_sync();
   const int64_t occ = a.num_occ[row];
   const int64_t cap = a.cap ? a.cap[row] : K;
-  auto cont_at = [&](int r, int d) -> int32_t { return cache[r * K + d]; };
+  auto cont_at = [&](int r, int d) -> int32_t { return cache[r * (K + 1) + d]; };
   const float* wrow = a.weights ? a.weights + row * R : nullptr;
   auto w_at = [&](int r) -> float { return wrow[r]; };
   ExpandResult er;

@@ -310,6 +310,7 @@ __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
   int d = 0;
 #ifdef SFX_TRACE
   const uint64_t t_start = wall_clock64();
+  const uint64_t c_start = __builtin_amdgcn_s_memtime();
   int st_quick = 0, st_hash = 0, st_full = 0, st_fast = 0;
 #endif
   if (!kWeighted && R <= 2 * kWave) {
@@ -368,6 +369,7 @@ __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
 #ifdef SFX_TRACE
         st_fast = d;
         SFX_TRACE_STAT(5, wall_clock64() - t_start);
+        SFX_TRACE_STAT(4, __builtin_amdgcn_s_memtime() - c_start);
 #endif
         if (!ended && d > 0) {
           // the full vote continues with the rows still on the chain
@@ -525,9 +527,8 @@ __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
 #ifdef SFX_TRACE
   SFX_TRACE_STAT(0, occ);
   SFX_TRACE_STAT(1, st_fast);
-  SFX_TRACE_STAT(2, st_full);
+  SFX_TRACE_STAT(2, st_full + 1000 * st_hash);
   SFX_TRACE_STAT(3, st_quick);
-  SFX_TRACE_STAT(4, st_hash);
   SFX_TRACE_STAT(6, wall_clock64() - t_start);
   SFX_TRACE_STAT(7, nv);
 #endif
