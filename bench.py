@@ -333,6 +333,10 @@ def main() -> int:
         f"us/step, drafting rows {(num_valid > 0).sum()}/{B}, "
         f"mean num_valid {num_valid.mean():.2f}")
 
+    compact = compact_index_step(dev, w, bt, (draft, num_valid),
+                                 args.steps, args.warmup)
+    log(f"index without search tables: {compact}")
+
     adapter_p50 = adapter_step_p50(d, dev, bt, args.steps, args.warmup)
     log(f"engine adapter step p50 {adapter_p50:.2f} us (step kernel + count "
         "feedback, captured)")
@@ -424,6 +428,7 @@ def main() -> int:
         "local_configs": local_cfgs,
         "latency_sweep": sweep,
         "vram": drafter_device_bytes(d, B, S),
+        "compact_index": compact,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
@@ -741,6 +746,39 @@ def latency_sweep(dev, reps: int) -> list:
         f"{'g' if r['global'] else 'l'} S={r['s']} B={r['b']}: "
         f"{r['graph_p50_us']}" for r in rows))
     return rows
+
+
+def compact_index_step(dev, w, bt, ref_out, steps: int,
+                       warmup: int) -> dict:
+    """The same step with the index built without search tables (no key
+    rows, no n-gram tables): the drafter's device memory against the
+    reference's, and what the smaller footprint costs per step.  The
+    drafts must equal the full index's."""
+    import numpy as np
+    import torch
+    from suffixgpu_amd import SuffixGPUDrafter
+    d = SuffixGPUDrafter(device=dev, enable_global=True,
+                         global_capacity=CAPACITY, delta_capacity=DELTA_CAP,
+                         rebuild_threshold=1 << 30,
+                         global_search_tables=False, **CFG)
+    gi = d.global_index
+    gi.load_documents([torch.from_numpy(x).to(dev) for x in w.active_docs])
+    gi.append_documents([torch.from_numpy(x).to(dev) for x in w.delta_docs])
+    tokens0 = torch.from_numpy(bt.tokens).to(dev)
+    nt = torch.from_numpy(bt.num_tokens).to(dev)
+    sampled = torch.from_numpy(bt.sampled).to(dev)
+    buf = tokens0.clone()
+    p50, wall, out, _ = replay_p50(
+        lambda: d.propose_with_update(nt, buf, sampled), steps, warmup,
+        before=lambda: buf.copy_(tokens0))
+    same = all(np.array_equal(a.cpu().numpy(), b)
+               for a, b in zip(out[:2], ref_out[:2]))
+    res = {"step_p50_us": round(p50, 3), "wall_us": round(wall, 3),
+           "drafts_equal_full_index": bool(same),
+           "vram": drafter_device_bytes(d, B, S)}
+    del d, gi
+    torch.cuda.empty_cache()
+    return res
 
 
 def drafter_device_bytes(d, b: int, s: int) -> dict:

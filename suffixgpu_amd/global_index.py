@@ -61,7 +61,8 @@ class GlobalIndex:
                  rebuild_threshold: int | None = None,
                  device: torch.device | str = "cuda",
                  rebuild_stream: torch.cuda.Stream | None = None,
-                 gram_slots: int | None = None):
+                 gram_slots: int | None = None,
+                 search_tables: bool = True):
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise _lib.SuffixGPUError(
@@ -92,18 +93,28 @@ class GlobalIndex:
         self.delta_len_t = torch.zeros((), dtype=torch.int64, device=dev)
         # Two key-row buffers and n-gram range tables; the device word
         # key_select names the live pair (the step reads it), a rebuild
-        # writes the other.
-        self._keys = [torch.empty(capacity * KEY_WIDTH, dtype=torch.int32,
-                                  device=dev) for _ in range(2)]
-        # gram_slots (a power of two) overrides the table size; a table
-        # too small for the corpus marks itself unusable and searches span
-        # the whole suffix array instead.
-        self.gram_slots = gram_slots or gram_slots_for(capacity)
-        gbytes = int(lib().sfx_gram_table_bytes(self.gram_slots))
-        self._grams = [torch.zeros(gbytes, dtype=torch.uint8, device=dev)
-                       for _ in range(2)]
+        # writes the other.  search_tables=False keeps neither (about
+        # 260 bytes per corpus position less) and releases the build
+        # workspace between builds: searches then compare through the
+        # suffix array and the corpus, exact but slower.
+        self.search_tables = bool(search_tables)
+        self._keys = None
+        self._grams = None
+        self.gram_slots = 0
+        self.key_select = None
+        if self.search_tables:
+            self._keys = [torch.empty(capacity * KEY_WIDTH,
+                                      dtype=torch.int32, device=dev)
+                          for _ in range(2)]
+            # gram_slots (a power of two) overrides the table size; a
+            # table too small for the corpus marks itself unusable and
+            # searches span the whole suffix array instead.
+            self.gram_slots = gram_slots or gram_slots_for(capacity)
+            gbytes = int(lib().sfx_gram_table_bytes(self.gram_slots))
+            self._grams = [torch.zeros(gbytes, dtype=torch.uint8,
+                                       device=dev) for _ in range(2)]
+            self.key_select = torch.zeros(1, dtype=torch.int32, device=dev)
         self._key_live = 0
-        self.key_select = torch.zeros(1, dtype=torch.int32, device=dev)
         # Per buffer: ranks from this one on hold padding-suffix rows (the
         # suffix array is the identity there and the corpus PAD), so the
         # next build into it rewrites only the rows below max(m, this).
@@ -130,16 +141,22 @@ class GlobalIndex:
     # device views
     # ------------------------------------------------------------------
     @property
-    def sa_key(self) -> torch.Tensor:
+    def sa_key(self) -> torch.Tensor | None:
         """Key rows of the live suffix array ([capacity * 32] int32)."""
-        return self._keys[self._key_live]
+        return self._keys[self._key_live] if self._keys else None
 
     @property
-    def staging_sa_key(self) -> torch.Tensor:
+    def staging_sa_key(self) -> torch.Tensor | None:
         """Key rows a rebuild writes (the idle buffer)."""
-        return self._keys[1 - self._key_live]
+        return self._keys[1 - self._key_live] if self._keys else None
 
     def index_struct(self) -> _lib.SfxIndex:
+        if not self.search_tables:
+            return _lib.SfxIndex(self.corpus.data_ptr(), self.sa.data_ptr(),
+                                 self.capacity, self.delta.data_ptr(),
+                                 self.delta_capacity,
+                                 self.delta_len_t.data_ptr(), None, 0, None,
+                                 None, None, None, 0)
         return _lib.SfxIndex(self.corpus.data_ptr(), self.sa.data_ptr(),
                              self.capacity, self.delta.data_ptr(),
                              self.delta_capacity,
@@ -156,8 +173,8 @@ class GlobalIndex:
         qws = sum(t.numel() for t in self._query_ws.values())
         return {
             "corpus_sa": 4 * 4 * self.capacity,  # live + staging, int32
-            "key_rows": 2 * 4 * KEY_WIDTH * self.capacity,
-            "gram_tables": sum(t.numel() for t in self._grams),
+            "key_rows": sum(t.numel() * 4 for t in self._keys or ()),
+            "gram_tables": sum(t.numel() for t in self._grams or ()),
             "delta": 4 * self.delta_capacity + 8,
             "sa_build_workspace": ws,
             "query_workspace": qws,
@@ -169,6 +186,8 @@ class GlobalIndex:
         the padding suffixes (sa the identity, corpus PAD): their rows are
         rewritten only where the buffer's previous build had real ones,
         and they hold no run of real tokens for the table."""
+        if not self.search_tables:
+            return
         keys, gram = self._keys[slot], self._grams[slot]
         st = stream_of(self.device)
         rows = max(m, self._key_rows[slot])
@@ -443,13 +462,18 @@ class GlobalIndex:
         check(lib().sfx_index_swap(
             self.corpus.data_ptr(), self.sa.data_ptr(),
             self.staging_corpus.data_ptr(), self.staging_sa.data_ptr(),
-            self.capacity, self.key_select.data_ptr(), live,
-            stream_of(self.device)), "swap")
+            self.capacity,
+            self.key_select.data_ptr() if self.search_tables else None,
+            live, stream_of(self.device)), "swap")
         self._key_live = live
         self.active_len = n_new
         self.active_doc_lens = new_doc_lens
         self._rebuild_event = None
         self._pending = None
+        if not self.search_tables:
+            # the smallest footprint: the build workspace is held only
+            # while a build runs (the next one allocates it again)
+            self._sa_ws = None
 
     def poll_rebuild(self) -> None:
         """Swap in a finished background rebuild."""

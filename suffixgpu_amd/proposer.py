@@ -58,6 +58,7 @@ class SuffixGPUDrafter:
         num_backoff: int = 8,
         vote_smoothing_alpha: float = 0.0,
         parallel_paths: bool = True,
+        global_search_tables: bool = True,
     ):
         self.k = k
         self.device = torch.device(device)
@@ -101,7 +102,8 @@ class SuffixGPUDrafter:
                 capacity=global_capacity, delta_capacity=delta_capacity,
                 k=k, max_occurrences=max_occurrences,
                 rebuild_threshold=rebuild_threshold, device=self.device,
-                rebuild_stream=rebuild_stream)
+                rebuild_stream=rebuild_stream,
+                search_tables=global_search_tables)
 
     # ------------------------------------------------------------------
     def poll(self) -> None:

@@ -30,7 +30,10 @@ def N(t):
 
 def key_arrays_equal(gi):
     """Key rows are the suffixes' first 32 tokens by rank, -1 past the end
-    of the corpus."""
+    of the corpus (an index without search tables has none)."""
+    if gi.sa_key is None:
+        assert not gi.search_tables
+        return
     corpus, sa = N(gi.corpus), N(gi.sa).astype(np.int64)
     n, kw = corpus.shape[0], 32
     pos = sa[:, None] + np.arange(kw)[None, :]
@@ -126,7 +129,10 @@ def test_global_ties_golden(gpu):
     np.testing.assert_array_equal(N(nv), z["num_valid"])
 
 
-def test_global_drafter_golden(gpu):
+@pytest.mark.parametrize("tables", [True, False])
+def test_global_drafter_golden(gpu, tables):
+    """The reference's drafter trace, with the search tables (key rows and
+    n-gram table) and without them."""
     from suffixgpu_amd import SuffixGPUDrafter
     z = golden("global_drafter")
     docs = _docs(z)
@@ -134,7 +140,8 @@ def test_global_drafter_golden(gpu):
                          max_occurrences=128, num_backoff=8,
                          max_spec_factor=2.0, min_token_prob=0.1,
                          enable_global=True, global_capacity=1 << 13,
-                         delta_capacity=1 << 10, rebuild_threshold=700)
+                         delta_capacity=1 << 10, rebuild_threshold=700,
+                         global_search_tables=tables)
     for step, lo in enumerate(range(0, len(docs), 8)):
         chunk = docs[lo:lo + 8]
         d.harvest_rows([T(x, gpu) for x in chunk], [len(x) for x in chunk])
@@ -664,19 +671,22 @@ def test_gram_table_matches_runs(gpu):
         keys_by_definition(g.corpus, g.sa, g.sa_key)
 
 
-@pytest.mark.parametrize("slots", [None, 1024])
+@pytest.mark.parametrize("slots", [None, 1024, 0])
 def test_queries_with_and_without_gram_table(gpu, slots):
     """Capped SA + delta queries, drafts and the fused step agree with the
     oracle with the table in use and with a table too small for the corpus
     (it marks itself unusable; every search spans the whole array);
-    queries holding separator, padding or -1 tokens skip the table."""
+    queries holding separator, padding or -1 tokens skip the table.
+    slots=0: no key rows and no table at all (search_tables=False); every
+    comparison reads the suffix array and the corpus."""
     from suffixgpu_amd.global_index import GlobalIndex
     from oracle.global_index import GlobalIndexOracle
     tc = synth.TemplateCorpus(seed=14, n_templates=6)
     docs = [tc.sequence(lo=200, hi=900) for _ in range(30)]
     kw = dict(capacity=1 << 15, delta_capacity=1 << 12, k=12,
               max_occurrences=32, rebuild_threshold=1 << 30)
-    g = GlobalIndex(device=gpu, gram_slots=slots, **kw)
+    g = GlobalIndex(device=gpu, gram_slots=slots or None,
+                    search_tables=slots != 0, **kw)
     o = GlobalIndexOracle(**kw)
     g.load_documents([T(d, gpu) for d in docs])
     o.load_documents(docs)
@@ -684,8 +694,11 @@ def test_queries_with_and_without_gram_table(gpu, slots):
     g.append_documents([T(d, gpu) for d in dd])
     o.append_documents(dd)
     torch.cuda.synchronize()
-    ok, _ = gpu_gram_table(g)
-    assert ok == (1 if slots is None else 0)
+    if slots != 0:
+        ok, _ = gpu_gram_table(g)
+        assert ok == (1 if slots is None else 0)
+    else:
+        assert g.sa_key is None and g.device_bytes()["key_rows"] == 0
     rng = np.random.default_rng(15)
     b, p = 48, 40
     q = np.zeros((b, p), I32)
