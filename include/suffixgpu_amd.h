@@ -32,7 +32,7 @@ extern "C" {
 
 #define SFX_EINVAL (-1)
 #define SFX_MAX_CANDIDATES 32
-#define SFX_ABI_VERSION 9
+#define SFX_ABI_VERSION 10
 
 /* Drafter configuration shared by the local and global paths.
  * Mirrors the constructor arguments of SuffixGPUDrafter
@@ -322,6 +322,70 @@ int sfx_delta_append(const sfx_append_doc* docs, int32_t ndocs,
  * from + n) in place -- and set *delta_len = n (skipped when NULL). */
 int sfx_delta_shift(int32_t* delta, int64_t delta_capacity, int64_t from,
                     int64_t n, int64_t* delta_len, hipStream_t stream);
+
+/* ---- device-side ingest (proposer.py:329-343 harvest_finished,
+ *      global_index.py:86-215 append_documents through the rebuild
+ *      snapshot) ---------------------------------------------------------- */
+
+/* The state's header: the index's document bookkeeping, kept in device
+ * memory.  The two doc-length lists (corpus documents oldest first, delta
+ * documents oldest first) are rings of int32 lengths, separator included,
+ * at the offsets sfx_ingest_layout reports. */
+typedef struct sfx_ingest_header {
+  int64_t active_len;      /* corpus tokens once a staged build is in */
+  int64_t live_active_len; /* corpus tokens of the live suffix array */
+  int64_t delta_len;       /* delta tokens */
+  int64_t active_head;     /* ring slot of the oldest corpus document */
+  int64_t active_docs;     /* corpus documents */
+  int64_t delta_head;      /* ring slot of the oldest delta document */
+  int64_t delta_docs;      /* delta documents */
+  int64_t in_flight;       /* 1: a snapshot is staged, not yet swapped in */
+  int64_t snap_seq;        /* snapshots staged so far */
+  int64_t snap_n_new;      /* tokens of the last staged corpus */
+  int64_t snap_m;          /* suffixes its build sorts (n_new + 1, capped) */
+  int64_t docs_in;         /* documents appended so far */
+  int64_t docs_dropped;    /* delta documents dropped to make room */
+  int64_t tokens_dropped;
+  int64_t bad_rows;        /* row indices outside the token buffer */
+  int64_t reserved;
+} sfx_ingest_header;
+
+#define SFX_INGEST_MAX_DOCS 4096
+
+/* No reference counterpart (the reference takes host lengths and decides
+ * on the host).  out[0] = state bytes for an index of this geometry,
+ * out[1], out[2] = corpus and delta ring slots, out[3], out[4] = byte
+ * offsets of the two rings, out[5] = of the scratch delta.  The state is
+ * 256-byte aligned; the caller fills the header and rings once (from its
+ * own bookkeeping) before the first sfx_ingest_docs. */
+int sfx_ingest_layout(int64_t capacity, int64_t delta_capacity,
+                      int64_t* out);
+
+/* harvest_finished with device row indices and lengths: appends
+ * tokens[row_idx[i], 0 : min(lengths[i], seq)] for i < ndocs (<=
+ * SFX_INGEST_MAX_DOCS; int32 or int64 indices and lengths), each followed
+ * by SEP, taking every decision of append_documents on the device --
+ * truncation to the last delta_capacity - 1 tokens, making room, dropping
+ * the oldest delta documents, and the rebuild snapshot (eviction, whole
+ * delta documents, the staging corpus written with PAD after it) of
+ * _make_room and maybe_rebuild.  A snapshot bumps header.snap_seq: the
+ * caller then builds staging_corpus[0 : snap_m] into the staging suffix
+ * array and swaps it in, calling sfx_ingest_swapped after the swap; until
+ * then the rebuild counts as running.  Rows outside [0, rows) are skipped
+ * and counted.  corpus, delta and delta_len are the index's (sfx_index);
+ * the delta and its length word are updated in place.  Three launches on
+ * `stream`, no host synchronisation. */
+int sfx_ingest_docs(void* state, const int32_t* corpus, int64_t capacity,
+                    int32_t* delta, int64_t delta_capacity,
+                    int64_t* delta_len, int32_t* staging_corpus,
+                    const int32_t* tokens, int64_t rows, int64_t seq,
+                    const void* row_idx, int32_t row_idx_is64,
+                    const void* lengths, int32_t lengths_is64, int64_t ndocs,
+                    int64_t rebuild_threshold, hipStream_t stream);
+
+/* The staged build is live (after sfx_index_swap): the rebuild is no
+ * longer running. */
+int sfx_ingest_swapped(void* state, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -36,13 +36,18 @@ class GlobalIndexOracle:
     global_index.py:213-215) a rebuild builds and swaps immediately.  With
     ``async_rebuild=True`` it behaves like a rebuild on a side stream that has
     finished by the next ``poll_rebuild`` -- the deterministic schedule the
-    GPU implementation uses in its blocking-poll mode.
+    GPU implementation uses in its blocking-poll mode.  Adding
+    ``finish_at_user_poll=True``, a rebuild is still running when
+    append_documents polls (global_index.py:111,140 find its event not yet
+    complete) and finishes at the caller's next poll_rebuild: the schedule
+    of the GPU's device-side ingest, whose builds start at that poll.
     """
 
     def __init__(self, capacity: int, delta_capacity: int, k: int,
                  max_occurrences: int = 32,
                  rebuild_threshold: int | None = None,
-                 async_rebuild: bool = False):
+                 async_rebuild: bool = False,
+                 finish_at_user_poll: bool = False):
         self.capacity = capacity
         self.delta_capacity = delta_capacity
         self.k = k
@@ -50,6 +55,7 @@ class GlobalIndexOracle:
         self.rebuild_threshold = rebuild_threshold or max(
             1, delta_capacity // 2)
         self.async_rebuild = async_rebuild
+        self.finish_at_user_poll = finish_at_user_poll
         self.corpus = np.full(capacity, PAD_TOKEN, dtype=np.int32)
         self.staging_corpus = self.corpus.copy()
         self.sa = np.arange(capacity, dtype=np.int32)
@@ -81,9 +87,14 @@ class GlobalIndexOracle:
             self.delta_doc_lens.append(n + 1)
         self.maybe_rebuild()
 
+    def _poll_internal(self) -> None:
+        """The polls inside append_documents (global_index.py:111,140)."""
+        if not self.finish_at_user_poll:
+            self.poll_rebuild()
+
     def _make_room(self, needed: int) -> None:
         """global_index.py:110-118."""
-        self.poll_rebuild()
+        self._poll_internal()
         if self._rebuild_event is None:
             self._launch_rebuild()
         if self.delta_len + needed <= self.delta_capacity:
@@ -107,7 +118,7 @@ class GlobalIndexOracle:
 
     def maybe_rebuild(self) -> None:
         """global_index.py:138-145."""
-        self.poll_rebuild()
+        self._poll_internal()
         if self._rebuild_event is not None or self.delta_len == 0:
             return
         if self.delta_len < self.rebuild_threshold:

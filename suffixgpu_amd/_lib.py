@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsuffixgpu_amd.so"
 MAX_CANDIDATES = 32
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -83,6 +83,11 @@ SIGNATURES = {
     "sfx_delta_append": (c_i32, [ctypes.POINTER(SfxAppendDoc), c_i32, c_p,
                                  c_i64, c_p, c_i64, c_p]),
     "sfx_delta_shift": (c_i32, [c_p, c_i64, c_i64, c_i64, c_p, c_p]),
+    "sfx_ingest_layout": (c_i32, [c_i64, c_i64, c_p]),
+    "sfx_ingest_docs": (c_i32, [c_p, c_p, c_i64, c_p, c_i64, c_p, c_p,
+                                c_p, c_i64, c_i64, c_p, c_i32, c_p, c_i32,
+                                c_i64, c_i64, c_p]),
+    "sfx_ingest_swapped": (c_i32, [c_p, c_p]),
     "sfx_scatter_append": (c_i32, [ctypes.POINTER(SfxBatch), c_p, c_p]),
     "sfx_match_back": (c_i32, [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p,
                                c_p]),
@@ -172,6 +177,13 @@ EINVAL = -1
 ENOSCRATCH = -2
 NOALLOC_SCRATCH_BYTES = 16 << 20
 NOALLOC_MAX_ROWS = 4096
+INGEST_MAX_DOCS = 4096
+# sfx_ingest_header, in order (int64 each)
+INGEST_HEADER_FIELDS = (
+    "active_len", "live_active_len", "delta_len", "active_head",
+    "active_docs", "delta_head", "delta_docs", "in_flight", "snap_seq",
+    "snap_n_new", "snap_m", "docs_in", "docs_dropped", "tokens_dropped",
+    "bad_rows", "reserved")
 
 
 def check(rc: int, what: str) -> None:

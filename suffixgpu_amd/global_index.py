@@ -25,6 +25,7 @@ delta-scan + merge kernel (csrc/global.hip).
 from __future__ import annotations
 
 from collections import deque
+from ctypes import c_int64 as ctypes_i64
 
 import torch
 
@@ -129,6 +130,20 @@ class GlobalIndex:
         self.delta_doc_lens: list[int] = []
         self._rebuild_event = None
         self._pending = None
+        # Device-side ingest (harvest_device): the bookkeeping lives in
+        # device memory while _ing_live; poll reads a pinned copy of its
+        # header, and the host lists above are refreshed only by
+        # sync_host_state (or any host-side write, which calls it).
+        self._ing: torch.Tensor | None = None
+        self._ing_layout: list[int] | None = None
+        self._ing_live = False
+        self._ing_mirror = torch.zeros(16, dtype=torch.int64,
+                                       pin_memory=True)
+        self._ing_event = None
+        self._ing_seen_seq = 0
+        # device-side ingest totals: documents appended, dropped to make
+        # room (and their tokens), rows outside the token buffer
+        self.ingest_counters: dict = {}
         # Background rebuilds run their doubling rounds in two chunks: the
         # first sized from the rounds the previous build needed (plus a
         # margin), the rest only if the device reports the array is not
@@ -210,6 +225,7 @@ class GlobalIndex:
         delta_capacity - 1 tokens, making room); the documents between two
         room-making steps are written by one sfx_delta_append launch.
         """
+        self.sync_host_state()
         pending: list[tuple[torch.Tensor, int, int]] = []
         for doc in docs:
             doc = doc.to(self.device).to(torch.int32).reshape(-1)
@@ -280,6 +296,7 @@ class GlobalIndex:
     def maybe_rebuild(self) -> None:
         """Start a background rebuild once the delta holds at least
         rebuild_threshold tokens and none is running."""
+        self.sync_host_state()
         self.poll_rebuild()
         if self._rebuild_event is not None or self.delta_len == 0:
             return
@@ -467,7 +484,12 @@ class GlobalIndex:
             live, stream_of(self.device)), "swap")
         self._key_live = live
         self.active_len = n_new
-        self.active_doc_lens = new_doc_lens
+        if new_doc_lens is not None:  # None: the device keeps them
+            self.active_doc_lens = new_doc_lens
+        if self._ing_live:
+            check(lib().sfx_ingest_swapped(self._ing.data_ptr(),
+                                           stream_of(self.device)),
+                  "ingest swap")
         self._rebuild_event = None
         self._pending = None
         if not self.search_tables:
@@ -476,7 +498,24 @@ class GlobalIndex:
             self._sa_ws = None
 
     def poll_rebuild(self) -> None:
-        """Swap in a finished background rebuild."""
+        """Swap in a finished background rebuild.  After device-side
+        ingest, first read a pinned copy of the device bookkeeping's header
+        (issued by an earlier poll and landed by now; with blocking_poll
+        issued now and waited for) and start the build of a snapshot the
+        device staged."""
+        if self._ing_live:
+            # the copy is issued here, never by harvest_device
+            if self._ing_event is None or self.blocking_poll:
+                self._ing_mirror.copy_(self._ing[:128].view(torch.int64),
+                                       non_blocking=True)
+                self._ing_event = torch.cuda.Event()
+                self._ing_event.record(torch.cuda.current_stream(
+                    self.device))
+            if self.blocking_poll:
+                self._ing_event.synchronize()
+            if self._ing_event.query():
+                self._ing_event = None
+                self._read_ingest_mirror()
         ev = self._rebuild_event
         if ev is None:
             return
@@ -492,11 +531,163 @@ class GlobalIndex:
             self.poll_rebuild()  # the remaining rounds, waited for too
 
     # ------------------------------------------------------------------
+    # device-side ingest (proposer.py:329-343 with device lengths)
+    # ------------------------------------------------------------------
+    def harvest_device(self, row_idx: torch.Tensor, lengths: torch.Tensor,
+                       tokens: torch.Tensor) -> None:
+        """append_documents of tokens[r, :n] for (r, n) in
+        zip(row_idx, lengths), with row_idx and lengths in device memory
+        (int32 or int64): every decision of append_documents -- truncation,
+        making room, dropping the oldest delta documents and the rebuild
+        snapshot -- is taken on the device and nothing is read back.  A
+        snapshot's build starts from the next poll_rebuild (until it is
+        swapped in, the rebuild counts as running), which also refreshes
+        delta_len and active_len; the host doc-length lists follow only
+        through sync_host_state.  At most 4096 rows per call; rows outside
+        the buffer are skipped and counted in ingest_counters."""
+        n = row_idx.numel()
+        if n != lengths.numel():
+            raise ValueError("harvest_device: row_idx and lengths differ "
+                             "in size")
+        if n == 0:
+            return
+        if n > _lib.INGEST_MAX_DOCS:
+            raise ValueError(f"harvest_device: at most "
+                             f"{_lib.INGEST_MAX_DOCS} rows per call")
+        for t in (row_idx, lengths, tokens):
+            if t.device != self.device:
+                raise ValueError("harvest_device: tensors must be on "
+                                 f"{self.device}")
+        if row_idx.dtype not in (torch.int32, torch.int64) or \
+                lengths.dtype not in (torch.int32, torch.int64):
+            raise TypeError("harvest_device: int32 or int64 indices")
+        if tokens.dtype != torch.int32 or tokens.dim() != 2:
+            raise TypeError("harvest_device: tokens must be [rows, seq] "
+                            "int32")
+        row_idx = row_idx.contiguous()
+        lengths = lengths.contiguous()
+        tokens = tokens.contiguous()
+        self._ingest_to_device()
+        check(lib().sfx_ingest_docs(
+            self._ing.data_ptr(), self.corpus.data_ptr(), self.capacity,
+            self.delta.data_ptr(), self.delta_capacity,
+            self.delta_len_t.data_ptr(), self.staging_corpus.data_ptr(),
+            tokens.data_ptr(), tokens.shape[0], tokens.shape[1],
+            row_idx.data_ptr(), int(row_idx.dtype == torch.int64),
+            lengths.data_ptr(), int(lengths.dtype == torch.int64), n,
+            self.rebuild_threshold, stream_of(self.device)), "ingest")
+
+    def _ingest_header(self, words) -> dict:
+        return dict(zip(_lib.INGEST_HEADER_FIELDS, (int(x) for x in words)))
+
+    def _ingest_to_device(self) -> None:
+        """Make the device bookkeeping authoritative (host lists uploaded;
+        a rebuild the host started counts as running there)."""
+        if self._ing_live:
+            return
+        if self._ing is None:
+            lay = (ctypes_i64 * 8)()
+            check(lib().sfx_ingest_layout(self.capacity, self.delta_capacity,
+                                          lay), "ingest layout")
+            self._ing_layout = [int(x) for x in lay]
+            self._ing = torch.zeros(self._ing_layout[0], dtype=torch.uint8,
+                                    device=self.device)
+        total, acap, dcap, aoff, doff = self._ing_layout[:5]
+        running = self._rebuild_event is not None
+        if running:
+            n_new, new_lens = self._pending
+            plan_len, plan_lens = n_new, list(new_lens)
+        else:
+            plan_len, plan_lens = self.active_len, list(self.active_doc_lens)
+        head = [0] * 16
+        head[0] = plan_len
+        head[1] = self.active_len
+        head[2] = self.delta_len
+        head[4] = len(plan_lens)
+        head[6] = len(self.delta_doc_lens)
+        head[7] = int(running)
+        for i, name in enumerate(("docs_in", "docs_dropped",
+                                  "tokens_dropped", "bad_rows")):
+            head[11 + i] = self.ingest_counters.get(name, 0)
+        self._ing[:128].view(torch.int64).copy_(
+            torch.tensor(head, dtype=torch.int64))
+        if plan_lens:
+            self._ing[aoff:aoff + 4 * len(plan_lens)].view(torch.int32) \
+                .copy_(torch.tensor(plan_lens, dtype=torch.int32))
+        if self.delta_doc_lens:
+            self._ing[doff:doff + 4 * len(self.delta_doc_lens)] \
+                .view(torch.int32).copy_(
+                    torch.tensor(self.delta_doc_lens, dtype=torch.int32))
+        self._ing_seen_seq = 0
+        self._ing_live = True
+
+    def _read_ingest_mirror(self) -> None:
+        h = self._ingest_header(self._ing_mirror.tolist())
+        self.delta_len = h["delta_len"]
+        self.active_len = h["live_active_len"]
+        self.ingest_counters = {k: h[k] for k in (
+            "docs_in", "docs_dropped", "tokens_dropped", "bad_rows")}
+        if h["snap_seq"] > self._ing_seen_seq:
+            self._ing_seen_seq = h["snap_seq"]
+            self._start_staged_build(h["snap_n_new"], h["snap_m"], None)
+
+    def _start_staged_build(self, n_new: int, m: int, new_doc_lens) -> None:
+        """Build staging_corpus[:m] (already written) and swap it in: in
+        the background on rebuild_stream, else now."""
+        dst = self.staging_corpus
+        if self.rebuild_stream is not None:
+            self.rebuild_stream.wait_stream(
+                torch.cuda.current_stream(self.device))
+            with torch.cuda.stream(self.rebuild_stream):
+                self._staged_build_begin(dst, m)
+            event = torch.cuda.Event()
+            event.record(self.rebuild_stream)
+            self._pending = (n_new, new_doc_lens)
+            self._rebuild_event = event
+        else:
+            self._build_staging_sa(dst, m)
+            self._finish_swap(n_new, new_doc_lens)
+
+    def sync_host_state(self) -> None:
+        """Bring the device bookkeeping of harvest_device back into the
+        host fields and lists (reads device memory; waits for the stream).
+        A staged snapshot whose build has not started is started first.
+        Host-side writes call this themselves."""
+        if not self._ing_live:
+            return
+        self._ing_event = None
+        raw = self._ing.cpu()
+        self._ing_mirror.copy_(raw[:128].view(torch.int64))
+        self._read_ingest_mirror()
+        h = self._ingest_header(raw[:128].view(torch.int64).tolist())
+        total, acap, dcap, aoff, doff = self._ing_layout[:5]
+
+        def ring(off, cap, head, cnt):
+            r = raw[off:off + 4 * cap].view(torch.int32)
+            idx = [(head + i) % cap for i in range(cnt)]
+            return r[idx].tolist() if cnt else []
+
+        plan = ring(aoff, acap, h["active_head"], h["active_docs"])
+        self.delta_doc_lens = ring(doff, dcap, h["delta_head"],
+                                   h["delta_docs"])
+        self.delta_len = h["delta_len"]
+        if self._rebuild_event is not None:
+            # running: the device lists already describe the corpus after
+            # the swap
+            n_new, _ = self._pending
+            self._pending = (n_new, deque(plan))
+        else:
+            self.active_len = h["active_len"]
+            self.active_doc_lens = deque(plan)
+        self._ing_live = False
+
+    # ------------------------------------------------------------------
     # persistence (this library's own format; suffixgpu_amd.persist)
     # ------------------------------------------------------------------
     def save(self, path) -> None:
         """Write the index to ``path``.  An in-flight rebuild is completed
         (and swapped in) first, so the file holds one consistent state."""
+        self.sync_host_state()
         from suffixgpu_amd.persist import write_index_file
         if self._rebuild_event is not None:
             blocking = self.blocking_poll
@@ -531,6 +722,7 @@ class GlobalIndex:
         """Load a saved index into this one, in place (tensor identities
         are kept, so captured graphs stay valid).  Capacities must match;
         any in-flight rebuild is dropped."""
+        self.sync_host_state()
         from suffixgpu_amd.persist import IndexFormatError, read_index_file
         meta, arrays = read_index_file(path)
         if (meta["capacity"] != self.capacity
@@ -592,6 +784,7 @@ class GlobalIndex:
         over the first min(n + 1, capacity) positions.  The delta is left
         untouched.  Synchronous on the current stream.
         """
+        self.sync_host_state()
         if self._rebuild_event is not None:
             raise RuntimeError("load_documents: a rebuild is in flight")
         lens = [int(d.numel()) + 1 for d in docs]

@@ -230,9 +230,21 @@ class SuffixGPUDrafter:
     def harvest_finished(self, row_indices: list[int], lengths: list[int],
                          token_ids_gpu: torch.Tensor) -> None:
         """Append rows[:length] of finished requests to the global memory
-        (proposer.py:329-343).  row_indices and lengths may also be
-        tensors; a device tensor costs one device-to-host copy, since the
-        room-making and rebuild decisions are taken on the host."""
+        (proposer.py:329-343).  With row_indices and lengths as tensors on
+        the drafter's device the appends and every decision about them run
+        on the device (GlobalIndex.harvest_device): nothing is read back,
+        and a rebuild they trigger starts at the next poll().  Host lists
+        (or host tensors) take the host path."""
+        if self.global_index is None:
+            return
+        if (isinstance(row_indices, torch.Tensor)
+                and isinstance(lengths, torch.Tensor)
+                and row_indices.device == self.device
+                and lengths.device == self.device):
+            self.global_index.harvest_device(row_indices.reshape(-1),
+                                             lengths.reshape(-1),
+                                             token_ids_gpu)
+            return
         if isinstance(row_indices, torch.Tensor):
             row_indices = row_indices.tolist()
         if isinstance(lengths, torch.Tensor):

@@ -546,3 +546,57 @@ def test_row_pool_matches_single_process():
     np.testing.assert_array_equal(tp, tok)
     for a, e in zip(got, exp):
         np.testing.assert_array_equal(a, e)
+
+
+def test_rebuild_finishing_at_the_callers_poll():
+    """finish_at_user_poll: a rebuild that an append starts is still
+    running at that append's later room-making, so the oldest delta
+    document is dropped (global_index.py:110-118) instead of a second
+    rebuild starting; the caller's poll swaps the first one in.  Worked by
+    hand: delta capacity 20, documents of 10, 10, 5, 15 and 3 tokens
+    (separator included)."""
+    docs = [np.arange(1, 10), np.arange(11, 20), np.arange(21, 25),
+            np.arange(31, 45), np.arange(51, 53)]
+    kw = dict(capacity=100, delta_capacity=20, k=4, rebuild_threshold=1000)
+    u = GlobalIndexOracle(async_rebuild=True, finish_at_user_poll=True, **kw)
+    u.append_documents(docs)
+    # the 5-token document made room by staging the first two; the
+    # 3-token one found that rebuild running and dropped the 5-token one
+    assert u.delta_doc_lens == [15, 3] and u.delta_len == 18
+    assert u.active_len == 0 and u._rebuild_event is not None
+    np.testing.assert_array_equal(
+        u.delta[:18], np.concatenate([docs[3], [-2], docs[4], [-2]]))
+    u.poll_rebuild()
+    assert u.active_len == 20 and list(u.active_doc_lens) == [10, 10]
+    np.testing.assert_array_equal(
+        u.corpus[:20], np.concatenate([docs[0], [-2], docs[1], [-2]]))
+    assert u._rebuild_event is None
+    # the schedule where a build is done by the next poll: the 3-token
+    # document's room-making swaps the first one in and stages the 5- and
+    # 15-token documents, which maybe_rebuild's poll swaps in too
+    a = GlobalIndexOracle(async_rebuild=True, **kw)
+    a.append_documents(docs)
+    assert a.delta_doc_lens == [3] and a.active_len == 40
+    assert list(a.active_doc_lens) == [10, 10, 5, 15]
+
+
+def test_user_poll_schedule_equals_next_poll_without_midcall_room():
+    """Without room-making inside a call, the two schedules leave the same
+    index after every caller poll (the only rebuilds start at the end of
+    a call, in maybe_rebuild)."""
+    rng = np.random.default_rng(35)
+    kw = dict(capacity=3000, delta_capacity=400, k=4, rebuild_threshold=150)
+    u = GlobalIndexOracle(async_rebuild=True, finish_at_user_poll=True, **kw)
+    a = GlobalIndexOracle(async_rebuild=True, **kw)
+    for _ in range(30):
+        docs = [rng.integers(0, 9, size=int(n))
+                for n in rng.integers(1, 40, size=3)]
+        for gi in (u, a):
+            gi.append_documents(docs)
+            gi.poll_rebuild()
+        assert u.delta_doc_lens == a.delta_doc_lens
+        assert list(u.active_doc_lens) == list(a.active_doc_lens)
+        np.testing.assert_array_equal(u.corpus, a.corpus)
+        np.testing.assert_array_equal(u.sa, a.sa)
+        np.testing.assert_array_equal(u.delta[:u.delta_len],
+                                      a.delta[:a.delta_len])
