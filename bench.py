@@ -797,9 +797,9 @@ def drafter_device_bytes(d, b: int, s: int) -> dict:
 def e2e_loop(dev, steps: int) -> dict:
     """Scripted decode loop (B=256, S=16384): captured propose_with_update
     per step with the sampled block and counts fed back on the device,
-    16 longest rows harvested into global memory every 64 steps and reset,
-    background rebuilds at delta_capacity // 2 on a side stream, poll()
-    every step."""
+    16 longest rows harvested into global memory every 64 steps (device
+    row indices and lengths: device-side ingest) and reset, background
+    rebuilds at delta_capacity // 2 on a side stream, poll() every step."""
     import torch
     from suffixgpu_amd import SuffixGPUDrafter, synth
     t0 = time.time()
@@ -818,9 +818,11 @@ def e2e_loop(dev, steps: int) -> dict:
     # New requests' rows arrive as an engine stages them: pinned host
     # buffers copied without blocking the host.
     fresh = {i: (torch.tensor(rows, dtype=torch.int64, device=dev),
+                 torch.tensor(lengths, dtype=torch.int64, device=dev),
                  torch.from_numpy(new_rows).pin_memory(),
                  torch.from_numpy(new_nt).pin_memory())
-             for i, (rows, _, new_rows, new_nt) in lp.harvests.items()}
+             for i, (rows, lengths, new_rows, new_nt)
+             in lp.harvests.items()}
     for _ in range(3):
         d.propose_with_update(nt, tok, samp)
     torch.cuda.synchronize()
@@ -845,18 +847,16 @@ def e2e_loop(dev, steps: int) -> dict:
         evs.append((e0, e1))
         nt.copy_(out[2])
         nv_log[i].copy_(out[1])
-        hv = lp.harvests.get(i)
-        if hv is not None:
-            rows, lengths, _, _ = hv
-            had = gi._rebuild_event is not None
-            d.harvest_finished(rows, lengths, tok)
-            launches += int(not had and gi._rebuild_event is not None)
-            idx, new_rows, new_nt = fresh[i]
+        if i in fresh:
+            idx, lens, new_rows, new_nt = fresh[i]
+            d.harvest_finished(idx, lens, tok)
             tok.index_copy_(0, idx, new_rows.to(dev, non_blocking=True))
             nt.index_copy_(0, idx, new_nt.to(dev, non_blocking=True))
-        pending = gi._rebuild_event is not None
-        d.poll()
-        swaps += int(pending and gi._rebuild_event is None)
+        before = gi._rebuild_event
+        d.poll()  # starts the build of a snapshot the device staged
+        now = gi._rebuild_event
+        swaps += int(before is not None and now is not before)
+        launches += int(now is not None and now is not before)
     torch.cuda.synchronize()
     wall = time.perf_counter() - tw
     per = [a.elapsed_time(b) * 1e3 for a, b in evs]
@@ -873,8 +873,9 @@ def e2e_loop(dev, steps: int) -> dict:
     torch.cuda.synchronize()
     queued = [a.elapsed_time(b) * 1e3 for a, b in qevs]
     return {"workload": "B=256 S=16384 k=16 nb=8 R=128, 1000-step "
-                        "captured decode loop, harvest 16 rows / 64 steps, "
-                        "rebuild at delta_capacity/2 on a side stream",
+                        "captured decode loop, harvest 16 rows / 64 steps "
+                        "(device row indices and lengths), rebuild at "
+                        "delta_capacity/2 on a side stream",
             "steps": steps, "replay_p50_us": round(statistics.median(per), 3),
             "replay_p99_us": round(float(np.percentile(per, 99)), 3),
             "queued_replay_p50_us": round(statistics.median(queued), 3),
@@ -1027,8 +1028,19 @@ def sync_check(d, w, dev) -> int:
     for _ in range(SYNC_CHECK_STEPS):
         graph.replay()
     torch.cuda.synchronize()
+    # Device-side ingest: harvest_finished with device rows and lengths
+    # (16 rows of the batch per call); the first call uploads the host
+    # doc-length lists, then the timed section must read nothing back.
+    rows = torch.arange(16, device=dev)
+    lengths = nt[:16].clone()
+    d.harvest_finished(rows, lengths, buf)
+    torch.cuda.synchronize()
+    for _ in range(SYNC_CHECK_STEPS):
+        d.harvest_finished(rows, lengths, buf)
+    torch.cuda.synchronize()
     log(f"sync check done: {SYNC_CHECK_STEPS} eager steps, "
-        f"{SYNC_CHECK_STEPS} graph replays")
+        f"{SYNC_CHECK_STEPS} graph replays, {SYNC_CHECK_STEPS} device "
+        "harvests")
     return 0
 
 
@@ -1072,12 +1084,17 @@ def summarize_api(trace_dir: str) -> dict:
              if s["calls"].get("hipExtLaunchKernel", 0)
              + s["calls"].get("hipLaunchKernel", 0)
              + s["calls"].get("hipModuleLaunchKernel", 0)
-             >= SYNC_CHECK_STEPS]
+             == SYNC_CHECK_STEPS]
     replay = [s for s in sections
               if s["calls"].get("hipGraphLaunch", 0) == SYNC_CHECK_STEPS]
+    # The last section: the device harvests (three launches each).
+    harvest = [s for s in sections
+               if s["calls"].get("hipLaunchKernel", 0)
+               == 3 * SYNC_CHECK_STEPS]
     return {"steps_per_section": SYNC_CHECK_STEPS,
             "eager_steps": eager[-1] if eager else None,
             "graph_replays": replay[-1] if replay else None,
+            "device_harvests": harvest[-1] if harvest else None,
             "sections": len(sections)}
 
 

@@ -39,7 +39,8 @@ class DrafterOracle:
                  max_spec_factor: float | None = None,
                  max_spec_offset: float = 0.0, min_token_prob: float = 0.0,
                  num_backoff: int = 8, vote_smoothing_alpha: float = 0.0,
-                 async_rebuild: bool = False):
+                 async_rebuild: bool = False,
+                 finish_at_user_poll: bool = False):
         self.k = k
         self.max_pattern_len = max_pattern_len
         self.min_token_prob = min_token_prob
@@ -61,7 +62,8 @@ class DrafterOracle:
                 capacity=global_capacity, delta_capacity=delta_capacity, k=k,
                 max_occurrences=max_occurrences,
                 rebuild_threshold=rebuild_threshold,
-                async_rebuild=async_rebuild)
+                async_rebuild=async_rebuild,
+                finish_at_user_poll=finish_at_user_poll)
 
     def poll(self) -> None:
         if self.global_index is not None:

@@ -235,13 +235,16 @@ def test_c4_background_rebuild_and_swap(c3, gpu):
 C5_CHECK = (0, 1, 2, 3, 62, 63, 64, 65, 69)
 
 
-def test_c5_decode_loop_matches_oracle(gpu):
+@pytest.mark.parametrize("device_harvest", [False, True])
+def test_c5_decode_loop_matches_oracle(gpu, device_harvest):
     """B=256, S=16384: 70 replays of a captured propose_with_update with
     the sampled block and counts fed back on the device, the step-63
     harvest of the 16 longest rows into global memory (background
     rebuilds at delta_capacity/2, blocking poll every step) and the rows
     reset; new counts every step, the full step and token rows on the
-    chosen steps, and the index after the harvest."""
+    chosen steps, and the index after the harvest.  device_harvest: the
+    rows and lengths are device tensors (device-side ingest; the oracle's
+    rebuilds then finish at the caller's poll)."""
     from suffixgpu_amd import SuffixGPUDrafter
     steps = 70
     lp = synth.decode_loop(seed=5, b=256, s=16384, steps=steps)
@@ -252,7 +255,8 @@ def test_c5_decode_loop_matches_oracle(gpu):
     d = SuffixGPUDrafter(device=gpu, rebuild_stream=side, **kw)
     gi = d.global_index
     gi.blocking_poll = True
-    o = DrafterOracle(async_rebuild=True, **kw)
+    o = DrafterOracle(async_rebuild=True, finish_at_user_poll=device_harvest,
+                      **kw)
     tok = T(lp.tokens, gpu)
     nt = T(lp.num_tokens, gpu)
     samp_all = T(lp.sampled, gpu)
@@ -282,21 +286,25 @@ def test_c5_decode_loop_matches_oracle(gpu):
         np.testing.assert_array_equal(N(out[2]), enew, err_msg=f"step {i}")
         ont = enew
         hv = lp.harvests.get(i)
+        before = gi.active_len
         if hv is not None:
             rows, lengths, new_rows, new_q = hv
-            before = gi.active_len
-            d.harvest_finished(rows, lengths, tok)
-            o.harvest_finished(rows, lengths, to)
             idx = torch.tensor(rows, dtype=torch.int64, device=gpu)
+            if device_harvest:
+                d.harvest_finished(idx, T(np.asarray(lengths), gpu), tok)
+            else:
+                d.harvest_finished(rows, lengths, tok)
+            o.harvest_finished(rows, lengths, to)
             tok.index_copy_(0, idx, T(new_rows, gpu))
             nt.index_copy_(0, idx, T(new_q, gpu))
             to[rows] = new_rows
             ont = ont.copy()
             ont[rows] = new_q
-            swaps += int(gi.active_len != before)
         d.poll()
         o.poll()
+        swaps += int(gi.active_len != before)
         if hv is not None:
             torch.cuda.synchronize()
+            gi.sync_host_state()
             index_equal(gi, o.global_index)
     assert swaps >= 1 and gi.active_len > 0
