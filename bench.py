@@ -955,10 +955,13 @@ PMC_STEP_LAUNCHES = 10
 PMC_SA_BUILDS = 2
 # kernels of one suffix-array build (csrc/sa_build.hip)
 SA_BUILD_KERNELS = ("k_sa_", "k_rs_", "k_grp_")
+# what a rebuild adds after the suffix array: key rows, n-gram table
+TABLE_KERNELS = ("k_rank_keys", "k_gram_")
 
 
 def pmc_workload(d, w, dev) -> int:
     import torch
+    from suffixgpu_amd import _lib
     src = torch.randint(0, 1 << 30, (PMC_COPY_ELEMS,), dtype=torch.int32,
                         device=dev)
     dst = torch.empty_like(src)
@@ -988,16 +991,30 @@ def pmc_workload(d, w, dev) -> int:
     build_suffix_array_rounds(text, m, out, ws, 40)
     torch.cuda.synchronize()
     final, needed = build_state(ws, m)
+    from suffixgpu_amd.global_index import KEY_WIDTH, gram_slots_for
+    L = _lib.lib()
+    keys = torch.empty(CAPACITY * KEY_WIDTH, dtype=torch.int32, device=dev)
+    slots = gram_slots_for(CAPACITY)
+    gram = torch.zeros(int(L.sfx_gram_table_bytes(slots)), dtype=torch.uint8,
+                       device=dev)
+    st = _lib.stream_of(dev)
     for _ in range(PMC_SA_BUILDS):
         build_suffix_array_rounds(text, m, out, ws, needed + 2)
+        # the key rows and n-gram table the index builds after it
+        _lib.check(L.sfx_sa_keys(text.data_ptr(), out.data_ptr(), CAPACITY,
+                                 m, KEY_WIDTH, keys.data_ptr(), st), "keys")
+        _lib.check(L.sfx_gram_build(keys.data_ptr(), KEY_WIDTH, m,
+                                    gram.data_ptr(), slots, st), "gram")
     torch.cuda.synchronize()
+    del keys, gram
     c5d, c5t, c5n, c5s = c5_local(dev)
     for _ in range(PMC_STEP_LAUNCHES):
         c5d.propose_with_update(c5n, c5t, c5s)
     torch.cuda.synchronize()
     log(f"pmc workload done: 3 calibration copies of {PMC_COPY_ELEMS * 4} "
         f"bytes, {PMC_STEP_LAUNCHES} step launches, {PMC_SA_BUILDS} SA "
-        f"rebuilds of m={m} ({needed + 2} rounds)")
+        f"rebuilds of m={m} ({needed + 2} rounds) with key rows and "
+        "n-gram table")
     return 0
 
 
@@ -1163,11 +1180,15 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> dict:
         # SA builds in dispatch order, each starting with k_sa_range; the
         # last PMC_SA_BUILDS are the rebuilds as the index runs them
         builds: list[list[float]] = []
+        tables: list[list[float]] = []
         for k, v in rows:
             if "k_sa_range" in k:
                 builds.append([])
+                tables.append([])
             if builds and any(p in k for p in SA_BUILD_KERNELS):
                 builds[-1].append(v)
+            if tables and any(p in k for p in TABLE_KERNELS):
+                tables[-1].append(v)
         if not cal or not step or len(builds) < PMC_SA_BUILDS:
             raise SystemExit(f"{counter}: calibration, k_step or SA build "
                              "dispatches missing")
@@ -1177,17 +1198,23 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> dict:
         sa_b = statistics.mean(
             sum(b) for b in builds[-PMC_SA_BUILDS:]) * 1024.0
         c5_b = statistics.mean(c5) * 1024.0 if c5 else 0.0
+        tab_b = statistics.mean(
+            sum(b) for b in tables[-PMC_SA_BUILDS:]) * 1024.0
         out[name] = {"counter": counter, "calibration_bytes": cal_b,
                      "scale": scale, "step_raw_bytes": step_b,
                      "step_bytes": step_b * scale,
                      "dispatches": len(step),
                      "sa_build_bytes": sa_b * scale,
                      "c5_local_dispatches": len(c5),
-                     "c5_local_bytes": c5_b * scale}
+                     "c5_local_bytes": c5_b * scale,
+                     "rebuild_tables_bytes": tab_b * scale}
     total = out["fetch"]["step_bytes"] + out["write"]["step_bytes"]
     sa_total = out["fetch"]["sa_build_bytes"] + out["write"]["sa_build_bytes"]
     c5_total = out["fetch"]["c5_local_bytes"] + out["write"]["c5_local_bytes"]
+    tab_total = (out["fetch"]["rebuild_tables_bytes"]
+                 + out["write"]["rebuild_tables_bytes"])
     return {"k_step": round(total), "sa_rebuild": round(sa_total),
+            "rebuild_tables": round(tab_total),
             "k_step_c5_local": round(c5_total) or None, "detail": out}
 
 
