@@ -150,6 +150,7 @@ def time_sa_builds(w, dev, side):
     from suffixgpu_amd.suffix_array import (build_state,
                                             build_suffix_array_into,
                                             build_suffix_array_rounds,
+                                            read_build_state,
                                             sa_workspace_bytes)
     flat = np.concatenate([np.append(x, -2) for x in w.active_docs]).astype(
         np.int32)
@@ -181,10 +182,11 @@ def time_sa_builds(w, dev, side):
         build_ms[name] = (min(times), mm)
         log(f"SA build {name}: m={mm} {min(times):.2f} ms")
         # As the index's background rebuild runs it at steady state: the
-        # rounds the previous build needed plus a margin of 2, then the
-        # output (the device confirms the array is final).
-        final, needed = build_state(ws, mm)
-        rounds = needed + 2
+        # rounds the previous build needed plus a margin of 2, with the
+        # radix path for the rounds that took it, then the output (the
+        # device confirms the array is final).
+        prev = read_build_state(ws, mm)
+        final, rounds, radix = prev.done, prev.needed + 2, prev.radix_mask & ~1
         times = []
         for rep in range(3):
             torch.cuda.synchronize()
@@ -193,7 +195,7 @@ def time_sa_builds(w, dev, side):
             e1 = torch.cuda.Event(enable_timing=True)
             with torch.cuda.stream(side):
                 e0.record(side)
-                build_suffix_array_rounds(text, mm, out, ws, rounds)
+                build_suffix_array_rounds(text, mm, out, ws, rounds, radix)
                 e1.record(side)
             e1.synchronize()
             times.append(e0.elapsed_time(e1))
@@ -201,6 +203,7 @@ def time_sa_builds(w, dev, side):
         if not (final and ok):
             raise RuntimeError("SA build: hinted rounds did not finish")
         build_ms[name + "_hinted"] = (min(times), rounds)
+        build_ms[name + "_radix"] = radix
         log(f"SA rebuild {name} ({rounds} rounds, as the index runs it): "
             f"{min(times):.2f} ms")
         if name == "corpus":
@@ -364,7 +367,8 @@ def main() -> int:
 
     copy_gbps = copy_peak_gbps(dev)
     cold_p50 = cold_step_p50(graph, dev)
-    conc = concurrent_rebuild(graph, w, dev, build_ms["corpus_hinted"][1])
+    conc = concurrent_rebuild(graph, w, dev, build_ms["corpus_hinted"][1],
+                              build_ms["corpus_radix"])
     log(f"copy peak {copy_gbps:.0f} GB/s; cold-cache step p50 "
         f"{cold_p50:.2f} us; rebuild during replays: {conc}")
     c5 = c5_local_step(dev, args.kernel_reps)
@@ -526,9 +530,10 @@ def cold_step_p50(graph, dev, reps: int = 40) -> float:
     return statistics.median(per)
 
 
-def concurrent_rebuild(graph, w, dev, rounds: int) -> dict:
+def concurrent_rebuild(graph, w, dev, rounds: int, radix: int) -> dict:
     """A 4.19M-token SA rebuild (as the index's background rebuild runs
-    it: ``rounds`` doubling rounds) enqueued on a side stream while the
+    it: ``rounds`` doubling rounds, the radix path for those in the mask
+    ``radix``) enqueued on a side stream while the
     captured step replays on the main stream: build time, decode steps
     completed before the build's end event, and the step p50 meanwhile."""
     import torch
@@ -554,7 +559,7 @@ def concurrent_rebuild(graph, w, dev, rounds: int) -> dict:
     b1 = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(side):
         b0.record(side)
-        build_suffix_array_rounds(text, m, out, ws, rounds)
+        build_suffix_array_rounds(text, m, out, ws, rounds, radix)
         b1.record(side)
     ends = []
     starts = []
@@ -977,8 +982,8 @@ def pmc_workload(d, w, dev) -> int:
     for _ in range(PMC_STEP_LAUNCHES):
         d.propose_with_update(nt, buf, sampled)
     torch.cuda.synchronize()
-    from suffixgpu_amd.suffix_array import (build_state,
-                                            build_suffix_array_rounds,
+    from suffixgpu_amd.suffix_array import (build_suffix_array_rounds,
+                                            read_build_state,
                                             sa_workspace_bytes)
     flat = np.concatenate([np.append(x, -2) for x in w.active_docs]).astype(
         np.int32)
@@ -990,7 +995,8 @@ def pmc_workload(d, w, dev) -> int:
                      device=dev)
     build_suffix_array_rounds(text, m, out, ws, 40)
     torch.cuda.synchronize()
-    final, needed = build_state(ws, m)
+    prev = read_build_state(ws, m)
+    needed, radix = prev.needed, prev.radix_mask & ~1
     from suffixgpu_amd.global_index import KEY_WIDTH, gram_slots_for
     L = _lib.lib()
     keys = torch.empty(CAPACITY * KEY_WIDTH, dtype=torch.int32, device=dev)
@@ -999,7 +1005,7 @@ def pmc_workload(d, w, dev) -> int:
                        device=dev)
     st = _lib.stream_of(dev)
     for _ in range(PMC_SA_BUILDS):
-        build_suffix_array_rounds(text, m, out, ws, needed + 2)
+        build_suffix_array_rounds(text, m, out, ws, needed + 2, radix)
         # the key rows and n-gram table the index builds after it
         _lib.check(L.sfx_sa_keys(text.data_ptr(), out.data_ptr(), CAPACITY,
                                  m, KEY_WIDTH, keys.data_ptr(), st), "keys")

@@ -32,7 +32,7 @@ extern "C" {
 
 #define SFX_EINVAL (-1)
 #define SFX_MAX_CANDIDATES 32
-#define SFX_ABI_VERSION 10
+#define SFX_ABI_VERSION 11
 
 /* Drafter configuration shared by the local and global paths.
  * Mirrors the constructor arguments of SuffixGPUDrafter
@@ -231,10 +231,11 @@ int sfx_propose_step_noalloc(const sfx_params* p, const sfx_index* index,
  *      global_index.py:217-223) ------------------------------------------ */
 
 /* sa[0:m] = suffix array of text[0:m] (signed int32 order, a proper prefix
- * first); sa[m:n_total] = m .. n_total-1.  Prefix doubling with LSD radix
- * sorts; each round re-sorts only the suffixes whose group is not yet a
- * singleton, and the rounds stop on the device once none is left, with no
- * host synchronisation.  sa_is64 selects int64 output. */
+ * first); sa[m:n_total] = m .. n_total-1.  Prefix doubling: each round
+ * re-sorts only the suffixes whose group is not yet a singleton (inside a
+ * workgroup for a group of at most 2048, by LSD radix sorts for a larger
+ * one), and the rounds stop on the device once none is left, with no host
+ * synchronisation.  sa_is64 selects int64 output. */
 size_t sfx_sa_build_workspace_size(int64_t m);
 
 /* keys[r * width + j] = j-th token of the suffix at sa[r] (corpus reads at
@@ -268,19 +269,32 @@ int sfx_gram_build(const int32_t* keys, int64_t key_width, int64_t m,
  * counterpart; global_index.py:201-252 runs the build as one call):
  *   begin  -- the token round;
  *   rounds -- doubling rounds first .. first+count-1 (round r doubles
- *             h = 2^(r-1); rounds past sfx_sa_build_rounds_total(m) are
- *             skipped; a round after the array is final returns at once);
+ *             h = h0 * 2^(r-1); rounds past sfx_sa_build_rounds_total(m)
+ *             are skipped; a round after the array is final returns at
+ *             once).  A round sorts its unsorted groups of at most
+ *             sfx_sa_group_cap() suffixes inside workgroups (one launch)
+ *             and its larger groups by radix launches, which are
+ *             enqueued only when global_path is 1.  With global_path 0 a
+ *             round that has a larger group marks the build stalled at
+ *             that round and every later launch returns; enqueueing
+ *             rounds again from the stalled round with global_path 1
+ *             resumes the build;
  *   finish -- sa[0:m] from the workspace, sa[m:n_total] the identity.
- * The workspace's u32 state block at sfx_sa_build_flag_offset(m) holds
- * [0] nonzero once the array is final and [2] the h of the round that
- * found it final, for an asynchronous copy to the host. */
+ * The workspace's u32 state block at sfx_sa_build_flag_offset(m) (64
+ * bytes to copy) holds [0] nonzero once the array is final, [2] the round
+ * that found it final, [7] the round the build stalled at (0: none) and
+ * [8] a mask with bit r set for every round r that ran radix launches,
+ * for an asynchronous copy to the host.  sfx_sa_build enqueues the radix
+ * launches for every round. */
 int sfx_sa_build_rounds_total(int64_t m);
 int64_t sfx_sa_build_flag_offset(int64_t m);
+/* The largest group a round sorts inside a workgroup (2048). */
+int sfx_sa_group_cap(void);
 int sfx_sa_build_begin(const int32_t* text, int64_t m, void* workspace,
                        size_t workspace_bytes, hipStream_t stream);
 int sfx_sa_build_rounds(int64_t m, int32_t first, int32_t count,
-                        void* workspace, size_t workspace_bytes,
-                        hipStream_t stream);
+                        int32_t global_path, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream);
 int sfx_sa_build_finish(int64_t m, int64_t n_total, void* sa, int32_t sa_is64,
                         void* workspace, size_t workspace_bytes,
                         hipStream_t stream);

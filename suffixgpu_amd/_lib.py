@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsuffixgpu_amd.so"
 MAX_CANDIDATES = 32
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -74,8 +74,9 @@ SIGNATURES = {
     "sfx_abi_version": (c_i32, []),
     "sfx_sa_build_rounds_total": (c_i32, [c_i64]),
     "sfx_sa_build_flag_offset": (c_i64, [c_i64]),
+    "sfx_sa_group_cap": (c_i32, []),
     "sfx_sa_build_begin": (c_i32, [c_p, c_i64, c_p, ctypes.c_size_t, c_p]),
-    "sfx_sa_build_rounds": (c_i32, [c_i64, c_i32, c_i32, c_p,
+    "sfx_sa_build_rounds": (c_i32, [c_i64, c_i32, c_i32, c_i32, c_p,
                                     ctypes.c_size_t, c_p]),
     "sfx_sa_build_finish": (c_i32, [c_i64, c_i64, c_p, c_i32, c_p,
                                     ctypes.c_size_t, c_p]),

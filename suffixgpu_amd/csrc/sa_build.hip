@@ -1,25 +1,38 @@
-// Suffix-array construction on the GPU: prefix doubling over LSD radix
-// sorts of the still-unsorted suffixes only, with no host synchronisation.
+// Suffix-array construction on the GPU: prefix doubling with no host
+// synchronisation, as suffix_gpu/suffix_array.py:15-63 specifies it (a
+// proper prefix sorts first), on state kept per SA position.
 //
 // Round 0 sorts all positions by their first two tokens when the text's
 // tokens span fewer than 2^18 values (every LLM vocabulary; found on the
 // device, so the doubling then starts at h = 2), else by their first token
-// (signed order) -- 4 passes of 9 bits either way.  Every later round
-// h = h0, 2 h0, 4 h0, ... re-sorts only the suffixes whose group still has
-// more than one member, by the key
-// (group head, rank[i+h]+1 or 0) -- a proper prefix sorts first, as in
-// suffix_gpu/suffix_array.py:15-63 -- and writes them back into the SA
-// positions their groups occupy, in order.  rank[i] is the SA position of
-// the first suffix of i's group (for a finished suffix, its final
-// position).  When no group of two or more is left the device sets a done
-// flag and every later launch returns at its first instruction, so the
-// fixed launch sequence (capturable, no host reads) is safe for any input.
+// (signed order) -- 4 LSD radix passes of 9 bits either way.  Round
+// r = 1, 2, ... doubles h = h0 << (r - 1): every group of two or more
+// suffixes that agree on their first h tokens (a run of SA positions) is
+// re-sorted by rank[i + h] + 1 (0 past the end), where rank[i] is the SA
+// position of the first suffix of i's group (for a finished suffix, its
+// final position).  Per SA position p the state holds sa[p], gp[p] (the
+// head position of p's group, or a finished mark) and, at a head, gsz[]
+// (the group's size); rank[] has two buffers, read and written by
+// alternate rounds, so that no round reads a rank the same round changes.
 //
-// A round works on its active list: the still-unsorted suffixes in SA
-// order, (key, suffix, SA position) per entry.  The round's last kernel
-// marks every entry whose new group is a singleton and counts the others
-// per tile; the next round's gather compacts the rest of the list into the
-// next list, so no round rescans the m SA positions.
+// A round sorts each group by one of two means, chosen per group on the
+// device from its size:
+//  * groups of at most kCap suffixes: one launch for the round.  A
+//    workgroup owns the groups whose head lies in its 4096-position tile
+//    (a group that started in the tile before is skipped, skip[] holding
+//    its length; one that runs on into the next tile is followed), sorts
+//    each of them by its keys in LDS (a 64-lane bitonic sort per
+//    64-position window, then a binary search in every other window of the
+//    group) and writes the new order, heads and sizes back;
+//  * groups above kCap (the radix part): their positions are compacted
+//    into a list keyed (head, rank[i + h] + 1) in SA order, LSD radix
+//    sorted, and the group heads of the sorted list are written back.
+// A round with a group above kCap whose radix launches the caller did not
+// enqueue only marks itself stalled: every later launch returns at once,
+// and a caller that enqueues the round again with the radix part resumes
+// it.  When no group of two or more is left the device sets a done flag
+// and every later launch returns at its first instruction, so a fixed
+// launch sequence (capturable, no host reads) is safe for any input.
 //
 // Each LSD pass is histogram (per 4096-element tile) -> per-digit row scan
 // across tiles -> stable scatter.  The scatter ranks equal digits inside a
@@ -31,40 +44,54 @@
 
 namespace sfx {
 
-constexpr int kTile = 4096;  // list entries per tile (one block per tile)
+constexpr int kTile = 4096;     // list entries / SA positions per radix tile
+constexpr int kPosTile = 4096;  // SA positions per local-round tile
+constexpr int kCap = 2048;      // largest group the local part sorts
+constexpr int kSlots = kPosTile + kCap;  // positions a local workgroup reads
+// One 1024-thread workgroup per CU measured faster than 2 x 512 threads or
+// 2048-position tiles: fewer windows per wave, and one barrier pair per
+// 4096 positions.
+constexpr int kLocalThreads = 1024;
 constexpr int kDigitBits = 9;
 constexpr int kRadix = 1 << kDigitBits;                 // 512
-constexpr uint32_t kFinished = 0xffffffffu;  // hd[] of a singleton entry
-// state[] words: [0] done, [1] / [6] list length of even / odd rounds,
-// [2] round that found none left, [3] / [4] least / largest token other
-// than PAD (INT32_MAX), [5] h of round 1.
-constexpr int kDone = 0, kLenEven = 1, kFoundNone = 2, kTokLo = 3,
-              kTokHi = 4, kH0 = 5, kLenOdd = 6;
-__host__ __device__ constexpr int len_slot(int round) {
-  return (round & 1) ? kLenOdd : kLenEven;
-}
+constexpr uint32_t kFinished = 0xffffffffu;  // gp[] of a finished position
+// gp[] of a position finished by the previous round: its final rank is in
+// that round's rank buffer only, and the next round copies it to the other
+constexpr uint32_t kJustFinished = 0xfffffffeu;
+// state[] words: [0] done, [1] global list length, [2] round that found no
+// group left, [3] / [4] least / largest token other than PAD (INT32_MAX),
+// [5] h of round 1, [7] round that stalled (0: none), [8] bit r set when
+// round r took the global path, [16 + r] largest group entering round r.
+constexpr int kDone = 0, kLen = 1, kFoundNone = 2, kTokLo = 3, kTokHi = 4,
+              kH0 = 5, kStalled = 7, kGlobalMask = 8, kMaxGrp = 16;
+constexpr int kStateWords = 64;
+static_assert(kMaxGrp + 33 <= kStateWords, "a round word per doubling");
+static_assert(kCap <= kPosTile, "a group spans at most two tiles");
 
 struct SaWs {
   uint64_t* keyA;
   uint64_t* keyB;
   uint32_t* valA;
   uint32_t* valB;
-  uint32_t* pos[2];  // SA positions of the list entries (ascending) of
-                     // even / odd rounds
-  uint32_t* rank;    // [m] group head of text position i
-  uint32_t* sa;      // [m] current suffix order
-  uint32_t* hd;      // [list] group head of a sorted entry, kFinished for a
-                     // singleton
-  uint32_t* hist;    // [512][NB] digit counts per tile, then offsets
-  uint32_t* rowsum;  // [512] digit totals
-  uint32_t* tcnt;    // [NB] unfinished entries per tile of the sorted list
-  uint32_t* blkmax;  // [NB] last group start per tile
-  uint32_t* state;   // the state[] words above
+  uint32_t* pos;      // SA positions of the global list (ascending)
+  uint32_t* rank[2];  // [m] group head of text position i; round r reads
+                      // rank[r & 1] and writes rank[(r + 1) & 1]
+  uint32_t* sa;       // [m] current suffix order
+  uint32_t* gp;       // [m] group head of SA position p, or a finished mark
+  uint32_t* gsz;      // [m] size of the group headed at p
+  uint32_t* hist;     // [512][NB] digit counts per tile, then offsets
+  uint32_t* rowsum;   // [512] digit totals
+  uint32_t* tcnt;     // [NB] unfinished positions per tile
+  uint32_t* blkmax;   // [NB] last group start per tile
+  uint32_t* skip[2];  // [NL + 1] leading positions of a local tile owned
+                      // by the tile before; round r reads skip[r & 1]
+  uint32_t* state;    // the state[] words above
 };
 
 static size_t sa_ws_layout(int64_t n, void* base, SaWs* w) {
   const size_t N = (size_t)(n > 0 ? n : 1);
   const size_t NB = (N + kTile - 1) / kTile;
+  const size_t NL = (N + kPosTile - 1) / kPosTile;
   size_t off = 0;
   char* c = (char*)base;
   auto take = [&](size_t bytes) -> void* {
@@ -77,22 +104,33 @@ static size_t sa_ws_layout(int64_t n, void* base, SaWs* w) {
   s.keyB = (uint64_t*)take(N * 8);
   s.valA = (uint32_t*)take(N * 4);
   s.valB = (uint32_t*)take(N * 4);
-  s.pos[0] = (uint32_t*)take(N * 4);
-  s.pos[1] = (uint32_t*)take(N * 4);
-  s.rank = (uint32_t*)take(N * 4);
+  s.pos = (uint32_t*)take(N * 4);
+  s.rank[0] = (uint32_t*)take(N * 4);
+  s.rank[1] = (uint32_t*)take(N * 4);
   s.sa = (uint32_t*)take(N * 4);
-  s.hd = (uint32_t*)take(N * 4);
+  s.gp = (uint32_t*)take(N * 4);
+  s.gsz = (uint32_t*)take(N * 4);
   s.hist = (uint32_t*)take((size_t)kRadix * NB * 4);
   s.rowsum = (uint32_t*)take(kRadix * 4);
   s.tcnt = (uint32_t*)take(NB * 4);
   s.blkmax = (uint32_t*)take(NB * 4);
-  s.state = (uint32_t*)take(256);
+  s.skip[0] = (uint32_t*)take((NL + 1) * 4);
+  s.skip[1] = (uint32_t*)take((NL + 1) * 4);
+  s.state = (uint32_t*)take(kStateWords * 4);
   if (w) *w = s;
   return off;
 }
 
 __device__ __forceinline__ int64_t tiles_of(int64_t a) {
   return (a + kTile - 1) / kTile;
+}
+
+// True when round r's radix launches have nothing to do: the array is
+// final, the build stalled, or the round is a local one (round 0 is
+// always a radix round).
+__device__ __forceinline__ bool radix_idle(const uint32_t* state, int round) {
+  return state[kDone] || state[kStalled] ||
+         (round > 0 && state[kMaxGrp + round] <= (uint32_t)kCap);
 }
 
 // Block-wide exclusive scan of one u32 per thread (NT threads); `red`
@@ -175,7 +213,8 @@ __global__ __launch_bounds__(256) void k_sa_init(const int32_t* text,
                                                  uint32_t* val, uint32_t* pos,
                                                  const int32_t* part_lo,
                                                  const int32_t* part_hi,
-                                                 int nparts,
+                                                 int nparts, uint32_t* skip0,
+                                                 uint32_t* skip1, int64_t nl,
                                                  uint32_t* state) {
   __shared__ int32_t red[2][256 / kWave];
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -185,12 +224,19 @@ __global__ __launch_bounds__(256) void k_sa_init(const int32_t* text,
   // thi < tlo: the text is all PAD
   const int64_t span = thi < tlo ? 0 : (int64_t)thi - (int64_t)tlo + 1;
   const bool pairs = span + 2 < ((int64_t)1 << kPairBits);
-  if (i == 0) {
-    state[kDone] = 0;
-    state[len_slot(0)] = (uint32_t)n;
-    state[kTokLo] = (uint32_t)tlo;
-    state[kTokHi] = (uint32_t)thi;
-    state[kH0] = pairs ? 2u : 1u;
+  if (i < kStateWords) {
+    uint32_t v = 0;
+    if (i == kLen) v = (uint32_t)n;
+    if (i == kTokLo) v = (uint32_t)tlo;
+    if (i == kTokHi) v = (uint32_t)thi;
+    if (i == kH0) v = pairs ? 2u : 1u;
+    if (i == kGlobalMask) v = 1u;  // round 0 is a radix round
+    state[i] = v;
+  }
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t e = i; e <= nl; e += stride) {
+    skip0[e] = 0;
+    skip1[e] = 0;
   }
   if (i >= n) return;
   if (pairs) {
@@ -235,11 +281,11 @@ constexpr int kRsHists = 4;  // LDS sub-histograms of the histogram pass
 template <int NT>
 __global__ __launch_bounds__(NT) void k_rs_hist(
     const uint64_t* __restrict__ key, int sh, uint32_t* hist, int64_t nb,
-    const uint32_t* state, int slot) {
+    const uint32_t* state, int round) {
   static_assert(kTile % NT == 0 && NT >= kRadix, "tile shape");
   constexpr int kItems = kTile / NT;
-  if (state[kDone]) return;
-  const int64_t A = state[slot];
+  if (radix_idle(state, round)) return;
+  const int64_t A = state[kLen];
   const int64_t base = (int64_t)blockIdx.x * kTile;
   if (base >= A) return;
   // Waves w, w + kRsHists, ... share a histogram; the sub-histograms are
@@ -284,10 +330,10 @@ __global__ __launch_bounds__(NT) void k_rs_hist(
 template <int NT>
 __global__ __launch_bounds__(NT) void k_rs_rowscan(
     uint32_t* hist, int64_t nb, uint32_t* rowsum, const uint32_t* state,
-    int slot) {
-  if (state[kDone]) return;
+    int round) {
+  if (radix_idle(state, round)) return;
   __shared__ uint32_t red[NT / kWave];
-  const int64_t nbA = tiles_of(state[slot]);
+  const int64_t nbA = tiles_of(state[kLen]);
   uint32_t* row = hist + (int64_t)blockIdx.x * nb;
   uint32_t carry = 0;
   for (int64_t c0 = 0; c0 < nbA; c0 += NT) {
@@ -313,13 +359,13 @@ __global__ __launch_bounds__(NT) void k_rs_scatter(
     const uint64_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint64_t* __restrict__ kout, uint32_t* __restrict__ vout, int sh,
     const uint32_t* __restrict__ hist, int64_t nb,
-    const uint32_t* __restrict__ rowsum, const uint32_t* state, int slot) {
+    const uint32_t* __restrict__ rowsum, const uint32_t* state, int round) {
   constexpr int NW = NT / kWave;
   constexpr int kSpan = kTile / NW;
   constexpr int kSteps = kSpan / kWave;
   static_assert(kTile % NT == 0 && NT >= kRadix, "tile shape");
-  if (state[kDone]) return;
-  const int64_t A = state[slot];
+  if (radix_idle(state, round)) return;
+  const int64_t A = state[kLen];
   const int64_t base = (int64_t)blockIdx.x * kTile;
   if (base >= A) return;
   __shared__ uint32_t woff[NW][kRadix];
@@ -394,11 +440,11 @@ __device__ __forceinline__ bool starts_group(const uint64_t* key, int64_t t,
 template <int NT>
 __global__ __launch_bounds__(NT) void k_grp_reduce(
     const uint64_t* __restrict__ key, const uint32_t* __restrict__ pos,
-    uint32_t* blkmax, const uint32_t* state, int slot) {
+    uint32_t* blkmax, const uint32_t* state, int round) {
   constexpr int NW = NT / kWave;
   constexpr int kSpan = kTile / NW;
-  if (state[kDone]) return;
-  const int64_t A = state[slot];
+  if (radix_idle(state, round)) return;
+  const int64_t A = state[kLen];
   const int64_t base = (int64_t)blockIdx.x * kTile;
   if (base >= A) return;
   __shared__ uint32_t smax[NW];
@@ -424,28 +470,33 @@ __global__ __launch_bounds__(NT) void k_grp_reduce(
   }
 }
 
-// rank[val[t]] = head, sa[pos[t]] = val[t]; hd[t] = head, or kFinished
-// when t's group is the singleton {t}; tcnt[tile] = the tile's entries
-// that are not finished.  The group start carried into a tile is the
-// largest start of all earlier tiles: each block reduces blkmax[0 .. tile)
-// itself.
+// Over the sorted list of round r: rank_next[val[t]] = head,
+// sa[pos[t]] = val[t], gp[pos[t]] = head, or kJustFinished when t's group
+// is the singleton {t}; at the last entry of a larger group its size goes
+// to gsz[head] and to the round's largest-group word, and a group that
+// runs from one local tile into the next sets the skip_next[] word of the
+// tile its last entry lies in (the round's local launch, which precedes
+// this one, cleared it).  The group start carried into a tile is the
+// largest start of all earlier tiles: each block reduces
+// blkmax[0 .. tile) itself.
 template <int NT>
 __global__ __launch_bounds__(NT) void k_grp_rank(
     const uint64_t* __restrict__ key, const uint32_t* __restrict__ val,
     const uint32_t* __restrict__ pos, const uint32_t* __restrict__ blkmax,
-    uint32_t* __restrict__ rank, uint32_t* __restrict__ sa,
-    uint32_t* __restrict__ hd, uint32_t* __restrict__ tcnt,
-    const uint32_t* state, int slot) {
+    uint32_t* __restrict__ rank_next, uint32_t* __restrict__ sa,
+    uint32_t* __restrict__ gp, uint32_t* __restrict__ gsz,
+    uint32_t* __restrict__ skip_next, uint32_t* state, int round) {
   constexpr int NW = NT / kWave;
   constexpr int kSpan = kTile / NW;
   constexpr int kSteps = kSpan / kWave;
-  if (state[kDone]) return;
-  const int64_t A = state[slot];
+  static_assert(kSteps <= 32, "per-entry bits in one word");
+  if (radix_idle(state, round)) return;
+  const int64_t A = state[kLen];
   const int64_t base = (int64_t)blockIdx.x * kTile;
   if (base >= A) return;
   __shared__ uint32_t smax[NW];
   __shared__ uint32_t cred[NW];
-  __shared__ uint32_t ucnt[NW];
+  __shared__ uint32_t gmax[NW];
   uint32_t cm = 0;
   for (int t = threadIdx.x; t < (int)blockIdx.x; t += NT)
     cm = max(cm, blkmax[t]);
@@ -456,6 +507,7 @@ __global__ __launch_bounds__(NT) void k_grp_rank(
   const int64_t wbase = base + (int64_t)wv * kSpan;
   uint32_t st[kSteps];  // start position of a group beginning here, or 0
   uint32_t single = 0;  // bit s: entry s is a group of its own
+  uint32_t lastb = 0;   // bit s: entry s ends its group
   uint32_t mx = 0;
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
@@ -467,6 +519,7 @@ __global__ __launch_bounds__(NT) void k_grp_rank(
       const bool last = t + 1 == A || key[t + 1] != kt;
       if (first) st[s] = pos[t];
       single |= (uint32_t)(first && last) << s;
+      lastb |= (uint32_t)last << s;
     }
     mx = max(mx, st[s]);
   }
@@ -476,70 +529,98 @@ __global__ __launch_bounds__(NT) void k_grp_rank(
   uint32_t run = 0;
   for (int w = 0; w < NW; ++w) run = max(run, cred[w]);
   for (int w = 0; w < wv; ++w) run = max(run, smax[w]);
-  uint32_t open = 0;
+  uint32_t big = 0;  // largest group ending in this lane's entries
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
     const int64_t t = wbase + s * kWave + ln;
     const uint32_t head = max(run, wave_incl_max(st[s]));
     run = max(run, (uint32_t)__builtin_amdgcn_readlane((int)head, kWave - 1));
     const bool fin = (single >> s) & 1u;
-    open += (uint32_t)popc(ballot(t < A && !fin));
     if (t < A) {
       const uint32_t i = val[t];
-      rank[i] = head;
-      sa[pos[t]] = i;
-      hd[t] = fin ? kFinished : head;
+      const uint32_t p = pos[t];
+      rank_next[i] = head;
+      sa[p] = i;
+      gp[p] = fin ? kJustFinished : head;
+      if (((lastb >> s) & 1u) && !fin) {
+        const uint32_t size = p - head + 1;
+        gsz[head] = size;
+        big = max(big, size);
+        const uint32_t c = p / kPosTile;
+        if (head / kPosTile < c) skip_next[c] = p + 1 - c * kPosTile;
+      }
     }
   }
-  if (ln == 0) ucnt[wv] = open;
+  big = (uint32_t)wave_max_i32((int)big);
+  if (ln == 0) gmax[wv] = big;
   __syncthreads();
   if (threadIdx.x == 0) {
-    uint32_t c = 0;
-    for (int w = 0; w < NW; ++w) c += ucnt[w];
-    tcnt[blockIdx.x] = c;
+    uint32_t g = 0;
+    for (int w = 0; w < NW; ++w) g = max(g, gmax[w]);
+    if (g) atomicMax(&state[kMaxGrp + round + 1], g);
   }
 }
 
-// ------------------------------------------------------ active suffixes
-// Round r's list: the unfinished entries of round r-1's sorted list (hd,
-// vold, pold; length in state[cin]) in the same SA order, keyed
-// head * (m + 1) + (rank[i + h] + 1, or 0 past the end), where round r
-// doubles h = state[kH0] << (r - 1).  Each block sums the earlier tiles'
-// counts for its output offset; block 0 also sums them all: that is the
-// new length (state[cout]), and none left means the array is final (the
-// done flag).
+// ------------------------------------------------------- radix part
+// The suffixes of a round's groups of more than kCap.  k_pos_count: per
+// tile of SA positions, how many lie in such a group (tcnt[]).  It runs
+// after the round's local launch, which changed only groups of at most
+// kCap.
+__device__ __forceinline__ bool in_big_group(const uint32_t* gsz, uint32_t g) {
+  return g < kJustFinished && gsz[g] > (uint32_t)kCap;
+}
+
 template <int NT>
-__global__ __launch_bounds__(NT) void k_sa_gather(
-    const uint32_t* __restrict__ hd, const uint32_t* __restrict__ vold,
-    const uint32_t* __restrict__ pold, const uint32_t* __restrict__ rank,
-    const uint32_t* __restrict__ tcnt, int64_t m, int round,
-    uint64_t* __restrict__ key, uint32_t* __restrict__ val,
-    uint32_t* __restrict__ pos, uint32_t* state, int cin, int cout) {
+__global__ __launch_bounds__(NT) void k_pos_count(
+    const uint32_t* __restrict__ gp, const uint32_t* __restrict__ gsz,
+    uint32_t* __restrict__ tcnt, int64_t m, const uint32_t* state,
+    int round) {
+  if (radix_idle(state, round)) return;
+  __shared__ uint32_t red[NT / kWave];
+  const int64_t base = (int64_t)blockIdx.x * kTile;
+  uint32_t c = 0;
+#pragma unroll
+  for (int s = 0; s < kTile / NT; ++s) {
+    const int64_t p = base + s * NT + threadIdx.x;
+    if (p < m) c += in_big_group(gsz, gp[p]);
+  }
+  uint32_t tot;
+  block_exscan1<NT>(c, red, &tot);
+  if (threadIdx.x == 0) tcnt[blockIdx.x] = tot;
+}
+
+// The round's list: the SA positions of its groups of more than kCap in
+// order, keyed head * (m + 1) + (rank[i + h] + 1, or 0 past the end) with
+// i = sa[p].
+// Each block sums the earlier tiles' counts for its output offset; block 0
+// also sums them all: the list length (state[kLen]).
+template <int NT>
+__global__ __launch_bounds__(NT) void k_pos_gather(
+    const uint32_t* __restrict__ gp, const uint32_t* __restrict__ gsz,
+    const uint32_t* __restrict__ sa,
+    const uint32_t* __restrict__ rank_cur, const uint32_t* __restrict__ tcnt,
+    int64_t m, int64_t nb, int round, uint64_t* __restrict__ key,
+    uint32_t* __restrict__ val, uint32_t* __restrict__ pos,
+    uint32_t* state) {
   constexpr int NW = NT / kWave;
   constexpr int kSpan = kTile / NW;
   constexpr int kSteps = kSpan / kWave;
-  if (state[kDone]) return;
-  const int64_t Aold = state[cin];
-  const int64_t base = (int64_t)blockIdx.x * kTile;
-  if (blockIdx.x > 0 && base >= Aold) return;  // block 0 writes the length
+  if (radix_idle(state, round)) return;
   const int64_t h = (int64_t)state[kH0] << (round - 1);
+  const int64_t base = (int64_t)blockIdx.x * kTile;
   __shared__ uint32_t scnt[NW];
   __shared__ uint32_t ored[NW];
   {
-    const int64_t upto = blockIdx.x == 0 ? tiles_of(Aold) : (int64_t)blockIdx.x;
+    const int64_t upto = blockIdx.x == 0 ? nb : (int64_t)blockIdx.x;
     uint32_t c = 0;
     for (int64_t t = threadIdx.x; t < upto; t += NT) c += tcnt[t];
     uint32_t tot;
     block_exscan1<NT>(c, ored, &tot);
     if (blockIdx.x == 0) {
       if (threadIdx.x == 0) {
-        state[cout] = tot;
-        if (tot == 0) {
-          state[kDone] = 1;
-          state[kFoundNone] = (uint32_t)round;
-        }
+        state[kLen] = tot;
+        state[kGlobalMask] |= 1u << round;
       }
-      if (tot == 0) return;
       ored[0] = 0;  // block 0's own offset (the barrier below publishes it)
     } else if (threadIdx.x == 0) {
       ored[0] = tot;
@@ -548,13 +629,14 @@ __global__ __launch_bounds__(NT) void k_sa_gather(
   const int wv = threadIdx.x / kWave;
   const int ln = lane_id();
   const int64_t wbase = base + (int64_t)wv * kSpan;
-  uint32_t hv[kSteps];
+  uint32_t gv[kSteps];
   uint32_t cnt = 0;
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
-    const int64_t t = wbase + s * kWave + ln;
-    hv[s] = t < Aold ? hd[t] : kFinished;
-    cnt += (uint32_t)popc(ballot(hv[s] != kFinished));
+    const int64_t p = wbase + s * kWave + ln;
+    gv[s] = p < m ? gp[p] : kFinished;
+    if (!in_big_group(gsz, gv[s])) gv[s] = kFinished;
+    cnt += (uint32_t)popc(ballot(gv[s] != kFinished));
   }
   if (ln == 0) scnt[wv] = cnt;
   __syncthreads();
@@ -563,19 +645,286 @@ __global__ __launch_bounds__(NT) void k_sa_gather(
   const uint64_t M1 = (uint64_t)m + 1;
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
-    const int64_t t = wbase + s * kWave + ln;
-    const bool a = hv[s] != kFinished;
+    const int64_t p = wbase + s * kWave + ln;
+    const bool a = gv[s] != kFinished;
     const uint64_t bm = ballot(a);
     if (a) {
       const uint32_t o = out + (uint32_t)rank_lt(bm);
-      const uint32_t i = vold[t];
+      const uint32_t i = sa[p];
       const uint64_t k2 =
-          (int64_t)i + h < m ? (uint64_t)rank[i + h] + 1 : 0;
-      key[o] = (uint64_t)hv[s] * M1 + k2;
+          (int64_t)i + h < m ? (uint64_t)rank_cur[i + h] + 1 : 0;
+      key[o] = (uint64_t)gv[s] * M1 + k2;
       val[o] = i;
-      pos[o] = pold[t];
+      pos[o] = (uint32_t)p;
     }
     out += (uint32_t)popc(bm);
+  }
+}
+
+// -------------------------------------------------------- local rounds
+// Ascending sort of one u64 per lane across the wave (bitonic network).
+__device__ __forceinline__ uint64_t wave_sort_u64(uint64_t v) {
+  const int ln = lane_id();
+#pragma unroll
+  for (int k = 2; k <= kWave; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      const uint32_t ol = (uint32_t)__shfl_xor((int)(uint32_t)v, j);
+      const uint32_t oh = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), j);
+      const uint64_t o = ((uint64_t)oh << 32) | ol;
+      const bool take_min = ((ln & j) == 0) == ((ln & k) == 0);
+      const bool less = v < o;
+      v = (take_min == less) ? v : o;
+    }
+  }
+  return v;
+}
+
+// The value of lane ln - 1 (lane 0: its own) and of lane ln + 1 (lane 63:
+// its own), by DPP wave shifts (wave_shr:1 / wave_shl:1).
+__device__ __forceinline__ uint32_t lane_prev(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x138, 0xf,
+                                               0xf, false);
+}
+__device__ __forceinline__ uint32_t lane_next(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, 0x130, 0xf,
+                                               0xf, false);
+}
+
+__device__ __forceinline__ uint64_t lanes_le(int ln) {
+  return ln == kWave - 1 ? ~0ull : (2ull << ln) - 1;
+}
+
+// Entries of c[0 .. len) (ascending, len <= 64) below key, or at most key
+// when `incl`.
+__device__ __forceinline__ int count_below(const uint32_t* c, int len,
+                                           uint32_t key, bool incl) {
+  int at = 0;
+#pragma unroll
+  for (int step = kWave; step >= 1; step >>= 1) {
+    const int q = at + step;
+    if (q <= len) {
+      const uint32_t v = c[q - 1];
+      if (incl ? v <= key : v < key) at = q;
+    }
+  }
+  return at;
+}
+
+// The local part of a round: the groups of at most kCap suffixes.
+// Workgroup b owns those whose head lies in its kPosTile-position tile b.
+// It reads the tile and the tail of a group running on into the next
+// tile (at most kCap - 1 positions) as slots s = p - ts; window
+// w = slots 64w .. 64w + 63, held by wave w mod NW, lane = slot mod 64.
+// The first skip_cur[b] positions belong to the group that runs in from
+// the tile before; that tile's workgroup rewrites them meanwhile, so they
+// are never read as owned.
+//  1. per slot: gp, then sa where unfinished, then for an owned one its
+//     group size and key rank_cur[i + h] + 1; positions of the tile the
+//     previous round finished get their final rank in rank_next;
+//  2. per window: the lanes of one group form a chunk; one bitonic sort by
+//     (chunk, key, lane) sorts every chunk in place; the sorted keys go to
+//     LDS, and equal-key runs inside the chunk are found by lane masks;
+//  3. per element: counts of keys below / at most its own in every other
+//     chunk of its group (binary search in LDS) give its new position
+//     (ties by old position), its new group's head and its size; it writes
+//     sa, gp, rank_next, and the head writes gsz; skip_next[b + 1] gets
+//     the length of the group running into the next tile, or 0 (the
+//     round's radix part then sets it for a group it sorted).
+// Groups above kCap are left to the round's radix launches; when the
+// caller enqueued none (global_follows == 0) this launch marks the round
+// stalled and does nothing.  A round with no group left sets the done
+// flag.
+template <int NT>
+__global__ __launch_bounds__(NT) void k_sa_local(
+    uint32_t* __restrict__ gp, uint32_t* __restrict__ gsz,
+    uint32_t* __restrict__ sa, const uint32_t* __restrict__ rank_cur,
+    uint32_t* __restrict__ rank_next, const uint32_t* __restrict__ skip_cur,
+    uint32_t* __restrict__ skip_next, int64_t m, int64_t nl, int round,
+    int global_follows, uint32_t* state) {
+  constexpr int NW = NT / kWave;
+  constexpr int kW = kSlots / kWave / NW;  // windows per wave
+  static_assert(kSlots % (kWave * NW) == 0, "windows per wave");
+  if (state[kDone]) return;
+  const uint32_t stalled = state[kStalled];
+  if (stalled != 0 && stalled < (uint32_t)round) return;
+  const uint32_t mg = state[kMaxGrp + round];
+  if (mg == 0) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+      state[kDone] = 1;
+      state[kFoundNone] = (uint32_t)round;
+    }
+    return;
+  }
+  if (mg > (uint32_t)kCap && !global_follows) {
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+      state[kStalled] = (uint32_t)round;
+    return;
+  }
+  // a resumed round clears its stall mark before its radix launches
+  if (stalled != 0 && blockIdx.x == 0 && threadIdx.x == 0)
+    state[kStalled] = 0;
+  __shared__ uint32_t sk[kSlots];  // sorted keys, chunk by chunk
+  __shared__ uint32_t gmax[NW];
+  __shared__ uint32_t skip_out;
+  const int64_t h = (int64_t)state[kH0] << (round - 1);
+  const int64_t b = blockIdx.x;
+  const int64_t ts = b * kPosTile;
+  const int64_t te = min(ts + (int64_t)kPosTile, m);
+  if (threadIdx.x == 0) skip_out = 0;
+  // slots cover [ts, ts + n): the tile and the tail of the group that
+  // runs on into the next tile (its skip word; a run of kCap or more
+  // belongs to a group above kCap, not sorted here)
+  const uint32_t sn = b + 1 < nl ? skip_cur[b + 1] : 0u;
+  const uint32_t ext = sn < (uint32_t)kCap ? sn : 0u;
+  const int n = (int)(min(m, te + (int64_t)ext) - ts);
+  const int wv = threadIdx.x / kWave;
+  const int ln = lane_id();
+
+  // 1. loads: gp, then sa where unfinished, then the group's size and key
+  // The first `skip` positions belong to a group the tile before owns
+  // (its workgroup rewrites them meanwhile): they are not read as ours.
+  const int skip = (int)skip_cur[b];
+  uint32_t g[kW], iv[kW], sz[kW], kv[kW];
+#pragma unroll
+  for (int k = 0; k < kW; ++k) {
+    const int slot = (wv + k * NW) * kWave + ln;
+    g[k] = slot < n && slot >= skip ? gp[ts + slot] : kFinished;
+  }
+#pragma unroll
+  for (int k = 0; k < kW; ++k) {
+    const int slot = (wv + k * NW) * kWave + ln;
+    iv[k] = g[k] != kFinished ? sa[ts + slot] : 0u;
+  }
+#pragma unroll
+  for (int k = 0; k < kW; ++k) {
+    const int slot = (wv + k * NW) * kWave + ln;
+    sz[k] = 0;
+    kv[k] = 0;
+    if (g[k] == kJustFinished && slot < kPosTile) {
+      rank_next[iv[k]] = (uint32_t)(ts + slot);
+      gp[ts + slot] = kFinished;
+    }
+    // owned: a group whose head lies in the tile
+    if (g[k] < kJustFinished && g[k] >= (uint32_t)ts && g[k] < (uint32_t)te) {
+      sz[k] = gsz[g[k]];
+      if ((int64_t)iv[k] + h < m) kv[k] = rank_cur[iv[k] + h] + 1;
+    } else {
+      g[k] = kFinished;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kW; ++k)  // a group above kCap is the radix part's
+    if (sz[k] > (uint32_t)kCap) g[k] = kFinished;
+
+  // 2. per window: sort each chunk; kept for step 3: the suffix now at
+  // the lane (iv), the group's first slot and size (gs: slot | size << 16,
+  // 0xffffffff for no group), the own-chunk counts and the lane the
+  // element came from (own, a byte each)
+  uint32_t gs[kW], own[kW];
+#pragma unroll
+  for (int k = 0; k < kW; ++k) {
+    own[k] = 0;
+    const bool act = g[k] != kFinished;
+    gs[k] = act ? (g[k] - (uint32_t)ts) | (sz[k] << 16) : 0xffffffffu;
+    const int base = (wv + k * NW) * kWave;
+    if (base >= n || ballot(act) == 0) continue;
+    const uint32_t gprev = lane_prev(g[k]);
+    const bool start = ln == 0 || !act || gprev != g[k];
+    const uint64_t starts = ballot(start);
+    const uint64_t le = starts & lanes_le(ln);
+    const int c0 = kWave - 1 - __builtin_clzll(le);
+    const uint64_t after = starts & ~lanes_le(ln);
+    const int c1 = after ? __builtin_ctzll(after) : kWave;
+    uint32_t ke = act ? kv[k] : 0u;
+    int from = ln;  // the lane this lane's element came from
+    // Most groups keep their order (keys equal or already ascending):
+    // the sort runs only for a window with a descent inside a chunk.
+    const uint32_t kin = lane_prev(ke);
+    if (ballot(ln > c0 && kin > ke)) {
+      const uint64_t key64 = ((uint64_t)(popc(le) - 1) << 37) |
+                             ((uint64_t)ke << 6) | (uint64_t)ln;
+      const uint64_t sorted = wave_sort_u64(key64);
+      ke = (uint32_t)(sorted >> 6) & 0x7fffffffu;
+      from = (int)(sorted & (kWave - 1));
+      iv[k] = (uint32_t)__shfl((int)iv[k], from);
+    }
+    sk[base + ln] = ke;
+    const uint32_t kprev = lane_prev(ke);
+    const uint32_t knext = lane_next(ke);
+    const bool eqprev = ln > c0 && kprev == ke;
+    const bool eqnext = ln + 1 < c1 && knext == ke;
+    const uint64_t rs = ballot(!eqprev) & lanes_le(ln);
+    const int js = kWave - 1 - __builtin_clzll(rs);
+    const uint64_t re = ballot(!eqnext) & ~(lanes_le(ln) >> 1);
+    const int je = __builtin_ctzll(re);
+    own[k] = (uint32_t)(ln - c0) | ((uint32_t)(js - c0) << 8) |
+             ((uint32_t)(je - c0 + 1) << 16) | ((uint32_t)from << 24);
+  }
+  __syncthreads();
+
+  // 3. counts in the group's other chunks, then the writes
+  uint32_t big = 0;
+#pragma unroll
+  for (int k = 0; k < kW; ++k) {
+    const int w = wv + k * NW;
+    const int base = w * kWave;
+    if (base >= n || gs[k] == 0xffffffffu) continue;
+    const int g0 = (int)(gs[k] & 0xffffu);
+    const uint32_t osz = gs[k] >> 16;  // the old group's size
+    const uint32_t oh = (uint32_t)(ts + g0);  // and head
+    const int g1 = min(g0 + (int)osz, n);
+    const uint32_t ke = sk[base + ln];
+    int stable = (int)(own[k] & 0xff);
+    int lt = (int)((own[k] >> 8) & 0xff);
+    int leq = (int)((own[k] >> 16) & 0xff);
+    const int64_t p_old = ts + base + (int)(own[k] >> 24);
+    for (int w2 = g0 / kWave; w2 <= (g1 - 1) / kWave; ++w2) {
+      if (w2 == w) continue;
+      const int a0 = max(g0, w2 * kWave);
+      const int len = min(g1, w2 * kWave + kWave) - a0;
+      const uint32_t lo_k = sk[a0], hi_k = sk[a0 + len - 1];
+      int l2, e2;
+      if (ke < lo_k) {
+        l2 = e2 = 0;
+      } else if (ke > hi_k) {
+        l2 = e2 = len;
+      } else if (lo_k == hi_k) {  // the whole chunk equals ke
+        l2 = 0;
+        e2 = len;
+      } else {
+        l2 = count_below(sk + a0, len, ke, false);
+        e2 = count_below(sk + a0, len, ke, true);
+      }
+      lt += l2;
+      leq += e2;
+      stable += w2 < w ? e2 : l2;
+    }
+    const int64_t np = ts + g0 + stable;
+    const uint32_t nh = (uint32_t)(ts + g0 + lt);
+    const uint32_t size = (uint32_t)(leq - lt);
+    const bool fin = size == 1;
+    rank_next[iv[k]] = nh;
+    // a group that keeps its order and head rewrites nothing else
+    if (np != p_old || nh != oh || fin) {
+      sa[np] = iv[k];
+      gp[np] = fin ? kJustFinished : nh;
+    }
+    if (!fin && stable == lt) {  // the first entry of its new group
+      if (nh != oh || size != osz) gsz[nh] = size;
+      big = max(big, size);
+      if (b + 1 < nl && (int64_t)nh < te && (int64_t)nh + size > te)
+        skip_out = (uint32_t)((int64_t)nh + size - te);
+    }
+  }
+  big = (uint32_t)wave_max_i32((int)big);
+  if (ln == 0) gmax[wv] = big;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t gm = 0;
+    for (int w = 0; w < NW; ++w) gm = max(gm, gmax[w]);
+    if (gm) atomicMax(&state[kMaxGrp + round + 1], gm);
+    if (b + 1 < nl) skip_next[b + 1] = skip_out;
   }
 }
 
@@ -636,54 +985,58 @@ static int round_bits(int64_t m) {
   return bits_for((uint64_t)(m - 1) * (uint64_t)(m + 1) + (uint64_t)m);
 }
 
-// Key buffer (0: A, 1: B) holding round r's list before its sort: round 0
-// starts in A, and each round's gather writes the buffer its predecessor's
-// sorted list is not in.
-static int list_buf(int64_t m, int round) {
-  const int p0 = passes_of(2 * kPairBits);
-  const int p = passes_of(round_bits(m));
-  int x = 0;
-  for (int q = 0; q < round; ++q) x = (x ^ ((q == 0 ? p0 : p) & 1)) ^ 1;
-  return x;
-}
-
-// Buffer holding round r's sorted list.
-static int sorted_buf(int64_t m, int round) {
-  const int p = round == 0 ? passes_of(2 * kPairBits)
-                           : passes_of(round_bits(m));
-  return list_buf(m, round) ^ (p & 1);
-}
-
-// LSD radix sort of round r's list by the low `nbits` bits of its keys,
-// then the group heads of the sorted order.
+// LSD radix sort of round r's list (written to keyA / valA) by the low
+// `nbits` bits of its keys, then the group heads of the sorted order.
 static int sort_and_rank(SaWs& w, int64_t nb, int64_t m, int round,
                          hipStream_t stream) {
   const int nbits = round == 0 ? 2 * kPairBits : round_bits(m);
-  const int slot = len_slot(round);
   uint64_t* keys[2] = {w.keyA, w.keyB};
   uint32_t* vals[2] = {w.valA, w.valB};
-  int x = list_buf(m, round);
+  int x = 0;
   for (int sh = 0; sh < nbits; sh += kDigitBits) {
     hipLaunchKernelGGL(k_rs_hist<kRsThreads>, dim3((unsigned)nb),
                        dim3(kRsThreads), 0, stream, keys[x], sh, w.hist, nb,
-                       w.state, slot);
+                       w.state, round);
     hipLaunchKernelGGL(k_rs_rowscan<kRsThreads>, dim3(kRadix),
                        dim3(kRsThreads), 0, stream, w.hist, nb, w.rowsum,
-                       w.state, slot);
+                       w.state, round);
     hipLaunchKernelGGL(k_rs_scatter<kRsThreads>, dim3((unsigned)nb),
                        dim3(kRsThreads), 0, stream, keys[x], vals[x],
                        keys[x ^ 1], vals[x ^ 1], sh, w.hist, nb, w.rowsum,
-                       w.state, slot);
+                       w.state, round);
     x ^= 1;
   }
-  uint32_t* pos = w.pos[round & 1];
+  const int nx = (round + 1) & 1;
   hipLaunchKernelGGL(k_grp_reduce<kRsThreads>, dim3((unsigned)nb),
-                     dim3(kRsThreads), 0, stream, keys[x], pos, w.blkmax,
-                     w.state, slot);
+                     dim3(kRsThreads), 0, stream, keys[x], w.pos, w.blkmax,
+                     w.state, round);
   hipLaunchKernelGGL(k_grp_rank<kRsThreads>, dim3((unsigned)nb),
-                     dim3(kRsThreads), 0, stream, keys[x], vals[x], pos,
-                     w.blkmax, w.rank, w.sa, w.hd, w.tcnt, w.state, slot);
+                     dim3(kRsThreads), 0, stream, keys[x], vals[x], w.pos,
+                     w.blkmax, w.rank[nx], w.sa, w.gp, w.gsz, w.skip[nx],
+                     w.state, round);
   return (int)hipGetLastError();
+}
+
+// Doubling round r >= 1: the local launch (groups of at most kCap; it
+// also finishes the build or stalls it), then, when `global_path`, the
+// radix launches for the groups above kCap.
+static int doubling_round(SaWs& w, int64_t nb, int64_t m, int round,
+                          int global_path, hipStream_t stream) {
+  const int cur = round & 1, nx = (round + 1) & 1;
+  const int64_t nl = (m + kPosTile - 1) / kPosTile;
+  hipLaunchKernelGGL(k_sa_local<kLocalThreads>, dim3((unsigned)nl),
+                     dim3(kLocalThreads), 0, stream, w.gp, w.gsz, w.sa,
+                     w.rank[cur], w.rank[nx], w.skip[cur], w.skip[nx], m, nl,
+                     round, global_path, w.state);
+  if (!global_path) return (int)hipGetLastError();
+  hipLaunchKernelGGL(k_pos_count<kRsThreads>, dim3((unsigned)nb),
+                     dim3(kRsThreads), 0, stream, w.gp, w.gsz, w.tcnt, m,
+                     w.state, round);
+  hipLaunchKernelGGL(k_pos_gather<kRsThreads>, dim3((unsigned)nb),
+                     dim3(kRsThreads), 0, stream, w.gp, w.gsz, w.sa,
+                     w.rank[cur], w.tcnt, m, nb, round, w.keyA, w.valA,
+                     w.pos, w.state);
+  return sort_and_rank(w, nb, m, round, stream);
 }
 
 }  // namespace sfx
@@ -756,30 +1109,22 @@ int build_begin(const int32_t* text, int64_t m, void* workspace,
   hipLaunchKernelGGL(k_sa_range, dim3((unsigned)parts), dim3(256), 0, stream,
                      text, m, plo, phi);
   hipLaunchKernelGGL(k_sa_init, dim3(eb), dim3(256), 0, stream, text, m,
-                     w.keyA, w.valA, w.pos[0], plo, phi, parts, w.state);
+                     w.keyA, w.valA, w.pos, plo, phi, parts, w.skip[0],
+                     w.skip[1], (m + kPosTile - 1) / kPosTile, w.state);
   return sort_and_rank(w, nb, m, 0, stream);
 }
 
 // Rounds first .. first + count - 1 (round r doubles h = h0 * 2^(r-1),
 // h0 = 1 or 2 as round 0 decided; with h0 = 2 the last round finds none).
-int build_rounds(int64_t m, int first, int count, void* workspace,
-                 hipStream_t stream) {
+int build_rounds(int64_t m, int first, int count, int global_path,
+                 void* workspace, hipStream_t stream) {
   if (m <= 1) return 0;
   SaWs w;
   sa_ws_layout(m, workspace, &w);
   const int64_t nb = (m + kTile - 1) / kTile;
   const int last = total_rounds(m);
-  uint64_t* keys[2] = {w.keyA, w.keyB};
-  uint32_t* vals[2] = {w.valA, w.valB};
   for (int r = first < 1 ? 1 : first; r < first + count && r <= last; ++r) {
-    const int src = sorted_buf(m, r - 1);
-    const int dst = list_buf(m, r);
-    hipLaunchKernelGGL(k_sa_gather<kRsThreads>, dim3((unsigned)nb),
-                       dim3(kRsThreads), 0, stream, w.hd, vals[src],
-                       w.pos[(r - 1) & 1], w.rank, w.tcnt, m, r, keys[dst],
-                       vals[dst], w.pos[r & 1], w.state, len_slot(r - 1),
-                       len_slot(r));
-    const int rc = sort_and_rank(w, nb, m, r, stream);
+    const int rc = doubling_round(w, nb, m, r, global_path, stream);
     if (rc) return rc;
   }
   return (int)hipGetLastError();
@@ -805,10 +1150,12 @@ extern "C" int sfx_sa_build(const int32_t* text, int64_t m, int64_t n_total,
   if (!ws_ok(m, workspace, workspace_bytes)) return SFX_EINVAL;
   int rc = build_begin(text, m, workspace, stream);
   if (rc) return rc;
-  rc = build_rounds(m, 1, total_rounds(m), workspace, stream);
+  rc = build_rounds(m, 1, total_rounds(m), 1, workspace, stream);
   if (rc) return rc;
   return build_finish(m, n_total, sa_out, sa_is64, workspace, stream);
 }
+
+extern "C" int sfx_sa_group_cap(void) { return kCap; }
 
 extern "C" int sfx_sa_build_rounds_total(int64_t m) {
   return m < 0 ? SFX_EINVAL : total_rounds(m);
@@ -833,11 +1180,13 @@ extern "C" int sfx_sa_build_begin(const int32_t* text, int64_t m,
 }
 
 extern "C" int sfx_sa_build_rounds(int64_t m, int32_t first, int32_t count,
-                                   void* workspace, size_t workspace_bytes,
+                                   int32_t global_path, void* workspace,
+                                   size_t workspace_bytes,
                                    hipStream_t stream) {
   if (m < 0 || m > 0x7fffffffLL || first < 1 || count < 0) return SFX_EINVAL;
   if (!ws_ok(m, workspace, workspace_bytes)) return SFX_EINVAL;
-  return build_rounds(m, first, count, workspace, stream);
+  if (global_path != 0 && global_path != 1) return SFX_EINVAL;
+  return build_rounds(m, first, count, global_path, workspace, stream);
 }
 
 extern "C" int sfx_sa_build_finish(int64_t m, int64_t n_total, void* sa_out,

@@ -32,7 +32,9 @@ import torch
 from suffixgpu_amd import _lib
 from suffixgpu_amd._lib import check, lib, require_gpu, stream_of
 from suffixgpu_amd.expand import expand_chain
-from suffixgpu_amd.suffix_array import sa_workspace_bytes
+from suffixgpu_amd.suffix_array import (DEFAULT_RADIX_MASK, STATE_WORDS,
+                                        BuildState, enqueue_rounds,
+                                        sa_workspace_bytes, state_view)
 
 PAD_TOKEN = torch.iinfo(torch.int32).max
 # Tokens of every suffix kept next to the suffix array (one 128-byte row
@@ -144,13 +146,17 @@ class GlobalIndex:
         # device-side ingest totals: documents appended, dropped to make
         # room (and their tokens), rows outside the token buffer
         self.ingest_counters: dict = {}
-        # Background rebuilds run their doubling rounds in two chunks: the
+        # Background rebuilds run their doubling rounds in chunks: the
         # first sized from the rounds the previous build needed (plus a
-        # margin), the rest only if the device reports the array is not
-        # final yet (a pinned copy of the build's state block).
+        # margin), with the radix path enqueued for the rounds that took it
+        # then; the rest only if the device reports the array is not final
+        # yet, or is stalled at a round that needs the radix path (a pinned
+        # copy of the build's state block).
         self.sa_round_hint = 12
+        self.sa_radix_hint = DEFAULT_RADIX_MASK
         self._build_state = None  # (m, next_round) while rounds may remain
-        self._flag_host = torch.zeros(4, dtype=torch.int32, pin_memory=True)
+        self._flag_host = torch.zeros(STATE_WORDS, dtype=torch.int32,
+                                      pin_memory=True)
 
     # ------------------------------------------------------------------
     # device views
@@ -398,8 +404,8 @@ class GlobalIndex:
         first = min(self.sa_round_hint, total)
         check(L.sfx_sa_build_begin(dst.data_ptr(), m, ws.data_ptr(),
                                    ws.numel(), st), "SA rebuild")
-        check(L.sfx_sa_build_rounds(m, 1, first, ws.data_ptr(), ws.numel(),
-                                    st), "SA rebuild")
+        enqueue_rounds(m, 1, first, self.sa_radix_hint, ws.data_ptr(),
+                       ws.numel(), st)
         self._copy_build_state(m)
         self._staged_build_finish(dst, m)
         # Kept even when every round was enqueued: the state copy then
@@ -408,11 +414,10 @@ class GlobalIndex:
 
     def _copy_build_state(self, m: int) -> None:
         if m <= 1:
-            self._flag_host.fill_(1)
+            self._flag_host.zero_()
+            self._flag_host[0] = 1
             return
-        off = int(lib().sfx_sa_build_flag_offset(m))
-        state = self._sa_ws[off:off + 16].view(torch.int32)
-        self._flag_host.copy_(state, non_blocking=True)
+        self._flag_host.copy_(state_view(self._sa_ws, m), non_blocking=True)
 
     def _staged_build_finish(self, dst: torch.Tensor, m: int) -> None:
         ws = self._sa_ws
@@ -425,34 +430,40 @@ class GlobalIndex:
 
     def _staged_build_check(self) -> bool:
         """After the build's event: True when the staged output is final;
-        otherwise the remaining rounds, the output and the key rows are
-        enqueued again under a new event.  Every state copy that comes back
-        sets the round hint to the rounds this text needed plus 2, so a
-        long-repeat text raises it only until a shorter one follows."""
+        otherwise the remaining rounds (from the stalled round, with its
+        radix path, when the build stalled), the output and the key rows
+        are enqueued again under a new event.  Every state copy of a final
+        build sets the round hint to the rounds this text needed plus 2 and
+        the radix hint to the rounds that took the radix path, so a
+        long-repeat text raises them only until a shorter one follows."""
         if self._build_state is None:
             return True
         m, nxt = self._build_state
         self._build_state = None
         if m <= 1:
-            return True  # nothing to sort; the hint stays as it is
-        flags = self._flag_host.tolist()
+            return True  # nothing to sort; the hints stay as they are
+        state = BuildState.of(self._flag_host.tolist())
         L = lib()
         total = int(L.sfx_sa_build_rounds_total(m))
-        if flags[0]:
-            # flags[2]: the doubling round that found no unsorted group
-            self.sa_round_hint = max(1, int(flags[2]) - 1) + 2
+        if state.done:
+            self.sa_round_hint = state.needed + 2
+            self.sa_radix_hint = state.radix_mask & ~1
             return True
-        if nxt > total:
+        if state.stalled:
+            nxt, radix = state.stalled, 1 << state.stalled
+        elif nxt > total:
             # Every round ran; only the round after the last one could
             # have raised the flag, so the array is final as it stands.
             self.sa_round_hint = total
+            self.sa_radix_hint = state.radix_mask & ~1
             return True
+        else:
+            radix = 0
         self.rebuild_stream.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(self.rebuild_stream):
             ws = self._sa_ws
-            check(L.sfx_sa_build_rounds(m, nxt, total - nxt + 1,
-                                        ws.data_ptr(), ws.numel(),
-                                        stream_of(self.device)), "SA rebuild")
+            enqueue_rounds(m, nxt, total - nxt + 1, radix, ws.data_ptr(),
+                           ws.numel(), stream_of(self.device))
             self._copy_build_state(m)
             self._staged_build_finish(self.staging_corpus, m)
         self._build_state = (m, total + 1)

@@ -1,9 +1,10 @@
 """Suffix-array construction (public API).
 
 Mirrors suffix_gpu/suffix_array.py:15-63.  The GPU build (csrc/sa_build.hip)
-is prefix doubling over LSD radix sorts that stops on the device once all
-ranks are distinct; the suffix array is unique, so it equals the
-reference's.
+is prefix doubling that stops on the device once all ranks are distinct:
+a round whose unsorted groups fit a workgroup sorts them there in one
+launch, a round with a larger group takes LSD radix sorts.  The suffix
+array is unique, so it equals the reference's.
 """
 
 from __future__ import annotations
@@ -20,6 +21,12 @@ def sa_workspace_bytes(n: int) -> int:
 # Doubling rounds enqueued between two reads of the build's done flag in
 # the adaptive build.
 SA_CHECK_ROUNDS = 3
+
+# int32 words of the build's state block a host copy reads, and the
+# default rounds that enqueue the radix path (round 1: on natural text its
+# two-token groups exceed a workgroup)
+STATE_WORDS = 16
+DEFAULT_RADIX_MASK = 1 << 1
 
 
 def _workspace_ok(workspace: torch.Tensor | None, text: torch.Tensor,
@@ -75,23 +82,28 @@ def _build_adaptive(text: torch.Tensor, m: int, out: torch.Tensor,
     st = stream_of(text.device)
     ws, nbytes = workspace.data_ptr(), workspace.numel()
     total = int(L.sfx_sa_build_rounds_total(m))
-    off = int(L.sfx_sa_build_flag_offset(m))
-    state = workspace[off:off + 16].view(torch.int32)
-    flag = torch.empty(4, dtype=torch.int32, pin_memory=True)
+    state = state_view(workspace, m)
+    flag = torch.empty(STATE_WORDS, dtype=torch.int32, pin_memory=True)
     check(L.sfx_sa_build_begin(text.data_ptr(), m, ws, nbytes, st),
           "build_suffix_array")
     first = 1
+    radix_first = True  # round 1 and a resumed round enqueue the radix path
     while first <= total:
         n = min(SA_CHECK_ROUNDS, total - first + 1)
-        check(L.sfx_sa_build_rounds(m, first, n, ws, nbytes, st),
-              "build_suffix_array")
-        first += n
+        enqueue_rounds(m, first, n, 1 << first if radix_first else 0, ws,
+                       nbytes, st)
         flag.copy_(state, non_blocking=True)
         done = torch.cuda.Event()
         done.record(torch.cuda.current_stream(text.device))
         done.synchronize()
-        if int(flag[0]):
+        s = BuildState.of(flag.tolist())
+        if s.done:
             break
+        if s.stalled:
+            first, radix_first = s.stalled, True
+            continue
+        first += n
+        radix_first = False
     check(L.sfx_sa_build_finish(m, out.shape[0], out.data_ptr(),
                                 int(out.dtype == torch.int64), ws, nbytes,
                                 st), "build_suffix_array")
@@ -110,30 +122,83 @@ def build_suffix_array(tokens: torch.Tensor) -> torch.Tensor:
 
 
 def build_suffix_array_rounds(text: torch.Tensor, m: int, out: torch.Tensor,
-                              workspace: torch.Tensor, rounds: int) -> None:
+                              workspace: torch.Tensor, rounds: int,
+                              radix_mask: int = DEFAULT_RADIX_MASK) -> None:
     """The build with only its first ``rounds`` doubling rounds enqueued
-    (then the output copy): the background rebuild's first chunk.  The
-    result is final iff :func:`build_is_final` says so afterwards."""
+    (then the output copy): the background rebuild's first chunk.  Rounds
+    whose bit is set in ``radix_mask`` enqueue the radix path too.  The
+    result is final iff :func:`build_state` says so afterwards."""
     require_gpu(text, out, workspace)
     workspace = _workspace_ok(workspace, text, sa_workspace_bytes(m))
     L = lib()
     st = stream_of(text.device)
-    check(L.sfx_sa_build_begin(text.data_ptr(), m, workspace.data_ptr(),
-                               workspace.numel(), st), "SA build")
-    check(L.sfx_sa_build_rounds(m, 1, max(0, rounds), workspace.data_ptr(),
-                                workspace.numel(), st), "SA build")
-    check(L.sfx_sa_build_finish(m, out.shape[0], out.data_ptr(),
-                                int(out.dtype == torch.int64),
-                                workspace.data_ptr(), workspace.numel(), st),
+    ws, nbytes = workspace.data_ptr(), workspace.numel()
+    check(L.sfx_sa_build_begin(text.data_ptr(), m, ws, nbytes, st),
           "SA build")
+    enqueue_rounds(m, 1, max(0, rounds), radix_mask, ws, nbytes, st)
+    check(L.sfx_sa_build_finish(m, out.shape[0], out.data_ptr(),
+                                int(out.dtype == torch.int64), ws, nbytes,
+                                st), "SA build")
+
+
+def enqueue_rounds(m: int, first: int, count: int, radix_mask: int,
+                   ws: int, nbytes: int, stream) -> None:
+    """Doubling rounds first .. first+count-1 on ``stream``: a round r with
+    bit r of ``radix_mask`` set enqueues the radix path too, the others
+    only the local launch (a round that needs the radix path then stalls
+    the build, see :class:`BuildState`)."""
+    L = lib()
+    r, end = first, first + count
+    while r < end:
+        g = (radix_mask >> r) & 1
+        r2 = r + 1
+        while r2 < end and ((radix_mask >> r2) & 1) == g:
+            r2 += 1
+        check(L.sfx_sa_build_rounds(m, r, r2 - r, g, ws, nbytes, stream),
+              "SA build")
+        r = r2
+
+
+def state_view(workspace: torch.Tensor, m: int) -> torch.Tensor:
+    """The device words of a build's state block (a view of the byte
+    workspace)."""
+    off = int(lib().sfx_sa_build_flag_offset(m))
+    return workspace[off:off + 4 * STATE_WORDS].view(torch.int32)
+
+
+class BuildState:
+    """A build's state words: done (the array is final), found_none (the
+    round that found no unsorted group), stalled (the round that needs the
+    radix path it was not given, 0 for none) and radix_mask (bit r for each
+    round that took the radix path; bit 0 is the token round)."""
+
+    def __init__(self, done: bool, found_none: int, stalled: int,
+                 radix_mask: int):
+        self.done = done
+        self.found_none = found_none
+        self.stalled = stalled
+        self.radix_mask = radix_mask
+
+    @classmethod
+    def of(cls, words: list[int]) -> "BuildState":
+        return cls(bool(words[0]), int(words[2]), int(words[7]),
+                   int(words[8]) & 0xffffffff)
+
+    @property
+    def needed(self) -> int:
+        """Doubling rounds the array needed (-1 while not final)."""
+        return max(self.found_none - 1, 0) if self.done else -1
+
+
+def read_build_state(workspace: torch.Tensor, m: int) -> BuildState:
+    """The state of a build (synchronises the current stream)."""
+    if m <= 1:
+        return BuildState(True, 1, 0, 0)
+    return BuildState.of(state_view(workspace, m).cpu().tolist())
 
 
 def build_state(workspace: torch.Tensor, m: int) -> tuple[bool, int]:
     """(final, rounds the array needed) from a build's workspace; reads the
     device (synchronises the current stream)."""
-    if m <= 1:
-        return True, 0
-    off = int(lib().sfx_sa_build_flag_offset(m))
-    st = workspace[off:off + 16].view(torch.int32).cpu().tolist()
-    # st[2]: the doubling round that found no unsorted group left
-    return bool(st[0]), (max(int(st[2]) - 1, 0) if st[0] else -1)
+    s = read_build_state(workspace, m)
+    return s.done, (s.needed if m > 1 else 0)

@@ -68,6 +68,8 @@ def test_abi_version_and_constants(so):
     assert _lib.ENOSCRATCH == header_define("SFX_ENOSCRATCH")
     assert (_lib.NOALLOC_SCRATCH_BYTES
             == header_define("SFX_NOALLOC_SCRATCH_BYTES"))
+    so.sfx_sa_group_cap.restype = ctypes.c_int32
+    assert so.sfx_sa_group_cap() == 2048  # the value the header documents
     assert _lib.NOALLOC_MAX_ROWS == header_define("SFX_NOALLOC_MAX_ROWS")
 
 

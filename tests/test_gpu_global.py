@@ -439,10 +439,11 @@ def test_async_rebuild_blocking_poll(gpu, hint):
 
 def test_round_hint_follows_the_last_build(gpu):
     """The background rebuild's first chunk of doubling rounds is sized
-    from the rounds the previous build needed: a long exact repeat (one
-    token 6000 times) raises the hint past the default; once that document
-    is evicted, a build over short-repeat documents lowers it again (the
-    state copy is read even when the first chunk held every round)."""
+    from the rounds the previous build needed, with the radix path for the
+    rounds that took it: a long exact repeat (one token 6000 times) raises
+    the hint past the default; once that document is evicted, a build over
+    short-repeat documents lowers it again (the state copy is read even
+    when the first chunk held every round)."""
     from suffixgpu_amd.global_index import GlobalIndex
     rng = np.random.default_rng(31)
     side = torch.cuda.Stream(gpu)
@@ -459,6 +460,9 @@ def test_round_hint_follows_the_last_build(gpu):
     gpu_state_equal(g, o)
     high = g.sa_round_hint
     assert high > 12
+    # rounds over the repeat's groups of up to 6000 suffixes took the radix
+    # path, and the next build enqueues it for them
+    assert g.sa_radix_hint & 2
     docs = [rng.integers(0, 1000, size=900).astype(I32) for _ in range(5)]
     g.append_documents([T(d, gpu) for d in docs])
     o.append_documents(docs)
@@ -468,6 +472,7 @@ def test_round_hint_follows_the_last_build(gpu):
     gpu_state_equal(g, o)
     assert list(g.active_doc_lens) == [901] * 5
     assert g.sa_round_hint < 8 < high
+    assert g.sa_radix_hint == 0
 
 
 def test_save_restore_bit_exact(gpu, tmp_path):

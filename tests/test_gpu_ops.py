@@ -114,6 +114,78 @@ def test_build_suffix_array_template_corpus(gpu):
     np.testing.assert_array_equal(N(got), o_build_sa(t))
 
 
+def _planted_bigram_text(count: int, seed: int) -> np.ndarray:
+    """Random large-alphabet text where the bigram (1, 2) occurs exactly
+    `count` times, after the suffixes starting with 0: the group of
+    suffixes starting with (1, 2) -- the largest after the token round --
+    occupies SA positions from there to there + count, across a
+    4096-position tile boundary (asserted)."""
+    rng = np.random.default_rng(seed)
+    n = 3 * count + 6000
+    t = rng.integers(3, 60000, size=n).astype(I32)
+    t[rng.choice(n, 4000, replace=False)] = 0
+    slots = rng.choice(n // 3 - 1, count, replace=False) * 3
+    t[slots] = 1
+    t[slots + 1] = 2
+    zeros = int(np.sum(t == 0))
+    assert zeros < 4096 < zeros + count
+    return t
+
+
+@pytest.mark.parametrize("extra", [0, 1])
+def test_build_suffix_array_group_cap(gpu, extra):
+    """A round whose largest group has sfx_sa_group_cap() suffixes sorts it
+    inside one workgroup (following it into the next tile); one more takes
+    the radix path.  The state's radix mask records which path round 1
+    took."""
+    from suffixgpu_amd import _lib
+    from suffixgpu_amd.suffix_array import (build_suffix_array_into,
+                                            read_build_state,
+                                            sa_workspace_bytes)
+    cap = int(_lib.lib().sfx_sa_group_cap())
+    count = cap + extra
+    t = _planted_bigram_text(count, count)
+    exp = o_build_sa(t)
+    assert np.sum((t[:-1] == 1) & (t[1:] == 2)) == count
+    for adaptive in (True, False):
+        ws = torch.empty(sa_workspace_bytes(t.shape[0]), dtype=torch.uint8,
+                         device=gpu)
+        out = torch.empty(t.shape[0], dtype=torch.int32, device=gpu)
+        build_suffix_array_into(T(t, gpu), t.shape[0], out, ws,
+                                adaptive=adaptive)
+        np.testing.assert_array_equal(N(out), exp)
+        st = read_build_state(ws, t.shape[0])
+        assert st.done and not st.stalled
+        assert bool(st.radix_mask & 2) == (count > cap)
+
+
+def test_build_suffix_array_stall_and_resume(gpu):
+    """Rounds enqueued without the radix path stop at the first round that
+    needs it (the state names the round, the rest return at once); the
+    same rounds enqueued again from there with the radix path finish the
+    array."""
+    from suffixgpu_amd import _lib
+    from suffixgpu_amd.suffix_array import (build_suffix_array_rounds,
+                                            enqueue_rounds, read_build_state,
+                                            sa_workspace_bytes)
+    t = _planted_bigram_text(5000, 3)
+    m = t.shape[0]
+    ws = torch.empty(sa_workspace_bytes(m), dtype=torch.uint8, device=gpu)
+    out = torch.empty(m, dtype=torch.int32, device=gpu)
+    L = _lib.lib()
+    total = int(L.sfx_sa_build_rounds_total(m))
+    build_suffix_array_rounds(T(t, gpu), m, out, ws, total, radix_mask=0)
+    st = read_build_state(ws, m)
+    assert not st.done and st.stalled == 1 and st.radix_mask == 1
+    enqueue_rounds(m, 1, total, 1 << 1, ws.data_ptr(), ws.numel(),
+                   _lib.stream_of(gpu))
+    _lib.check(L.sfx_sa_build_finish(m, m, out.data_ptr(), 0, ws.data_ptr(),
+                                     ws.numel(), _lib.stream_of(gpu)), "sa")
+    st = read_build_state(ws, m)
+    assert st.done and not st.stalled and st.radix_mask == 3
+    np.testing.assert_array_equal(N(out), o_build_sa(t))
+
+
 def test_build_suffix_array_identity_tail(gpu):
     from suffixgpu_amd.suffix_array import build_suffix_array_into
     rng = np.random.default_rng(4)

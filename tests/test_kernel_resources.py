@@ -53,3 +53,20 @@ def test_step_kernels_fit_two_workgroups_per_cu(src, kernel, tmp_path):
         assert r["ScratchSize"] == 0, (name, r)
         assert r["VGPRs"] <= 128, (name, r)
         assert r["Occupancy"] >= 4, (name, r)
+
+
+@pytest.mark.skipif(shutil.which(HIPCC) is None and
+                    not __import__("os").path.exists(HIPCC),
+                    reason="needs hipcc")
+def test_sa_local_round_fits_two_workgroups_per_cu(tmp_path):
+    """The suffix-array build's local round (1024 threads, 24 KiB of LDS):
+    at most 64 VGPRs (eight waves per SIMD) and no scratch.  A cross-lane
+    read feeding its sort decision once pushed it to 128 VGPRs with 376
+    bytes of scratch per lane."""
+    res = _resources("sa_build.hip", tmp_path)
+    found = {k: v for k, v in res.items() if "k_sa_local" in k}
+    assert found, "no k_sa_local in the resource report"
+    for name, r in found.items():
+        assert r["ScratchSize"] == 0, (name, r)
+        assert r["VGPRs"] <= 64, (name, r)
+        assert r["Occupancy"] >= 8, (name, r)
