@@ -207,16 +207,18 @@ def time_sa_builds(w, dev, side):
         log(f"SA rebuild {name} ({rounds} rounds, as the index runs it): "
             f"{min(times):.2f} ms")
         if name == "corpus":
-            build_ms["tables"] = index_tables_ms(text, out, dev, side)
+            build_ms["tables"] = index_tables_ms(text, out, dev, side, ws)
             log(f"key rows + n-gram table of the corpus: "
                 f"{build_ms['tables']}")
     del ws
     return build_ms
 
 
-def index_tables_ms(text, sa, dev, side) -> dict:
+def index_tables_ms(text, sa, dev, side, ws) -> dict:
     """What a rebuild adds after the suffix array, on the rebuild stream:
-    the key rows and the n-gram range table (best of 3, HIP events)."""
+    the key rows and the n-gram range table (best of 3, HIP events), the
+    table read from the ranks' first four tokens that the key-row launch
+    writes into the SA build workspace ``ws``, as the index does."""
     import torch
     from suffixgpu_amd import _lib
     from suffixgpu_amd.global_index import KEY_WIDTH, gram_slots_for
@@ -235,9 +237,10 @@ def index_tables_ms(text, sa, dev, side) -> dict:
             ev[0].record(side)
             _lib.check(L.sfx_sa_keys(text.data_ptr(), sa.data_ptr(), n, n,
                                      KEY_WIDTH, keys.data_ptr(),
-                                     side.cuda_stream), "keys")
+                                     ws.data_ptr(), side.cuda_stream),
+                       "keys")
             ev[1].record(side)
-            _lib.check(L.sfx_gram_build(keys.data_ptr(), KEY_WIDTH, n,
+            _lib.check(L.sfx_gram_build(ws.data_ptr(), 4, n,
                                         gram.data_ptr(), slots,
                                         side.cuda_stream), "gram")
             ev[2].record(side)
@@ -1008,9 +1011,10 @@ def pmc_workload(d, w, dev) -> int:
         build_suffix_array_rounds(text, m, out, ws, needed + 2, radix)
         # the key rows and n-gram table the index builds after it
         _lib.check(L.sfx_sa_keys(text.data_ptr(), out.data_ptr(), CAPACITY,
-                                 m, KEY_WIDTH, keys.data_ptr(), st), "keys")
-        _lib.check(L.sfx_gram_build(keys.data_ptr(), KEY_WIDTH, m,
-                                    gram.data_ptr(), slots, st), "gram")
+                                 m, KEY_WIDTH, keys.data_ptr(),
+                                 ws.data_ptr(), st), "keys")
+        _lib.check(L.sfx_gram_build(ws.data_ptr(), 4, m, gram.data_ptr(),
+                                    slots, st), "gram")
     torch.cuda.synchronize()
     del keys, gram
     c5d, c5t, c5n, c5s = c5_local(dev)

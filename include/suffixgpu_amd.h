@@ -32,7 +32,7 @@ extern "C" {
 
 #define SFX_EINVAL (-1)
 #define SFX_MAX_CANDIDATES 32
-#define SFX_ABI_VERSION 11
+#define SFX_ABI_VERSION 12
 
 /* Drafter configuration shared by the local and global paths.
  * Mirrors the constructor arguments of SuffixGPUDrafter
@@ -240,10 +240,12 @@ size_t sfx_sa_build_workspace_size(int64_t m);
 
 /* keys[r * width + j] = j-th token of the suffix at sa[r] (corpus reads at
  * or past n give -1), for r < rows <= n and j < width (4..32, multiple of
- * 4).  A rebuild whose ranks from some r on are the padding suffixes of
- * the previous build in the same buffer rewrites only the rows below. */
+ * 4); when first4 (16-byte aligned) is not NULL, first4[r * 4 + j] holds
+ * the same for j < 4, a compact input for sfx_gram_build (key_width 4).
+ * A rebuild whose ranks from some r on are the padding suffixes of the
+ * previous build in the same buffer rewrites only the rows below. */
 int sfx_sa_keys(const int32_t* corpus, const int32_t* sa, int64_t n,
-                int64_t rows, int64_t width, int32_t* keys,
+                int64_t rows, int64_t width, int32_t* keys, int32_t* first4,
                 hipStream_t stream);
 int sfx_sa_build(const int32_t* text, int64_t m, int64_t n_total, void* sa,
                  int32_t sa_is64, void* workspace, size_t workspace_bytes,
@@ -285,7 +287,10 @@ int sfx_gram_build(const int32_t* keys, int64_t key_width, int64_t m,
  * that found it final, [7] the round the build stalled at (0: none) and
  * [8] a mask with bit r set for every round r that ran radix launches,
  * for an asynchronous copy to the host.  sfx_sa_build enqueues the radix
- * launches for every round. */
+ * launches for every round.  The first 16 * m bytes of the workspace carry
+ * nothing from one launch of a build to the next (the radix key buffers):
+ * between launches, e.g. after finish, a caller may use them, as the
+ * first4 output of sfx_sa_keys. */
 int sfx_sa_build_rounds_total(int64_t m);
 int64_t sfx_sa_build_flag_offset(int64_t m);
 /* The largest group a round sorts inside a workgroup (2048). */

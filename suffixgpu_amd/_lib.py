@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsuffixgpu_amd.so"
 MAX_CANDIDATES = 32
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -123,7 +123,7 @@ SIGNATURES = {
                                          ctypes.POINTER(SfxBatch), c_p, c_p,
                                          c_p, c_p]),
     "sfx_sa_build_workspace_size": (ctypes.c_size_t, [c_i64]),
-    "sfx_sa_keys": (c_i32, [c_p, c_p, c_i64, c_i64, c_i64, c_p, c_p]),
+    "sfx_sa_keys": (c_i32, [c_p, c_p, c_i64, c_i64, c_i64, c_p, c_p, c_p]),
     "sfx_gram_table_bytes": (ctypes.c_size_t, [c_i64]),
     "sfx_gram_build": (c_i32, [c_p, c_i64, c_i64, c_p, c_i64, c_p]),
     "sfx_sa_build": (c_i32, [c_p, c_i64, c_i64, c_p, c_i32, c_p,

@@ -929,17 +929,21 @@ __global__ __launch_bounds__(NT) void k_sa_local(
 }
 
 // ------------------------------------------------------------ outputs
-// keys[r * W + j] = corpus[sa[r] + j] (-1 at or past n), ranks r < rows.
+// keys[r * W + j] = corpus[sa[r] + j] (-1 at or past n), ranks r < rows;
+// first4[r * 4 + j] the same for j < 4 when first4 is not null.
 __global__ __launch_bounds__(256) void k_rank_keys(const int32_t* corpus,
                                                  const int32_t* sa, int64_t n,
                                                  int64_t rows, int W,
-                                                 int32_t* keys) {
+                                                 int32_t* keys,
+                                                 int32_t* first4) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= rows * W) return;
   const int64_t r = e / W;
   const int j = (int)(e - r * W);
   const int64_t p = (int64_t)sa[r] + j;
-  keys[e] = p < n && p >= 0 ? corpus[p] : -1;
+  const int32_t v = p < n && p >= 0 ? corpus[p] : -1;
+  keys[e] = v;
+  if (first4 && j < 4) first4[r * 4 + j] = v;
 }
 
 // The same rows four tokens per thread with one 16-byte store (keys
@@ -948,7 +952,8 @@ __global__ __launch_bounds__(256) void k_rank_keys(const int32_t* corpus,
 __global__ __launch_bounds__(256) void k_rank_keys4(const int32_t* corpus,
                                                   const int32_t* sa, int64_t n,
                                                   int64_t rows, int W,
-                                                  int32_t* keys) {
+                                                  int32_t* keys,
+                                                  int32_t* first4) {
   const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int W4 = W >> 2;
   if (e >= rows * W4) return;
@@ -960,6 +965,7 @@ __global__ __launch_bounds__(256) void k_rank_keys4(const int32_t* corpus,
   v.z = p + 2 < n && p + 2 >= 0 ? corpus[p + 2] : -1;
   v.w = p + 3 < n && p + 3 >= 0 ? corpus[p + 3] : -1;
   reinterpret_cast<int4*>(keys)[e] = v;
+  if (first4 && e == r * W4) reinterpret_cast<int4*>(first4)[r] = v;
 }
 
 template <typename T>
@@ -1045,9 +1051,10 @@ using namespace sfx;
 
 extern "C" int sfx_sa_keys(const int32_t* corpus, const int32_t* sa,
                            int64_t n, int64_t rows, int64_t width,
-                           int32_t* keys, hipStream_t stream) {
+                           int32_t* keys, int32_t* first4,
+                           hipStream_t stream) {
   if (n < 0 || rows < 0 || rows > n || n > 0x7fffffffLL || width < 4 ||
-      width > 32 || (width & 3))
+      width > 32 || (width & 3) || (((uintptr_t)first4) & 15))
     return SFX_EINVAL;
   if (rows == 0) return 0;
   if (!corpus || !sa || !keys) return SFX_EINVAL;
@@ -1056,11 +1063,11 @@ extern "C" int sfx_sa_keys(const int32_t* corpus, const int32_t* sa,
     const int64_t total4 = total / 4;
     hipLaunchKernelGGL(k_rank_keys4, dim3((unsigned)((total4 + 255) / 256)),
                        dim3(256), 0, stream, corpus, sa, n, rows, (int)width,
-                       keys);
+                       keys, first4);
   } else {
     hipLaunchKernelGGL(k_rank_keys, dim3((unsigned)((total + 255) / 256)),
                        dim3(256), 0, stream, corpus, sa, n, rows, (int)width,
-                       keys);
+                       keys, first4);
   }
   return (int)hipGetLastError();
 }

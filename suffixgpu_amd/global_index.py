@@ -212,10 +212,15 @@ class GlobalIndex:
         keys, gram = self._keys[slot], self._grams[slot]
         st = stream_of(self.device)
         rows = max(m, self._key_rows[slot])
+        # the table reads each rank's first four tokens, written compactly
+        # by the same launch into the SA build workspace's key buffers
+        # (free between build launches) rather than read from the rows
+        first4 = self._sa_workspace().data_ptr() if m > 0 else None
         check(lib().sfx_sa_keys(corpus.data_ptr(), sa.data_ptr(),
                                 self.capacity, rows, KEY_WIDTH,
-                                keys.data_ptr(), st), "SA key rows")
-        check(lib().sfx_gram_build(keys.data_ptr(), KEY_WIDTH, m,
+                                keys.data_ptr(), first4, st), "SA key rows")
+        check(lib().sfx_gram_build(first4 or keys.data_ptr(),
+                                   4 if first4 else KEY_WIDTH, m,
                                    gram.data_ptr(), self.gram_slots, st),
               "n-gram table")
         self._key_rows[slot] = m

@@ -86,9 +86,11 @@ def test_workspace_sizes_are_host_only(so):
 def test_argument_errors_are_reported_before_any_launch():
     lib = _lib.lib()
     # invalid sizes are rejected on the host: nothing is enqueued
-    assert lib.sfx_sa_keys(None, None, 16, 16, 3, None, None) == -1
-    assert lib.sfx_sa_keys(None, None, 16, 17, 32, None, None) == -1
-    assert lib.sfx_sa_keys(None, None, 16, 0, 32, None, None) == 0
+    assert lib.sfx_sa_keys(None, None, 16, 16, 3, None, None, None) == -1
+    assert lib.sfx_sa_keys(None, None, 16, 17, 32, None, None, None) == -1
+    assert lib.sfx_sa_keys(None, None, 16, 0, 32, None, None, None) == 0
+    # first4 must be 16-byte aligned (checked before any launch)
+    assert lib.sfx_sa_keys(None, None, 16, 0, 32, None, 8, None) == -1
     assert lib.sfx_sa_build(None, -1, 0, None, 0, None, 0, None) == -1
     assert lib.sfx_index_swap(None, None, None, None, -1, None, 0,
                               None) == -1

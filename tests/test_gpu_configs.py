@@ -146,7 +146,8 @@ def test_c3_step_matches_oracle(c3, gpu):
 def test_c4_from_scratch_builds(c3, gpu):
     """The 4,193,511-token corpus and 2^22 uniform tokens, built from
     scratch by the adaptive and the fixed-sequence form, against the
-    oracle's own builds; key rows of the uniform build by definition."""
+    oracle's own builds; key rows of the uniform build by definition, and
+    the compact first-four-token array beside them."""
     from suffixgpu_amd.suffix_array import build_suffix_array_into
     from suffixgpu_amd.global_index import PAD_TOKEN
     w, o, d = c3
@@ -169,10 +170,14 @@ def test_c4_from_scratch_builds(c3, gpu):
         np.testing.assert_array_equal(N(out), exp)
     from suffixgpu_amd import _lib
     keys = torch.empty(N22 * 32, dtype=torch.int32, device=gpu)
+    first4 = torch.empty(N22 * 4, dtype=torch.int32, device=gpu)
     _lib.check(_lib.lib().sfx_sa_keys(tu.data_ptr(), out.data_ptr(), N22,
                                       N22, 32, keys.data_ptr(),
+                                      first4.data_ptr(),
                                       _lib.stream_of(gpu)), "keys")
     keys_by_definition(tu, out, keys)
+    # the compact first-token output of the same launch
+    assert torch.equal(first4.view(N22, 4), keys.view(N22, 32)[:, :4])
 
 
 def test_c2_b64_local_matches_oracle(gpu):
