@@ -65,10 +65,13 @@ constexpr int kMinStreamChunk = 1024;
 constexpr size_t kHalfLds = kMaxLds / 2;
 
 int check_local(const sfx_params& p, const sfx_batch& bt);
-// Local layout within `cap` bytes of LDS: 0 = whole row, > 0 = streamed
-// chunk length, -1 = nothing fits.
-int local_chunk(const sfx_params& p, int64_t S, size_t cap = kMaxLds);
-size_t local_lds_bytes(const sfx_params& p, int64_t S, int chunk);
+// Local layout within `cap` bytes of LDS for `nthreads` per row: 0 = whole
+// row, > 0 = streamed chunk length, -1 = nothing fits.
+constexpr int kLocalThreadsDefault = 512;
+int local_chunk(const sfx_params& p, int64_t S, size_t cap = kMaxLds,
+                int nthreads = kLocalThreadsDefault);
+size_t local_lds_bytes(const sfx_params& p, int64_t S, int chunk,
+                       int nthreads = kLocalThreadsDefault);
 
 int check_global(const sfx_params& p, const sfx_index& ix, int64_t batch);
 int mb_lds_bytes(const sfx_index& ix, int parts);

@@ -1,4 +1,5 @@
-// Local (per-request) suffix matcher: one 512-thread workgroup per row.
+// Local (per-request) suffix matcher: one 512-thread workgroup per row
+// (1024 threads for the local-only decode step).
 //
 // The row is staged once in LDS (coalesced int4 loads), the step's sampled
 // tokens are scattered into LDS and HBM, and everything else runs out of
@@ -18,29 +19,59 @@
 
 namespace sfx {
 
+static_assert(kLocalThreads == kLocalThreadsDefault,
+              "launch.h's default thread count");
+
 template <bool kStream>
 __global__ __launch_bounds__(kLocalThreads) void k_local(LocalArgs a) {
   extern __shared__ __align__(16) unsigned char smem[];
   local_body<kStream>(a, smem, blockIdx.x);
 }
 
-static size_t layout_bytes(const sfx_params& p, int64_t S, int chunk) {
+template <bool kStream>
+__global__ __launch_bounds__(kWideThreads) void k_local_wide(LocalArgs a) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  local_body<kStream, kWideThreads>(a, smem, blockIdx.x);
+}
+
+static size_t layout_bytes(const sfx_params& p, int64_t S, int chunk,
+                           int nthreads) {
   if (chunk == 0 && S > (int64_t)kMaxLds / 4) return (size_t)-1;
   const LocalLayout L =
       local_layout((int)S, p.max_pattern_len, p.num_thresholds,
-                   p.max_occurrences, p.k, kLocalThreads / kWave, chunk);
+                   p.max_occurrences, p.k, nthreads / kWave, chunk);
   return (size_t)L.total;
 }
 
-int local_chunk(const sfx_params& p, int64_t S, size_t cap) {
-  if (layout_bytes(p, S, 0) <= cap) return 0;
+int local_chunk(const sfx_params& p, int64_t S, size_t cap, int nthreads) {
+  if (layout_bytes(p, S, 0, nthreads) <= cap) return 0;
   for (int chunk = kMaxStreamChunk; chunk >= kMinStreamChunk; chunk /= 2)
-    if (layout_bytes(p, S, chunk) <= cap) return chunk;
+    if (layout_bytes(p, S, chunk, nthreads) <= cap) return chunk;
   return -1;
 }
 
-size_t local_lds_bytes(const sfx_params& p, int64_t S, int chunk) {
-  return chunk < 0 ? (size_t)-1 : layout_bytes(p, S, chunk);
+size_t local_lds_bytes(const sfx_params& p, int64_t S, int chunk,
+                       int nthreads) {
+  return chunk < 0 ? (size_t)-1 : layout_bytes(p, S, chunk, nthreads);
+}
+
+int launch_local_step(LocalArgs a, hipStream_t stream) {
+  a.chunk = local_chunk(a.p, a.bt.seq, kMaxLds, kWideThreads);
+  if (a.chunk < 0) return -1;
+  if (a.bt.batch == 0) return 0;
+  const size_t lds = local_lds_bytes(a.p, a.bt.seq, a.chunk, kWideThreads);
+  if (a.chunk == 0) {
+    static std::atomic<uint64_t> lds_opt{0};
+    allow_max_lds((const void*)k_local_wide<false>, lds_opt);
+    hipLaunchKernelGGL(k_local_wide<false>, dim3((unsigned)a.bt.batch),
+                       dim3(kWideThreads), lds, stream, a);
+  } else {
+    static std::atomic<uint64_t> lds_opt{0};
+    allow_max_lds((const void*)k_local_wide<true>, lds_opt);
+    hipLaunchKernelGGL(k_local_wide<true>, dim3((unsigned)a.bt.batch),
+                       dim3(kWideThreads), lds, stream, a);
+  }
+  return (int)hipGetLastError();
 }
 
 int check_local(const sfx_params& p, const sfx_batch& bt) {

@@ -79,16 +79,24 @@ __host__ __device__ inline LocalLayout local_layout(int S, int P, int C,
 }
 
 constexpr int kLocalThreads = 512;
+// The local-only decode step over rows of kWideMinSeq tokens or more runs
+// one 1024-thread workgroup per row: the row scans (match lengths,
+// histogram, first-R compaction) spread over 16 waves, and a CU holds one
+// such row.  At B = 256, S = 16384 the step measured 33.6 us against
+// 38.6 us with 512 threads; at S = 4096 it was 1.3 us slower (the row
+// scans are short and the 16-wave barriers cost more), at S = 16384 and
+// B <= 128 the same.
+constexpr int kWideThreads = 1024;
+constexpr int64_t kWideMinSeq = 8192;
 
 // kStream: the row stays in HBM.  match_back is computed over chunks of
 // a.chunk positions staged through LDS, once to histogram the match
 // lengths and once more, in order, to compact the first R ends per
 // candidate with the counts carried from chunk to chunk (stopping once
 // every candidate holds R); the expansion reads continuations from HBM.
-template <bool kStream>
+template <bool kStream, int NT = kLocalThreads>
 __device__ __forceinline__ void local_body(const LocalArgs& a,
                                            unsigned char* smem, int b) {
-  constexpr int NT = kLocalThreads;
   constexpr int NW = NT / kWave;
   const sfx_params& p = a.p;
   const int tid = threadIdx.x;
@@ -490,5 +498,10 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
   if (block_arrive(a.ws.pick + b, 3u, misc + 2))
     final_pick(p, a.ws, b, a.draft, a.num_valid, misc + 4);
 }
+
+// The local-only decode step with kWideThreads per row (local.hip); -1
+// when its layout does not fit a CU's LDS (the caller keeps the fused
+// step's 512-thread form).
+int launch_local_step(LocalArgs a, hipStream_t stream);
 
 }  // namespace sfx

@@ -101,6 +101,12 @@ int launch_step(const sfx_params* p, const sfx_index* ix, const sfx_batch* bt,
   a.l.draft = draft;
   a.l.num_valid = num_valid;
   a.l.new_counts = new_counts;
+  if (!global_on && bt->seq >= kWideMinSeq) {
+    // local-only rows of 8192 tokens or more: one 1024-thread workgroup
+    // per row when its layout fits
+    rc = launch_local_step(a.l, stream);
+    if (rc >= 0) return rc;
+  }
   const int dparts =
       global_on ? delta_parts_for(bt->batch, ix->delta_capacity) : 0;
   const unsigned blocks =

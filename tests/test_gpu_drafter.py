@@ -270,8 +270,10 @@ def test_ingest_then_cross_request_draft(gpu):
 @pytest.mark.parametrize("enable_global", [False, True])
 def test_step_long_rows_vs_oracle(gpu, enable_global):
     """Rows of 40000 tokens (streamed local role) in the fused step, with
-    and without the global index: rows are windows of the document stream
-    at committed lengths around the 16384-position chunk boundaries."""
+    and without the global index (without it, rows this long run the
+    1024-thread local-only kernel): rows are windows of the document
+    stream at committed lengths around the 16384-position chunk
+    boundaries."""
     from suffixgpu_amd import SuffixGPUDrafter
     s, t = 40000, 17
     w, d, o = _global_pair(gpu, seed=9, b=4, s=2048)
