@@ -35,6 +35,7 @@ struct GlobalArgs {
 
 struct GlobalLayout {
   int rpat, lb, ub, found, scan, red, misc, lo, ulo, umap, dlen, dcnt, dpc,
+      dmap,
       sal, sas, sae, caps, dtok, dmb, mpos, mcache, mA, mH, chain, nv, score,
       rlen, rocc, total;
 };
@@ -73,6 +74,7 @@ __host__ __device__ inline GlobalLayout global_layout(int P, int C, int R,
   L.dlen = g_take(off, C * 4);
   L.dcnt = g_take(off, C * 4);
   L.dpc = g_take(off, C * kMaxDeltaParts * 4);
+  L.dmap = g_take(off, C * kMaxDeltaParts * 4);
   L.sal = g_take(off, C * 4);
   L.sas = g_take(off, C * 4);
   L.sae = g_take(off, C * 4);
@@ -271,25 +273,37 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
 
 // Row-level delta result per cap from the parts (run by the merging
 // workgroup): dlen[c] = min(max mb, cap), dpc[c][k] = part k's kept hits,
-// dcnt[c] = min(sum, R).
+// dcnt[c] = min(sum, R), dmap[c][k] = part k's list index for cap c.
 __device__ __forceinline__ void delta_combine(const GlobalArgs& a, int b,
                                               const int32_t* caps,
                                               int32_t* dlen, int32_t* dcnt,
-                                              int32_t* dpc) {
+                                              int32_t* dpc, int32_t* dmap) {
   const int C = a.p.num_caps;
   const int R = a.p.max_occurrences;
   const int KD = a.dparts;
   for (int c = threadIdx.x; c < C; c += blockDim.x) {
     const int cap = caps[c];
+    // every part's maximum and count in one round of loads (the parts
+    // wrote them from other workgroups: each read goes past this L2)
+    int pmx[kMaxDeltaParts], pcnt[kMaxDeltaParts], pmap[kMaxDeltaParts];
     int mx = 0;
-    for (int k = 0; k < KD; ++k) mx = max(mx, a.ws.d_mx[(int64_t)b * KD + k]);
+#pragma unroll
+    for (int k = 0; k < kMaxDeltaParts; ++k) {
+      const int64_t slot = (int64_t)b * KD + k;
+      pmx[k] = k < KD ? a.ws.d_mx[slot] : 0;
+      pcnt[k] = k < KD ? a.ws.d_cnt[slot * C + c] : 0;
+      pmap[k] = k < KD ? a.ws.d_map[slot * C + c] : 0;
+      mx = max(mx, pmx[k]);
+    }
     const int lo = min(mx, cap);
     int total = 0;
-    for (int k = 0; k < KD; ++k) {
-      const int64_t slot = (int64_t)b * KD + k;
-      const bool keep = lo > 0 && min(a.ws.d_mx[slot], cap) == lo;
-      const int h = keep ? a.ws.d_cnt[slot * C + c] : 0;
+#pragma unroll
+    for (int k = 0; k < kMaxDeltaParts; ++k) {
+      if (k >= KD) break;
+      const bool keep = lo > 0 && min(pmx[k], cap) == lo;
+      const int h = keep ? pcnt[k] : 0;
       dpc[c * kMaxDeltaParts + k] = h;
+      dmap[c * kMaxDeltaParts + k] = pmap[k];
       total += h;
     }
     dlen[c] = lo;
@@ -344,12 +358,23 @@ __device__ __forceinline__ ExpandResult gather_expand(
   const int64_t D = a.ix.delta_capacity;
   int32_t* mpos = (int32_t*)(smem + L.mpos) + wv * Rp;
   int32_t* mcache = (int32_t*)(smem + L.mcache) + (int64_t)wv * R * (K + 1);
+  // delta: each part's list index for this cap, read with the parts'
+  // counts by delta_combine (one dependent load per hit here)
+  const int32_t* dmap = (const int32_t*)(smem + L.dmap) + c * kMaxDeltaParts;
   for (int r = ln; r < occ; r += kWave) {
     int32_t pos;
     if (src == 1) {
       pos = sa_sample(a, sa_s, ilen, r);
     } else {
-      const int64_t e = (int64_t)delta_end_at(a, b, c, r, dpc) - len;
+      int k = 0, rr = r;
+      while (k < a.dparts - 1 && rr >= dpc[c * kMaxDeltaParts + k]) {
+        rr -= dpc[c * kMaxDeltaParts + k];
+        ++k;
+      }
+      const int m = dmap[k];
+      const int64_t slot = (int64_t)b * a.dparts + k;
+      const int64_t e =
+          (int64_t)a.ws.d_end[(slot * p.num_caps + m) * R + rr] - len;
       pos = (int32_t)(e < 0 ? 0 : e);
     }
     mpos[r] = pos;
@@ -639,7 +664,8 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
       int32_t* dlen = (int32_t*)(smem + L.dlen);
       int32_t* dcnt = (int32_t*)(smem + L.dcnt);
       int32_t* dpc = (int32_t*)(smem + L.dpc);
-      delta_combine(a, b, (const int32_t*)(smem + L.caps), dlen, dcnt, dpc);
+      delta_combine(a, b, (const int32_t*)(smem + L.caps), dlen, dcnt, dpc,
+                    (int32_t*)(smem + L.dmap));
       __syncthreads();
       for (int c = tid; c < C; c += NT) a.ws.dl_c[(int64_t)b * C + c] = dlen[c];
       SFX_TRACE_POINT(5);
@@ -660,7 +686,8 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
   int32_t* dlen = (int32_t*)(smem + L.dlen);
   int32_t* dcnt = (int32_t*)(smem + L.dcnt);
   int32_t* dpc = (int32_t*)(smem + L.dpc);
-  delta_combine(a, b, (const int32_t*)(smem + L.caps), dlen, dcnt, dpc);
+  delta_combine(a, b, (const int32_t*)(smem + L.caps), dlen, dcnt, dpc,
+                (int32_t*)(smem + L.dmap));
   __syncthreads();
   if (a.out.d_len || a.out.d_cnt)
     for (int c = tid; c < C; c += NT) {

@@ -51,7 +51,7 @@ constexpr int kSlots = kPosTile + kCap;  // positions a local workgroup reads
 // One 1024-thread workgroup per CU measured faster than 2 x 512 threads or
 // 2048-position tiles: fewer windows per wave, and one barrier pair per
 // 4096 positions.
-constexpr int kLocalThreads = 1024;
+constexpr int kSaLocalThreads = 1024;
 constexpr int kDigitBits = 9;
 constexpr int kRadix = 1 << kDigitBits;                 // 512
 constexpr uint32_t kFinished = 0xffffffffu;  // gp[] of a finished position
@@ -1030,8 +1030,8 @@ static int doubling_round(SaWs& w, int64_t nb, int64_t m, int round,
                           int global_path, hipStream_t stream) {
   const int cur = round & 1, nx = (round + 1) & 1;
   const int64_t nl = (m + kPosTile - 1) / kPosTile;
-  hipLaunchKernelGGL(k_sa_local<kLocalThreads>, dim3((unsigned)nl),
-                     dim3(kLocalThreads), 0, stream, w.gp, w.gsz, w.sa,
+  hipLaunchKernelGGL(k_sa_local<kSaLocalThreads>, dim3((unsigned)nl),
+                     dim3(kSaLocalThreads), 0, stream, w.gp, w.gsz, w.sa,
                      w.rank[cur], w.rank[nx], w.skip[cur], w.skip[nx], m, nl,
                      round, global_path, w.state);
   if (!global_path) return (int)hipGetLastError();
