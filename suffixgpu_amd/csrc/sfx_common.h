@@ -6,6 +6,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "suffixgpu_amd.h"
 
 // Phase timestamps for profiling builds (-DSFX_TRACE): thread 0 of each
@@ -94,6 +96,15 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
   v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf,
                                              false);  // row_bcast:31
   return v;
+}
+
+// Lane l of each row of 16 lanes takes lane l - 1's value; lane 0 of each
+// row takes `first`.
+__device__ __forceinline__ float lane_shr1(float v, float first) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, first),
+                                         __builtin_bit_cast(int, v), 0x111,
+                                         0xf, 0xf, false));  // row_shr:1
 }
 
 // Inclusive max-scan over the 64 lanes of a wave (unsigned; lanes shifted
@@ -264,8 +275,8 @@ __device__ __forceinline__ void hash_vote(int32_t v0, int32_t v1,
   wave_lds_sync();  // the table is rewritten by the next depth
 }
 
-// Depths the unit vote settles by counting alone (the fast path below).
-constexpr int kFastDepths = 32;
+// Depths of one segment of the unit vote (below).
+constexpr int kSegDepths = 16;
 
 // Wave-cooperative depth-wise majority vote of one candidate
 // (suffix_gpu/expand.py:59-147 == triton_kernels.py:139-215).
@@ -275,16 +286,22 @@ constexpr int kFastDepths = 32;
 // called for rows r < occ.  chain_out[0..K) receives the chain (-1 past
 // the first invalid depth).
 //
-// Unit votes with R <= 128 (two rows per lane) first take the fast path:
-// with r* the first active row, P the lane masks of the rows on the chain
-// (they agreed with every winner so far) and E those holding r*'s token at
-// depth d, |P & E| rows vote for r*'s token and |P & ~E| rows with a
-// token split among other values.  When the former is the larger count
-// r*'s token wins outright whatever the others hold, so such a depth costs
-// two ballots and the fp32 update of a full vote (the factor g / (g + 0)
-// is exactly 1 and skipped).  The first depth without that majority
-// continues in the full vote below with the rows still on the chain.  Most
-// candidates' rows agree, so most chains end on the fast path.
+// Unit votes with R <= 128 (two rows per lane) run in segments of up to
+// kSegDepths depths.  A segment starts at depth d from r*, the first row
+// on the chain (it agreed with every winner so far) that holds a token at
+// d.  Each row measures how many depths it agrees with r* for (its LDS
+// tokens compared four depths at a time, no cross-lane step), and one
+// ballot pass turns these lengths into, for every depth j of the window,
+// g_j rows holding r*'s token among those still on the chain and x_j rows
+// there holding another token.  Where g_j > x_j, r*'s token wins the full
+// vote outright whatever the others hold, with count g_j and denominator
+// g_j + x_j + alpha: every depth's factor is then one lane of a single
+// vector division (exactly 1, skipped, when x_j and alpha are 0), and the
+// chain probability and score are the same fp32 products and sums in
+// depth order, branch-free.  So a run of majority depths costs a fixed
+// number of steps, not one dependent ballot-and-divide round per depth.
+// The first depth without a majority takes one full vote, and the next
+// segment starts after it from the winner's rows.
 //
 // The full vote: up to kQuickVotes distinct
 // values are counted one at a time with two ballots (the first remaining
@@ -311,140 +328,238 @@ __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
 #ifdef SFX_TRACE
   const uint64_t t_start = wall_clock64();
   const uint64_t c_start = __builtin_amdgcn_s_memtime();
-  int st_quick = 0, st_hash = 0, st_full = 0, st_fast = 0;
+  int st_quick = 0, st_hash = 0, st_full = 0, st_seg = 0;
 #endif
   if (!kWeighted && R <= 2 * kWave) {
     const int r0 = ln;
     const int r1 = ln + kWave;
-    bool ok0 = r0 < R && (int64_t)r0 < occ;
-    bool ok1 = r1 < R && (int64_t)r1 < occ;
-    int v0 = ok0 && K > 0 ? cont_at(r0, 0) : -1;
-    int v1 = ok1 && K > 0 ? cont_at(r1, 0) : -1;
+    const bool in0 = r0 < R && (int64_t)r0 < occ;
+    const bool in1 = r1 < R && (int64_t)r1 < occ;
+    // Tokens at depth d of the rows on the chain (they agreed with every
+    // winner so far), -1 for the others and for rows without a token there
+    // (they leave the chain at d).
+    int v0 = in0 && K > 0 ? cont_at(r0, 0) : -1;
+    int v1 = in1 && K > 0 ? cont_at(r1, 0) : -1;
     bool ended = false;
-    {
+    bool vote = false;  // depth d is voted in full
+    int last_run = kSegDepths;  // depths the last segment settled
+    while (!ended && d < K) {
+      if (vote) {
+        // ---- one full vote at depth d over the rows on the chain; the
+        // voters' tokens at depth d + 1 (a superset of the survivors') are
+        // loaded meanwhile
+#ifdef SFX_TRACE
+        ++st_full;
+#endif
+        const bool nx = d + 1 < K;
+        const int n0 = nx && v0 != -1 ? cont_at(r0, d + 1) : -1;
+        const int n1 = nx && v1 != -1 ? cont_at(r1, d + 1) : -1;
+        uint64_t rem0 = ballot(v0 != -1);
+        uint64_t rem1 = ballot(v1 != -1);
+        const int nact = popc(rem0) + popc(rem1);
+        if (nact == 0) break;
+        const float denom = __fadd_rn((float)(nact > 1 ? nact : 1), alpha);
+        int bcnt = 0;
+        int btok = 0x7fffffff;
+        int left = nact;
+        for (int it = 0; it < kQuickVotes && left > 0 && left >= bcnt; ++it) {
+#ifdef SFX_TRACE
+          ++st_quick;
+#endif
+          int x;
+          if (rem0)
+            x = __builtin_amdgcn_readlane(v0, __builtin_ctzll(rem0));
+          else
+            x = __builtin_amdgcn_readlane(v1, __builtin_ctzll(rem1));
+          const uint64_t e0 = ballot(v0 == x) & rem0;
+          const uint64_t e1 = ballot(v1 == x) & rem1;
+          const int cnt = popc(e0) + popc(e1);
+          if (vote_better(cnt, x, bcnt, btok)) {
+            bcnt = cnt;
+            btok = x;
+          }
+          rem0 &= ~e0;
+          rem1 &= ~e1;
+          left -= cnt;
+        }
+        if (left > 0 && left >= bcnt) {
+          // Fewest votes that keep the chain probability >= min_prob: if
+          // neither the best so far nor any remaining value can reach it,
+          // the chain ends here whichever token wins.
+          const int vmin = min_votes(prob, denom, min_prob, nact);
+          if (vmin > nact || (left < vmin && bcnt < vmin)) break;
+#ifdef SFX_TRACE
+          ++st_hash;
+#endif
+          hash_vote(v0, v1, rem0, rem1, H, bcnt, btok);
+        }
+        const float vf = (float)bcnt;
+        prob = __fmul_rn(prob, __fdiv_rn(vf, denom));
+        const bool valid = (vf > 0.0f) && (prob >= min_prob);
+        if (!valid) break;
+        if (ln == 0) chain_out[d] = btok;
+        if ((int64_t)d < cap) score = __fadd_rn(score, prob);
+        v0 = v0 != -1 && v0 == btok ? n0 : -1;
+        v1 = v1 != -1 && v1 == btok ? n1 : -1;
+        ++d;
+        // A segment pays off over a run of majority depths: the next depth
+        // starts one when a single row is left (the bcnt winners stay),
+        // every voter agreed here, or this depth had a majority after a
+        // segment of several depths; otherwise it is voted in full as well.
+        vote = !(bcnt == 1 || bcnt == nact ||
+                 (2 * bcnt > nact && last_run >= 4));
+        continue;
+      }
+      // ---- one segment: depths d .. d + W - 1 against r*, the first row
+      // on the chain with a token at d
       const uint64_t s0 = ballot(v0 != -1);
       const uint64_t s1 = ballot(v1 != -1);
-      const int kf = K < kFastDepths ? K : kFastDepths;
-      if (s0 | s1) {
-        const int rs = s0 ? __builtin_ctzll(s0) : kWave + __builtin_ctzll(s1);
-        // rows past occ read row rs (their results are masked off)
-        const int q0 = ok0 ? r0 : rs;
-        const int q1 = ok1 ? r1 : rs;
-        // rows on the chain; depth d's tokens (a: row rs's, made scalar so
-        // that every test on it is uniform), depth d + 1's loaded ahead
-        uint64_t P0 = ballot(ok0), P1 = ballot(ok1);
-        int na = cont_at(rs, 0), t0 = v0, t1 = v1;
-        int n0 = -1, n1 = -1;
-        for (; d < kf; ++d) {
-          const int a = __builtin_amdgcn_readfirstlane(na);
-          if (d + 1 < kf) {
-            na = cont_at(rs, d + 1);
-            n0 = cont_at(q0, d + 1);
-            n1 = cont_at(q1, d + 1);
-          }
-          const uint64_t E0 = a != -1 ? ballot(t0 == a) : 0;
-          const uint64_t E1 = a != -1 ? ballot(t1 == a) : 0;
-          const uint64_t A0 = P0 & E0, A1 = P1 & E1;  // votes for a
-          const int g = popc(A0) + popc(A1);
-          const int x = popc(P0 & ~E0 & ballot(t0 != -1)) +
-                        popc(P1 & ~E1 & ballot(t1 != -1));
-          if (g <= x) break;  // no outright winner: full vote from here
-          // g / (g + 0) is exactly 1: the division is skipped then
-          float f = 1.0f;
-          if (x != 0 || alpha != 0.0f)
-            f = __fdiv_rn((float)g, __fadd_rn((float)(g + x), alpha));
-          prob = __fmul_rn(prob, f);
-          if (!(prob >= min_prob)) {
-            ended = true;
-            break;
-          }
-          if ((int64_t)d < cap) score = __fadd_rn(score, prob);
-          P0 = A0;
-          P1 = A1;
-          t0 = n0;
-          t1 = n1;
-        }
-        for (int dd = ln; dd < d; dd += kWave) chain_out[dd] = cont_at(rs, dd);
-        nv = d;
+      if (!(s0 | s1)) break;  // no row votes: the chain ends
 #ifdef SFX_TRACE
-        st_fast = d;
-        SFX_TRACE_STAT(5, wall_clock64() - t_start);
-        SFX_TRACE_STAT(4, __builtin_amdgcn_s_memtime() - c_start);
+      ++st_seg;
 #endif
-        if (!ended && d > 0) {
-          // the full vote continues with the rows still on the chain
-          ok0 = (P0 >> ln) & 1;
-          ok1 = (P1 >> ln) & 1;
-          if (d == kf && d < K) {  // not loaded ahead
-            t0 = ok0 ? cont_at(r0, d) : -1;
-            t1 = ok1 ? cont_at(r1, d) : -1;
-          }
-          v0 = ok0 ? t0 : -1;
-          v1 = ok1 ? t1 : -1;
+      const bool p0 = v0 != -1;
+      const bool p1 = v1 != -1;
+      const int rs = s0 ? __builtin_ctzll(s0) : kWave + __builtin_ctzll(s1);
+      const int nP = popc(s0) + popc(s1);
+      {
+        // Depth d itself without a majority for r*'s token: no segment
+        const int a0 = __builtin_amdgcn_readlane(s0 ? v0 : v1, rs & 63);
+        const int g0 = popc(ballot(v0 == a0)) + popc(ballot(v1 == a0));
+        if (2 * g0 <= nP) {
+          vote = true;
+          continue;
         }
       }
+      const int W = K - d < kSegDepths ? K - d : kSegDepths;
+      // lane j < W: r*'s token at depth d + j; no row agrees with r* from
+      // its first -1 on (We >= 1: r* holds a token at d)
+      const int refv = ln < W ? cont_at(rs, d + ln) : -1;
+      const uint64_t rend = ballot(ln < W && refv == -1);
+      const int We = rend ? __builtin_ctzll(rend) : W;
+      // Agreement of each row with r*: the first depth of the window where
+      // its token differs and that token, found by visiting the depths from
+      // the last, eight loads in flight per row (rows off the chain read
+      // r*'s tokens and are dropped below; depths past the window reread
+      // its last one).
+      const int q0 = p0 ? r0 : rs;
+      const int q1 = p1 ? r1 : rs;
+      int au0 = W, au1 = W, dt0 = -1, dt1 = -1;
+      auto agree8 = [&](int jb, auto two) {
+        int t0[8], t1[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int jj = jb + u < W ? jb + u : W - 1;
+          t0[u] = cont_at(q0, d + jj);
+          if (two) t1[u] = cont_at(q1, d + jj);
+        }
+#pragma unroll
+        for (int u = 7; u >= 0; --u) {
+          const int a = __builtin_amdgcn_readlane(refv, jb + u);
+          au0 = t0[u] != a ? jb + u : au0;
+          dt0 = t0[u] != a ? t0[u] : dt0;
+          if (two) {
+            au1 = t1[u] != a ? jb + u : au1;
+            dt1 = t1[u] != a ? t1[u] : dt1;
+          }
+        }
+      };
+      static_assert(kSegDepths == 16, "two batches of eight depths");
+      // (depth We itself is scanned too: a vote there takes its tokens)
+      if (s1 != 0) {
+        if (We >= 8) agree8(8, std::true_type());
+        agree8(0, std::true_type());
+      } else {
+        if (We >= 8) agree8(8, std::false_type());
+        agree8(0, std::false_type());
+      }
+      // agreement lengths within the window (-1 off the chain)
+      const int ag0 = p0 ? (au0 < We ? au0 : We) : -1;
+      const int ag1 = p1 ? (au1 < We ? au1 : We) : -1;
+      // Per depth j (lane j): g rows holding r*'s token at depth d + j
+      // among those still on the chain there (agreement > j), x rows there
+      // voting for another token (agreement == j, a token there).  r*'s
+      // token wins outright when g > x, with the full vote's count g and
+      // denominator g + x.  The agreement histogram (hg) and the voters'
+      // one (hx) are counted in H.
+      int* hg = H;
+      int* hx = H + 32;
+      H[ln] = 0;
+      wave_lds_sync();
+      if (ag0 >= 0) {
+        atomicAdd(&hg[ag0], 1);
+        if (ag0 < We && dt0 != -1) atomicAdd(&hx[ag0], 1);
+      }
+      if (ag1 >= 0) {
+        atomicAdd(&hg[ag1], 1);
+        if (ag1 < We && dt1 != -1) atomicAdd(&hx[ag1], 1);
+      }
+      wave_lds_sync();
+      const int gv =
+          nP - (int)wave_incl_scan(ln < 32 ? (uint32_t)hg[ln] : 0u);
+      const int xv = ln < 32 ? hx[ln] : 0;
+      const uint64_t maj = ballot(ln < We && gv > xv);
+      const int m = __builtin_ctzll(~maj);  // <= We (lanes >= We: 0)
+      // g / (g + 0) is exactly 1: no division then
+      float f = 1.0f;
+      if (xv != 0 || alpha != 0.0f)
+        f = __fdiv_rn((float)gv, __fadd_rn((float)(gv + xv), alpha));
+      // Lane j: the chain probability after depth d + j, the fp32 product
+      // in depth order -- each step takes the left neighbour's product
+      // (lane 0: the probability before the window), so after step s
+      // lanes 0 .. s hold their final values.
+      float pv = f;
+#pragma unroll
+      for (int sb = 0; sb < kSegDepths; sb += 4) {
+        if (sb >= m) break;
+#pragma unroll
+        for (int s = sb; s < sb + 4; ++s)
+          pv = __fmul_rn(lane_shr1(pv, prob), f);
+      }
+      const uint64_t okp = ballot(ln < m && pv >= min_prob);
+      const int jn = __builtin_ctzll(~okp);  // depths kept, <= m
+      // the score: the same in-order fp32 sum over depths below cap
+      const int64_t room = cap - (int64_t)d;
+      const int lim = room < (int64_t)jn ? (room < 0 ? 0 : (int)room) : jn;
+      if (lim > 0) {
+        const float av = ln < lim ? pv : 0.0f;
+        float sv = av;
+#pragma unroll
+        for (int sb = 0; sb < kSegDepths; sb += 4) {
+          if (sb >= lim) break;
+#pragma unroll
+          for (int s = sb; s < sb + 4; ++s)
+            sv = __fadd_rn(lane_shr1(sv, score), av);
+        }
+        score = __builtin_bit_cast(
+            float,
+            __builtin_amdgcn_readlane(__builtin_bit_cast(int, sv), lim - 1));
+      }
+      if (jn > 0)
+        prob = __builtin_bit_cast(
+            float,
+            __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv), jn - 1));
+      if (ln < jn) chain_out[d + ln] = refv;
+      last_run = jn;
+      const bool k0 = ag0 >= jn;
+      const bool k1 = ag1 >= jn;
+      if (jn < m) {
+        ended = true;  // the chain probability fell below min_prob
+      } else if (jn < W) {
+        // Depth d + jn has no majority for r*'s token: voted in full, with
+        // the tokens there already known -- r*'s for rows that agree with
+        // it there, else the row's first differing token.
+        vote = true;
+        const int rj = __builtin_amdgcn_readlane(refv, jn);
+        v0 = k0 ? (au0 > jn ? rj : dt0) : -1;
+        v1 = k1 ? (au1 > jn ? rj : dt1) : -1;
+      } else if (d + jn < K) {
+        v0 = k0 ? cont_at(r0, d + jn) : -1;
+        v1 = k1 ? cont_at(r1, d + jn) : -1;
+      }
+      d += jn;
     }
-    for (; !ended && d < K; ++d) {
-      const bool a0 = ok0 && v0 != -1;
-      const bool a1 = ok1 && v1 != -1;
-      // next depth's tokens for every row still on the chain (a superset
-      // of the survivors), loaded while this depth votes
-      const int n0 = a0 && d + 1 < K ? cont_at(r0, d + 1) : -1;
-      const int n1 = a1 && d + 1 < K ? cont_at(r1, d + 1) : -1;
-      uint64_t rem0 = ballot(a0);
-      uint64_t rem1 = ballot(a1);
-      const int nact = popc(rem0) + popc(rem1);
-      if (nact == 0) break;
-      const float denom = __fadd_rn((float)(nact > 1 ? nact : 1), alpha);
-      int bcnt = 0;
-      int btok = 0x7fffffff;
-      int left = nact;
-#ifdef SFX_TRACE
-      ++st_full;
-#endif
-      for (int it = 0; it < kQuickVotes && left > 0 && left >= bcnt; ++it) {
-#ifdef SFX_TRACE
-        ++st_quick;
-#endif
-        int x;
-        if (rem0)
-          x = __builtin_amdgcn_readlane(v0, __builtin_ctzll(rem0));
-        else
-          x = __builtin_amdgcn_readlane(v1, __builtin_ctzll(rem1));
-        const uint64_t e0 = ballot(v0 == x) & rem0;
-        const uint64_t e1 = ballot(v1 == x) & rem1;
-        const int cnt = popc(e0) + popc(e1);
-        if (vote_better(cnt, x, bcnt, btok)) {
-          bcnt = cnt;
-          btok = x;
-        }
-        rem0 &= ~e0;
-        rem1 &= ~e1;
-        left -= cnt;
-      }
-      if (left > 0 && left >= bcnt) {
-        // Fewest votes that keep the chain probability >= min_prob: if
-        // neither the best so far nor any remaining value can reach it,
-        // the chain ends here whichever token wins.
-        const int vmin = min_votes(prob, denom, min_prob, nact);
-        if (vmin > nact || (left < vmin && bcnt < vmin)) break;
-#ifdef SFX_TRACE
-        ++st_hash;
-#endif
-        hash_vote(v0, v1, rem0, rem1, H, bcnt, btok);
-      }
-      const float vf = (float)bcnt;
-      prob = __fmul_rn(prob, __fdiv_rn(vf, denom));
-      const bool valid = (vf > 0.0f) && (prob >= min_prob);
-      if (!valid) break;
-      if (ln == 0) chain_out[d] = btok;
-      if ((int64_t)d < cap) score = __fadd_rn(score, prob);
-      ++nv;
-      ok0 = a0 && v0 == btok;
-      ok1 = a1 && v1 == btok;
-      v0 = n0;
-      v1 = n1;
-    }
+    nv = d;
   } else {
     const int nslot = (R + kWave - 1) / kWave;  // <= 32 (R <= 2048)
     uint32_t ok = 0;
@@ -526,7 +641,7 @@ __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
   for (int dd = d + ln; dd < K; dd += kWave) chain_out[dd] = -1;
 #ifdef SFX_TRACE
   SFX_TRACE_STAT(0, occ);
-  SFX_TRACE_STAT(1, st_fast);
+  SFX_TRACE_STAT(1, st_seg);
   SFX_TRACE_STAT(2, st_full + 1000 * st_hash);
   SFX_TRACE_STAT(3, st_quick);
   SFX_TRACE_STAT(6, wall_clock64() - t_start);
