@@ -65,7 +65,7 @@ __host__ __device__ inline GlobalLayout global_layout(int P, int C, int R,
   L.lb = g_take(off, P * 8);
   L.ub = g_take(off, P * 8);
   L.found = g_take(off, C * 4);
-  L.scan = g_take(off, 4 * NW * 8);
+  L.scan = g_take(off, 2 * 4 * NW * 8);
   L.red = g_take(off, NW * 4);
   L.misc = g_take(off, 64);
   L.lo = g_take(off, C * 4);
@@ -261,7 +261,7 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
   for (int g0 = 0; g0 < nu; g0 += 8)
     compact_first_r<NT>(mb, phi - plo, ulo + g0, min(8, nu - g0), R,
                         a.ws.d_end + (slot * C + g0) * R, (int32_t)plo,
-                        found + g0, scan);
+                        found + g0, scan, (g0 >> 3) & 1);
   __syncthreads();
   SFX_TRACE_POINT(3);
   for (int c = tid; c < C; c += NT) {

@@ -66,7 +66,7 @@ __host__ __device__ inline LocalLayout local_layout(int S, int P, int C,
   L.cand = lds_take(off, C * 4);
   L.found = lds_take(off, C * 4);
   L.thr = lds_take(off, C * 4);
-  L.scan = lds_take(off, 4 * nwaves * 8);
+  L.scan = lds_take(off, 2 * 4 * nwaves * 8);
   L.occ = lds_take(off, C * R * 4);
   L.A = lds_take(off, nwaves * ((R + 3) & ~3) * 4);
   L.H = lds_take(off, nwaves * 2 * kHashSlots * 4);
@@ -375,7 +375,7 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
   if (!kStream) {
     for (int g0 = 0; g0 < C; g0 += 8)
       compact_first_r<NT>(mbuf, qe, cand + g0, min(8, C - g0), R,
-                          occ + g0 * R, 0, found + g0, scan);
+                          occ + g0 * R, 0, found + g0, scan, (g0 >> 3) & 1);
     __syncthreads();
   } else {
     // Chunks in ascending order; a single chunk's match lengths are still
@@ -392,7 +392,8 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
       }
       for (int g0 = 0; g0 < C; g0 += 8)
         compact_first_r<NT, true>(mbuf, cend - c0, cand + g0, min(8, C - g0),
-                                  R, occ + g0 * R, c0, found + g0, scan);
+                                  R, occ + g0 * R, c0, found + g0, scan,
+                                  (g0 >> 3) & 1);
       __syncthreads();
       bool open = false;
       for (int c = 0; c < C; ++c) open |= cand[c] > 0 && found[c] < R;

@@ -658,41 +658,65 @@ struct NoWeight {
 };
 
 // ------------------------------------------------- ordered compaction
-// Block-wide exclusive prefix sums of 8 per-thread counters.  `scratch`
-// holds 8 * (NT/64) u32 in LDS.  Two barriers.
+// Inclusive prefix sum over the 16 lanes of each row (DPP row shifts).
+__device__ __forceinline__ uint32_t row16_incl_scan(uint32_t v) {
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf,
+                                             false);  // row_shr:1
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf,
+                                             false);  // row_shr:2
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf,
+                                             false);  // row_shr:4
+  v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf,
+                                             false);  // row_shr:8
+  return v;
+}
+
+// Block-wide exclusive prefix sums of up to 8 per-thread counters (those
+// with on[c]; the others read 0), and their block totals, with one
+// barrier: the waves' inclusive scans leave each wave's totals in
+// `scratch` (8 * (NT/64) u32 of LDS), and every wave then scans the
+// waves' totals itself -- lane w holds wave w's, one 16-lane scan per
+// counter -- instead of every thread adding up all the waves.  A
+// following call must use another scratch area (or come after a barrier):
+// waves leave while slower ones still read this one's.
 template <int NT>
 __device__ __forceinline__ void block_exscan8(const uint32_t (&v)[8],
+                                              const bool (&on)[8],
                                               uint32_t (&pre)[8],
                                               uint32_t (&tot)[8],
                                               uint32_t* scratch) {
   constexpr int NW = NT / kWave;
+  static_assert(NW <= 16, "one row of 16 lanes holds the waves' totals");
   const int ln = lane_id();
   const int wv = threadIdx.x / kWave;
   uint32_t inc[8];
 #pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    inc[c] = wave_incl_scan(v[c]);
-    if (ln == kWave - 1) scratch[wv * 8 + c] = inc[c];
+  for (int c = 0; c < 8; ++c) inc[c] = on[c] ? wave_incl_scan(v[c]) : 0u;
+  if (ln == kWave - 1) {
+    reinterpret_cast<uint4*>(scratch + wv * 8)[0] =
+        make_uint4(inc[0], inc[1], inc[2], inc[3]);
+    reinterpret_cast<uint4*>(scratch + wv * 8)[1] =
+        make_uint4(inc[4], inc[5], inc[6], inc[7]);
   }
   __syncthreads();
-  uint32_t before[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  uint32_t all[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int w = 0; w < NW; ++w) {
-    const uint4 lo = *reinterpret_cast<const uint4*>(scratch + w * 8);
-    const uint4 hi = *reinterpret_cast<const uint4*>(scratch + w * 8 + 4);
-    const uint32_t t8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+  uint4 lo = make_uint4(0u, 0u, 0u, 0u), hi = lo;
+  if (ln < NW) {
+    lo = reinterpret_cast<const uint4*>(scratch + ln * 8)[0];
+    hi = reinterpret_cast<const uint4*>(scratch + ln * 8)[1];
+  }
+  const uint32_t t8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      if (w < wv) before[c] += t8[c];
-      all[c] += t8[c];
+  for (int c = 0; c < 8; ++c) {
+    uint32_t before = 0, all = 0;
+    if (on[c]) {
+      const uint32_t x = row16_incl_scan(t8[c]);
+      before = wv > 0 ? (uint32_t)__builtin_amdgcn_readlane((int)x, wv - 1)
+                      : 0u;
+      all = (uint32_t)__builtin_amdgcn_readlane((int)x, NW - 1);
     }
+    pre[c] = before + inc[c] - v[c];
+    tot[c] = all;
   }
-#pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    pre[c] = before[c] + inc[c] - v[c];
-    tot[c] = all[c];
-  }
-  __syncthreads();
 }
 
 // Per-byte test x >= t (1 <= t <= 255) on four u8 match lengths at once,
@@ -740,24 +764,37 @@ __device__ __forceinline__ uint4 clear_from(uint4 q, int r) {
 // below R.  out[c * R + slot] = out_base + position; count[c] =
 // min(hits, R).  With kAcc the call continues an earlier one over the
 // preceding positions: count[c] holds the hits kept so far, new hits take
-// the slots after them and count[c] = min(count[c] + hits, R).  thr, out
-// and count may be LDS or global.  All threads of the block must call it.
+// the slots after them and count[c] = min(count[c] + hits, R) (the calls
+// are separated by a barrier).  thr is LDS holding nthr thresholds; out
+// and count may be LDS or global.  scratch holds 2 * 8 * (NT/64) u32 of
+// LDS: consecutive calls alternate its halves (buf 0, 1, 0, ...) or are
+// separated by a barrier.  All threads of the block must call it.
 template <int NT, bool kAcc = false, typename MbPtr>
 __device__ __forceinline__ void compact_first_r(MbPtr mb, int64_t n,
                                                 const int* thr, int nthr,
                                                 int R, int32_t* out,
                                                 int32_t out_base, int* count,
-                                                uint32_t* scratch) {
+                                                uint32_t* scratch, int buf) {
   int64_t seg = (n + NT - 1) / NT;
   seg = (seg + 15) & ~(int64_t)15;
   const int64_t beg = (int64_t)threadIdx.x * seg;
   const int64_t end = beg + seg < n ? beg + seg : n;
-  ByteGe ge[8];
-  uint32_t kept[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  // the thresholds (and kept counts) as independent loads
+  int tv[8];
+  uint32_t kept[8];
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
-    if (kAcc && c < nthr) kept[c] = (uint32_t)count[c];
-    ge[c] = byte_ge_init(c < nthr && kept[c] < (uint32_t)R ? thr[c] : 0);
+    const int cc = c < nthr ? c : 0;
+    tv[c] = thr[cc];
+    kept[c] = kAcc ? (uint32_t)count[cc] : 0u;
+  }
+  ByteGe ge[8];
+  bool on[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    if (c >= nthr) kept[c] = 0u;
+    ge[c] = byte_ge_init(c < nthr && kept[c] < (uint32_t)R ? tv[c] : 0);
+    on[c] = ge[c].on;
   }
   uint32_t cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   for (int64_t i0 = beg; i0 < end; i0 += 16) {
@@ -774,7 +811,7 @@ __device__ __forceinline__ void compact_first_r(MbPtr mb, int64_t n,
   }
   uint32_t off[8], tot[8];
   SFX_TRACE_POINT(7);
-  block_exscan8<NT>(cnt, off, tot, scratch);
+  block_exscan8<NT>(cnt, on, off, tot, scratch + buf * (8 * (NT / kWave)));
   SFX_TRACE_POINT(8);
 #pragma unroll
   for (int c = 0; c < 8; ++c) {
