@@ -171,28 +171,6 @@ __device__ __forceinline__ bool vote_better(int cnt, int tok, int bcnt,
   return cnt > bcnt || (cnt == bcnt && tok < btok);
 }
 
-// Smallest v in [1, nact] with fl32(prob * fl32(v / denom)) >= min_prob,
-// or nact + 1 when none (the product is monotone in v for denom > 0 and
-// prob >= 0).  Returns 1 when the early exit does not apply.  The rounded
-// product stays within a few ulps of prob * v / denom while consecutive v
-// differ by a factor of at least 1 + 1/nact, so the real-valued threshold
-// rounded up is within one of the answer; exact checks settle it.
-__device__ __forceinline__ int min_votes(float prob, float denom,
-                                         float min_prob, int nact) {
-  if (!(min_prob > 0.0f) || !(denom > 0.0f) || !(prob > 0.0f)) return 1;
-  auto pass = [&](int v) {
-    return __fmul_rn(prob, __fdiv_rn((float)v, denom)) >= min_prob;
-  };
-  if (!pass(nact)) return nact + 1;
-  float t = __fdividef(min_prob, prob) * denom;
-  t = t < (float)nact ? t : (float)nact;
-  int v = (int)ceilf(t);
-  v = v < 1 ? 1 : v;
-  while (v > 1 && pass(v - 1)) --v;
-  while (!pass(v)) ++v;  // ends: pass(nact) holds
-  return v;
-}
-
 // ---------------------------------------------------------- vote helpers
 // Uniform maximum of an unsigned value over the wave.
 __device__ __forceinline__ uint32_t wave_all_max(uint32_t v) {
@@ -206,73 +184,56 @@ __device__ __forceinline__ int32_t wave_all_min(int32_t v) {
   return (int32_t)(~m ^ 0x80000000u);
 }
 
-constexpr int kHashSlots = 256;  // per wave: keys then counts (2 KiB)
-constexpr int kQuickVotes = 4;   // distinct values counted one at a time
+constexpr int kHashSlots = 256;  // per wave LDS area H: 2 * kHashSlots ints
+constexpr int kVoteSlots = 2 * kHashSlots;
 
-__device__ __forceinline__ int hash_slot(int32_t v) {
-  return (int)(((uint32_t)v * 0x9E3779B1u) >> 24);
+__device__ __forceinline__ int vote_slot(int32_t v) {
+  return (int)(((uint32_t)v * 0x9E3779B1u) >> 23);  // 9 bits
 }
 
-// Slot of v (!= INT32_MIN) in an open-addressing table of kHashSlots
-// keys (INT32_MIN = empty) with its count incremented.
-__device__ __forceinline__ int hash_add(int32_t* keys, int32_t* cnts,
-                                        int32_t v) {
-  int h = hash_slot(v);
-  while (true) {
-    const int32_t old = atomicCAS(&keys[h], (int32_t)0x80000000, v);
-    if (old == (int32_t)0x80000000 || old == v) {
-      atomicAdd(&cnts[h], 1);
-      return h;
-    }
-    h = (h + 1) & (kHashSlots - 1);
-  }
-}
-
-// Folds the remaining rows' values (lane masks rem0 over v0, rem1 over v1;
-// every row of a value is remaining or none is) into the running vote
-// (bcnt, btok): all their counts at once in the LDS table H.
-__device__ __forceinline__ void hash_vote(int32_t v0, int32_t v1,
-                                          uint64_t rem0, uint64_t rem1,
-                                          int32_t* H, int& bcnt, int& btok) {
+// Folds the vote over the rows' values v0, v1 (-1: no vote) into the
+// running best (bcnt, btok): most rows, then the smallest value.  The rows
+// of btok are counted already.  Every row adds one to its value's slot of
+// an LDS count table H (kVoteSlots ints, by hash; plain atomics, no
+// probing), so a slot's count bounds the count of each value in it from
+// above.  The value with the largest bound (the smallest value on ties) is
+// counted exactly with two ballots; when the bound was exact no other
+// value can beat it, otherwise values are taken in bound order until no
+// remaining bound can beat the best.
+__device__ __forceinline__ void count_vote(int32_t v0, int32_t v1,
+                                           int32_t* H, int& bcnt, int& btok) {
   const int ln = lane_id();
-  const uint64_t me = 1ull << ln;
-  // INT32_MIN marks empty slots: count that value, if present, directly.
-  {
-    const uint64_t e0 = ballot(v0 == (int32_t)0x80000000) & rem0;
-    const uint64_t e1 = ballot(v1 == (int32_t)0x80000000) & rem1;
-    const int cnt = popc(e0) + popc(e1);
-    if (cnt > 0 && vote_better(cnt, (int32_t)0x80000000, bcnt, btok)) {
-      bcnt = cnt;
-      btok = (int32_t)0x80000000;
+  int4* H4 = reinterpret_cast<int4*>(H);
+  H4[ln] = make_int4(0, 0, 0, 0);
+  H4[ln + kWave] = make_int4(0, 0, 0, 0);
+  wave_lds_sync();
+  const bool a0 = v0 != -1;
+  const bool a1 = v1 != -1;
+  const int h0 = vote_slot(v0);
+  const int h1 = vote_slot(v1);
+  if (a0) atomicAdd(&H[h0], 1);
+  if (a1) atomicAdd(&H[h1], 1);
+  wave_lds_sync();
+  const bool known = bcnt > 0;
+  uint32_t u0 = a0 && !(known && v0 == btok) ? (uint32_t)H[h0] : 0u;
+  uint32_t u1 = a1 && !(known && v1 == btok) ? (uint32_t)H[h1] : 0u;
+  wave_lds_sync();  // the table is rewritten by the next call
+  while (true) {
+    const uint32_t mu = wave_all_max(u0 > u1 ? u0 : u1);
+    if (mu == 0u || (int)mu < bcnt) break;
+    const int32_t t0 = u0 == mu ? v0 : 0x7fffffff;
+    const int32_t t1 = u1 == mu ? v1 : 0x7fffffff;
+    const int32_t x = wave_all_min(t0 < t1 ? t0 : t1);
+    if ((int)mu == bcnt && x > btok) break;
+    const int c = popc(ballot(v0 == x)) + popc(ballot(v1 == x));
+    if (vote_better(c, x, bcnt, btok)) {
+      bcnt = c;
+      btok = x;
     }
-    rem0 &= ~e0;
-    rem1 &= ~e1;
+    if ((uint32_t)c == mu) break;  // an exact bound: x beats the rest
+    u0 = v0 == x ? 0u : u0;
+    u1 = v1 == x ? 0u : u1;
   }
-  if ((rem0 | rem1) == 0) return;
-  int32_t* keys = H;
-  int32_t* cnts = H + kHashSlots;
-  reinterpret_cast<int4*>(keys)[ln] =
-      make_int4((int32_t)0x80000000, (int32_t)0x80000000,
-                (int32_t)0x80000000, (int32_t)0x80000000);
-  reinterpret_cast<int4*>(cnts)[ln] = make_int4(0, 0, 0, 0);
-  wave_lds_sync();
-  const bool in0 = (rem0 & me) != 0;
-  const bool in1 = (rem1 & me) != 0;
-  int h0 = 0, h1 = 0;
-  if (in0) h0 = hash_add(keys, cnts, v0);
-  if (in1) h1 = hash_add(keys, cnts, v1);
-  wave_lds_sync();
-  const uint32_t c0 = in0 ? (uint32_t)cnts[h0] : 0u;
-  const uint32_t c1 = in1 ? (uint32_t)cnts[h1] : 0u;
-  const uint32_t mc = wave_all_max(c0 > c1 ? c0 : c1);
-  const int32_t t0 = c0 == mc ? v0 : 0x7fffffff;
-  const int32_t t1 = c1 == mc ? v1 : 0x7fffffff;
-  const int32_t mt = wave_all_min(t0 < t1 ? t0 : t1);
-  if (vote_better((int)mc, mt, bcnt, btok)) {
-    bcnt = (int)mc;
-    btok = mt;
-  }
-  wave_lds_sync();  // the table is rewritten by the next depth
 }
 
 // Depths of one segment of the unit vote (below).
@@ -289,30 +250,32 @@ constexpr int kSegDepths = 16;
 // Unit votes with R <= 128 (two rows per lane) run in segments of up to
 // kSegDepths depths.  A segment starts at depth d from r*, the first row
 // on the chain (it agreed with every winner so far) that holds a token at
-// d.  Each row measures how many depths it agrees with r* for (its LDS
-// tokens compared four depths at a time, no cross-lane step), and one
-// ballot pass turns these lengths into, for every depth j of the window,
-// g_j rows holding r*'s token among those still on the chain and x_j rows
-// there holding another token.  Where g_j > x_j, r*'s token wins the full
-// vote outright whatever the others hold, with count g_j and denominator
+// d.  Each row finds the first depth of the window where its token differs
+// from r*'s (its LDS tokens loaded eight at a time, compared by selects,
+// no cross-lane step), and an LDS histogram of these agreement lengths and
+// one DPP scan give, for every depth j of the window, g_j rows holding
+// r*'s token among those still on the chain and x_j rows there holding
+// another token.  Where g_j > x_j, r*'s token wins the full vote outright
+// whatever the others hold, with count g_j and denominator
 // g_j + x_j + alpha: every depth's factor is then one lane of a single
 // vector division (exactly 1, skipped, when x_j and alpha are 0), and the
 // chain probability and score are the same fp32 products and sums in
-// depth order, branch-free.  So a run of majority depths costs a fixed
-// number of steps, not one dependent ballot-and-divide round per depth.
-// The first depth without a majority takes one full vote, and the next
-// segment starts after it from the winner's rows.
+// depth order, computed lane after lane with DPP shifts.  So a run of
+// majority depths costs a fixed number of steps, not one dependent
+// ballot-and-divide round per depth.  A segment starts only where depth d
+// holds a majority for r*'s token (two ballots); a depth without one takes
+// a full vote, after which another segment starts when a single row is
+// left, all voters agreed, or the depth had a majority after a segment of
+// several depths -- else the next depth is voted in full too.  The tokens
+// of the next depth are in flight during a full vote, and a segment that
+// stops at a depth without a majority hands that depth's tokens on.
 //
-// The full vote: up to kQuickVotes distinct
-// values are counted one at a time with two ballots (the first remaining
-// row's value is broadcast, its matches counted and retired), stopping as
-// soon as the remaining rows cannot outvote the best -- which settles most
-// depths, where the rows mostly agree.  Otherwise the min_prob bound may
-// already end the chain, and if not, every remaining value is counted at
-// once in a per-wave LDS hash table H (2 * kHashSlots ints).  Larger R and
-// weighted votes compact the active rows into A (row order) and count by
-// broadcast LDS reads.  A holds R ints; W (weighted votes only) R floats,
-// both LDS.
+// The full vote: the first voter's value is counted with two ballots and
+// settles a depth where it holds a majority; otherwise every value is
+// counted at once (count_vote).  Larger R and weighted votes compact the
+// active rows into A (row order) and count by broadcast LDS reads.  A
+// holds R ints; W (weighted votes only) R floats, both LDS.  H is a
+// per-wave LDS area of 2 * kHashSlots ints.
 template <bool kWeighted, class ContFn, class WeightFn>
 __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
                                                     WeightFn weight_at,
@@ -328,7 +291,7 @@ __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
 #ifdef SFX_TRACE
   const uint64_t t_start = wall_clock64();
   const uint64_t c_start = __builtin_amdgcn_s_memtime();
-  int st_quick = 0, st_hash = 0, st_full = 0, st_seg = 0;
+  int st_hash = 0, st_full = 0, st_seg = 0;
 #endif
   if (!kWeighted && R <= 2 * kWave) {
     const int r0 = ln;
@@ -354,44 +317,22 @@ __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
         const bool nx = d + 1 < K;
         const int n0 = nx && v0 != -1 ? cont_at(r0, d + 1) : -1;
         const int n1 = nx && v1 != -1 ? cont_at(r1, d + 1) : -1;
-        uint64_t rem0 = ballot(v0 != -1);
-        uint64_t rem1 = ballot(v1 != -1);
+        const uint64_t rem0 = ballot(v0 != -1);
+        const uint64_t rem1 = ballot(v1 != -1);
         const int nact = popc(rem0) + popc(rem1);
         if (nact == 0) break;
         const float denom = __fadd_rn((float)(nact > 1 ? nact : 1), alpha);
-        int bcnt = 0;
-        int btok = 0x7fffffff;
-        int left = nact;
-        for (int it = 0; it < kQuickVotes && left > 0 && left >= bcnt; ++it) {
-#ifdef SFX_TRACE
-          ++st_quick;
-#endif
-          int x;
-          if (rem0)
-            x = __builtin_amdgcn_readlane(v0, __builtin_ctzll(rem0));
-          else
-            x = __builtin_amdgcn_readlane(v1, __builtin_ctzll(rem1));
-          const uint64_t e0 = ballot(v0 == x) & rem0;
-          const uint64_t e1 = ballot(v1 == x) & rem1;
-          const int cnt = popc(e0) + popc(e1);
-          if (vote_better(cnt, x, bcnt, btok)) {
-            bcnt = cnt;
-            btok = x;
-          }
-          rem0 &= ~e0;
-          rem1 &= ~e1;
-          left -= cnt;
-        }
-        if (left > 0 && left >= bcnt) {
-          // Fewest votes that keep the chain probability >= min_prob: if
-          // neither the best so far nor any remaining value can reach it,
-          // the chain ends here whichever token wins.
-          const int vmin = min_votes(prob, denom, min_prob, nact);
-          if (vmin > nact || (left < vmin && bcnt < vmin)) break;
+        // The first voter's value, counted with two ballots, settles a
+        // depth where it holds a majority; otherwise every value is counted
+        // at once.
+        int btok = rem0 ? __builtin_amdgcn_readlane(v0, __builtin_ctzll(rem0))
+                        : __builtin_amdgcn_readlane(v1, __builtin_ctzll(rem1));
+        int bcnt = popc(ballot(v0 == btok)) + popc(ballot(v1 == btok));
+        if (2 * bcnt <= nact) {
 #ifdef SFX_TRACE
           ++st_hash;
 #endif
-          hash_vote(v0, v1, rem0, rem1, H, bcnt, btok);
+          count_vote(v0, v1, H, bcnt, btok);
         }
         const float vf = (float)bcnt;
         prob = __fmul_rn(prob, __fdiv_rn(vf, denom));
@@ -643,7 +584,6 @@ __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
   SFX_TRACE_STAT(0, occ);
   SFX_TRACE_STAT(1, st_seg);
   SFX_TRACE_STAT(2, st_full + 1000 * st_hash);
-  SFX_TRACE_STAT(3, st_quick);
   SFX_TRACE_STAT(6, wall_clock64() - t_start);
   SFX_TRACE_STAT(7, nv);
 #endif
