@@ -234,8 +234,8 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
     // is tested against the newest pattern token first and only ends that
     // pass walk further back.  Match lengths are stored as one u32 of four
     // bytes; positions from qe on are never read (the compaction stops
-    // there).  Each wave adds equal lengths to the histogram with one LDS
-    // atomic (matches pile onto hist[1] and hist[2] on repetitive rows).
+    // there).  Every nonzero length adds one to the histogram with an LDS
+    // atomic.
     // The first four pattern tokens are tested at every end without a
     // branch (two 16-byte reads give x(i0 - 4) .. x(i0 + 3)); only ends
     // matching all four walk further back.  On rows whose newest token is
@@ -291,14 +291,7 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int m = (int)((word >> (8 * u)) & 0xffu);
-        uint64_t pend = ballot(m > 0);
-        while (pend) {
-          const int lead = __builtin_ctzll(pend);
-          const int mv = __builtin_amdgcn_readlane(m, lead);
-          const uint64_t same = ballot(m == mv) & pend;
-          if (ln == lead) atomicAdd(&hist[mv], popc(same));
-          pend &= ~same;
-        }
+        if (m > 0) atomicAdd(&hist[m], 1);
       }
     }
     __syncthreads();
