@@ -243,18 +243,36 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
   const int32_t* caps = (const int32_t*)(smem + L.caps);
   int32_t* ulo = (int32_t*)(smem + L.ulo);
   int32_t* umap = (int32_t*)(smem + L.umap);
-  if (tid == 0) {
-    // distinct thresholds in cap order; list u serves every cap mapped to u
-    int nu = 0;
-    for (int c = 0; c < C; ++c) {
-      const int t = min(part_max, caps[c]);
-      lo_lds[c] = t;
-      int u = 0;
-      while (u < nu && ulo[u] != t) ++u;
-      if (u == nu) ulo[nu++] = t;
-      umap[c] = u;
+  // Distinct thresholds in cap order; list u serves every cap mapped to u.
+  // Caps are non-increasing (the drafter's cap set), so equal thresholds
+  // are adjacent and wave 0 numbers the distinct ones with one ballot; any
+  // other cap order takes thread 0's search.
+  if (wv == 0) {
+    const int t = ln < C ? min(part_max, caps[ln]) : 0;
+    const int tp = __shfl_up(t, 1);
+    const bool sorted = ballot(ln > 0 && ln < C && t > tp) == 0ull;
+    if (sorted) {
+      const bool fresh = ln < C && (ln == 0 || t != tp);
+      const uint64_t fm = ballot(fresh);
+      if (ln < C) {
+        const int u = rank_lt(fm) + (fresh ? 0 : -1);
+        lo_lds[ln] = t;
+        umap[ln] = u;
+        if (fresh) ulo[u] = t;
+      }
+      if (ln == 0) ulo[C] = popc(fm);
+    } else if (ln == 0) {
+      int nu = 0;
+      for (int c = 0; c < C; ++c) {
+        const int tc = min(part_max, caps[c]);
+        lo_lds[c] = tc;
+        int u = 0;
+        while (u < nu && ulo[u] != tc) ++u;
+        if (u == nu) ulo[nu++] = tc;
+        umap[c] = u;
+      }
+      ulo[C] = nu;
     }
-    ulo[C] = nu;
   }
   __syncthreads();
   const int nu = ulo[C];
