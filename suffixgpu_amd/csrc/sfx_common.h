@@ -417,45 +417,58 @@ __device__ __forceinline__ ExpandResult expand_wave(ContFn cont_at,
       // agreement lengths within the window (-1 off the chain)
       const int ag0 = p0 ? (au0 < We ? au0 : We) : -1;
       const int ag1 = p1 ? (au1 < We ? au1 : We) : -1;
-      // Per depth j (lane j): g rows holding r*'s token at depth d + j
-      // among those still on the chain there (agreement > j), x rows there
-      // voting for another token (agreement == j, a token there).  r*'s
-      // token wins outright when g > x, with the full vote's count g and
-      // denominator g + x.  The agreement histogram (hg) and the voters'
-      // one (hx) are counted in H.
-      int* hg = H;
-      int* hx = H + 32;
-      H[ln] = 0;
-      wave_lds_sync();
-      if (ag0 >= 0) {
-        atomicAdd(&hg[ag0], 1);
-        if (ag0 < We && dt0 != -1) atomicAdd(&hx[ag0], 1);
-      }
-      if (ag1 >= 0) {
-        atomicAdd(&hg[ag1], 1);
-        if (ag1 < We && dt1 != -1) atomicAdd(&hx[ag1], 1);
-      }
-      wave_lds_sync();
-      const int gv =
-          nP - (int)wave_incl_scan(ln < 32 ? (uint32_t)hg[ln] : 0u);
-      const int xv = ln < 32 ? hx[ln] : 0;
-      const uint64_t maj = ballot(ln < We && gv > xv);
-      const int m = __builtin_ctzll(~maj);  // <= We (lanes >= We: 0)
-      // g / (g + 0) is exactly 1: no division then
-      float f = 1.0f;
-      if (xv != 0 || alpha != 0.0f)
-        f = __fdiv_rn((float)gv, __fadd_rn((float)(gv + xv), alpha));
-      // Lane j: the chain probability after depth d + j, the fp32 product
-      // in depth order -- each step takes the left neighbour's product
-      // (lane 0: the probability before the window), so after step s
-      // lanes 0 .. s hold their final values.
-      float pv = f;
+      // Every row on the chain agreeing with r* through the window (one
+      // wave minimum): each depth j < We has all of them voting for r*'s
+      // token and no other vote, so with alpha 0 its factor is exactly 1
+      // and the probability stays; the depth We (if < W) has no majority.
+      const int amin = wave_all_min(min(ag0 >= 0 ? ag0 : 0x7fffffff,
+                                        ag1 >= 0 ? ag1 : 0x7fffffff));
+      int m;
+      float pv;
+      if (amin >= We && alpha == 0.0f) {
+        m = We;
+        pv = prob;
+      } else {
+        // Per depth j (lane j): g rows holding r*'s token at depth d + j
+        // among those still on the chain there (agreement > j), x rows
+        // there voting for another token (agreement == j, a token there).
+        // r*'s token wins outright when g > x, with the full vote's count g
+        // and denominator g + x.  The agreement histogram (hg) and the
+        // voters' one (hx) are counted in H.
+        int* hg = H;
+        int* hx = H + 32;
+        H[ln] = 0;
+        wave_lds_sync();
+        if (ag0 >= 0) {
+          atomicAdd(&hg[ag0], 1);
+          if (ag0 < We && dt0 != -1) atomicAdd(&hx[ag0], 1);
+        }
+        if (ag1 >= 0) {
+          atomicAdd(&hg[ag1], 1);
+          if (ag1 < We && dt1 != -1) atomicAdd(&hx[ag1], 1);
+        }
+        wave_lds_sync();
+        const int gv =
+            nP - (int)wave_incl_scan(ln < 32 ? (uint32_t)hg[ln] : 0u);
+        const int xv = ln < 32 ? hx[ln] : 0;
+        const uint64_t maj = ballot(ln < We && gv > xv);
+        m = __builtin_ctzll(~maj);  // <= We (lanes >= We: 0)
+        // g / (g + 0) is exactly 1: no division then
+        float f = 1.0f;
+        if (xv != 0 || alpha != 0.0f)
+          f = __fdiv_rn((float)gv, __fadd_rn((float)(gv + xv), alpha));
+        // Lane j: the chain probability after depth d + j, the fp32
+        // product in depth order -- each step takes the left neighbour's
+        // product (lane 0: the probability before the window), so after
+        // step s lanes 0 .. s hold their final values.
+        pv = f;
 #pragma unroll
-      for (int sb = 0; sb < kSegDepths; sb += 4) {
-        if (sb >= m) break;
+        for (int sb = 0; sb < kSegDepths; sb += 4) {
+          if (sb >= m) break;
 #pragma unroll
-        for (int s = sb; s < sb + 4; ++s)
-          pv = __fmul_rn(lane_shr1(pv, prob), f);
+          for (int s = sb; s < sb + 4; ++s)
+            pv = __fmul_rn(lane_shr1(pv, prob), f);
+        }
       }
       const uint64_t okp = ballot(ln < m && pv >= min_prob);
       const int jn = __builtin_ctzll(~okp);  // depths kept, <= m
