@@ -277,16 +277,17 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
   __syncthreads();
   const int nu = ulo[C];
   for (int g0 = 0; g0 < nu; g0 += 8)
-    compact_first_r<NT>(mb, phi - plo, ulo + g0, min(8, nu - g0), R,
-                        a.ws.d_end + (slot * C + g0) * R, (int32_t)plo,
-                        found + g0, scan, (g0 >> 3) & 1);
+    compact_first_r<NT, false, true>(
+        mb, phi - plo, ulo + g0, min(8, nu - g0), R,
+        a.ws.d_end + (slot * C + g0) * R, (int32_t)plo, found + g0, scan,
+        (g0 >> 3) & 1);
   __syncthreads();
   SFX_TRACE_POINT(3);
   for (int c = tid; c < C; c += NT) {
-    a.ws.d_cnt[slot * C + c] = lo_lds[c] > 0 ? found[umap[c]] : 0;
-    a.ws.d_map[slot * C + c] = umap[c];
+    ws_store(a.ws.d_cnt + slot * C + c, lo_lds[c] > 0 ? found[umap[c]] : 0);
+    ws_store(a.ws.d_map + slot * C + c, umap[c]);
   }
-  if (tid == 0) a.ws.d_mx[slot] = part_max;
+  if (tid == 0) ws_store(a.ws.d_mx + slot, part_max);
 }
 
 // Row-level delta result per cap from the parts (run by the merging
@@ -488,10 +489,10 @@ __device__ __forceinline__ void source_expand(
     for (int cc = c; cc < end; ++cc) {
       const int64_t i = (int64_t)b * C + cc;
       for (int d = ln; d < K; d += kWave)
-        if (d < er.nv) chain_out[i * K + d] = chain[c * K + d];
+        if (d < er.nv) ws_store(chain_out + i * K + d, chain[c * K + d]);
       if (ln == 0) {
-        nv_out[i] = er.nv;
-        score_out[i] = er.score;
+        ws_store(nv_out + i, er.nv);
+        ws_store(score_out + i, er.score);
       }
     }
   }
@@ -645,9 +646,9 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
         sal[c] = best;
         sas[c] = (int32_t)s0;
         sae[c] = (int32_t)e0;
-        a.ws.sa_len[(int64_t)b * C + c] = best;
-        a.ws.sa_s[(int64_t)b * C + c] = (int32_t)s0;
-        a.ws.sa_e[(int64_t)b * C + c] = (int32_t)e0;
+        ws_store(a.ws.sa_len + (int64_t)b * C + c, best);
+        ws_store(a.ws.sa_s + (int64_t)b * C + c, (int32_t)s0);
+        ws_store(a.ws.sa_e + (int64_t)b * C + c, (int32_t)e0);
         if (a.out.sa_len) a.out.sa_len[(int64_t)b * C + c] = best;
         if (a.out.sa_start) a.out.sa_start[(int64_t)b * C + c] = s0;
         if (a.out.sa_end) a.out.sa_end[(int64_t)b * C + c] = e0;
@@ -685,7 +686,8 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
       delta_combine(a, b, (const int32_t*)(smem + L.caps), dlen, dcnt, dpc,
                     (int32_t*)(smem + L.dmap));
       __syncthreads();
-      for (int c = tid; c < C; c += NT) a.ws.dl_c[(int64_t)b * C + c] = dlen[c];
+      for (int c = tid; c < C; c += NT)
+        ws_store(a.ws.dl_c + (int64_t)b * C + c, dlen[c]);
       SFX_TRACE_POINT(5);
       source_expand(a, L, smem, b, 2, dlen, dcnt, nullptr, dpc, a.ws.dn_nv,
                     a.ws.dn_score, a.ws.dn_chain);

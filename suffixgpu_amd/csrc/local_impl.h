@@ -484,10 +484,10 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
     return;
   }
   for (int j = tid; j < K; j += NT)
-    a.ws.l_chain[(int64_t)b * K + j] = bchain[j];
+    ws_store(a.ws.l_chain + (int64_t)b * K + j, bchain[j]);
   if (tid == 0) {
-    a.ws.l_emit[b] = emit;
-    a.ws.l_score[b] = res_score[best];
+    ws_store(a.ws.l_emit + b, emit);
+    ws_store(a.ws.l_score + b, res_score[best]);
   }
   if (block_arrive(a.ws.pick + b, 3u, misc + 2))
     final_pick(p, a.ws, b, a.draft, a.num_valid, misc + 4);
