@@ -898,25 +898,35 @@ def e2e_loop(dev, steps: int) -> dict:
                          reference_l20_persistent_mb=96.3)}
 
 
+def launches_us(fn, cur, reps: int) -> float:
+    """Average duration of `reps` back-to-back launches of fn on stream
+    `cur`, between one pair of HIP events recorded on that stream: the
+    launches queue ahead of the GPU, so the events bracket the kernels
+    and the gaps between them (an event pair around every launch adds
+    ~3 us to each)."""
+    import torch
+    for _ in range(5):
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(cur)
+    for _ in range(reps):
+        fn()
+    e1.record(cur)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / reps
+
+
 def step_kernel_us(d, dev, tokens0, nt, sampled, reps):
     """Average duration of the fused step kernel: propose_with_update
-    launched directly on the current stream `reps` times between HIP
-    events recorded on that stream (launches queue ahead of the GPU, so
-    the events bracket the kernel alone)."""
+    launched directly on the current stream `reps` times back to back
+    (launches_us)."""
     import torch
     cur = torch.cuda.current_stream(dev)
     buf = tokens0.clone()
-    for _ in range(5):
-        d.propose_with_update(nt, buf, sampled)
-    torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True),
-            torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    for e0, e1 in evs:
-        e0.record(cur)
-        d.propose_with_update(nt, buf, sampled)
-        e1.record(cur)
-    torch.cuda.synchronize()
-    return statistics.mean(e0.elapsed_time(e1) * 1e3 for e0, e1 in evs)
+    return launches_us(lambda: d.propose_with_update(nt, buf, sampled), cur,
+                       reps)
 
 
 # The local step at the decode-loop shape (B=256 rows of S=16384 tokens,
@@ -1184,9 +1194,11 @@ def summarize_pmc(fetch_dir: str, write_dir: str) -> dict:
         rows = _pmc_rows(d_, counter)
         cal = [v for k, v in rows if "bitwise_not" in k]
         # the first PMC_STEP_LAUNCHES step launches are the B=64 global-on
-        # step; the ones after them the B=256 S=16384 local step
+        # step; the B=256 S=16384 local step launches k_local_wide (one
+        # 1024-thread workgroup per row)
         steps = [v for k, v in rows if "k_step" in k]
-        step, c5 = steps[:PMC_STEP_LAUNCHES], steps[PMC_STEP_LAUNCHES:]
+        step = steps[:PMC_STEP_LAUNCHES]
+        c5 = [v for k, v in rows if "k_local_wide" in k]
         # SA builds in dispatch order, each starting with k_sa_range; the
         # last PMC_SA_BUILDS are the rebuilds as the index runs them
         builds: list[list[float]] = []
@@ -1245,7 +1257,7 @@ def row_tails(counts, rows, P):
 
 def kernel_timings(d, dev, tokens0, nt, sampled, reps):
     """Average duration of the local and the global kernel, each launched
-    alone on the current stream between HIP events."""
+    alone on the current stream (launches_us)."""
     import torch
 
     from suffixgpu_amd import _lib
@@ -1297,20 +1309,7 @@ def kernel_timings(d, dev, tokens0, nt, sampled, reps):
                                       go, ws.data_ptr(), nbytes,
                                       cur.cuda_stream), "global")
 
-    res = []
-    for fn in (local_launch, global_launch):
-        for _ in range(5):
-            fn()
-        torch.cuda.synchronize()
-        evs = [(torch.cuda.Event(enable_timing=True),
-                torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-        for e0, e1 in evs:
-            e0.record(cur)
-            fn()
-            e1.record(cur)
-        torch.cuda.synchronize()
-        res.append(statistics.mean(e0.elapsed_time(e1) * 1e3
-                                   for e0, e1 in evs))
+    res = [launches_us(fn, cur, reps) for fn in (local_launch, global_launch)]
     del keep
     return res[0], res[1]
 
