@@ -1,6 +1,7 @@
 """HIP operators vs the oracle: scatter, match_back, first occurrences,
 SA build and search, majority-vote expansion (bit-exact; weighted-vote
-scores within rtol 1e-4 as in the reference's own test)."""
+scores within rtol 1e-5, the tolerance the path is held to; the
+reference's own test allows 1e-4)."""
 
 from __future__ import annotations
 
@@ -256,8 +257,8 @@ def test_expand_alpha_weights_golden(gpu, i):
                        cap=T(cap, gpu), weights=T(z[f"w_{i}"], gpu))
     for g, key in zip(got[:3], ("wchain", "wnv", "wemit")):
         np.testing.assert_array_equal(N(g), z[f"{key}_{i}"], err_msg=key)
-    np.testing.assert_allclose(N(got[3]), z[f"wscore_{i}"], rtol=1e-4,
-                               atol=1e-5)
+    np.testing.assert_allclose(N(got[3]), z[f"wscore_{i}"], rtol=1e-5,
+                               atol=0)
 
 
 def test_expand_division_table(gpu):
