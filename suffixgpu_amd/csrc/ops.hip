@@ -281,8 +281,8 @@ __global__ __launch_bounds__(256) void k_expand(ExpandArgs a) {
 using namespace sfx;
 
 #ifdef SFX_TRACE
-__device__ uint64_t* sfx_trace_buf = nullptr;
-__device__ uint64_t* sfx_trace_stats = nullptr;
+__constant__ uint64_t* sfx_trace_buf = nullptr;
+__constant__ uint64_t* sfx_trace_stats = nullptr;
 
 // Profiling builds only: per-wave expansion counters (8 u64 per wave).
 extern "C" int sfx_trace_stats_set(uint64_t* buf) {

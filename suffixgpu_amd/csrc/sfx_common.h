@@ -13,7 +13,7 @@
 // Phase timestamps for profiling builds (-DSFX_TRACE): thread 0 of each
 // block stores wall_clock64() into sfx_trace_buf[block * 16 + slot].
 #ifdef SFX_TRACE
-extern __device__ uint64_t* sfx_trace_buf;
+extern __constant__ uint64_t* sfx_trace_buf;
 #define SFX_TRACE_POINT(slot)                                          \
   do {                                                                 \
     if (threadIdx.x == 0 && sfx_trace_buf)                             \
@@ -26,7 +26,7 @@ extern __device__ uint64_t* sfx_trace_buf;
       sfx_trace_buf[(uint64_t)blockIdx.x * 16 + (slot)] = wall_clock64(); \
   } while (0)
 // Per-wave counters of the last expansion (8 u64 per wave of 8).
-extern __device__ uint64_t* sfx_trace_stats;
+extern __constant__ uint64_t* sfx_trace_stats;
 #define SFX_TRACE_STAT(idx, val)                                       \
   do {                                                                 \
     if (__lane_id() == 0 && sfx_trace_stats)                           \

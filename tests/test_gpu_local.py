@@ -85,7 +85,9 @@ def test_local_ties_golden(gpu):
 
 @pytest.mark.parametrize("vocab,s,r,p", [(3, 200, 8, 6), (5, 1000, 16, 12),
                                          (50, 3000, 128, 32),
-                                         (2, 257, 300, 40)])
+                                         (2, 257, 300, 40), (4, 999, 16, 2),
+                                         (60, 20000, 64, 70),
+                                         (3, 20001, 32, 100)])
 def test_local_random(gpu, vocab, s, r, p):
     rng = np.random.default_rng(vocab * 1000 + s)
     b = 9
@@ -181,3 +183,53 @@ def test_local_long_rows_small_chunks(gpu):
                      max_spec_factor=None, min_token_prob=0.0,
                      support_thresholds=(1, 2, 3, 5, 8, 16, 64, 1000))
         _check(gpu, g, o, nt, tok, np.ones(len(q_list), bool))
+
+
+@pytest.mark.parametrize("s,t,vocab,p,holes", [(8192, 17, 1000, 32, False),
+                                                (20000, 17, 4, 32, False),
+                                                (20001, 80, 50, 100, True),
+                                                (16384, 17, 3, 3, True)])
+def test_step_resident_rows_vs_oracle(gpu, s, t, vocab, p, holes):
+    """Local-only propose_with_update on rows that fit in LDS (each thread
+    matches 16, 32 or 48 consecutive ends): committed lengths at 16-end
+    chunk edges, the row start and past the buffer; copy-span rows over
+    small vocabularies (long matches that walk past the first four
+    pattern tokens); more sampled ids than a wave has lanes; an explicit
+    valid count with -1 holes among the counted ids; S not a multiple of 4;
+    patterns longer than 64 and shorter than 4."""
+    from suffixgpu_amd import SuffixGPUDrafter
+    rng = np.random.default_rng(s + t + vocab)
+    q_list = [0, 1, 15, 16, 17, 4095, 8191, 8192, 12000, s - t - 1, s - 3, s,
+              s + 5]
+    b = len(q_list)
+    draw = synth.uniform_draw(vocab)
+    hidden = np.stack([synth.build_row(rng, s + t, draw) for _ in range(b)])
+    rows = hidden[:, :s].copy()
+    nt = np.array([min(q, s) if q >= 0 else 0 for q in q_list], dtype=I32)
+    nt[-1] = s + 5
+    sampled = np.full((b, t), -1, dtype=I32)
+    cnt = np.zeros(b, dtype=I32)
+    for i in range(b):
+        acc = int(rng.integers(0, t + 1)) if i % 4 else t
+        st = int(min(nt[i], s))
+        seg = hidden[i, st:st + acc]
+        sampled[i, :seg.shape[0]] = seg
+        cnt[i] = acc
+        if holes and acc > 2:
+            sampled[i, acc // 2] = -1
+    kw = dict(k=16, max_pattern_len=p, max_occurrences=128, num_backoff=8,
+              max_spec_factor=2.0, min_token_prob=0.1)
+    d = SuffixGPUDrafter(device=gpu, **kw)
+    o = DrafterOracle(**kw)
+    tg = T(rows, gpu)
+    vc = T(cnt, gpu) if holes else None
+    draft, nv, new = d.propose_with_update(T(nt, gpu), tg, T(sampled, gpu),
+                                           vc)
+    to = rows.copy()
+    ed, env, enew = o.propose_with_update(nt, to, sampled,
+                                          cnt if holes else None)
+    np.testing.assert_array_equal(N(tg), to)
+    np.testing.assert_array_equal(N(new), enew)
+    np.testing.assert_array_equal(N(draft), ed)
+    np.testing.assert_array_equal(N(nv), env)
+    assert (env > 0).sum() > 0
