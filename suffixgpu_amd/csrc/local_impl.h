@@ -326,24 +326,26 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
       carry = __shfl(x, kWave - 1);
     }
     wave_lds_sync();
+    // Lane c holds threshold c, copied to LDS at the start of the block
+    // (a varying index into the kernel arguments is a vector load from the
+    // argument segment in device memory; issued there, its latency hides
+    // behind the row staging).
+    const int thr_l = ln < C ? thr_lds[ln] : (int)0x80000000;
     if (in_reg) {
-      // Eight thresholds per step, read at uniform offsets of the kernel
-      // arguments (scalar loads issued together); each takes one ballot,
-      // and the min_match_len, mask and duplicate rules are scalar
-      // selects.  A threshold above S qualifies no L.
+      // Eight thresholds per step, unrolled: each takes one ballot, and the
+      // min_match_len, mask and duplicate rules are scalar selects, with no
+      // branch per threshold.  A threshold above S qualifies no L.
       const int mml = p.min_match_len;
       const bool live = ln < P;
       int prev_raw = -1;
       for (int c0 = 0; c0 < C; c0 += 8) {
-        int thr[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) thr[j] = p.thresholds[c0 + j];
         int outv = 0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const int t = thr[j] < 1 ? 1 : thr[j];
+          const int thr = __builtin_amdgcn_readlane(thr_l, c0 + j);
+          const int t = thr < 1 ? 1 : thr;
           int v = popc(ballot(live && sfx >= t));
-          if (!(thr[j] <= S && v >= mml && st.mask)) v = 0;
+          if (!(thr <= S && v >= mml && st.mask)) v = 0;
           const int raw = v;
           if (c0 + j > 0 && raw == prev_raw) v = 0;
           prev_raw = raw;
@@ -352,11 +354,6 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
         if (ln < 8 && c0 + ln < C) cand[c0 + ln] = outv;
       }
     } else {
-      // Lane c holds threshold c, copied to LDS at the start of the block
-      // (a varying index into the kernel arguments is a vector load from
-      // the argument segment in device memory; issued there, its latency
-      // hides behind the row staging).
-      const int thr_l = ln < C ? thr_lds[ln] : (int)0x80000000;
       const int maxthr = (int)(wave_all_max((uint32_t)thr_l ^ 0x80000000u) ^
                                0x80000000u);
       const int w = min(maxthr, S);
