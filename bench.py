@@ -28,6 +28,13 @@ from pathlib import Path
 
 import numpy as np
 
+# HIP graph launch path: with CLR's graph packet capture (on by default in
+# ROCm 7.2) a replay of the one-kernel step graph spends about 2.6 us more
+# between kernels than with it off (pipelined replays 35.4 -> 32.7 us at
+# B=64, S=8192).  Read once when the HIP runtime starts, so it is set before
+# torch is imported; a value already in the environment is kept.
+os.environ.setdefault("DEBUG_CLR_GRAPH_PACKET_CAPTURE", "0")
+
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
@@ -409,7 +416,9 @@ def main() -> int:
                    "spec_factor=2.0 min_prob=0.1, corpus 2^22 (template "
                    "sequences, SA prebuilt) + delta 2^15/2^16, hipGraph "
                    "replay", "global_batch": B, "seq_len": S,
-                   "parallelism": "none (1 GPU)"},
+                   "parallelism": "none (1 GPU)",
+                   "hip_env": {"DEBUG_CLR_GRAPH_PACKET_CAPTURE": os.environ.get(
+                       "DEBUG_CLR_GRAPH_PACKET_CAPTURE")}},
         "step_hbm_gbps": round(step_bytes / (p50 * 1e-6) / 1e9, 3),
         "step_algorithmic_bytes": step_bytes,
         "sa_build_mtok_s": round(sa_m / (sa_corpus_ms * 1e-3) / 1e6, 2),
