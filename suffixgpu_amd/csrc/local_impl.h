@@ -247,8 +247,40 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
     const int32_t p3 = P > 3 ? pat[3] : 0;
     const int4* row4 = reinterpret_cast<const int4*>(row);
     const int ng = (qe + 3) / 4;
+    // Ends that match all four first tokens are queued per wave (in the
+    // wave's expansion scratch, free until the expansion) and walked after
+    // the scan, one per lane, so a wave pays for its longest walk rather
+    // than for every group and end position that holds one.  A full queue
+    // walks in place.
+    constexpr int kWalkQ = 256;
+    int32_t* wq = (int32_t*)(smem + L.H) + wv * 2 * kHashSlots;
+    int32_t* wq_n = wq + kWalkQ;
+    if (ln == 0) *wq_n = 0;
+    auto walk = [&](int i) -> int {
+      // Walk back four tokens per step from m = 4: the four row tokens and
+      // pattern tokens of a step are independent LDS reads.
+      const int base = i - 1;  // row index of x(i - 1)
+      int m = 4;
+      while (m < P) {
+        int32_t x4[4], p4[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int j = base - m - k;
+          x4[k] = j >= 0 ? row[j] : -1;
+          p4[k] = pat[m + k < P ? m + k : P - 1];
+        }
+        int k = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          k += (k == e && m + e < P && x4[e] == p4[e]) ? 1 : 0;
+        m += k;
+        if (k < 4) break;
+      }
+      return m;
+    };
     for (int g = tid; g - tid < ng; g += NT) {
       uint32_t word = 0;
+      uint32_t queued = 0;
       if (g < ng) {
         const int i0 = 4 * g;
         const int4 lo4 = g > 0 ? row4[g - 1] : make_int4(-1, -1, -1, -1);
@@ -265,23 +297,12 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
           const bool e3 = e2 && P > 3 && w[u] == p3;
           int m = (int)e0 + (int)e1 + (int)e2 + (int)e3;
           if (e3 && P > 4) {
-            // Walk back four tokens per step: the four row tokens and
-            // pattern tokens of a step are independent LDS reads.
-            const int base = i0 + u - 1;  // row index of x(i - 1)
-            while (m < P) {
-              int32_t x4[4], p4[4];
-#pragma unroll
-              for (int k = 0; k < 4; ++k) {
-                const int j = base - m - k;
-                x4[k] = j >= 0 ? row[j] : -1;
-                p4[k] = pat[m + k < P ? m + k : P - 1];
-              }
-              int k = 0;
-#pragma unroll
-              for (int e = 0; e < 4; ++e)
-                k += (k == e && m + e < P && x4[e] == p4[e]) ? 1 : 0;
-              m += k;
-              if (k < 4) break;
+            const int slot = atomicAdd(wq_n, 1);
+            if (slot < kWalkQ) {
+              wq[slot] = i0 + u;  // walked below; m stays 4 until then
+              queued |= 1u << u;
+            } else {
+              m = walk(i0 + u);
             }
           }
           word |= (uint32_t)m << (8 * u);
@@ -291,8 +312,17 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int m = (int)((word >> (8 * u)) & 0xffu);
-        if (m > 0) atomicAdd(&hist[m], 1);
+        if (m > 0 && !((queued >> u) & 1u)) atomicAdd(&hist[m], 1);
       }
+    }
+    // The wave's queued walks (its own LDS writes: in issue order).
+    wave_lds_sync();
+    const int nq = min(*wq_n, kWalkQ);
+    for (int k = ln; k < nq; k += kWave) {
+      const int i = wq[k];
+      const int m = walk(i);
+      mbuf[i] = (uint8_t)m;
+      atomicAdd(&hist[m], 1);
     }
     __syncthreads();
   }
