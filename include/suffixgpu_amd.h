@@ -32,7 +32,7 @@ extern "C" {
 
 #define SFX_EINVAL (-1)
 #define SFX_MAX_CANDIDATES 32
-#define SFX_ABI_VERSION 12
+#define SFX_ABI_VERSION 13
 
 /* Drafter configuration shared by the local and global paths.
  * Mirrors the constructor arguments of SuffixGPUDrafter
@@ -390,8 +390,11 @@ int sfx_ingest_layout(int64_t capacity, int64_t delta_capacity,
  * _make_room and maybe_rebuild.  A snapshot bumps header.snap_seq: the
  * caller then builds staging_corpus[0 : snap_m] into the staging suffix
  * array and swaps it in, calling sfx_ingest_swapped after the swap; until
- * then the rebuild counts as running.  Rows outside [0, rows) are skipped
- * and counted.  corpus, delta and delta_len are the index's (sfx_index);
+ * then the rebuild counts as running.  A row index is a Python index:
+ * -rows <= r < 0 counts from the end (token_ids_gpu[r],
+ * proposer.py:342); rows outside [-rows, rows), where the reference raises
+ * IndexError, are skipped and counted in header.bad_rows.  Lengths <= 0
+ * append nothing.  corpus, delta and delta_len are the index's (sfx_index);
  * the delta and its length word are updated in place.  Three launches on
  * `stream`, no host synchronisation. */
 int sfx_ingest_docs(void* state, const int32_t* corpus, int64_t capacity,
@@ -401,6 +404,28 @@ int sfx_ingest_docs(void* state, const int32_t* corpus, int64_t capacity,
                     const void* row_idx, int32_t row_idx_is64,
                     const void* lengths, int32_t lengths_is64, int64_t ndocs,
                     int64_t rebuild_threshold, hipStream_t stream);
+
+/* proposer.py:354-390 ingest_active with device slot keys and lengths:
+ * in-flight responses fed to the index in chunks.  For i < ndocs, in
+ * order, with key = keys[i] (a slot in [0, nslots); others are skipped
+ * and counted in header.bad_rows), ln = lengths[i] and done =
+ * ingested[key]: when ln - done >= chunk, or final and ln > done, the
+ * document tokens[i, max(0, done - overlap) : ln] (a Python slice of row
+ * i; overlap is max_pattern_len + k in the reference) is appended and
+ * ingested[key] = ln; with final, ingested[key] = 0 afterwards (the
+ * reference forgets the key).  The documents then take the same
+ * append_documents decisions as sfx_ingest_docs.  ingested is the
+ * caller's int64 table of per-slot progress (zeroed once), rows >= ndocs;
+ * three launches on `stream`, no host synchronisation. */
+int sfx_ingest_active(void* state, const int32_t* corpus, int64_t capacity,
+                      int32_t* delta, int64_t delta_capacity,
+                      int64_t* delta_len, int32_t* staging_corpus,
+                      const int32_t* tokens, int64_t rows, int64_t seq,
+                      const void* keys, int32_t keys_is64,
+                      const void* lengths, int32_t lengths_is64,
+                      int64_t ndocs, int64_t* ingested, int64_t nslots,
+                      int32_t final, int64_t chunk, int64_t overlap,
+                      int64_t rebuild_threshold, hipStream_t stream);
 
 /* The staged build is live (after sfx_index_swap): the rebuild is no
  * longer running. */

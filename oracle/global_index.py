@@ -67,6 +67,10 @@ class GlobalIndexOracle:
         self.delta_doc_lens: list[int] = []
         self._rebuild_event = None
         self._pending = None
+        # what an async rebuild's event is: by default complete at the next
+        # poll_rebuild; tests replace it with one that completes at the
+        # poll where another index (the GPU's) swapped
+        self.rebuild_event_factory = _DoneAtPoll
 
     # ---------------------------------------------------------------- writes
     def append_documents(self, docs) -> None:
@@ -180,7 +184,7 @@ class GlobalIndexOracle:
         self._build_staging_sa(dst, m)
         if self.async_rebuild:
             self._pending = (n_new, new_lens)
-            self._rebuild_event = _DoneAtPoll()
+            self._rebuild_event = self.rebuild_event_factory()
         else:
             self._finish_swap(n_new, new_lens)
 

@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsuffixgpu_amd.so"
 MAX_CANDIDATES = 32
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -88,6 +88,10 @@ SIGNATURES = {
     "sfx_ingest_docs": (c_i32, [c_p, c_p, c_i64, c_p, c_i64, c_p, c_p,
                                 c_p, c_i64, c_i64, c_p, c_i32, c_p, c_i32,
                                 c_i64, c_i64, c_p]),
+    "sfx_ingest_active": (c_i32, [c_p, c_p, c_i64, c_p, c_i64, c_p, c_p,
+                                  c_p, c_i64, c_i64, c_p, c_i32, c_p, c_i32,
+                                  c_i64, c_p, c_i64, c_i32, c_i64, c_i64,
+                                  c_i64, c_p]),
     "sfx_ingest_swapped": (c_i32, [c_p, c_p]),
     "sfx_scatter_append": (c_i32, [ctypes.POINTER(SfxBatch), c_p, c_p]),
     "sfx_match_back": (c_i32, [c_p, c_i64, c_p, c_i64, c_i64, c_i64, c_p,

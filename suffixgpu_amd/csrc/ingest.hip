@@ -105,6 +105,11 @@ struct IngestArgs {
   int32_t len_is64;
   int64_t ndocs;
   int64_t threshold;      // rebuild_threshold
+  // ingest_active (active != 0): row_idx holds slot keys, document i is
+  // tokens[i, ...], and ingested[nslots] the tokens taken per slot so far
+  int32_t active, final;
+  int64_t* ingested;
+  int64_t nslots, chunk, overlap;
 };
 
 __device__ __forceinline__ int64_t ld_idx(const void* p, int is64,
@@ -139,6 +144,10 @@ __global__ void k_ingest_plan(IngestArgs a) {
   int64_t Fs = 0, sa = 0, s_old_off = 0, s_old_len = 0, keep_start = 0,
           n_keep = 0, n_new = 0;
   int64_t dropped_docs = 0, dropped_tok = 0, bad = 0;
+  // the reference calls append_documents (and so maybe_rebuild) only when
+  // the call yields a document, even an empty one (proposer.py:349-352,
+  // 387-390)
+  bool any_doc = false;
 
   auto pop_delta = [&]() -> int64_t {  // the oldest delta document
     const int64_t ln = dring[d_head];
@@ -206,17 +215,53 @@ __global__ void k_ingest_plan(IngestArgs a) {
   };
 
   for (int64_t i = 0; i < a.ndocs; ++i) {  // global_index.py:86-108
-    const int64_t r = ld_idx(a.row_idx, a.row_is64, i);
-    int64_t n = ld_idx(a.lengths, a.len_is64, i);
-    if (n <= 0) continue;
-    if (r < 0 || r >= a.rows) {
-      ++bad;
-      continue;
+    int64_t r, start, n;
+    if (!a.active) {
+      // harvest_finished / harvest_rows (proposer.py:329-352):
+      // token_ids_gpu[r][:ln] for ln > 0, r a Python index (negative
+      // counts from the end; outside [-rows, rows) the reference raises,
+      // here the row is skipped and counted)
+      r = ld_idx(a.row_idx, a.row_is64, i);
+      if (r < -a.rows || r >= a.rows) {
+        ++bad;
+        continue;
+      }
+      if (r < 0) r += a.rows;
+      const int64_t ln = ld_idx(a.lengths, a.len_is64, i);
+      if (ln <= 0) continue;
+      any_doc = true;
+      start = 0;
+      n = ln < a.seq ? ln : a.seq;
+    } else {
+      // ingest_active (proposer.py:354-390): a slot emits row[start:ln]
+      // once ln - done >= chunk (or, when final, anything new), start =
+      // max(0, done - overlap), as a Python slice of the row; final
+      // forgets the slot (done reads 0 again)
+      const int64_t key = ld_idx(a.row_idx, a.row_is64, i);
+      if (key < 0 || key >= a.nslots) {
+        ++bad;
+        continue;
+      }
+      const int64_t ln = ld_idx(a.lengths, a.len_is64, i);
+      const int64_t done = a.ingested[key];
+      r = i;
+      start = 0;
+      n = 0;
+      if (ln - done >= a.chunk || (a.final && ln > done)) {
+        int64_t st = done - a.overlap;
+        st = st < 0 ? 0 : (st > a.seq ? a.seq : st);
+        const int64_t stop = ln < 0 ? (a.seq + ln > 0 ? a.seq + ln : 0)
+                                    : (ln < a.seq ? ln : a.seq);
+        start = st;
+        n = stop > st ? stop - st : 0;
+        a.ingested[key] = ln;
+        any_doc = true;
+      }
+      if (a.final) a.ingested[key] = 0;
+      if (n <= 0) continue;  // append_documents skips empty documents
     }
-    n = n < a.seq ? n : a.seq;  // row[:ln]
-    int64_t start = 0;
     if (n + 1 > D) {  // the last D - 1 tokens
-      start = n - (D - 1);
+      start += n - (D - 1);
       n = D - 1;
     }
     if (delta_len + n + 1 > D) {  // _make_room(n + 1)
@@ -240,7 +285,7 @@ __global__ void k_ingest_plan(IngestArgs a) {
     delta_len += n + 1;
   }
   // maybe_rebuild (global_index.py:138-145)
-  if (!in_flight && delta_len != 0 && delta_len >= a.threshold)
+  if (any_doc && !in_flight && delta_len != 0 && delta_len >= a.threshold)
     launch_rebuild();
 
   // ---- destinations.  Final delta: [F, T); snapshot: [Fs, Fs + sa).
@@ -407,23 +452,30 @@ extern "C" int sfx_ingest_layout(int64_t capacity, int64_t delta_capacity,
   return 0;
 }
 
-extern "C" int sfx_ingest_docs(void* state, const int32_t* corpus,
-                               int64_t capacity, int32_t* delta,
-                               int64_t delta_capacity, int64_t* delta_len,
-                               int32_t* staging_corpus, const int32_t* tokens,
-                               int64_t rows, int64_t seq,
-                               const void* row_idx, int32_t row_idx_is64,
-                               const void* lengths, int32_t lengths_is64,
-                               int64_t ndocs, int64_t rebuild_threshold,
-                               hipStream_t stream) {
-  if (!state || !corpus || !delta || !delta_len || !staging_corpus ||
-      ndocs < 0 || ndocs > SFX_INGEST_MAX_DOCS || capacity < 1 ||
-      capacity > 0x7fffffffLL || delta_capacity < 1 ||
-      delta_capacity > 0x7fffffffLL ||
-      (ndocs > 0 && (!tokens || !row_idx || !lengths || rows < 1 ||
-                     seq < 1 || rows > (INT64_MAX / seq))) ||
-      ((uintptr_t)state & 255))
-    return SFX_EINVAL;
+namespace {
+
+bool ingest_geometry_ok(const void* state, const int32_t* corpus,
+                        int64_t capacity, const int32_t* delta,
+                        int64_t delta_capacity, const int64_t* delta_len,
+                        const int32_t* staging_corpus, const int32_t* tokens,
+                        int64_t rows, int64_t seq, const void* row_idx,
+                        const void* lengths, int64_t ndocs) {
+  return state && corpus && delta && delta_len && staging_corpus &&
+         ndocs >= 0 && ndocs <= SFX_INGEST_MAX_DOCS && capacity >= 1 &&
+         capacity <= 0x7fffffffLL && delta_capacity >= 1 &&
+         delta_capacity <= 0x7fffffffLL &&
+         !(ndocs > 0 && (!tokens || !row_idx || !lengths || rows < 1 ||
+                         seq < 1 || rows > (INT64_MAX / seq))) &&
+         !((uintptr_t)state & 255);
+}
+
+IngestArgs ingest_args(void* state, const int32_t* corpus, int64_t capacity,
+                       int32_t* delta, int64_t delta_capacity,
+                       int64_t* delta_len, int32_t* staging_corpus,
+                       const int32_t* tokens, int64_t rows, int64_t seq,
+                       const void* row_idx, int32_t row_idx_is64,
+                       const void* lengths, int32_t lengths_is64,
+                       int64_t ndocs, int64_t rebuild_threshold) {
   IngestArgs a;
   a.state = (unsigned char*)state;
   a.N = capacity;
@@ -441,12 +493,74 @@ extern "C" int sfx_ingest_docs(void* state, const int32_t* corpus,
   a.len_is64 = lengths_is64 ? 1 : 0;
   a.ndocs = ndocs;
   a.threshold = rebuild_threshold;
+  a.active = 0;
+  a.final = 0;
+  a.ingested = nullptr;
+  a.nslots = 0;
+  a.chunk = 0;
+  a.overlap = 0;
+  return a;
+}
+
+int ingest_launch(const IngestArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL(k_ingest_plan, dim3(1), dim3(64), 0, stream, a);
   hipLaunchKernelGGL(k_ingest_move, dim3(1024), dim3(kMoveThreads), 0,
                      stream, a);
   hipLaunchKernelGGL(k_ingest_commit, dim3(64), dim3(kMoveThreads), 0,
                      stream, a);
   return (int)hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" int sfx_ingest_docs(void* state, const int32_t* corpus,
+                               int64_t capacity, int32_t* delta,
+                               int64_t delta_capacity, int64_t* delta_len,
+                               int32_t* staging_corpus, const int32_t* tokens,
+                               int64_t rows, int64_t seq,
+                               const void* row_idx, int32_t row_idx_is64,
+                               const void* lengths, int32_t lengths_is64,
+                               int64_t ndocs, int64_t rebuild_threshold,
+                               hipStream_t stream) {
+  if (!ingest_geometry_ok(state, corpus, capacity, delta, delta_capacity,
+                          delta_len, staging_corpus, tokens, rows, seq,
+                          row_idx, lengths, ndocs))
+    return SFX_EINVAL;
+  return ingest_launch(
+      ingest_args(state, corpus, capacity, delta, delta_capacity, delta_len,
+                  staging_corpus, tokens, rows, seq, row_idx, row_idx_is64,
+                  lengths, lengths_is64, ndocs, rebuild_threshold),
+      stream);
+}
+
+extern "C" int sfx_ingest_active(void* state, const int32_t* corpus,
+                                 int64_t capacity, int32_t* delta,
+                                 int64_t delta_capacity, int64_t* delta_len,
+                                 int32_t* staging_corpus,
+                                 const int32_t* tokens, int64_t rows,
+                                 int64_t seq, const void* keys,
+                                 int32_t keys_is64, const void* lengths,
+                                 int32_t lengths_is64, int64_t ndocs,
+                                 int64_t* ingested, int64_t nslots,
+                                 int32_t final, int64_t chunk,
+                                 int64_t overlap, int64_t rebuild_threshold,
+                                 hipStream_t stream) {
+  if (!ingest_geometry_ok(state, corpus, capacity, delta, delta_capacity,
+                          delta_len, staging_corpus, tokens, rows, seq, keys,
+                          lengths, ndocs) ||
+      (ndocs > 0 && (!ingested || nslots < 1 || rows < ndocs)))
+    return SFX_EINVAL;
+  IngestArgs a =
+      ingest_args(state, corpus, capacity, delta, delta_capacity, delta_len,
+                  staging_corpus, tokens, rows, seq, keys, keys_is64,
+                  lengths, lengths_is64, ndocs, rebuild_threshold);
+  a.active = 1;
+  a.final = final ? 1 : 0;
+  a.ingested = ingested;
+  a.nslots = nslots;
+  a.chunk = chunk;
+  a.overlap = overlap;
+  return ingest_launch(a, stream);
 }
 
 extern "C" int sfx_ingest_swapped(void* state, hipStream_t stream) {

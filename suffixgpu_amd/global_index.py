@@ -132,6 +132,8 @@ class GlobalIndex:
         self.delta_doc_lens: list[int] = []
         self._rebuild_event = None
         self._pending = None
+        # swaps of a rebuild into the live buffers so far
+        self.swap_count = 0
         # Device-side ingest (harvest_device): the bookkeeping lives in
         # device memory while _ing_live; poll reads a pinned copy of its
         # header, and the host lists above are refreshed only by
@@ -142,6 +144,9 @@ class GlobalIndex:
         self._ing_mirror = torch.zeros(16, dtype=torch.int64,
                                        pin_memory=True)
         self._ing_event = None
+        # swap_count when the pinned header copy was issued: a header
+        # copied before a swap holds the corpus length from before it
+        self._ing_mirror_swaps = 0
         self._ing_seen_seq = 0
         # device-side ingest totals: documents appended, dropped to make
         # room (and their tokens), rows outside the token buffer
@@ -499,6 +504,7 @@ class GlobalIndex:
             self.key_select.data_ptr() if self.search_tables else None,
             live, stream_of(self.device)), "swap")
         self._key_live = live
+        self.swap_count += 1
         self.active_len = n_new
         if new_doc_lens is not None:  # None: the device keeps them
             self.active_doc_lens = new_doc_lens
@@ -524,6 +530,7 @@ class GlobalIndex:
             if self._ing_event is None or self.blocking_poll:
                 self._ing_mirror.copy_(self._ing[:128].view(torch.int64),
                                        non_blocking=True)
+                self._ing_mirror_swaps = self.swap_count
                 self._ing_event = torch.cuda.Event()
                 self._ing_event.record(torch.cuda.current_stream(
                     self.device))
@@ -549,6 +556,29 @@ class GlobalIndex:
     # ------------------------------------------------------------------
     # device-side ingest (proposer.py:329-343 with device lengths)
     # ------------------------------------------------------------------
+    def _device_docs_args(self, what: str, idx: torch.Tensor,
+                          lengths: torch.Tensor, tokens: torch.Tensor):
+        """Checked (idx, lengths, tokens, n) of a device-side ingest call:
+        zip() semantics (the shorter of idx and lengths), int32 tokens."""
+        for t in (idx, lengths, tokens):
+            if not isinstance(t, torch.Tensor) or t.device != self.device:
+                raise ValueError(f"{what}: tensors must be on {self.device}")
+        if idx.dtype not in (torch.int32, torch.int64) or \
+                lengths.dtype not in (torch.int32, torch.int64):
+            raise TypeError(f"{what}: int32 or int64 indices and lengths")
+        if tokens.dim() != 2:
+            raise TypeError(f"{what}: tokens must be a [rows, seq] tensor")
+        if tokens.is_floating_point() or tokens.is_complex():
+            raise TypeError(f"{what}: integer token ids")
+        idx = idx.reshape(-1)
+        lengths = lengths.reshape(-1)
+        n = min(idx.numel(), lengths.numel())
+        if n > _lib.INGEST_MAX_DOCS:
+            raise ValueError(f"{what}: at most {_lib.INGEST_MAX_DOCS} "
+                             "documents per call")
+        tokens = tokens.to(torch.int32).contiguous()
+        return idx[:n].contiguous(), lengths[:n].contiguous(), tokens, n
+
     def harvest_device(self, row_idx: torch.Tensor, lengths: torch.Tensor,
                        tokens: torch.Tensor) -> None:
         """append_documents of tokens[r, :n] for (r, n) in
@@ -559,30 +589,14 @@ class GlobalIndex:
         snapshot's build starts from the next poll_rebuild (until it is
         swapped in, the rebuild counts as running), which also refreshes
         delta_len and active_len; the host doc-length lists follow only
-        through sync_host_state.  At most 4096 rows per call; rows outside
-        the buffer are skipped and counted in ingest_counters."""
-        n = row_idx.numel()
-        if n != lengths.numel():
-            raise ValueError("harvest_device: row_idx and lengths differ "
-                             "in size")
+        through sync_host_state.  At most 4096 rows per call.  Row indices
+        are Python indices (negative ones count from the end); rows outside
+        [-rows, rows), where the reference raises IndexError, are skipped
+        and counted in ingest_counters["bad_rows"]."""
+        row_idx, lengths, tokens, n = self._device_docs_args(
+            "harvest_device", row_idx, lengths, tokens)
         if n == 0:
             return
-        if n > _lib.INGEST_MAX_DOCS:
-            raise ValueError(f"harvest_device: at most "
-                             f"{_lib.INGEST_MAX_DOCS} rows per call")
-        for t in (row_idx, lengths, tokens):
-            if t.device != self.device:
-                raise ValueError("harvest_device: tensors must be on "
-                                 f"{self.device}")
-        if row_idx.dtype not in (torch.int32, torch.int64) or \
-                lengths.dtype not in (torch.int32, torch.int64):
-            raise TypeError("harvest_device: int32 or int64 indices")
-        if tokens.dtype != torch.int32 or tokens.dim() != 2:
-            raise TypeError("harvest_device: tokens must be [rows, seq] "
-                            "int32")
-        row_idx = row_idx.contiguous()
-        lengths = lengths.contiguous()
-        tokens = tokens.contiguous()
         self._ingest_to_device()
         check(lib().sfx_ingest_docs(
             self._ing.data_ptr(), self.corpus.data_ptr(), self.capacity,
@@ -592,6 +606,35 @@ class GlobalIndex:
             row_idx.data_ptr(), int(row_idx.dtype == torch.int64),
             lengths.data_ptr(), int(lengths.dtype == torch.int64), n,
             self.rebuild_threshold, stream_of(self.device)), "ingest")
+
+    def ingest_active_device(self, keys: torch.Tensor, rows: torch.Tensor,
+                             lengths: torch.Tensor, ingested: torch.Tensor,
+                             final: bool, chunk: int, overlap: int) -> None:
+        """ingest_active's chunking (proposer.py:354-390) on the device:
+        keys are slots of the int64 progress table `ingested`, row i of
+        `rows` belongs to keys[i]; the documents it emits go through the
+        same device-side append_documents as harvest_device.  Keys outside
+        the table are skipped and counted in ingest_counters["bad_rows"]."""
+        keys, lengths, rows, n = self._device_docs_args(
+            "ingest_active", keys, lengths, rows)
+        n = min(n, rows.shape[0])
+        if n == 0:
+            return
+        if ingested.dtype != torch.int64 or ingested.device != self.device \
+                or not ingested.is_contiguous():
+            raise TypeError("ingest_active: the progress table must be a "
+                            f"contiguous int64 tensor on {self.device}")
+        self._ingest_to_device()
+        check(lib().sfx_ingest_active(
+            self._ing.data_ptr(), self.corpus.data_ptr(), self.capacity,
+            self.delta.data_ptr(), self.delta_capacity,
+            self.delta_len_t.data_ptr(), self.staging_corpus.data_ptr(),
+            rows.data_ptr(), rows.shape[0], rows.shape[1],
+            keys.data_ptr(), int(keys.dtype == torch.int64),
+            lengths.data_ptr(), int(lengths.dtype == torch.int64), n,
+            ingested.data_ptr(), ingested.numel(), int(bool(final)),
+            int(chunk), int(overlap), self.rebuild_threshold,
+            stream_of(self.device)), "ingest_active")
 
     def _ingest_header(self, words) -> dict:
         return dict(zip(_lib.INGEST_HEADER_FIELDS, (int(x) for x in words)))
@@ -640,7 +683,10 @@ class GlobalIndex:
     def _read_ingest_mirror(self) -> None:
         h = self._ingest_header(self._ing_mirror.tolist())
         self.delta_len = h["delta_len"]
-        self.active_len = h["live_active_len"]
+        if self._ing_mirror_swaps == self.swap_count:
+            # (a copy issued before a swap since then holds the corpus
+            # length from before it; _finish_swap has set the new one)
+            self.active_len = h["live_active_len"]
         self.ingest_counters = {k: h[k] for k in (
             "docs_in", "docs_dropped", "tokens_dropped", "bad_rows")}
         if h["snap_seq"] > self._ing_seen_seq:
@@ -664,17 +710,10 @@ class GlobalIndex:
             self._build_staging_sa(dst, m)
             self._finish_swap(n_new, new_doc_lens)
 
-    def sync_host_state(self) -> None:
-        """Bring the device bookkeeping of harvest_device back into the
-        host fields and lists (reads device memory; waits for the stream).
-        A staged snapshot whose build has not started is started first.
-        Host-side writes call this themselves."""
-        if not self._ing_live:
-            return
-        self._ing_event = None
+    def _read_device_state(self) -> dict:
+        """Header fields and both doc-length rings of the device
+        bookkeeping (one device read; waits for the current stream)."""
         raw = self._ing.cpu()
-        self._ing_mirror.copy_(raw[:128].view(torch.int64))
-        self._read_ingest_mirror()
         h = self._ingest_header(raw[:128].view(torch.int64).tolist())
         total, acap, dcap, aoff, doff = self._ing_layout[:5]
 
@@ -683,19 +722,56 @@ class GlobalIndex:
             idx = [(head + i) % cap for i in range(cnt)]
             return r[idx].tolist() if cnt else []
 
-        plan = ring(aoff, acap, h["active_head"], h["active_docs"])
-        self.delta_doc_lens = ring(doff, dcap, h["delta_head"],
+        h["corpus_doc_lens"] = ring(aoff, acap, h["active_head"],
+                                    h["active_docs"])
+        h["delta_doc_lens"] = ring(doff, dcap, h["delta_head"],
                                    h["delta_docs"])
+        h["_raw_header"] = raw[:128].view(torch.int64)
+        return h
+
+    def sync_host_state(self) -> None:
+        """Bring the device bookkeeping of harvest_device back into the
+        host fields and lists (reads device memory; waits for the stream).
+        A staged snapshot whose build has not started is started first.
+        Host-side writes call this themselves."""
+        if not self._ing_live:
+            return
+        self._ing_event = None
+        h = self._read_device_state()
+        self._ing_mirror.copy_(h["_raw_header"])
+        self._ing_mirror_swaps = self.swap_count
+        self._read_ingest_mirror()
+        self.delta_doc_lens = h["delta_doc_lens"]
         self.delta_len = h["delta_len"]
         if self._rebuild_event is not None:
             # running: the device lists already describe the corpus after
             # the swap
             n_new, _ = self._pending
-            self._pending = (n_new, deque(plan))
+            self._pending = (n_new, deque(h["corpus_doc_lens"]))
         else:
             self.active_len = h["active_len"]
-            self.active_doc_lens = deque(plan)
+            self.active_doc_lens = deque(h["corpus_doc_lens"])
         self._ing_live = False
+
+    def device_state(self) -> dict:
+        """The bookkeeping of device-side ingest as the device holds it,
+        read without handing it back to the host (so later harvests stay
+        device-resident): the header fields, and the two doc-length lists
+        -- "corpus_doc_lens" describes the corpus once a staged or running
+        rebuild is swapped in, "delta_doc_lens" the delta.  Waits for the
+        current stream.  Before any device-side ingest: the host's."""
+        if not self._ing_live:
+            running = self._rebuild_event is not None
+            return {"active_len": (self._pending[0] if running
+                                   else self.active_len),
+                    "live_active_len": self.active_len,
+                    "delta_len": self.delta_len, "in_flight": int(running),
+                    "corpus_doc_lens": list(self._pending[1] if running
+                                            else self.active_doc_lens),
+                    "delta_doc_lens": list(self.delta_doc_lens)}
+        h = self._read_device_state()
+        del h["_raw_header"]
+        return h
 
     # ------------------------------------------------------------------
     # persistence (this library's own format; suffixgpu_amd.persist)

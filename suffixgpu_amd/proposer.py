@@ -22,6 +22,10 @@ from suffixgpu_amd._lib import check, lib, stream_of
 from suffixgpu_amd.global_index import GlobalIndex
 from suffixgpu_amd.local_matcher import LocalMatchKernel
 
+# Slots of the device table behind ingest_active with device keys: one
+# int64 of progress per in-flight request slot.
+INGEST_SLOTS = 1 << 16
+
 
 def backoff_thresholds(num_backoff: int) -> tuple[int, ...]:
     return tuple(2 ** i for i in range(max(1, int(num_backoff))))
@@ -96,6 +100,8 @@ class SuffixGPUDrafter:
             self.vote_smoothing_alpha)
         self.global_index: GlobalIndex | None = None
         self._ingested: dict = {}
+        # per-slot progress of ingest_active with device keys
+        self._ingested_dev: torch.Tensor | None = None
         self._ws: dict[tuple, torch.Tensor] = {}
         if enable_global:
             self.global_index = GlobalIndex(
@@ -263,10 +269,33 @@ class SuffixGPUDrafter:
     def ingest_active(self, keys: list, rows: list[torch.Tensor],
                       lengths: list[int], final: bool = False,
                       chunk: int = 64) -> None:
-        """Feed in-flight responses in chunks overlapping by P + k tokens."""
+        """Feed in-flight responses in chunks overlapping by P + k tokens
+        (proposer.py:354-390).
+
+        With keys and lengths as integer tensors on the drafter's device
+        and rows a [n, seq] device tensor (row i for keys[i]), everything
+        runs on the device: the keys are slots in [0, INGEST_SLOTS) of a
+        device table of per-slot progress, the chunk / overlap / final
+        rules and every append_documents decision are taken there, and
+        nothing is read back (GlobalIndex.ingest_active_device).  Slot
+        keys outside the table are skipped and counted in the index's
+        ingest_counters["bad_rows"].  Host keys keep the reference's
+        dict (``_ingested``); the two tables are separate."""
         if self.global_index is None:
             return
         overlap = self.max_pattern_len + self.k
+        if (isinstance(keys, torch.Tensor) and isinstance(rows, torch.Tensor)
+                and isinstance(lengths, torch.Tensor)
+                and keys.device == self.device
+                and lengths.device == self.device
+                and rows.device == self.device and rows.dim() == 2):
+            if self._ingested_dev is None:
+                self._ingested_dev = torch.zeros(
+                    INGEST_SLOTS, dtype=torch.int64, device=self.device)
+            self.global_index.ingest_active_device(
+                keys, rows, lengths, self._ingested_dev, final, chunk,
+                overlap)
+            return
         docs = []
         for key, row, ln in zip(keys, rows, lengths):
             done = self._ingested.get(key, 0)

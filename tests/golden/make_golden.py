@@ -12,7 +12,9 @@ form pins are recorded here:
   local+global) -- they depend on torch.topk tie order, torch's fp32 scalar
   casts in _spec_cap / select_local_best and the hierarchical selection;
 * the GlobalIndex host state machine over scripted append / rebuild /
-  eviction / in-flight sequences;
+  eviction / in-flight sequences, and harvest_finished / ingest_active
+  under rebuilds that finish only at the script's own polls (the schedule
+  of device-side ingest);
 * expand_chain with vote smoothing (alpha) and with per-occurrence weights.
 
 The reference runs on CPU tensors, i.e. its pure-torch path (the Triton
@@ -238,6 +240,117 @@ def trace_cases() -> None:
          docs_blob_offs=np.cumsum([0] + [len(x) for x in docs_flat]), **outs)
 
 
+class _UserPollEvent:
+    """A rebuild event that is complete only inside the script's own polls
+    that it marks done: append_documents' polls (global_index.py:111,140)
+    find the rebuild still running, as a device-side ingest does."""
+
+    def __init__(self):
+        self.in_user_poll = False
+        self.done = False
+
+    def query(self) -> bool:
+        return self.in_user_poll and self.done
+
+
+def _defer_swaps(gi, event: _UserPollEvent) -> None:
+    """On a CPU index the reference builds and swaps inside _launch_rebuild
+    (global_index.py:213-215); keep its build (the staging buffers are not
+    written again before the swap) and defer the swap to the poll where
+    `event` completes, as a rebuild on a side stream would."""
+    launch, finish = gi._launch_rebuild, gi._finish_swap
+    state = {"launching": False}
+
+    def deferred_launch():
+        state["launching"] = True
+        try:
+            launch()
+        finally:
+            state["launching"] = False
+
+    def deferred_finish(n_new, lens):
+        if state["launching"]:
+            gi._pending = (n_new, lens)
+            gi._rebuild_event = event
+        else:
+            finish(n_new, lens)
+
+    gi._launch_rebuild = deferred_launch
+    gi._finish_swap = deferred_finish
+
+
+def ingest_cases() -> None:
+    """harvest_finished (row indices as Python indices, lengths <= 0 and
+    past the row, documents longer than the delta) and ingest_active
+    (chunks, overlap, final) on a small index whose rebuilds finish only
+    at the script's polls, some of which find them still running."""
+    rng = np.random.default_rng(41)
+    kw = dict(k=4, device="cpu", max_pattern_len=8, max_occurrences=8,
+              num_backoff=3, enable_global=True, global_capacity=200,
+              delta_capacity=64, rebuild_threshold=32)
+    d = SuffixGPUDrafter(**kw)
+    gi = d.global_index
+    ev = _UserPollEvent()
+    _defer_swaps(gi, ev)
+    rows, seq_a = 6, 96
+    resp = {}  # slot -> (response row, current length)
+    outs = {}
+    kinds = []
+    for i in range(90):
+        kind = 2 if i % 4 == 3 else int(rng.random() < 0.5)
+        kinds.append(kind)
+        if kind == 0:
+            seq = int(rng.choice([24, 80]))
+            tok = rng.integers(0, 6, size=(rows, seq)).astype(np.int32)
+            n = int(rng.integers(1, 5))
+            idx = rng.integers(-rows, rows, size=n).astype(np.int64)
+            lens = rng.integers(-3, seq + 10, size=n).astype(np.int64)
+            d.harvest_finished([int(x) for x in idx], [int(x) for x in lens],
+                               torch.from_numpy(tok))
+            outs.update({f"tok_{i}": tok, f"idx_{i}": idx, f"len_{i}": lens})
+        elif kind == 1:
+            n = int(rng.integers(1, 4))
+            keys = rng.choice(5, size=n, replace=False).astype(np.int64)
+            final = bool(rng.random() < 0.2)
+            chunk = int(rng.choice([16, 32]))
+            tok = np.zeros((n, seq_a), np.int32)
+            lens = np.zeros(n, np.int64)
+            for j, key in enumerate(keys):
+                row, ln = resp.get(int(key), (None, 0))
+                if row is None:
+                    row = rng.integers(0, 6, size=seq_a).astype(np.int32)
+                ln = min(seq_a + 4, ln + int(rng.integers(0, 40)))
+                resp[int(key)] = (row, ln)
+                tok[j], lens[j] = row, ln
+            d.ingest_active([int(x) for x in keys],
+                            [torch.from_numpy(r) for r in tok],
+                            [int(x) for x in lens], final=final, chunk=chunk)
+            if final:
+                for key in keys:
+                    resp.pop(int(key), None)
+            outs.update({f"tok_{i}": tok, f"keys_{i}": keys,
+                         f"len_{i}": lens, f"final_{i}": np.array(final),
+                         f"chunk_{i}": np.array(chunk)})
+        else:
+            done = bool(rng.random() < 0.75)
+            ev.done, ev.in_user_poll = done, True
+            d.poll()
+            ev.in_user_poll = False
+            outs[f"done_{i}"] = np.array(done)
+        running = gi._rebuild_event is not None
+        for key, v in index_state(gi).items():
+            outs[f"{key}_{i}"] = v
+        outs[f"in_flight_{i}"] = np.array(running)
+        outs[f"pend_n_new_{i}"] = np.array(gi._pending[0] if running else 0)
+        outs[f"pend_lens_{i}"] = np.array(
+            list(gi._pending[1]) if running else [], np.int64)
+        outs[f"staging_{i}"] = np_(gi.staging_corpus)
+        ing = sorted(d._ingested.items())
+        outs[f"ing_keys_{i}"] = np.array([k for k, _ in ing], np.int64)
+        outs[f"ing_vals_{i}"] = np.array([v for _, v in ing], np.int64)
+    save("ingest_trace", kinds=np.array(kinds, np.int64), **outs)
+
+
 def expand_cases() -> None:
     rng = torch.Generator().manual_seed(99)
     outs = {}
@@ -269,4 +382,5 @@ if __name__ == "__main__":
     local_cases()
     global_cases()
     trace_cases()
+    ingest_cases()
     expand_cases()

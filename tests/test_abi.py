@@ -124,6 +124,57 @@ def test_argument_errors_are_reported_before_any_launch():
                                     1 << 40, None) == rc
 
 
+def test_noalloc_step_rejects_batches_beyond_the_scratch():
+    """sfx_propose_step_noalloc checks on the host, before it touches the
+    device, that the batch fits the static scratch: more rows than its
+    counter arrays hold, or a workspace larger than the array.  Stand-in
+    addresses, so this runs only where no GPU is visible."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("host-only check with stand-in addresses")
+    lib = _lib.lib()
+    p = _lib.make_params(16, 32, 128, 1, [1, 2, 4, 8, 16, 32, 64, 128],
+                         [32, 16, 8, 4, 2], 2.0, 0.0, 0.1, 0.0)
+    for b, dcap in ((_lib.NOALLOC_MAX_ROWS + 1, 1 << 12), (600, 1 << 22)):
+        ix = _lib.SfxIndex(0x200000, 0x300000, 1 << 12, 0x400000, dcap,
+                           0x500000, None, 0, None, None, None, None, 0)
+        bt = _lib.SfxBatch()
+        bt.tokens = 0x100000
+        bt.batch = b
+        bt.seq = 64
+        bt.num_tokens = 0x200000
+        bt.sampled = 0x300000
+        bt.num_sampled = 17
+        bt.limit = 64
+        rc = lib.sfx_propose_step_noalloc(ctypes.byref(p), ctypes.byref(ix),
+                                          ctypes.byref(bt), 0x400000,
+                                          0x500000, 0x600000, None)
+        assert rc == _lib.ENOSCRATCH, (b, dcap, rc)
+    with pytest.raises(_lib.SuffixGPUError, match="static step scratch"):
+        _lib.check(_lib.ENOSCRATCH, "step")
+
+
+def test_ingest_entry_points_check_arguments_on_the_host():
+    """Device-side ingest rejects bad geometry before any launch."""
+    lib = _lib.lib()
+    lay = (ctypes.c_int64 * 8)()
+    assert lib.sfx_ingest_layout(0, 16, lay) == -1
+    assert lib.sfx_ingest_layout(1 << 10, 1 << 8, lay) == 0
+    # unaligned state, too many documents, missing progress table
+    args = (0x100100, 0x200000, 1 << 10, 0x300000, 1 << 8, 0x400000,
+            0x500000, 0x600000, 4, 8, 0x700000, 0, 0x800000, 0)
+    assert lib.sfx_ingest_docs(0x100104, *args[1:], 4, 100, None) == -1
+    assert lib.sfx_ingest_docs(*args, _lib.INGEST_MAX_DOCS + 1, 100,
+                               None) == -1
+    assert lib.sfx_ingest_active(*args, 4, None, 16, 0, 64, 48, 100,
+                                 None) == -1
+    assert lib.sfx_ingest_active(*args, 4, 0x900000, 0, 0, 64, 48, 100,
+                                 None) == -1
+    # more documents than rows of the token buffer
+    assert lib.sfx_ingest_active(*args, 5, 0x900000, 16, 0, 64, 48, 100,
+                                 None) == -1
+
+
 STRUCT_PROBE = r"""
 #include <stddef.h>
 #include <stdio.h>

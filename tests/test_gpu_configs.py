@@ -201,35 +201,68 @@ def test_c2_b64_local_matches_oracle(gpu):
     np.testing.assert_array_equal(N(nv), env)
 
 
-def test_c4_background_rebuild_and_swap(c3, gpu):
+def test_c4_steps_overlap_the_background_rebuild(c3, gpu):
     """The snapshot rebuild of the 2^22 index (oldest documents evicted so
     that the corpus and the delta's whole documents fit) on the rebuild
-    stream while local-only B=64 steps run on the main stream; then the
-    swap, the index against the oracle's, and a global step on it.  Runs
-    last on the shared index: it changes it."""
-    from suffixgpu_amd import SuffixGPUDrafter
+    stream, with global-on B=64 S=8192 steps of the rebuilding drafter
+    itself on the main stream meanwhile -- 40 replays of the captured step
+    and 4 eager calls, no poll in between -- each equal to the oracle's
+    step on the index as it stands before the swap (the snapshot staged,
+    the delta compacted).  HIP events on both streams show the replays ran
+    while the build did.  Then the swap, the index against the oracle's,
+    and a step on the new index.  Runs last on the shared index: it
+    changes it."""
     w, o, d = c3
     o = copy.deepcopy(o)
     gi, og = d.global_index, o.global_index
-    lw = synth.local_zipf(seed=2, b=64, s=8192)
-    dl = SuffixGPUDrafter(device=gpu, **CFG)
-    nt, samp = T(lw.num_tokens, gpu), T(lw.sampled, gpu)
-    ref = dl.propose_with_update(nt, T(lw.tokens, gpu), samp)
+    bt = w.batch
+    tok = T(bt.tokens, gpu)
+    nt, samp = T(bt.num_tokens, gpu), T(bt.sampled, gpu)
+    d.propose_with_update(nt, tok, samp)
     torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = d.propose_with_update(nt, tok, samp)
+    torch.cuda.synchronize()
+    main = torch.cuda.current_stream(gpu)
     gi.rebuild_threshold = og.rebuild_threshold = 1
     gi.blocking_poll = False
     gi.maybe_rebuild()
     assert gi._rebuild_event is not None
-    outs = [dl.propose_with_update(nt, T(lw.tokens, gpu), samp)
-            for _ in range(8)]
+    side_end = torch.cuda.Event(enable_timing=True)
+    side_end.record(gi.rebuild_stream)
+    outs, ends = [], []
+    for i in range(44):
+        if i % 11 == 10:  # an eager call on the step's own workspace
+            res = d.propose_with_update(nt, tok, samp)
+        else:
+            graph.replay()
+            res = out
+        outs.append([t.clone() for t in res])
+        e = torch.cuda.Event(enable_timing=True)
+        e.record(main)
+        ends.append(e)
+    side_end.synchronize()
+    main.synchronize()
+    # steps that ended before the build did ran beside it: the build was
+    # enqueued, behind the main stream's staging copies, before them all
+    overlapped = sum(e.elapsed_time(side_end) > 0 for e in ends)
+    assert overlapped >= 8, overlapped
+    og.async_rebuild = True
+    og.maybe_rebuild()  # staged: pending until the oracle's next poll
+    assert og._rebuild_event is not None
+    to = bt.tokens.copy()
+    ed, env, enew = o.propose_with_update(bt.num_tokens, to, bt.sampled)
+    assert (env > 0).sum() >= 48
+    for i, got in enumerate(outs):
+        for a, e in zip(got, (ed, env, enew)):
+            np.testing.assert_array_equal(N(a), e, err_msg=f"step {i}")
+    np.testing.assert_array_equal(N(tok), to)
     gi.blocking_poll = True
     gi.poll_rebuild()
-    og.maybe_rebuild()  # the oracle builds and swaps at once
+    og.poll_rebuild()
     torch.cuda.synchronize()
-    assert gi._rebuild_event is None
-    for got in outs:
-        for a, e in zip(got, ref):
-            np.testing.assert_array_equal(N(a), N(e))
+    assert gi._rebuild_event is None and og._rebuild_event is None
     index_equal(gi, og)
     assert gi.active_len + gi.delta_len > 0 and gi.delta_len == 0
     gi.rebuild_threshold = og.rebuild_threshold = 1 << 30
@@ -313,3 +346,92 @@ def test_c5_decode_loop_matches_oracle(gpu, device_harvest):
             gi.sync_host_state()
             index_equal(gi, o.global_index)
     assert swaps >= 1 and gi.active_len > 0
+
+
+def test_c5_nonblocking_loop_follows_gpu_swaps(gpu):
+    """B=256, S=16384: 200 replays of the captured step with device-side
+    harvests of the 16 longest rows at steps 63, 127 and 191, and a poll
+    every step that queries the rebuild's event without waiting (the
+    reference's poll_rebuild): rebuilds run on the side stream while the
+    steps replay, and swap in at whichever poll finds them done.  The
+    oracle's rebuilds complete at the polls where the GPU's swapped.  New
+    counts every step; the full step and token rows right after every
+    harvest (while its snapshot is staged or building) and every swap,
+    and at the first and last step; the device bookkeeping and buffers
+    after every harvest and every swap."""
+    from suffixgpu_amd import SuffixGPUDrafter
+    from tests.test_gpu_ingest import oracle_device_state_equal
+    from tests.test_oracle_golden import ScriptedEvent
+    steps = 200
+    lp = synth.decode_loop(seed=5, b=256, s=16384, steps=steps)
+    assert sorted(lp.harvests) == [63, 127, 191]
+    kw = dict(enable_global=True, global_capacity=N22, delta_capacity=D16,
+              rebuild_threshold=D16 // 2, **CFG)
+    d = SuffixGPUDrafter(device=gpu, rebuild_stream=torch.cuda.Stream(gpu),
+                         **kw)
+    gi = d.global_index
+    assert not gi.blocking_poll
+    o = DrafterOracle(async_rebuild=True, finish_at_user_poll=True, **kw)
+    og = o.global_index
+    ev = ScriptedEvent()
+    og.rebuild_event_factory = lambda: ev
+    tok = T(lp.tokens, gpu)
+    nt = T(lp.num_tokens, gpu)
+    samp_all = T(lp.sampled, gpu)
+    samp = samp_all[0].clone()
+    for _ in range(3):
+        d.propose_with_update(nt, tok, samp)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = d.propose_with_update(nt, tok, samp)
+    torch.cuda.synchronize()
+    to = lp.tokens.copy()
+    ont = lp.num_tokens.copy()
+    swap_polls, full_in_flight = [], 0
+    check_next = {0, steps - 1}
+    for i in range(steps):
+        samp.copy_(samp_all[i])
+        graph.replay()
+        nt.copy_(out[2])
+        if i in check_next:
+            in_flight = og._rebuild_event is not None
+            ed, env, enew = o.propose_with_update(ont, to, lp.sampled[i])
+            np.testing.assert_array_equal(N(out[0]), ed, err_msg=f"step {i}")
+            np.testing.assert_array_equal(N(out[1]), env, err_msg=f"step {i}")
+            np.testing.assert_array_equal(N(tok), to, err_msg=f"step {i}")
+            full_in_flight += in_flight
+        else:
+            enew = o.update_state(ont, to, lp.sampled[i])
+        np.testing.assert_array_equal(N(out[2]), enew, err_msg=f"step {i}")
+        ont = enew
+        hv = lp.harvests.get(i)
+        if hv is not None:
+            rows, lengths, new_rows, new_q = hv
+            idx = torch.tensor(rows, dtype=torch.int64, device=gpu)
+            d.harvest_finished(idx, T(np.asarray(lengths), gpu), tok)
+            o.harvest_finished(rows, lengths, to)
+            assert og._rebuild_event is not None  # a snapshot is staged
+            oracle_device_state_equal(gi, og)
+            tok.index_copy_(0, idx, T(new_rows, gpu))
+            nt.index_copy_(0, idx, T(new_q, gpu))
+            to[rows] = new_rows
+            ont = ont.copy()
+            ont[rows] = new_q
+            check_next.update((i + 1, i + 2, i + 3))
+        before = gi.swap_count
+        d.poll()
+        ev.done = gi.swap_count != before
+        assert not ev.done or og._rebuild_event is not None, f"poll {i}"
+        o.poll()
+        ev.done = False
+        if gi.swap_count != before:
+            swap_polls.append(i)
+            assert og._rebuild_event is None
+            oracle_device_state_equal(gi, og)
+            check_next.add(i + 1)
+    print(f"swaps at polls {swap_polls}; full steps checked {len(check_next)},"
+          f" {full_in_flight} with a rebuild staged or running")
+    assert len(swap_polls) >= 2
+    assert full_in_flight >= 3
+    assert gi.active_len > 0

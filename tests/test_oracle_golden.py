@@ -164,6 +164,81 @@ def test_index_trace():
         _state_equal(gi, z, f"_{step}")
 
 
+# ingest trace: the reference's harvest_finished / ingest_active under
+# rebuilds that finish only at the script's polls marked done
+INGEST_KW = dict(k=4, max_pattern_len=8, max_occurrences=8, num_backoff=3,
+                 enable_global=True, global_capacity=200, delta_capacity=64,
+                 rebuild_threshold=32)
+HARVEST, ACTIVE, POLL = 0, 1, 2
+
+
+class ScriptedEvent:
+    """A rebuild event whose completion the test sets before each poll."""
+
+    def __init__(self):
+        self.done = False
+
+    def query(self) -> bool:
+        return self.done
+
+
+def ingest_ops(z):
+    """Yield (i, kind, args) of the ingest trace: HARVEST (tok, idx, len),
+    ACTIVE (tok, keys, len, final, chunk), POLL (done,)."""
+    for i, kind in enumerate(z["kinds"]):
+        if kind == HARVEST:
+            yield i, HARVEST, (z[f"tok_{i}"], z[f"idx_{i}"], z[f"len_{i}"])
+        elif kind == ACTIVE:
+            yield i, ACTIVE, (z[f"tok_{i}"], z[f"keys_{i}"], z[f"len_{i}"],
+                              bool(z[f"final_{i}"]), int(z[f"chunk_{i}"]))
+        else:
+            yield i, POLL, (bool(z[f"done_{i}"]),)
+
+
+def ingest_state_equal(gi, ingested: dict, z, i) -> None:
+    """Index state after op i (live buffers, lists, the running rebuild's
+    staged corpus and doc lengths) and ingest_active's progress dict."""
+    _state_equal(gi, z, f"_{i}")
+    running = gi._rebuild_event is not None
+    assert running == bool(z[f"in_flight_{i}"])
+    if running:
+        assert gi._pending[0] == int(z[f"pend_n_new_{i}"])
+        np.testing.assert_array_equal(np.array(list(gi._pending[1]),
+                                               np.int64), z[f"pend_lens_{i}"])
+        np.testing.assert_array_equal(gi.staging_corpus, z[f"staging_{i}"])
+    items = sorted(ingested.items())
+    assert [k for k, _ in items] == z[f"ing_keys_{i}"].tolist()
+    assert [v for _, v in items] == z[f"ing_vals_{i}"].tolist()
+
+
+def test_ingest_trace_finish_at_user_poll():
+    """The oracle's schedule behind device-side ingest (a rebuild is still
+    running at append_documents' own polls and completes at a caller's
+    poll) against the reference driven that way: Python row indices,
+    lengths <= 0 and past the row, documents longer than the delta, drops
+    while a snapshot is running, evictions, ingest_active's chunk /
+    overlap / final rules, and polls that find the rebuild running."""
+    z = golden("ingest_trace")
+    o = DrafterOracle(async_rebuild=True, finish_at_user_poll=True,
+                      **INGEST_KW)
+    ev = ScriptedEvent()
+    o.global_index.rebuild_event_factory = lambda: ev
+    for i, kind, args in ingest_ops(z):
+        if kind == HARVEST:
+            tok, idx, lens = args
+            o.harvest_finished([int(r) for r in idx], [int(x) for x in lens],
+                               tok)
+        elif kind == ACTIVE:
+            tok, keys, lens, final, chunk = args
+            o.ingest_active([int(k) for k in keys], list(tok),
+                            [int(x) for x in lens], final=final, chunk=chunk)
+        else:
+            ev.done = args[0]
+            o.poll()
+            ev.done = False
+        ingest_state_equal(o.global_index, o._ingested, z, i)
+
+
 @pytest.mark.parametrize("i", range(4))
 def test_expand_alpha_and_weights(i):
     z = golden("expand_alpha_weights")

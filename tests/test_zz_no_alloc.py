@@ -1,8 +1,9 @@
 """sfx_propose_step_noalloc (the step with its scratch in a static device
 array, for callers that cannot allocate) against sfx_propose_step with a
 caller workspace, both called through the C ABI on identical inputs: two
-calls in a row, the second with a smaller batch, then a local-only call;
-and the host-side rejection of batches beyond the static scratch."""
+calls in a row, the second with a smaller batch, then a local-only call.
+The host-side rejection of batches beyond the static scratch is checked
+without a GPU in test_abi.py."""
 
 from __future__ import annotations
 
@@ -87,29 +88,3 @@ def test_noalloc_step_matches_workspace_step(gpu):
     exp = _run(dl, None, *args, with_ws=True)
     for g, e in zip(got, exp):
         np.testing.assert_array_equal(g, e)
-
-
-def test_noalloc_step_rejects_batches_beyond_the_scratch(gpu):
-    """Checked on the host before any launch: more rows than the counter
-    arrays hold, or a step whose workspace exceeds the static array."""
-    from suffixgpu_amd import _lib, SuffixGPUDrafter
-    L = _lib.lib()
-    d = SuffixGPUDrafter(device=gpu, enable_global=True,
-                         global_capacity=1 << 12, delta_capacity=1 << 22,
-                         **CFG)
-    ix = d.global_index.index_struct()
-    for b, dcap in ((_lib.NOALLOC_MAX_ROWS + 1, 1 << 12), (600, 1 << 22)):
-        ix.delta_capacity = dcap
-        bt = _lib.SfxBatch()
-        bt.tokens = 0x100000
-        bt.batch = b
-        bt.seq = 64
-        bt.num_tokens = 0x200000
-        bt.sampled = 0x300000
-        bt.num_sampled = 17
-        bt.limit = 64
-        rc = L.sfx_propose_step_noalloc(d._params, ctypes.byref(ix), bt,
-                                        0x400000, 0x500000, 0x600000, None)
-        assert rc == _lib.ENOSCRATCH, (b, dcap, rc)
-    with pytest.raises(_lib.SuffixGPUError, match="static step scratch"):
-        _lib.check(_lib.ENOSCRATCH, "step")
