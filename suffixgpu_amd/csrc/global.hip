@@ -38,7 +38,7 @@ int mb_lds_bytes(const sfx_index& ix, int parts) {
 }
 
 int merge_waves_for(const sfx_params& p, const sfx_index& ix, int parts,
-                    size_t* lds, size_t cap) {
+                    size_t* lds, size_t cap, int dend_parts) {
   const int NW = kGlobalThreads / kWave;
   const int C = p.num_caps;
   int nmw = C < NW ? C : NW;
@@ -46,13 +46,37 @@ int merge_waves_for(const sfx_params& p, const sfx_index& ix, int parts,
   for (; nmw >= 1; --nmw) {
     const GlobalLayout L = global_layout(p.max_pattern_len, C,
                                          p.max_occurrences, p.k, nmw,
-                                         mb_lds_bytes(ix, parts));
+                                         mb_lds_bytes(ix, parts), 0,
+                                         dend_parts);
     if ((size_t)L.total <= cap) {
       *lds = (size_t)L.total;
       return nmw;
     }
   }
   return 0;
+}
+
+int delta_chunk_for(const sfx_params& p, const sfx_index& ix, int parts,
+                    int nmw, int dend_parts, size_t cap, size_t* lds) {
+  const int P = p.max_pattern_len;
+  const int halo = (P + 3) & ~3;
+  const int mb = mb_lds_bytes(ix, parts);
+  const GlobalLayout L0 = global_layout(P, p.num_caps, p.max_occurrences,
+                                        p.k, nmw, mb, kDeltaChunk,
+                                        dend_parts);
+  *lds = (size_t)L0.total;
+  // the staged words and the match bytes sit after the header
+  const int64_t avail = (int64_t)cap - L0.dtok - ((mb + 15) & ~15);
+  const int64_t most = (delta_part_cap(ix.delta_capacity, parts) + 255) &
+                       ~(int64_t)255;
+  int64_t ch = (avail / 4 - halo) & ~(int64_t)255;
+  ch = ch < most ? ch : most;
+  if (ch <= kDeltaChunk) return kDeltaChunk;
+  const GlobalLayout L = global_layout(P, p.num_caps, p.max_occurrences, p.k,
+                                       nmw, mb, (int)ch, dend_parts);
+  if ((size_t)L.total > cap) return kDeltaChunk;
+  *lds = (size_t)L.total;
+  return (int)ch;
 }
 
 int check_global(const sfx_params& p, const sfx_index& ix, int64_t batch) {
@@ -92,6 +116,8 @@ static int launch_global(GlobalArgs& a, hipStream_t stream) {
   a.dparts = delta_parts_for(a.B, a.ix.delta_capacity);
   a.merge_waves = merge_waves_for(a.p, a.ix, a.dparts, &lds);
   a.mb_lds = mb_lds_bytes(a.ix, a.dparts);
+  a.dchunk = delta_chunk_for(a.p, a.ix, a.dparts, a.merge_waves, 0,
+                             kMaxLds, &lds);
   static std::atomic<uint64_t> lds_opt{0};
   allow_max_lds((const void*)k_global, lds_opt);
   const unsigned blocks = (unsigned)((1 + a.dparts) * a.B);

@@ -31,18 +31,21 @@ struct GlobalArgs {
   int merge_waves;
   int mb_lds;  // bytes of LDS for a delta part's match lengths (0: workspace)
   int dparts;  // delta workgroups per row (delta_parts_for)
+  int dchunk;  // delta positions staged in LDS at a time (0: kDeltaChunk)
+  int dend;    // step: the parts' end lists are copied into LDS at the join
 };
 
 struct GlobalLayout {
   int rpat, lb, ub, found, scan, red, misc, lo, ulo, umap, dlen, dcnt, dpc,
       dmap,
-      sal, sas, sae, caps, dtok, dmb, mpos, mcache, mA, mH, chain, nv, score,
-      rlen, rocc, total;
+      sal, sas, sae, caps, dtok, dmb, mpos, mcache, mA, mH, dend, chain, nv,
+      score, rlen, rocc, total;
 };
 
-// Delta tokens staged per chunk (after a halo of P rounded up to 4
-// tokens); a part's match_back bytes stay in LDS up to kMbLdsMax
-// positions, longer parts keep them in the workspace.
+// Delta tokens staged per chunk, at least (after a halo of P rounded up to
+// 4 tokens): the host grows the chunk while the layout fits, up to a whole
+// part; a part's match_back bytes stay in LDS up to kMbLdsMax positions,
+// longer parts keep them in the workspace.
 constexpr int kDeltaChunk = 8192;
 constexpr int kMbLdsMax = (int)kDeltaMbLdsMax;
 
@@ -54,9 +57,13 @@ __host__ __device__ inline int g_take(int& off, int bytes) {
 
 // Shared header, then a union: the SA/delta role buffers are dead by the
 // time the block (if it arrives second) merges the row.
+// dparts > 0 (decode step): the merge side also holds every delta part's
+// end lists, copied in at the parts' join.
 __host__ __device__ inline GlobalLayout global_layout(int P, int C, int R,
                                                       int K, int nmw,
-                                                      int mb_lds) {
+                                                      int mb_lds,
+                                                      int dchunk = 0,
+                                                      int dparts = 0) {
   constexpr int NW = kGlobalThreads / kWave;
   const int Rp = (R + 3) & ~3;
   GlobalLayout L;
@@ -85,7 +92,8 @@ __host__ __device__ inline GlobalLayout global_layout(int P, int C, int R,
   L.rlen = g_take(off, C * 4);
   L.rocc = g_take(off, C * 4);
   const int ubase = off;
-  L.dtok = g_take(off, (kDeltaChunk + ((P + 3) & ~3)) * 4);
+  L.dtok = g_take(off, ((dchunk > 0 ? dchunk : kDeltaChunk) +
+                        ((P + 3) & ~3)) * 4);
   L.dmb = g_take(off, mb_lds);
   const int delta_end = off;
   off = ubase;
@@ -93,8 +101,71 @@ __host__ __device__ inline GlobalLayout global_layout(int P, int C, int R,
   L.mcache = g_take(off, nmw * R * (K + 1) * 4);
   L.mA = g_take(off, nmw * Rp * 4);
   L.mH = g_take(off, nmw * 2 * kHashSlots * 4);
+  L.dend = g_take(off, dparts * C * R * 4);
   L.total = off > delta_end ? off : delta_end;
   return L;
+}
+
+// Stage x(c0 - halo) .. x(cend - 2) of the delta into dtok as 16-byte
+// words.  Words wholly inside the delta go from memory straight into LDS
+// (global_load_lds_dwordx4: no registers, so every load of the chunk is in
+// flight at once); the edge words -- before position 0 (-1) or past the
+// capacity (0) -- are formed here.  The caller waits for the loads
+// (wait_all_loads) and syncs the block before reading dtok.
+// Waves from `wfirst` on issue the loads (a wave's loads complete in
+// order, so waves that load anything they need sooner stay out of it).
+__device__ __forceinline__ void delta_stage(const GlobalArgs& a,
+                                            int32_t* dtok, int64_t c0,
+                                            int64_t cend, int halo,
+                                            int wfirst = 0) {
+  const int64_t D = a.ix.delta_capacity;
+  const int64_t j0 = c0 - halo;
+  const int nk4 = (int)((cend - 1 - j0 + 3) / 4);
+  const int wv = threadIdx.x / kWave;
+  const int ln = lane_id();
+  if (wv < wfirst) return;
+  const int4* d4 = reinterpret_cast<const int4*>(a.ix.delta);
+  const int stride = kGlobalThreads - wfirst * kWave;
+  for (int w0 = (wv - wfirst) * kWave; w0 < nk4; w0 += stride) {
+    const int w = w0 + ln;  // one wave covers 64 consecutive words
+    const int64_t j = j0 + 4 * (int64_t)w;
+    if (w < nk4) {
+      if (j >= 0 && j + 3 < D) {
+        __builtin_amdgcn_global_load_lds(
+            (const void*)(d4 + (j >> 2)),
+            (__attribute__((address_space(3))) void*)(dtok + 4 * w0), 16, 0,
+            0);
+      } else {
+        int4 v;
+        v.x = j < 0 ? -1 : (j < D ? a.ix.delta[j] : 0);
+        v.y = j + 1 < 0 ? -1 : (j + 1 < D ? a.ix.delta[j + 1] : 0);
+        v.z = j + 2 < 0 ? -1 : (j + 2 < D ? a.ix.delta[j + 2] : 0);
+        v.w = j + 3 < 0 ? -1 : (j + 3 < D ? a.ix.delta[j + 3] : 0);
+        reinterpret_cast<int4*>(dtok)[w] = v;
+      }
+    }
+  }
+}
+
+// Every load this wave issued has landed (memory-to-LDS ones included).
+__device__ __forceinline__ void wait_all_loads() {
+  __builtin_amdgcn_s_waitcnt(0);
+}
+
+// A delta part's chunk of positions [c0, c0 + dchunk) clipped to phi.
+__device__ __forceinline__ int64_t delta_chunk_end(const GlobalArgs& a,
+                                                   int64_t c0, int64_t phi) {
+  const int64_t ch = a.dchunk > 0 ? a.dchunk : kDeltaChunk;
+  return c0 + ch < phi ? c0 + ch : phi;
+}
+
+// [plo, phi) of this row's delta part `part` over the live delta.
+__device__ __forceinline__ void delta_part_of(const GlobalArgs& a, int part,
+                                              int64_t* plo, int64_t* phi) {
+  const int64_t D = a.ix.delta_capacity;
+  int64_t dl = *a.ix.delta_len;
+  dl = dl < 0 ? 0 : (dl > D ? D : dl);
+  delta_part_range(dl + 1, a.dparts, part, plo, phi);
 }
 
 // ---- Delta role, one part of the row: match_back over ends i in
@@ -134,58 +205,22 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
   uint8_t* mb = kMbLds ? (uint8_t*)(smem + L.dmb)
                        : a.ws.d_mb + slot * delta_mb_stride(
                                                 delta_part_cap(D, KD));
-  int64_t dl = *a.ix.delta_len;
-  dl = dl < 0 ? 0 : (dl > D ? D : dl);
   int64_t plo, phi;
-  delta_part_range(dl + 1, KD, part, &plo, &phi);
+  delta_part_of(a, part, &plo, &phi);
   const int halo = (P + 3) & ~3;
-  const int4* d4 = reinterpret_cast<const int4*>(a.ix.delta);
-  // Staged words per chunk: x(j0 .. cend - 2) with j0 = c0 - halo, in
-  // int4 words; a thread holds at most kStage4 of them in registers so the
-  // next chunk's loads are in flight while the current one is scanned.
-  constexpr int kStage4 = (kDeltaChunk + 256) / 4 / NT + 1;
-  auto chunk_words = [&](int64_t c0) -> int {
-    const int64_t cend = c0 + kDeltaChunk < phi ? c0 + kDeltaChunk : phi;
-    return (int)((cend - 1 - (c0 - halo) + 3) / 4);
-  };
-  auto load_chunk = [&](int64_t c0, int4 (&v)[kStage4]) {
-    const int nk4 = chunk_words(c0);
-    const int64_t j0 = c0 - halo;
-#pragma unroll
-    for (int u = 0; u < kStage4; ++u) {
-      const int k4 = tid + u * NT;
-      const int64_t j = j0 + 4 * (int64_t)k4;
-      if (k4 < nk4) {
-        if (j >= 0 && j + 3 < D) {
-          v[u] = d4[j >> 2];
-        } else {
-          v[u].x = j < 0 ? -1 : (j < D ? a.ix.delta[j] : 0);
-          v[u].y = j + 1 < 0 ? -1 : (j + 1 < D ? a.ix.delta[j + 1] : 0);
-          v[u].z = j + 2 < 0 ? -1 : (j + 2 < D ? a.ix.delta[j + 2] : 0);
-          v[u].w = j + 3 < 0 ? -1 : (j + 3 < D ? a.ix.delta[j + 3] : 0);
-        }
-      }
-    }
-  };
   const int32_t r0 = rpat[0];
   const int32_t r1 = P > 1 ? rpat[1] : 0;
   const int32_t r2 = P > 2 ? rpat[2] : 0;
   const int32_t r3 = P > 3 ? rpat[3] : 0;
-  int4 stage[kStage4];
-  if (plo < phi) load_chunk(plo, stage);
   int mx = 0;
-  for (int64_t c0 = plo; c0 < phi; c0 += kDeltaChunk) {
-    const int64_t cend = c0 + kDeltaChunk < phi ? c0 + kDeltaChunk : phi;
-    {
-      const int nk4 = chunk_words(c0);
-#pragma unroll
-      for (int u = 0; u < kStage4; ++u) {
-        const int k4 = tid + u * NT;
-        if (k4 < nk4) reinterpret_cast<int4*>(dtok)[k4] = stage[u];
-      }
-    }
+  // The first chunk's loads were issued before the row setup (global_body)
+  // so that their latency overlaps it; each later chunk is staged after
+  // the previous one's scan.
+  for (int64_t c0 = plo; c0 < phi; ) {
+    const int64_t cend = delta_chunk_end(a, c0, phi);
+    if (c0 != plo) delta_stage(a, dtok, c0, cend, halo);
+    wait_all_loads();
     __syncthreads();
-    if (c0 + kDeltaChunk < phi) load_chunk(c0 + kDeltaChunk, stage);
     // Ends i0 .. i0 + 3 (i0 = c0 + 4g) from two 16-byte LDS reads, which
     // give x(i0 - 4) .. x(i0 + 3) (the halo is at least 4): the four
     // newest pattern tokens are tested at every end without a branch, and
@@ -232,6 +267,7 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
       *reinterpret_cast<uint32_t*>(mb + (i0 - plo)) = word;
     }
     __syncthreads();
+    c0 = cend;
   }
   // match lengths are >= 0: the unsigned DPP max is the signed one
   mx = (int)wave_all_max((uint32_t)mx);
@@ -366,7 +402,8 @@ __device__ __forceinline__ int32_t sa_sample(const GlobalArgs& a, int64_t s,
 __device__ __forceinline__ ExpandResult gather_expand(
     const GlobalArgs& a, const GlobalLayout& L, unsigned char* smem, int b,
     int c, int src, int len, int occ, int64_t sa_s, int64_t ilen,
-    const int32_t* dpc, int32_t* cont_out, bool expand, int32_t* chain_out) {
+    const int32_t* dpc, int32_t* cont_out, bool expand, int32_t* chain_out,
+    const int32_t* dend = nullptr) {
   const sfx_params& p = a.p;
   const int ln = lane_id();
   const int wv = threadIdx.x / kWave;
@@ -392,8 +429,12 @@ __device__ __forceinline__ ExpandResult gather_expand(
       }
       const int m = dmap[k];
       const int64_t slot = (int64_t)b * a.dparts + k;
-      const int64_t e =
-          (int64_t)a.ws.d_end[(slot * p.num_caps + m) * R + rr] - len;
+      // the end lists: copied into LDS at the parts' join (dend), or read
+      // from the workspace
+      const int32_t end_r =
+          dend ? dend[(k * p.num_caps + m) * R + rr]
+               : a.ws.d_end[(slot * p.num_caps + m) * R + rr];
+      const int64_t e = (int64_t)end_r - len;
       pos = (int32_t)(e < 0 ? 0 : e);
     }
     mpos[r] = pos;
@@ -457,7 +498,7 @@ __device__ __forceinline__ void source_expand(
     const GlobalArgs& a, const GlobalLayout& L, unsigned char* smem, int b,
     int src, const int32_t* lens, const int32_t* aux0, const int32_t* aux1,
     const int32_t* dpc, int32_t* nv_out, float* score_out,
-    int32_t* chain_out) {
+    int32_t* chain_out, const int32_t* needed = nullptr) {
   const sfx_params& p = a.p;
   const int C = p.num_caps;
   const int R = p.max_occurrences;
@@ -471,6 +512,11 @@ __device__ __forceinline__ void source_expand(
     if (c > 0 && lens[c - 1] == len) continue;  // expanded by the run head
     int end = c + 1;
     while (end < C && lens[end] == len) ++end;
+    if (needed) {  // no cap of the run can pick this candidate
+      bool any = false;
+      for (int cc = c; cc < end; ++cc) any = any || needed[cc] != 0;
+      if (!any) continue;
+    }
     ExpandResult er{0, 0.0f};
     if (len > 0) {
       int occ;
@@ -483,7 +529,10 @@ __device__ __forceinline__ void source_expand(
         occ = aux0[c];
       }
       er = gather_expand(a, L, smem, b, c, src, len, occ, s0, ilen, dpc,
-                         nullptr, true, chain + c * K);
+                         nullptr, true, chain + c * K,
+                         src == 2 && a.dend
+                             ? (const int32_t*)(smem + L.dend)
+                             : nullptr);
     }
     wave_lds_sync();  // lane 0 wrote the chain
     for (int cc = c; cc < end; ++cc) {
@@ -526,7 +575,8 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
   const int R = p.max_occurrences;
   const int K = p.k;
   const int Rp = (R + 3) & ~3;
-  const GlobalLayout L = global_layout(P, C, R, K, a.merge_waves, a.mb_lds);
+  const GlobalLayout L = global_layout(P, C, R, K, a.merge_waves, a.mb_lds,
+                                       a.dchunk, a.dend ? a.dparts : 0);
   int32_t* rpat = (int32_t*)(smem + L.rpat);
   int64_t* lbs = (int64_t*)(smem + L.lb);
   int64_t* ubs = (int64_t*)(smem + L.ub);
@@ -541,26 +591,47 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
   // varying index into the kernel arguments is a vector load from device
   // memory, so it is issued once here, ahead of the first barrier.
   if (tid < C) ((int32_t*)(smem + L.caps))[tid] = p.caps[tid];
+  // A delta part's first chunk goes from memory into LDS while the row's
+  // pattern is read: the waves past the pattern's threads load the delta
+  // length and issue it (a wave's loads complete in order, so they read
+  // nothing of the row themselves); delta_role waits for it.  dtok lies
+  // past the header the setup writes.
+  const int wpat = (P + kWave - 1) / kWave;  // waves holding pattern threads
+  auto stage_first_chunk = [&]() {
+    if (role > 0 && wv >= wpat) {
+      int64_t plo, phi;
+      delta_part_of(a, role - 1, &plo, &phi);
+      if (plo < phi)
+        delta_stage(a, (int32_t*)(smem + L.dtok), plo,
+                    delta_chunk_end(a, plo, phi), (P + 3) & ~3, wpat);
+    }
+  };
 
   // Query tail, newest first: rpat[t] = tail token t back from the end;
   // -3 past the start (global_index.py:493-501).
-  int64_t qlen;
+  int64_t qlen = 0;
   if (a.step) {
-    const RowState st = row_state(a.bt, b);
-    if (!st.mask) return;  // masked rows: the local kernel writes them
-    const int64_t q = st.q;
-    qlen = q < P ? q : P;
-    for (int t = tid; t < P; t += NT) {
-      const int64_t idx = q - 1 - t;
-      int32_t v = -3;
-      if (idx >= 0) {
-        const int64_t x = idx < a.bt.seq - 1 ? idx : a.bt.seq - 1;
-        v = updated_token(a.bt, b, st, x);
-      }
-      rpat[t] = v;
+    if (role > 0 && wv >= wpat) {
+      stage_first_chunk();
+    } else {
+      const RowState st = row_state(a.bt, b);
+      if (tid == 0) misc[12] = st.mask ? 1 : 0;
+      const int64_t q = st.q;
+      qlen = q < P ? q : P;
+      if (st.mask)
+        for (int t = tid; t < P; t += NT) {
+          const int64_t idx = q - 1 - t;
+          int32_t v = -3;
+          if (idx >= 0) {
+            const int64_t x = idx < a.bt.seq - 1 ? idx : a.bt.seq - 1;
+            v = updated_token(a.bt, b, st, x);
+          }
+          rpat[t] = v;
+        }
     }
   } else {
     qlen = a.qlen[b];
+    stage_first_chunk();
     const int64_t Q = a.qwidth;
     for (int t = tid; t < P; t += NT) {
       const int64_t idx = qlen - 1 - t;
@@ -569,8 +640,13 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
       rpat[t] = v;
     }
   }
+  // (plen is read by the SA role, whose waves all read the row)
   const int plen = (int)(qlen < 0 ? 0 : (qlen < P ? qlen : P));
   __syncthreads();
+  if (a.step && !misc[12]) {  // masked rows: the local kernel writes them
+    wait_all_loads();  // no load into this block's LDS outlives it
+    return;
+  }
   SFX_TRACE_POINT(1);
 
   if (role == 0) {
@@ -649,6 +725,11 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
         ws_store(a.ws.sa_len + (int64_t)b * C + c, best);
         ws_store(a.ws.sa_s + (int64_t)b * C + c, (int32_t)s0);
         ws_store(a.ws.sa_e + (int64_t)b * C + c, (int32_t)e0);
+        // for the delta workgroups (decode step): a word of its own per
+        // cap, so a reader sees either 0 or the length, no fence needed
+        if (a.step)
+          ws_store(a.ws.sa_known + (int64_t)b * SFX_MAX_CANDIDATES + c,
+                   best + 1);
         if (a.out.sa_len) a.out.sa_len[(int64_t)b * C + c] = best;
         if (a.out.sa_start) a.out.sa_start[(int64_t)b * C + c] = s0;
         if (a.out.sa_end) a.out.sa_end[(int64_t)b * C + c] = e0;
@@ -683,14 +764,48 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
       int32_t* dlen = (int32_t*)(smem + L.dlen);
       int32_t* dcnt = (int32_t*)(smem + L.dcnt);
       int32_t* dpc = (int32_t*)(smem + L.dpc);
+      // Every part's end lists go into LDS in the same round of loads as
+      // the parts' maxima and counts, so the gather reads its positions
+      // there instead of one more dependent round from the workspace.
+      const int nend = a.dend ? a.dparts * C * R : 0;
+      const int32_t* ends = a.ws.d_end + (int64_t)b * a.dparts * C * R;
+      int32_t* dend = (int32_t*)(smem + L.dend);
+      constexpr int kPre = 4;
+      int32_t pre[kPre];
+#pragma unroll
+      for (int u = 0; u < kPre; ++u) {
+        const int e = tid + u * NT;
+        pre[u] = e < nend ? ends[e] : 0;
+      }
+      // The SA lengths its workgroup has published so far (agent-scope
+      // loads: it wrote them from another CU), with the same round.
+      int sa1 = 0;
+      if (tid < C)
+        sa1 = __hip_atomic_load(
+            a.ws.sa_known + (int64_t)b * SFX_MAX_CANDIDATES + tid,
+            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       delta_combine(a, b, (const int32_t*)(smem + L.caps), dlen, dcnt, dpc,
                     (int32_t*)(smem + L.dmap));
+#pragma unroll
+      for (int u = 0; u < kPre; ++u) {
+        const int e = tid + u * NT;
+        if (e < nend) dend[e] = pre[u];
+      }
+      for (int e = tid + kPre * NT; e < nend; e += NT) dend[e] = ends[e];
       __syncthreads();
-      for (int c = tid; c < C; c += NT)
+      // A cap's delta candidate counts only when its match is longer than
+      // the SA's (global_index.py:321-325); where the SA length is known
+      // and at least as long, its expansion is skipped (the pick never
+      // reads it).
+      int32_t* need = (int32_t*)(smem + L.found);
+      for (int c = tid; c < C; c += NT) {
         ws_store(a.ws.dl_c + (int64_t)b * C + c, dlen[c]);
+        need[c] = sa1 == 0 || dlen[c] > sa1 - 1;
+      }
+      __syncthreads();
       SFX_TRACE_POINT(5);
       source_expand(a, L, smem, b, 2, dlen, dcnt, nullptr, dpc, a.ws.dn_nv,
-                    a.ws.dn_score, a.ws.dn_chain);
+                    a.ws.dn_score, a.ws.dn_chain, need);
       SFX_TRACE_POINT(6);
       if (block_arrive(a.ws.pick + b, 3u, misc + 2))
         final_pick(p, a.ws, b, a.draft, a.num_valid, misc + 4);

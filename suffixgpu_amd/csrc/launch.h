@@ -75,7 +75,14 @@ size_t local_lds_bytes(const sfx_params& p, int64_t S, int chunk,
 
 int check_global(const sfx_params& p, const sfx_index& ix, int64_t batch);
 int mb_lds_bytes(const sfx_index& ix, int parts);
+// Merge waves (one per cap expansion) whose layout fits `cap`, with the
+// delta parts' end lists in LDS when dend_parts > 0 (decode step).
 int merge_waves_for(const sfx_params& p, const sfx_index& ix, int parts,
-                    size_t* lds, size_t cap = kMaxLds);
+                    size_t* lds, size_t cap = kMaxLds, int dend_parts = 0);
+// Delta positions a part stages per chunk: the most that fit `cap` beside
+// the rest of the layout (a whole part when it fits), at least 8192; *lds
+// = the layout's bytes.
+int delta_chunk_for(const sfx_params& p, const sfx_index& ix, int parts,
+                    int nmw, int dend_parts, size_t cap, size_t* lds);
 
 }  // namespace sfx

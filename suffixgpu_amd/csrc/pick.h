@@ -40,6 +40,9 @@ __device__ __forceinline__ void final_pick(const sfx_params& p,
     }
     const float lscore = ws.l_score[b];
     const int lemit = ws.l_emit[b];
+    // the SA lengths published for the delta workgroups: every producer
+    // has arrived, so none reads them again this step
+    if (on) ws.sa_known[(int64_t)b * SFX_MAX_CANDIDATES + c] = 0;
     const bool use_sa = sl >= dl && sl > 0;
     const bool use_d = dl > sl && dl > 0;
     const int len = use_sa ? sl : (use_d ? dl : 0);

@@ -144,8 +144,19 @@ int launch_step(const sfx_params* p, const sfx_index* ix, const sfx_batch* bt,
     a.g.ws = a.l.ws;
     size_t glds = 0;
     a.g.dparts = dparts;
-    a.g.merge_waves = merge_waves_for(*p, *ix, dparts, &glds, cap);
+    // the parts' end lists in LDS at the join, unless they would take a
+    // merge wave away
+    a.g.dend = 1;
+    a.g.merge_waves = merge_waves_for(*p, *ix, dparts, &glds, cap, dparts);
+    size_t glds0 = 0;
+    const int nmw0 = merge_waves_for(*p, *ix, dparts, &glds0, cap, 0);
+    if (nmw0 > a.g.merge_waves) {
+      a.g.dend = 0;
+      a.g.merge_waves = nmw0;
+    }
     a.g.mb_lds = mb_lds_bytes(*ix, dparts);
+    a.g.dchunk = delta_chunk_for(*p, *ix, dparts, a.g.merge_waves,
+                                 a.g.dend ? dparts : 0, cap, &glds);
     lds = lds > glds ? lds : glds;
   }
   if (lds > kMaxLds) return SFX_EINVAL;
@@ -186,7 +197,8 @@ int scratch_of_current_device(hipStream_t stream, void** out) {
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return (int)e;
     if (!ptr) return SFX_EINVAL;
-    const int64_t words = 3 * kScratchRows;  // join, djoin, pick
+    // join, djoin, pick and sa_known: the words every step leaves zero
+    const int64_t words = kZeroWordsPerRow * kScratchRows;
     hipLaunchKernelGGL(k_zero_words, dim3(64), dim3(256), 0, stream,
                        (uint32_t*)ptr, words);
     e = hipGetLastError();

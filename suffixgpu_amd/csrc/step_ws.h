@@ -17,6 +17,9 @@ struct StepWs {
   unsigned* join;     // [B] SA-search + delta-part arrivals (query)
   unsigned* djoin;    // [B] delta-part arrivals (step)
   unsigned* pick;     // [B] step: SA, last delta part and local arrivals
+  int32_t* sa_known;  // [B,SFX_MAX_CANDIDATES] step: SA length of cap c + 1,
+                      // published by the SA workgroup, 0 until then (the
+                      // final pick clears it)
   int32_t* l_chain;   // [B,K] best local chain (uncapped)
   int32_t* l_emit;    // [B]
   float* l_score;     // [B]
@@ -94,9 +97,12 @@ __host__ __device__ inline int64_t delta_mb_stride(int64_t part_cap) {
 inline size_t ws_align(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // Returns the byte size; fills `ws` when base != nullptr.  The three
-// handover counter arrays come first, each sized for `counter_rows` rows
-// (B when negative), so a caller that fixes counter_rows keeps them at the
-// same offsets for every batch size.
+// handover counter arrays and sa_known (the words that must be zero when
+// a call starts and that every call leaves zero) come first, sized for
+// `counter_rows` rows (B when negative), so a caller that fixes
+// counter_rows keeps them at the same offsets for every batch size:
+// kZeroWordsPerRow words per row.
+constexpr int64_t kZeroWordsPerRow = 3 + SFX_MAX_CANDIDATES;
 inline size_t step_ws_layout(const sfx_params& p, int64_t B,
                              int64_t delta_capacity, void* base,
                              StepWs* ws, int64_t counter_rows = -1) {
@@ -116,6 +122,7 @@ inline size_t step_ws_layout(const sfx_params& p, int64_t B,
   w.join = (unsigned*)take(cr * 4);
   w.djoin = (unsigned*)take(cr * 4);
   w.pick = (unsigned*)take(cr * 4);
+  w.sa_known = (int32_t*)take(cr * SFX_MAX_CANDIDATES * 4);
   w.l_chain = (int32_t*)take(b * K * 4);
   w.l_emit = (int32_t*)take(b * 4);
   w.l_score = (float*)take(b * 4);

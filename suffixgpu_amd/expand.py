@@ -59,15 +59,44 @@ def expand_chain(cont: torch.Tensor, num_occ: torch.Tensor, k: int,
                             torch.Tensor]:
     """Majority-vote chain expansion with fused scoring (expand.py:59-147).
 
-    Returns (chain [B, k] int32, num_valid [B] i64, num_emit [B] i64,
-    score [B] f32).  ``sentinel`` must be -1 (the padding value of every
-    continuation block in the drafter).
+    Returns (chain [B, k], num_valid [B] i64, num_emit [B] i64, score [B]
+    f32); the chain is int32 for the drafter's sentinel -1 and of cont's
+    dtype otherwise, as the reference's two paths return.
+
+    The kernel marks inactive continuation slots with -1.  Another
+    sentinel s (any int32 value; -1 may then be a real token) is moved
+    onto -1 by an order-preserving bijection of the int32 values without
+    s onto those without -1: for s < -1 the values in (s, -1] move down
+    by one, for s > -1 those in [-1, s) move up by one, and s becomes -1.
+    Votes compare tokens for equality and break ties by the smallest
+    token, both of which the bijection keeps, so the chain maps back
+    exactly (slots the kernel leaves at -1 become s).
     """
-    if sentinel != -1:
-        raise ValueError("expand_chain: only sentinel -1 is supported")
     require_gpu(cont, num_occ, cap, weights)
     b = cont.shape[0]
     if cap is None:
         cap = torch.full((b,), k, dtype=torch.int64, device=cont.device)
-    return kernels.expand_chain(cont, num_occ, k, min_token_prob, cap,
-                                weights=weights, alpha=alpha)
+    if sentinel == -1:
+        return kernels.expand_chain(cont, num_occ, k, min_token_prob, cap,
+                                    weights=weights, alpha=alpha)
+    s = int(sentinel)
+    if not -2 ** 31 <= s < 2 ** 31:
+        raise ValueError("expand_chain: the sentinel must be an int32 value")
+    if cont.dtype not in (torch.int32, torch.int64):
+        raise TypeError("expand_chain: integer continuation tokens")
+    c = cont.to(torch.int64)
+    if s < -1:
+        mapped = torch.where((c > s) & (c <= -1), c - 1, c)
+    else:
+        mapped = torch.where((c >= -1) & (c < s), c + 1, c)
+    mapped = torch.where(c == s, torch.full_like(c, -1), mapped)
+    chain, nv, ne, score = kernels.expand_chain(
+        mapped.to(torch.int32).contiguous(), num_occ, k, min_token_prob,
+        cap, weights=weights, alpha=alpha)
+    ch = chain.to(torch.int64)
+    if s < -1:
+        back = torch.where((ch >= s) & (ch <= -2), ch + 1, ch)
+    else:
+        back = torch.where((ch >= 0) & (ch <= s), ch - 1, ch)
+    back = torch.where(ch == -1, torch.full_like(ch, s), back)
+    return back.to(cont.dtype), nv, ne, score

@@ -243,6 +243,41 @@ def test_expand_chain(gpu, r, minp):
             np.testing.assert_array_equal(N(g), e)
 
 
+@pytest.mark.parametrize("sentinel", [-7, -2, 0, 4])
+def test_expand_chain_other_sentinels(gpu, sentinel):
+    """A sentinel other than -1 pads the continuations and -1 is then a
+    real token (expand.py:59-66, 107-147): the chain, counts and scores
+    equal the oracle's, with and without weights, and int64 blocks keep
+    their dtype."""
+    from suffixgpu_amd.expand import expand_chain
+    rng = np.random.default_rng(77 + sentinel)
+    b, r, k = 41, 48, 10
+    for lo, hi in ((-3, 6), (sentinel - 2, sentinel + 3)):
+        cont = rng.integers(lo, hi, size=(b, r, k))
+        tail = rng.integers(0, k + 1, size=(b, r))
+        cont = np.where(np.arange(k)[None, None, :] < tail[:, :, None], cont,
+                        sentinel)
+        occ = rng.integers(0, r + 1, size=b).astype(np.int64)
+        cap = rng.integers(-1, k + 2, size=b).astype(np.int64)
+        w = rng.random((b, r)).astype(np.float32) + 0.05
+        for dt, weights in ((I32, None), (np.int64, None), (I32, w)):
+            c = cont.astype(dt)
+            got = expand_chain(T(c, gpu), T(occ, gpu), k, sentinel=sentinel,
+                               min_token_prob=0.05, cap=T(cap, gpu),
+                               weights=None if weights is None
+                               else T(weights, gpu))
+            exp = o_expand(c, occ, k, sentinel=sentinel, min_token_prob=0.05,
+                           cap=cap, weights=weights)
+            assert got[0].dtype == T(c, gpu).dtype
+            for g, e in zip(got[:3], exp[:3]):
+                np.testing.assert_array_equal(N(g), e)
+            if weights is None:
+                np.testing.assert_array_equal(N(got[3]), exp[3])
+            else:
+                np.testing.assert_allclose(N(got[3]), exp[3], rtol=1e-5,
+                                           atol=0)
+
+
 @pytest.mark.parametrize("i", range(4))
 def test_expand_alpha_weights_golden(gpu, i):
     from suffixgpu_amd.expand import expand_chain

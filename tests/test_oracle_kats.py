@@ -600,3 +600,17 @@ def test_user_poll_schedule_equals_next_poll_without_midcall_room():
         np.testing.assert_array_equal(u.sa, a.sa)
         np.testing.assert_array_equal(u.delta[:u.delta_len],
                                       a.delta[:a.delta_len])
+
+
+def test_expand_other_sentinel_kat():
+    """expand.py:107-147 with sentinel -7: -1 is a real token.  Depth 0:
+    -1 holds 2 of 3 votes; depth 1: the two rows on the chain agree on 5;
+    depth 2: both are padding.  Worked by hand."""
+    from oracle.expand import expand_chain
+    cont = np.array([[[-1, 5, -7], [-1, 5, -7], [3, -7, -7]]], np.int32)
+    chain, nv, emit, score = expand_chain(cont, np.array([3]), 3,
+                                          sentinel=-7)
+    assert chain.tolist() == [[-1, 5, -7]]
+    assert nv.tolist() == [2] and emit.tolist() == [2]
+    p = np.float32(2) / np.float32(3)
+    assert score[0] == np.float32(p + np.float32(p * np.float32(1)))
