@@ -32,7 +32,7 @@ extern "C" {
 
 #define SFX_EINVAL (-1)
 #define SFX_MAX_CANDIDATES 32
-#define SFX_ABI_VERSION 13
+#define SFX_ABI_VERSION 14
 
 /* Drafter configuration shared by the local and global paths.
  * Mirrors the constructor arguments of SuffixGPUDrafter
@@ -81,7 +81,7 @@ typedef struct sfx_index {
     const void* gram;          /* n-gram range table of sa_key's suffix
                                   array (sfx_gram_build), or NULL         */
     const void* gram_alt;      /* the table of sa_key_alt's, or NULL      */
-    int64_t gram_slots;        /* slots per table, a power of two >= 16   */
+    int64_t gram_slots;        /* slots per table, a multiple of 16      */
 } sfx_index;
 
 /* One decode step's batch (suffix_gpu/proposer.py:135-214).
@@ -256,8 +256,9 @@ int sfx_sa_build(const int32_t* text, int64_t m, int64_t n_total, void* sa,
  * only) among the sorted suffixes, the rank range of the suffixes that
  * start with it, so that an interval search starts inside the range of its
  * pattern's first tokens.  `table` (256-byte aligned, sfx_gram_table_bytes
- * bytes for `slots` slots, a power of two >= 16, in buckets of 16) is
- * rebuilt in place from the key rows (key_width 4..32, 16-byte aligned) of
+ * bytes for `slots` slots, a multiple of 16 in buckets of 16, 24 bytes a
+ * slot) is rebuilt in place from the key rows (key_width 4..32, 16-byte
+ * aligned) of
  * ranks 0..m-1, enqueued on `stream` with no host read; it needs no
  * initial contents (a zero-filled table reads as unusable).  A build whose
  * runs overflow the buckets marks the table unusable and searches then

@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsuffixgpu_amd.so"
 MAX_CANDIDATES = 32
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64

@@ -100,7 +100,7 @@ int check_global(const sfx_params& p, const sfx_index& ix, int64_t batch) {
   // n-gram tables: a power-of-two slot count of at least one bucket,
   // 256-byte aligned tables, the second one only with a selector
   if ((ix.gram || ix.gram_alt) &&
-      (ix.gram_slots < kGramBucket || (ix.gram_slots & (ix.gram_slots - 1)) ||
+      (ix.gram_slots < kGramBucket || ix.gram_slots % kGramBucket ||
        ix.gram_slots > (1ll << 31) || ((uintptr_t)ix.gram & 255) ||
        ((uintptr_t)ix.gram_alt & 255) || (ix.gram_alt && !ix.key_select)))
     return SFX_EINVAL;

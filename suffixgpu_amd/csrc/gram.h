@@ -8,17 +8,20 @@
 // from 6 dependent rounds to at most 3 (one lookup plus two rounds).
 //
 // Layout: a 256-byte header {ok}, then one u32 fill count per bucket
-// (padded to 256 bytes), then the buckets: kGramBucket consecutive 32-byte
-// slots {t[4], lo, hi, k, pad} each (512 bytes, aligned).  A run hashes to
-// bucket b; an insert takes position atomicAdd(&count[b], 1) and, when b
-// is full, moves on to b + 1, b + 2, ... (at most kGramSpill buckets).
-// The counts keep counting past kGramBucket, so count[b] > kGramBucket
-// tells a lookup that runs hashed to b (or before) may sit further on.
-// The counts live in a 4 MiB array for 2^24 slots, so the inserts' atomics
-// stay in cache while the slot stores stream out; a lookup is one round of
-// loads (the bucket's slots and its count together) unless its bucket
-// overflowed.  An insert that finds no room sets ok = 0 and searches then
-// ignore the table (exact, only slower).
+// (padded to 256 bytes), then the buckets, each kGramBucket 16-byte keys
+// {t0, t1, t2, t3} (-1 past the run's length, which no real token equals,
+// so a key also tells its length) followed by their kGramBucket 8-byte
+// rank ranges {lo, hi}: 384 bytes a bucket.  A table has any number of
+// buckets; a run hashes to bucket (h * buckets) >> 32, and an insert
+// takes position atomicAdd(&count[b], 1) and, when b is full, moves on to
+// b + 1, b + 2, ... (wrapping; at most kGramSpill buckets).  The counts
+// keep counting past kGramBucket, so count[b] > kGramBucket tells a
+// lookup that runs hashed to b (or before) may sit further on.  The
+// counts are 4 B a bucket, so the inserts' atomics stay in cache while the
+// slot stores stream out; a lookup is one round of loads (the bucket's
+// keys, ranges and count together) unless its bucket overflowed.  An
+// insert that finds no room sets ok = 0 and searches then ignore the
+// table (exact, only slower).
 //
 // Only runs of real tokens are stored (0 <= t < INT32_MAX): query patterns
 // hold real tokens, and the separator, the corpus padding and the -1 read
@@ -33,15 +36,8 @@ namespace sfx {
 constexpr int kGramMax = 4;
 constexpr int kGramBucket = 16;  // slots per bucket
 constexpr int kGramSpill = 8;    // buckets an insert or lookup may visit
-
-struct GramSlot {
-  int32_t t[4];  // the run's tokens, zero past k
-  uint32_t lo;   // first rank
-  uint32_t hi;   // one past the last rank
-  uint32_t k;    // run length in tokens
-  uint32_t pad;
-};
-static_assert(sizeof(GramSlot) == 32, "one slot is two 16-byte words");
+// bytes of a bucket: its keys, then their ranges
+constexpr int kGramBucketBytes = kGramBucket * (16 + 8);
 
 struct GramHeader {
   uint32_t ok;  // every run of the last build was stored
@@ -49,7 +45,7 @@ struct GramHeader {
 };
 static_assert(sizeof(GramHeader) == 256, "counts start 256-byte aligned");
 
-// Buckets of a table of `slots` slots (a power of two >= kGramBucket).
+// Buckets of a table of `slots` slots (a multiple of kGramBucket).
 __host__ __device__ inline int64_t gram_buckets(int64_t slots) {
   return slots / kGramBucket;
 }
@@ -60,7 +56,7 @@ __host__ __device__ inline size_t gram_counts_bytes(int64_t slots) {
 
 __host__ __device__ inline size_t gram_table_bytes(int64_t slots) {
   return sizeof(GramHeader) + gram_counts_bytes(slots) +
-         (size_t)slots * sizeof(GramSlot);
+         (size_t)gram_buckets(slots) * kGramBucketBytes;
 }
 
 __device__ __forceinline__ uint32_t* gram_counts(void* table) {
@@ -72,28 +68,44 @@ __device__ __forceinline__ const uint32_t* gram_counts(const void* table) {
                                            sizeof(GramHeader));
 }
 
-__device__ __forceinline__ GramSlot* gram_slots(void* table, int64_t slots) {
-  return reinterpret_cast<GramSlot*>((char*)table + sizeof(GramHeader) +
-                                     gram_counts_bytes(slots));
+// Bucket b: its keys at the returned address, its ranges 256 bytes on.
+__device__ __forceinline__ char* gram_bucket(void* table, int64_t slots,
+                                             uint32_t b) {
+  return (char*)table + sizeof(GramHeader) + gram_counts_bytes(slots) +
+         (size_t)b * kGramBucketBytes;
 }
 
-__device__ __forceinline__ const GramSlot* gram_slots(const void* table,
-                                                      int64_t slots) {
-  return reinterpret_cast<const GramSlot*>(
-      (const char*)table + sizeof(GramHeader) + gram_counts_bytes(slots));
+__device__ __forceinline__ const char* gram_bucket(const void* table,
+                                                   int64_t slots,
+                                                   uint32_t b) {
+  return (const char*)table + sizeof(GramHeader) + gram_counts_bytes(slots) +
+         (size_t)b * kGramBucketBytes;
+}
+
+// The s-th bucket a run of hash h may sit in (its home bucket first).
+__device__ __forceinline__ uint32_t gram_probe(uint32_t h, uint32_t nb,
+                                               int s) {
+  uint32_t b = (uint32_t)(((uint64_t)h * nb) >> 32) + (uint32_t)s;
+  while (b >= nb) b -= nb;
+  return b;
 }
 
 __device__ __forceinline__ bool gram_real(int32_t t) {
   return t >= 0 && t != kPad;
 }
 
-// Hash of a run (tokens past k are zero): a multiply-xorshift mix of each
-// word (the MurmurHash3 finalizer constants).
-__device__ __forceinline__ uint32_t gram_hash(int32_t t0, int32_t t1,
-                                              int32_t t2, int32_t t3, int k) {
-  uint32_t h = 0x9e3779b9u * (uint32_t)(k + 1);
-  const uint32_t w[4] = {(uint32_t)t0, (uint32_t)t1, (uint32_t)t2,
-                         (uint32_t)t3};
+// The stored key of a run of k tokens: -1 past k.
+__device__ __forceinline__ int4 gram_key(int32_t t0, int32_t t1, int32_t t2,
+                                         int32_t t3, int k) {
+  return make_int4(t0, k > 1 ? t1 : -1, k > 2 ? t2 : -1, k > 3 ? t3 : -1);
+}
+
+// Hash of a run's key: a multiply-xorshift mix of each word (the
+// MurmurHash3 finalizer constants).
+__device__ __forceinline__ uint32_t gram_hash(const int4& t) {
+  uint32_t h = 0x9e3779b9u;
+  const uint32_t w[4] = {(uint32_t)t.x, (uint32_t)t.y, (uint32_t)t.z,
+                         (uint32_t)t.w};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     h ^= w[j] + 0x7f4a7c15u + (h << 6) + (h >> 2);
@@ -118,31 +130,32 @@ __device__ __forceinline__ int gram_lookup(const void* table, int64_t slots,
   static_assert(kGramBucket % G == 0, "lanes split a bucket evenly");
   constexpr int PL = kGramBucket / G;  // slots per lane
   const uint32_t* counts = gram_counts(table);
-  const GramSlot* sl = gram_slots(table, slots);
-  const uint32_t bmask = (uint32_t)(gram_buckets(slots) - 1);
+  const uint32_t nb = (uint32_t)gram_buckets(slots);
   const int ln = lane_id();
   const int gl = ln % G;
   const int gbase = ln - gl;
   const uint32_t full = G == 32 ? 0xffffffffu : ((1u << G) - 1u);
-  const uint32_t h = gram_hash(t0, t1, t2, t3, k);
+  const int4 key = gram_key(t0, t1, t2, t3, k);
+  const uint32_t h = gram_hash(key);
   for (int s = 0; s < kGramSpill; ++s) {
-    const uint32_t bk = (h + (uint32_t)s) & bmask;
+    const uint32_t bk = gram_probe(h, nb, s);
     const uint32_t cnt = counts[bk];
+    const char* bucket = gram_bucket(table, slots, bk);
     int4 a[PL];
-    uint4 w[PL];
+    uint2 w[PL];
 #pragma unroll
     for (int i = 0; i < PL; ++i) {
-      const GramSlot* q = sl + (size_t)bk * kGramBucket + gl * PL + i;
-      a[i] = *reinterpret_cast<const int4*>(&q->t[0]);
-      w[i] = *reinterpret_cast<const uint4*>(&q->lo);
+      const int slot = gl * PL + i;
+      a[i] = reinterpret_cast<const int4*>(bucket)[slot];
+      w[i] = reinterpret_cast<const uint2*>(bucket + 16 * kGramBucket)[slot];
     }
     bool hit = false;
     uint32_t hl = 0, hh = 0;
 #pragma unroll
     for (int i = 0; i < PL; ++i) {
       const uint32_t pos = (uint32_t)(gl * PL + i);
-      const bool h1 = pos < cnt && (int)w[i].z == k && a[i].x == t0 &&
-                      a[i].y == t1 && a[i].z == t2 && a[i].w == t3;
+      const bool h1 = pos < cnt && a[i].x == key.x && a[i].y == key.y &&
+                      a[i].z == key.z && a[i].w == key.w;
       hl = h1 ? w[i].x : hl;
       hh = h1 ? w[i].y : hh;
       hit = hit || h1;

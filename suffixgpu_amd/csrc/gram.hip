@@ -41,10 +41,6 @@ __device__ __forceinline__ int real4(const int4& a) {
   return gram_real(a.w) ? 4 : 3;
 }
 
-__device__ __forceinline__ int4 first4(const int4& a, int k) {
-  return make_int4(a.x, k > 1 ? a.y : 0, k > 2 ? a.z : 0, k > 3 ? a.w : 0);
-}
-
 // The rank's leading tokens and its common prefixes with both neighbours.
 struct RankRuns {
   int4 cur;
@@ -75,22 +71,21 @@ __global__ __launch_bounds__(256) void k_gram_insert(
   const RankRuns q = rank_runs(keys, kw, m, r);
   if (q.nreal <= q.lcp_prev) return;  // every run here started earlier
   uint32_t* counts = gram_counts(table);
-  GramSlot* sl = gram_slots(table, slots);
-  const uint32_t bmask = (uint32_t)(gram_buckets(slots) - 1);
+  const uint32_t nb = (uint32_t)gram_buckets(slots);
   for (int k = q.lcp_prev + 1; k <= q.nreal; ++k) {
-    const int4 t = first4(q.cur, k);
-    const uint32_t h = gram_hash(t.x, t.y, t.z, t.w, k);
+    const int4 t = gram_key(q.cur.x, q.cur.y, q.cur.z, q.cur.w, k);
+    const uint32_t h = gram_hash(t);
     // hi is known now when the run ends here; else the close pass sets it
     const uint32_t hi = k > q.lcp_next ? (uint32_t)r + 1 : 0u;
     bool placed = false;
     for (int s = 0; s < kGramSpill && !placed; ++s) {
-      const uint32_t bk = (h + (uint32_t)s) & bmask;
+      const uint32_t bk = gram_probe(h, nb, s);
       const uint32_t pos = atomicAdd(&counts[bk], 1u);
       if (pos < (uint32_t)kGramBucket) {
-        GramSlot* d = sl + (size_t)bk * kGramBucket + pos;
-        *reinterpret_cast<int4*>(&d->t[0]) = t;
-        *reinterpret_cast<uint4*>(&d->lo) =
-            make_uint4((uint32_t)r, hi, (uint32_t)k, 0u);
+        char* bucket = gram_bucket(table, slots, bk);
+        reinterpret_cast<int4*>(bucket)[pos] = t;
+        reinterpret_cast<uint2*>(bucket + 16 * kGramBucket)[pos] =
+            make_uint2((uint32_t)r, hi);
         placed = true;
       }
     }
@@ -108,22 +103,22 @@ __global__ __launch_bounds__(256) void k_gram_close(
   const int kmax = q.lcp_prev < q.nreal ? q.lcp_prev : q.nreal;
   if (kmax <= q.lcp_next) return;
   const uint32_t* counts = gram_counts(table);
-  GramSlot* sl = gram_slots(table, slots);
-  const uint32_t bmask = (uint32_t)(gram_buckets(slots) - 1);
+  const uint32_t nb = (uint32_t)gram_buckets(slots);
   for (int k = q.lcp_next + 1; k <= kmax; ++k) {
-    const int4 t = first4(q.cur, k);
-    const uint32_t h = gram_hash(t.x, t.y, t.z, t.w, k);
+    const int4 t = gram_key(q.cur.x, q.cur.y, q.cur.z, q.cur.w, k);
+    const uint32_t h = gram_hash(t);
     bool done = false;
     for (int s = 0; s < kGramSpill && !done; ++s) {
-      const uint32_t bk = (h + (uint32_t)s) & bmask;
+      const uint32_t bk = gram_probe(h, nb, s);
       const uint32_t cnt = counts[bk];
       const uint32_t n = cnt < (uint32_t)kGramBucket ? cnt : kGramBucket;
-      GramSlot* b = sl + (size_t)bk * kGramBucket;
+      char* bucket = gram_bucket(table, slots, bk);
+      const int4* bkeys = reinterpret_cast<const int4*>(bucket);
+      uint2* ranges = reinterpret_cast<uint2*>(bucket + 16 * kGramBucket);
       for (uint32_t i = 0; i < n; ++i) {
-        const int4 a = *reinterpret_cast<const int4*>(&b[i].t[0]);
-        if ((int)b[i].k == k && a.x == t.x && a.y == t.y && a.z == t.z &&
-            a.w == t.w) {
-          b[i].hi = (uint32_t)r + 1;
+        const int4 a = bkeys[i];
+        if (a.x == t.x && a.y == t.y && a.z == t.z && a.w == t.w) {
+          ranges[i].y = (uint32_t)r + 1;
           done = true;
           break;
         }
@@ -138,7 +133,7 @@ __global__ __launch_bounds__(256) void k_gram_close(
 using namespace sfx;
 
 static bool gram_slots_ok(int64_t slots) {
-  return slots >= kGramBucket && !(slots & (slots - 1)) &&
+  return slots >= kGramBucket && slots % kGramBucket == 0 &&
          slots <= (1ll << 31);
 }
 

@@ -40,16 +40,16 @@ PAD_TOKEN = torch.iinfo(torch.int32).max
 # Tokens of every suffix kept next to the suffix array (one 128-byte row
 # per rank) so an interval-search probe is a single row load.
 KEY_WIDTH = 32
-# Slots of the n-gram range table per corpus position (a power of two in
-# all, in buckets of 16): a corpus of real text holds about 1.6 distinct
-# runs of 1-4 tokens per position, so the buckets stay about 40% full and
-# almost never overflow.
-GRAM_SLOTS_PER_TOKEN = 4
+# Slots of the n-gram range table per corpus position (in buckets of 16,
+# 24 bytes a slot): a corpus of real text holds about 1.6 distinct runs of
+# 1-4 tokens per position, so the buckets stay about half full and rarely
+# overflow into the next one.
+GRAM_SLOTS_PER_TOKEN = 3
 
 
 def gram_slots_for(capacity: int) -> int:
     n = max(1024, GRAM_SLOTS_PER_TOKEN * capacity)
-    return 1 << (n - 1).bit_length()
+    return (n + 15) // 16 * 16
 # Written between documents; negative, so no query token (>= 0) can match
 # it and neither matches nor continuations cross document boundaries.
 SEP_TOKEN = -2
@@ -109,11 +109,20 @@ class GlobalIndex:
             self._keys = [torch.empty(capacity * KEY_WIDTH,
                                       dtype=torch.int32, device=dev)
                           for _ in range(2)]
-            # gram_slots (a power of two) overrides the table size; a
+            # gram_slots (a multiple of 16) overrides the table size; a
             # table too small for the corpus marks itself unusable and
             # searches span the whole suffix array instead.
             self.gram_slots = gram_slots or gram_slots_for(capacity)
-            gbytes = int(lib().sfx_gram_table_bytes(self.gram_slots))
+            # Each table's buffer: the table, then each rank's first four
+            # tokens (written with the key rows, read by the table build).
+            # The idle buffer also lends its table region to the suffix
+            # array build as workspace: a build's table is written only
+            # once the host has seen its suffix array is final.
+            tbytes = int(lib().sfx_gram_table_bytes(self.gram_slots))
+            self._gram_bytes = max(tbytes,
+                                   sa_workspace_bytes(capacity) + 255) \
+                // 256 * 256
+            gbytes = self._gram_bytes + 16 * capacity
             self._grams = [torch.zeros(gbytes, dtype=torch.uint8,
                                        device=dev) for _ in range(2)]
             self.key_select = torch.zeros(1, dtype=torch.int32, device=dev)
@@ -159,7 +168,9 @@ class GlobalIndex:
         # copy of the build's state block).
         self.sa_round_hint = 12
         self.sa_radix_hint = DEFAULT_RADIX_MASK
-        self._build_state = None  # (m, next_round) while rounds may remain
+        # (m, next_round) while rounds may remain; (m, None) once the suffix
+        # array is final and its n-gram table is being built
+        self._build_state = None
         self._flag_host = torch.zeros(STATE_WORDS, dtype=torch.int32,
                                       pin_memory=True)
 
@@ -194,8 +205,11 @@ class GlobalIndex:
                              self._grams[1].data_ptr(), self.gram_slots)
 
     def device_bytes(self) -> dict:
-        """Device memory held by the index, by role (bytes)."""
-        ws = self._sa_ws.numel() if self._sa_ws is not None else 0
+        """Device memory held by the index, by role (bytes).  With search
+        tables the suffix-array build workspace lies inside the idle
+        table's buffer (counted under gram_tables)."""
+        ws = (self._sa_ws.numel() if self._sa_ws is not None
+              and not self.search_tables else 0)
         qws = sum(t.numel() for t in self._query_ws.values())
         return {
             "corpus_sa": 4 * 4 * self.capacity,  # live + staging, int32
@@ -206,29 +220,41 @@ class GlobalIndex:
             "query_workspace": qws,
         }
 
-    def _build_keys(self, corpus, sa, slot: int, m: int) -> None:
-        """Key rows and n-gram range table of (corpus, sa) into buffer
-        pair `slot` (0 or 1), on the current stream.  Ranks from m on are
-        the padding suffixes (sa the identity, corpus PAD): their rows are
-        rewritten only where the buffer's previous build had real ones,
-        and they hold no run of real tokens for the table."""
+    def _build_keys(self, corpus, sa, slot: int, m: int,
+                    table: bool = True) -> None:
+        """Key rows (and, with `table`, the n-gram range table) of
+        (corpus, sa) into buffer pair `slot` (0 or 1), on the current
+        stream.  Ranks from m on are the padding suffixes (sa the identity,
+        corpus PAD): their rows are rewritten only where the buffer's
+        previous build had real ones, and they hold no run of real tokens
+        for the table."""
         if not self.search_tables:
             return
-        keys, gram = self._keys[slot], self._grams[slot]
+        keys = self._keys[slot]
         st = stream_of(self.device)
         rows = max(m, self._key_rows[slot])
-        # the table reads each rank's first four tokens, written compactly
-        # by the same launch into the SA build workspace's key buffers
-        # (free between build launches) rather than read from the rows
-        first4 = self._sa_workspace().data_ptr() if m > 0 else None
+        # each rank's first four tokens, written compactly by the same
+        # launch after the table in its buffer, for the table build
+        first4 = self._first4(slot) if m > 0 else None
         check(lib().sfx_sa_keys(corpus.data_ptr(), sa.data_ptr(),
                                 self.capacity, rows, KEY_WIDTH,
                                 keys.data_ptr(), first4, st), "SA key rows")
-        check(lib().sfx_gram_build(first4 or keys.data_ptr(),
-                                   4 if first4 else KEY_WIDTH, m,
-                                   gram.data_ptr(), self.gram_slots, st),
-              "n-gram table")
         self._key_rows[slot] = m
+        if table:
+            self._build_table(slot, m)
+
+    def _first4(self, slot: int) -> int:
+        return self._grams[slot].data_ptr() + self._gram_bytes
+
+    def _build_table(self, slot: int, m: int) -> None:
+        """The n-gram range table of buffer pair `slot` from the first
+        four tokens its key-row launch wrote (m ranks), on the current
+        stream."""
+        first4 = self._first4(slot) if m > 0 else self._keys[slot].data_ptr()
+        check(lib().sfx_gram_build(first4, 4 if m > 0 else KEY_WIDTH, m,
+                                   self._grams[slot].data_ptr(),
+                                   self.gram_slots, stream_of(self.device)),
+              "n-gram table")
 
     # ------------------------------------------------------------------
     # writes (global_index.py:86-133)
@@ -388,8 +414,13 @@ class GlobalIndex:
             self._finish_swap(n_new, new_doc_lens)
 
     def _sa_workspace(self) -> torch.Tensor:
+        """The suffix-array build workspace: the table region of the idle
+        buffer pair with search tables (nothing reads it until the build's
+        own table is written there), else an allocation of its own."""
         need = sa_workspace_bytes(self.capacity)
-        if self._sa_ws is None or self._sa_ws.numel() < need:
+        if self.search_tables:
+            self._sa_ws = self._grams[1 - self._key_live][:max(need, 1)]
+        elif self._sa_ws is None or self._sa_ws.numel() < need:
             self._sa_ws = torch.empty(max(need, 1), dtype=torch.uint8,
                                       device=self.device)
         return self._sa_ws
@@ -401,6 +432,7 @@ class GlobalIndex:
                                  self.staging_sa.data_ptr(), 0,
                                  ws.data_ptr(), ws.numel(),
                                  stream_of(self.device)), "SA rebuild")
+        # (the workspace is dead once the build wrote staging_sa)
         self._build_keys(dst, self.staging_sa, 1 - self._key_live, m)
 
     # Background builds, enqueued on the current (rebuild) stream.
@@ -430,13 +462,17 @@ class GlobalIndex:
         self._flag_host.copy_(state_view(self._sa_ws, m), non_blocking=True)
 
     def _staged_build_finish(self, dst: torch.Tensor, m: int) -> None:
+        """The output and key rows, speculatively (the host has not seen
+        whether the array is final yet); the table only once it has, as
+        the workspace may still be needed for more rounds."""
         ws = self._sa_ws
         check(lib().sfx_sa_build_finish(m, self.capacity,
                                         self.staging_sa.data_ptr(), 0,
                                         ws.data_ptr(), ws.numel(),
                                         stream_of(self.device)),
               "SA rebuild")
-        self._build_keys(dst, self.staging_sa, 1 - self._key_live, m)
+        self._build_keys(dst, self.staging_sa, 1 - self._key_live, m,
+                         table=False)
 
     def _staged_build_check(self) -> bool:
         """After the build's event: True when the staged output is final;
@@ -450,15 +486,17 @@ class GlobalIndex:
             return True
         m, nxt = self._build_state
         self._build_state = None
+        if nxt is None:
+            return True  # the table of a final array is built
         if m <= 1:
-            return True  # nothing to sort; the hints stay as they are
+            return self._staged_table(m)  # nothing to sort
         state = BuildState.of(self._flag_host.tolist())
         L = lib()
         total = int(L.sfx_sa_build_rounds_total(m))
         if state.done:
             self.sa_round_hint = state.needed + 2
             self.sa_radix_hint = state.radix_mask & ~1
-            return True
+            return self._staged_table(m)
         if state.stalled:
             nxt, radix = state.stalled, 1 << state.stalled
         elif nxt > total:
@@ -466,7 +504,7 @@ class GlobalIndex:
             # have raised the flag, so the array is final as it stands.
             self.sa_round_hint = total
             self.sa_radix_hint = state.radix_mask & ~1
-            return True
+            return self._staged_table(m)
         else:
             radix = 0
         self.rebuild_stream.wait_stream(torch.cuda.current_stream(self.device))
@@ -477,6 +515,22 @@ class GlobalIndex:
             self._copy_build_state(m)
             self._staged_build_finish(self.staging_corpus, m)
         self._build_state = (m, total + 1)
+        event = torch.cuda.Event()
+        event.record(self.rebuild_stream)
+        self._rebuild_event = event
+        return False
+
+    def _staged_table(self, m: int) -> bool:
+        """The suffix array of a background build is final: with search
+        tables, enqueue its n-gram table (over the workspace, dead now) on
+        the rebuild stream under a new event and report the build as not
+        done yet; else it is done."""
+        if not self.search_tables:
+            return True
+        self.rebuild_stream.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(self.rebuild_stream):
+            self._build_table(1 - self._key_live, m)
+        self._build_state = (m, None)
         event = torch.cuda.Event()
         event.record(self.rebuild_stream)
         self._rebuild_event = event

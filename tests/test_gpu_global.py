@@ -485,6 +485,8 @@ def test_save_restore_bit_exact(gpu, tmp_path):
     g = GlobalIndex(capacity=5000, delta_capacity=600, k=6,
                     max_occurrences=16, rebuild_threshold=250, device=gpu,
                     rebuild_stream=side)
+    # a rebuild swaps in at the next poll, as the oracle's does
+    g.blocking_poll = True
     o = GlobalIndexOracle(capacity=5000, delta_capacity=600, k=6,
                           max_occurrences=16, rebuild_threshold=250,
                           async_rebuild=True)
@@ -634,22 +636,28 @@ def gram_runs(corpus, sa):
 def gpu_gram_table(g):
     """(ok, entries) of the live table: a 256-byte header {ok}, one u32
     fill count per bucket of 16 slots (padded to 256 bytes), then the
-    32-byte slots {t0..t3, lo, hi, k, pad}; a bucket's first
-    min(count, 16) slots are filled."""
+    buckets of 384 bytes: 16 keys {t0..t3} (-1 past the run's length k)
+    and their 16 ranges {lo, hi}; a bucket's first min(count, 16) slots
+    are filled.  Entries are keyed (k, t0, t1, t2, t3), tokens past k 0."""
     raw = N(g._grams[g._key_live])
     slots_n = g.gram_slots
     nb = slots_n // 16
     cbytes = (nb * 4 + 255) // 256 * 256
     ok = int(raw[:4].view(np.uint32)[0])
     counts = raw[256:256 + nb * 4].view(np.uint32)
-    slots = raw[256 + cbytes:].view(np.int32).reshape(nb, 16, 8)
+    buckets = raw[256 + cbytes:256 + cbytes + nb * 384].view(
+        np.int32).reshape(nb, 96)
     tab = {}
     for b in np.flatnonzero(counts):
-        for row in slots[b, :min(int(counts[b]), 16)]:
-            key = (int(row[6]), int(row[0]), int(row[1]), int(row[2]),
-                   int(row[3]))
+        keys = buckets[b, :64].reshape(16, 4)
+        ranges = buckets[b, 64:].reshape(16, 2)
+        for key4, rng in zip(keys[:min(int(counts[b]), 16)],
+                             ranges[:min(int(counts[b]), 16)]):
+            k = int((key4 != -1).sum())
+            assert (key4[:k] >= 0).all() and (key4[k:] == -1).all(), key4
+            key = (k, *[int(x) if j < k else 0 for j, x in enumerate(key4)])
             assert key not in tab, key
-            tab[key] = (int(row[4]), int(row[5]))
+            tab[key] = (int(np.uint32(rng[0])), int(np.uint32(rng[1])))
     return ok, tab
 
 
