@@ -213,10 +213,9 @@ def time_sa_builds(w, dev, side):
         build_ms[name + "_radix"] = radix
         log(f"SA rebuild {name} ({rounds} rounds, as the index runs it): "
             f"{min(times):.2f} ms")
-        if name == "corpus":
-            build_ms["tables"] = index_tables_ms(text, out, dev, side, ws)
-            log(f"key rows + n-gram table of the corpus: "
-                f"{build_ms['tables']}")
+        key = "tables" if name == "corpus" else "tables_" + name
+        build_ms[key] = index_tables_ms(text, out, dev, side, ws)
+        log(f"key rows + n-gram table of the {name} text: {build_ms[key]}")
     del ws
     return build_ms
 
@@ -254,11 +253,12 @@ def index_tables_ms(text, sa, dev, side, ws) -> dict:
         ev[2].synchronize()
         res["keys"].append(ev[0].elapsed_time(ev[1]))
         res["gram"].append(ev[1].elapsed_time(ev[2]))
-    ok = int(gram[0:4].view(torch.int32).item())  # header word 0: ok
+    # header word 0: the longest run length the table holds (0: unusable)
+    kmax = int(gram[0:4].view(torch.int32).item())
     del keys, gram
     return {"key_rows_ms": round(min(res["keys"]), 3),
             "gram_table_ms": round(min(res["gram"]), 3),
-            "gram_slots": slots, "gram_table_usable": bool(ok)}
+            "gram_slots": slots, "gram_table_kmax": kmax}
 
 
 # ------------------------------------------------------------------ main
@@ -430,6 +430,7 @@ def main() -> int:
         "sa_rebuild_hinted_mtok_s": round(sa_m / (sa_reb_ms * 1e-3) / 1e6, 2),
         "sa_rebuild_hbm": sa_rebuild_hbm(sa_reb_ms),
         "rebuild_tables": build_ms["tables"],
+        "rebuild_tables_uniform": build_ms["tables_uniform"],
         "kernels_us": {"k_step": round(step_us, 3),
                        "k_local_alone": round(k_local_us, 3),
                        "k_global_alone": round(k_global_us, 3)},

@@ -260,9 +260,12 @@ int sfx_sa_build(const int32_t* text, int64_t m, int64_t n_total, void* sa,
  * slot) is rebuilt in place from the key rows (key_width 4..32, 16-byte
  * aligned) of
  * ranks 0..m-1, enqueued on `stream` with no host read; it needs no
- * initial contents (a zero-filled table reads as unusable).  A build whose
- * runs overflow the buckets marks the table unusable and searches then
- * ignore it. */
+ * initial contents (a zero-filled table reads as unusable).  The build
+ * counts the distinct runs of each length and stores those of 1..k
+ * tokens for the largest k whose runs fill at most 3/4 of the slots; the
+ * table's first word then holds the longest length all of whose runs are
+ * stored (0..4; 0 if an insert of a 1-token run found no room), and
+ * searches look up at most that many leading tokens. */
 size_t sfx_gram_table_bytes(int64_t slots);
 int sfx_gram_build(const int32_t* keys, int64_t key_width, int64_t m,
                    void* table, int64_t slots, hipStream_t stream);

@@ -656,18 +656,20 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
     const int g = tid / G;
     const int32_t* keys = live_keys(a.ix);
     // The n-gram table narrows each search to the ranks that share its
-    // pattern's first min(l, kGramMax) tokens (the whole answer for
-    // l <= kGramMax); without a usable table every search spans [0, N).
+    // pattern's first min(l, kmax) tokens (the whole answer for
+    // l <= kmax, the longest run length the table holds); without a
+    // usable table every search spans [0, N).
     const void* gram = live_gram(a.ix);
-    if (gram && !reinterpret_cast<const GramHeader*>(gram)->ok)
-      gram = nullptr;
+    int kg = gram ? (int)reinterpret_cast<const GramHeader*>(gram)->kmax : 0;
+    kg = kg < kGramMax ? kg : kGramMax;
+    if (kg <= 0) gram = nullptr;
     for (int l = g + 1; l <= P; l += ngroups) {
       int64_t lo = 0, hi = 0;
       if (l <= plen) {
         auto pat_at = [&](int j) -> int32_t { return rpat[l - 1 - j]; };
         uint32_t r0 = 0, r1 = (uint32_t)N;
         int found = -1;
-        const int k = l < kGramMax ? l : kGramMax;
+        const int k = l < kg ? l : kg;
         int32_t t[4] = {0, 0, 0, 0};
         bool real = true;
 #pragma unroll

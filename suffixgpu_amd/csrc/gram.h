@@ -7,7 +7,7 @@
 // 2^22-token template corpus this cuts the slowest of a row's 32 searches
 // from 6 dependent rounds to at most 3 (one lookup plus two rounds).
 //
-// Layout: a 256-byte header {ok}, then one u32 fill count per bucket
+// Layout: a 256-byte header {kmax, runs[4]}, then one u32 fill count per bucket
 // (padded to 256 bytes), then the buckets, each kGramBucket 16-byte keys
 // {t0, t1, t2, t3} (-1 past the run's length, which no real token equals,
 // so a key also tells its length) followed by their kGramBucket 8-byte
@@ -19,9 +19,18 @@
 // lookup that runs hashed to b (or before) may sit further on.  The
 // counts are 4 B a bucket, so the inserts' atomics stay in cache while the
 // slot stores stream out; a lookup is one round of loads (the bucket's
-// keys, ranges and count together) unless its bucket overflowed.  An
-// insert that finds no room sets ok = 0 and searches then ignore the
-// table (exact, only slower).
+// keys, ranges and count together) unless its bucket overflowed.
+//
+// A build first counts the distinct runs of each length (runs[k - 1]) and
+// stores the runs of 1 .. kcap tokens, kcap the longest length whose runs
+// together fill at most 3/4 of the slots; an insert that still finds no
+// room lowers kmax below its length.  kmax (0 .. kGramMax) is then the
+// longest length whose runs are all stored, and a search looks up its
+// pattern's first min(l, kmax) tokens: text with about 1.6 distinct runs
+// of 1-4 tokens per position keeps all four lengths in 3 slots per
+// position, while uniform random tokens over a large vocabulary (about 3
+// per position) keep three, and kmax = 0 turns the table off (exact,
+// only slower).
 //
 // Only runs of real tokens are stored (0 <= t < INT32_MAX): query patterns
 // hold real tokens, and the separator, the corpus padding and the -1 read
@@ -35,13 +44,20 @@ namespace sfx {
 
 constexpr int kGramMax = 4;
 constexpr int kGramBucket = 16;  // slots per bucket
-constexpr int kGramSpill = 8;    // buckets an insert or lookup may visit
+constexpr int kGramSpill = 16;   // buckets an insert or lookup may visit
 // bytes of a bucket: its keys, then their ranges
 constexpr int kGramBucketBytes = kGramBucket * (16 + 8);
 
+// Runs of all lengths may fill at most kGramLoadNum / kGramLoadDen of
+// the slots.
+constexpr int kGramLoadNum = 3;
+constexpr int kGramLoadDen = 4;
+
 struct GramHeader {
-  uint32_t ok;  // every run of the last build was stored
-  uint32_t pad[63];
+  uint32_t kmax;  // every run of 1 .. kmax tokens is stored (0: unusable)
+  uint32_t pad0;
+  unsigned long long runs[kGramMax];  // distinct runs of k + 1 tokens
+  uint32_t pad[54];
 };
 static_assert(sizeof(GramHeader) == 256, "counts start 256-byte aligned");
 

@@ -1,7 +1,9 @@
 // Building the n-gram range table (gram.h) of a suffix array from its key
 // rows, on the caller's stream with no host synchronisation: the bucket
-// counts are cleared, then one pass inserts every run at the rank that
-// starts it, and one pass stores hi for the runs longer than one rank.
+// counts are cleared, one pass counts the distinct runs of each length,
+// one pass inserts every run of up to the length that fits at the rank
+// that starts it, and one pass stores hi for the runs longer than one
+// rank.
 // Rank r starts the run of its first k tokens for every k above the common
 // prefix (capped at kGramMax) of suffixes r - 1 and r, and ends it for
 // every k above that of r and r + 1; all three come from the first 16
@@ -21,8 +23,11 @@ __global__ __launch_bounds__(256) void k_gram_clear(void* table,
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
        i < buckets; i += stride)
     counts[i] = 0;
-  if (blockIdx.x == 0 && threadIdx.x == 0)
-    reinterpret_cast<GramHeader*>(table)->ok = 1;
+  if (blockIdx.x == 0 && threadIdx.x < kGramMax) {
+    GramHeader* hd = reinterpret_cast<GramHeader*>(table);
+    hd->runs[threadIdx.x] = 0;
+    if (threadIdx.x == 0) hd->kmax = kGramMax;
+  }
 }
 
 // Leading tokens two runs share (0 .. kGramMax).
@@ -63,16 +68,67 @@ __device__ __forceinline__ RankRuns rank_runs(const int32_t* __restrict__ keys,
   return q;
 }
 
+// Distinct runs of each length: rank r starts one of k tokens for every
+// k in (lcp_prev, nreal].  Each thread counts a strided share of the
+// ranks; the counts are summed per wave, then per block, then added with
+// one atomic per length and block (at most kGramCountBlocks blocks, so
+// the few global atomics on the header do not serialise the pass).
+constexpr int kGramCountBlocks = 512;
+
+__global__ __launch_bounds__(256) void k_gram_count(
+    const int32_t* __restrict__ keys, int kw, int64_t m, void* table) {
+  __shared__ uint32_t c[kGramMax];
+  if (threadIdx.x < kGramMax) c[threadIdx.x] = 0;
+  __syncthreads();
+  uint32_t n[kGramMax] = {0, 0, 0, 0};
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < m;
+       r += stride) {
+    const RankRuns q = rank_runs(keys, kw, m, r);
+#pragma unroll
+    for (int k = 1; k <= kGramMax; ++k)
+      n[k - 1] += (k > q.lcp_prev && k <= q.nreal) ? 1u : 0u;
+  }
+#pragma unroll
+  for (int k = 0; k < kGramMax; ++k) {
+    const uint32_t t = (uint32_t)__shfl((int)wave_incl_scan(n[k]), kWave - 1);
+    if (lane_id() == 0 && t) atomicAdd(&c[k], t);
+  }
+  __syncthreads();
+  if (threadIdx.x < kGramMax && c[threadIdx.x])
+    atomicAdd(&reinterpret_cast<GramHeader*>(table)->runs[threadIdx.x],
+              (unsigned long long)c[threadIdx.x]);
+}
+
+// The longest run length whose runs of 1 .. k tokens fit the load limit.
+__device__ __forceinline__ int gram_kcap(const GramHeader* hd,
+                                         int64_t slots) {
+  const unsigned long long lim =
+      (unsigned long long)slots * kGramLoadNum / kGramLoadDen;
+  unsigned long long n = 0;
+  int k = 0;
+  while (k < kGramMax) {
+    n += hd->runs[k];
+    if (n > lim) break;
+    ++k;
+  }
+  return k;
+}
+
 __global__ __launch_bounds__(256) void k_gram_insert(
     const int32_t* __restrict__ keys, int kw, int64_t m, void* table,
     int64_t slots) {
+  GramHeader* hd = reinterpret_cast<GramHeader*>(table);
+  const int kcap = gram_kcap(hd, slots);
+  if (blockIdx.x == 0 && threadIdx.x == 0) atomicMin(&hd->kmax, (uint32_t)kcap);
   const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= m) return;
   const RankRuns q = rank_runs(keys, kw, m, r);
-  if (q.nreal <= q.lcp_prev) return;  // every run here started earlier
+  const int kend = q.nreal < kcap ? q.nreal : kcap;
+  if (kend <= q.lcp_prev) return;  // every run here started earlier
   uint32_t* counts = gram_counts(table);
   const uint32_t nb = (uint32_t)gram_buckets(slots);
-  for (int k = q.lcp_prev + 1; k <= q.nreal; ++k) {
+  for (int k = q.lcp_prev + 1; k <= kend; ++k) {
     const int4 t = gram_key(q.cur.x, q.cur.y, q.cur.z, q.cur.w, k);
     const uint32_t h = gram_hash(t);
     // hi is known now when the run ends here; else the close pass sets it
@@ -89,7 +145,7 @@ __global__ __launch_bounds__(256) void k_gram_insert(
         placed = true;
       }
     }
-    if (!placed) reinterpret_cast<GramHeader*>(table)->ok = 0;
+    if (!placed) atomicMin(&hd->kmax, (uint32_t)(k - 1));
   }
 }
 
@@ -99,8 +155,11 @@ __global__ __launch_bounds__(256) void k_gram_close(
   const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= m) return;
   const RankRuns q = rank_runs(keys, kw, m, r);
-  // runs ending at r that started before r: lcp_next < k <= lcp_prev
-  const int kmax = q.lcp_prev < q.nreal ? q.lcp_prev : q.nreal;
+  // runs ending at r that started before r: lcp_next < k <= lcp_prev,
+  // of the lengths the table holds
+  const int kt = (int)reinterpret_cast<const GramHeader*>(table)->kmax;
+  int kmax = q.lcp_prev < q.nreal ? q.lcp_prev : q.nreal;
+  kmax = kmax < kt ? kmax : kt;
   if (kmax <= q.lcp_next) return;
   const uint32_t* counts = gram_counts(table);
   const uint32_t nb = (uint32_t)gram_buckets(slots);
@@ -157,6 +216,11 @@ extern "C" int sfx_gram_build(const int32_t* keys, int64_t key_width,
                      table, nb);
   if (m > 0) {
     const unsigned blocks = (unsigned)((m + 255) / 256);
+    hipLaunchKernelGGL(k_gram_count,
+                       dim3(blocks < (unsigned)kGramCountBlocks
+                                ? blocks
+                                : (unsigned)kGramCountBlocks),
+                       dim3(256), 0, stream, keys, (int)key_width, m, table);
     hipLaunchKernelGGL(k_gram_insert, dim3(blocks), dim3(256), 0, stream,
                        keys, (int)key_width, m, table, slots);
     hipLaunchKernelGGL(k_gram_close, dim3(blocks), dim3(256), 0, stream,

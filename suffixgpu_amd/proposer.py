@@ -63,6 +63,7 @@ class SuffixGPUDrafter:
         vote_smoothing_alpha: float = 0.0,
         parallel_paths: bool = True,
         global_search_tables: bool = True,
+        global_gram_slots: int | None = None,
     ):
         self.k = k
         self.device = torch.device(device)
@@ -109,7 +110,8 @@ class SuffixGPUDrafter:
                 k=k, max_occurrences=max_occurrences,
                 rebuild_threshold=rebuild_threshold, device=self.device,
                 rebuild_stream=rebuild_stream,
-                search_tables=global_search_tables)
+                search_tables=global_search_tables,
+                gram_slots=global_gram_slots)
 
     # ------------------------------------------------------------------
     def poll(self) -> None:

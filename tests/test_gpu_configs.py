@@ -225,8 +225,18 @@ def test_c4_steps_overlap_the_background_rebuild(c3, gpu):
         out = d.propose_with_update(nt, tok, samp)
     torch.cuda.synchronize()
     main = torch.cuda.current_stream(gpu)
+    with torch.cuda.stream(gi.rebuild_stream):  # the stream's first use
+        torch.zeros(1, device=gpu)
+    torch.cuda.synchronize()
     gi.rebuild_threshold = og.rebuild_threshold = 1
     gi.blocking_poll = False
+    # The build waits for the main stream's staging copies; holding the
+    # main stream for about 3 ms first lets the host enqueue the steps
+    # below before the build (about 2 ms) can have finished, however long
+    # the host takes.
+    t0 = torch.cuda.Event(enable_timing=True)
+    t0.record(main)
+    torch.cuda._sleep(6_000_000)
     gi.maybe_rebuild()
     assert gi._rebuild_event is not None
     side_end = torch.cuda.Event(enable_timing=True)
@@ -247,7 +257,8 @@ def test_c4_steps_overlap_the_background_rebuild(c3, gpu):
     # steps that ended before the build did ran beside it: the build was
     # enqueued, behind the main stream's staging copies, before them all
     overlapped = sum(e.elapsed_time(side_end) > 0 for e in ends)
-    assert overlapped >= 8, overlapped
+    assert overlapped >= 8, (overlapped, t0.elapsed_time(side_end),
+                             [round(t0.elapsed_time(e), 3) for e in ends])
     og.async_rebuild = True
     og.maybe_rebuild()  # staged: pending until the oracle's next poll
     assert og._rebuild_event is not None

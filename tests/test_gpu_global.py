@@ -633,17 +633,31 @@ def gram_runs(corpus, sa):
     return out
 
 
+def runs_capacity_kmax(exp, slots):
+    """The longest run length k whose runs of 1..k tokens together fill at
+    most 3/4 of the table's slots: the lengths a build stores."""
+    n, kmax = 0, 0
+    for k in range(1, 5):
+        n += sum(1 for key in exp if key[0] == k)
+        if 4 * n > 3 * slots:
+            break
+        kmax = k
+    return kmax
+
+
 def gpu_gram_table(g):
-    """(ok, entries) of the live table: a 256-byte header {ok}, one u32
-    fill count per bucket of 16 slots (padded to 256 bytes), then the
-    buckets of 384 bytes: 16 keys {t0..t3} (-1 past the run's length k)
-    and their 16 ranges {lo, hi}; a bucket's first min(count, 16) slots
-    are filled.  Entries are keyed (k, t0, t1, t2, t3), tokens past k 0."""
+    """(kmax, entries) of the live table: a 256-byte header {kmax, pad,
+    runs[4] u64}, one u32 fill count per bucket of 16 slots (padded to
+    256 bytes), then the buckets of 384 bytes: 16 keys {t0..t3} (-1 past
+    the run's length k) and their 16 ranges {lo, hi}; a bucket's first
+    min(count, 16) slots are filled.  Entries are keyed (k, t0, t1, t2,
+    t3), tokens past k 0; kmax is the longest length whose runs are all
+    stored."""
     raw = N(g._grams[g._key_live])
     slots_n = g.gram_slots
     nb = slots_n // 16
     cbytes = (nb * 4 + 255) // 256 * 256
-    ok = int(raw[:4].view(np.uint32)[0])
+    kmax = int(raw[:4].view(np.uint32)[0])
     counts = raw[256:256 + nb * 4].view(np.uint32)
     buckets = raw[256 + cbytes:256 + cbytes + nb * 384].view(
         np.int32).reshape(nb, 96)
@@ -658,7 +672,7 @@ def gpu_gram_table(g):
             key = (k, *[int(x) if j < k else 0 for j, x in enumerate(key4)])
             assert key not in tab, key
             tab[key] = (int(np.uint32(rng[0])), int(np.uint32(rng[1])))
-    return ok, tab
+    return kmax, tab
 
 
 def test_gram_table_matches_runs(gpu):
@@ -676,19 +690,70 @@ def test_gram_table_matches_runs(gpu):
                 for _ in range(nd)]
         g.load_documents([T(d, gpu) for d in docs])
         torch.cuda.synchronize()
-        ok, tab = gpu_gram_table(g)
-        assert ok == 1
+        kmax, tab = gpu_gram_table(g)
+        assert kmax == 4
         exp = gram_runs(N(g.corpus), N(g.sa))
         assert len(exp) > 200
         assert tab == exp
         keys_by_definition(g.corpus, g.sa, g.sa_key)
 
 
+def test_gram_table_keeps_the_lengths_that_fit(gpu):
+    """Uniform random tokens over a 2^17 vocabulary hold about 3 distinct
+    runs of 1-4 tokens per position, more than the 3 slots per position
+    hold at 3/4 load: the table keeps every run of the lengths that fit
+    (the 1- and 2-token runs here) and exactly those, and capped queries
+    and drafts still equal the oracle's (searches start from the first
+    two tokens' range)."""
+    from suffixgpu_amd.global_index import GlobalIndex
+    from oracle.global_index import GlobalIndexOracle
+    rng = np.random.default_rng(21)
+    # 48 documents, 59,182 tokens: 47,684 distinct tokens, then 59,086,
+    # 59,038 and 58,990 runs of 2, 3 and 4 tokens, against 147,456 slots
+    # at 3/4 of 3 x 2^16
+    docs = [rng.integers(0, 1 << 17, size=int(rng.integers(1150, 1300)))
+            .astype(I32) for _ in range(48)]
+    kw = dict(capacity=1 << 16, delta_capacity=1 << 12, k=12,
+              max_occurrences=32, rebuild_threshold=1 << 30)
+    g = GlobalIndex(device=gpu, **kw)
+    o = GlobalIndexOracle(**kw)
+    g.load_documents([T(d, gpu) for d in docs])
+    o.load_documents(docs)
+    torch.cuda.synchronize()
+    kmax, tab = gpu_gram_table(g)
+    exp = gram_runs(N(g.corpus), N(g.sa))
+    assert runs_capacity_kmax(exp, g.gram_slots) == 2
+    assert kmax == 2
+    assert tab == {key: v for key, v in exp.items() if key[0] <= kmax}
+    b, p = 48, 24
+    q = np.zeros((b, p), I32)
+    ql = np.zeros(b, np.int64)
+    for i in range(b):
+        n = int(rng.integers(1, p + 1))
+        if i % 3 == 2:  # absent patterns
+            q[i, :n] = rng.integers(0, 1 << 17, size=n)
+        else:
+            src = docs[i % len(docs)]
+            st = int(rng.integers(0, len(src) - n + 1))
+            q[i, :n] = src[st:st + n]
+        ql[i] = n
+    caps = np.array([24, 12, 6, 3, 2, 1], np.int64)
+    tq, tl, tc_ = T(q, gpu), T(ql, gpu), T(caps, gpu)
+    for got, e in zip(g._query_backoff(tq, tl, p, tc_),
+                      o._query_backoff(q, ql, p, caps)):
+        np.testing.assert_array_equal(N(got), e)
+    for got, e in zip(g.draft(tq, tl, p, 12, min_token_prob=0.05,
+                              caps=tc_),
+                      o.draft(q, ql, p, 12, min_token_prob=0.05,
+                              caps=caps)):
+        np.testing.assert_array_equal(N(got), e)
+
+
 @pytest.mark.parametrize("slots", [None, 1024, 0])
 def test_queries_with_and_without_gram_table(gpu, slots):
-    """Capped SA + delta queries, drafts and the fused step agree with the
-    oracle with the table in use and with a table too small for the corpus
-    (it marks itself unusable; every search spans the whole array);
+    """Capped SA + delta queries and drafts agree with the oracle with the
+    table in use and with a table too small for the corpus (it keeps the
+    run lengths that fit, possibly none, and searches start from those);
     queries holding separator, padding or -1 tokens skip the table.
     slots=0: no key rows and no table at all (search_tables=False); every
     comparison reads the suffix array and the corpus."""
@@ -708,8 +773,18 @@ def test_queries_with_and_without_gram_table(gpu, slots):
     o.append_documents(dd)
     torch.cuda.synchronize()
     if slots != 0:
-        ok, _ = gpu_gram_table(g)
-        assert ok == (1 if slots is None else 0)
+        kmax, tab = gpu_gram_table(g)
+        exp = gram_runs(N(g.corpus), N(g.sa))
+        if slots is None:
+            assert kmax == 4
+        else:
+            kcap = runs_capacity_kmax(exp, slots)
+            assert kmax <= kcap < 4
+            # only runs of the lengths that fit were inserted; an insert
+            # that found no room lowered kmax below its own length
+            assert all(key[0] <= kcap for key in tab)
+        assert {key: v for key, v in tab.items() if key[0] <= kmax} == \
+            {key: v for key, v in exp.items() if key[0] <= kmax}
     else:
         assert g.sa_key is None and g.device_bytes()["key_rows"] == 0
     rng = np.random.default_rng(15)
