@@ -66,12 +66,13 @@ constexpr size_t kHalfLds = kMaxLds / 2;
 
 int check_local(const sfx_params& p, const sfx_batch& bt);
 // Local layout within `cap` bytes of LDS for `nthreads` per row: 0 = whole
-// row, > 0 = streamed chunk length, -1 = nothing fits.
+// row, > 0 = streamed chunk length, -1 = nothing fits; *mb_full tells
+// whether a streamed layout holds the whole row's match lengths.
 constexpr int kLocalThreadsDefault = 512;
 int local_chunk(const sfx_params& p, int64_t S, size_t cap = kMaxLds,
-                int nthreads = kLocalThreadsDefault);
+                int nthreads = kLocalThreadsDefault, int* mb_full = nullptr);
 size_t local_lds_bytes(const sfx_params& p, int64_t S, int chunk,
-                       int nthreads = kLocalThreadsDefault);
+                       int nthreads = kLocalThreadsDefault, int mb_full = 0);
 
 int check_global(const sfx_params& p, const sfx_index& ix, int64_t batch);
 int mb_lds_bytes(const sfx_index& ix, int parts);

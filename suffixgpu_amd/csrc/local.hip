@@ -35,31 +35,43 @@ __global__ __launch_bounds__(kWideThreads) void k_local_wide(LocalArgs a) {
 }
 
 static size_t layout_bytes(const sfx_params& p, int64_t S, int chunk,
-                           int nthreads) {
+                           int nthreads, int mb_full) {
+  if ((chunk == 0 || mb_full) && S > (int64_t)kMaxLds) return (size_t)-1;
   if (chunk == 0 && S > (int64_t)kMaxLds / 4) return (size_t)-1;
   const LocalLayout L =
       local_layout((int)S, p.max_pattern_len, p.num_thresholds,
-                   p.max_occurrences, p.k, nthreads / kWave, chunk);
+                   p.max_occurrences, p.k, nthreads / kWave, chunk, mb_full);
   return (size_t)L.total;
 }
 
-int local_chunk(const sfx_params& p, int64_t S, size_t cap, int nthreads) {
-  if (layout_bytes(p, S, 0, nthreads) <= cap) return 0;
+// A streamed row keeps its whole match array in LDS where some chunk
+// length allows it (one staging pass instead of two).
+int local_chunk(const sfx_params& p, int64_t S, size_t cap, int nthreads,
+                int* mb_full) {
+  if (mb_full) *mb_full = 0;
+  if (layout_bytes(p, S, 0, nthreads, 0) <= cap) return 0;
   for (int chunk = kMaxStreamChunk; chunk >= kMinStreamChunk; chunk /= 2)
-    if (layout_bytes(p, S, chunk, nthreads) <= cap) return chunk;
+    if (layout_bytes(p, S, chunk, nthreads, 1) <= cap) {
+      if (mb_full) *mb_full = 1;
+      return chunk;
+    }
+  for (int chunk = kMaxStreamChunk; chunk >= kMinStreamChunk; chunk /= 2)
+    if (layout_bytes(p, S, chunk, nthreads, 0) <= cap) return chunk;
   return -1;
 }
 
 size_t local_lds_bytes(const sfx_params& p, int64_t S, int chunk,
-                       int nthreads) {
-  return chunk < 0 ? (size_t)-1 : layout_bytes(p, S, chunk, nthreads);
+                       int nthreads, int mb_full) {
+  return chunk < 0 ? (size_t)-1
+                   : layout_bytes(p, S, chunk, nthreads, mb_full);
 }
 
 int launch_local_step(LocalArgs a, hipStream_t stream) {
-  a.chunk = local_chunk(a.p, a.bt.seq, kMaxLds, kWideThreads);
+  a.chunk = local_chunk(a.p, a.bt.seq, kMaxLds, kWideThreads, &a.mb_full);
   if (a.chunk < 0) return -1;
   if (a.bt.batch == 0) return 0;
-  const size_t lds = local_lds_bytes(a.p, a.bt.seq, a.chunk, kWideThreads);
+  const size_t lds =
+      local_lds_bytes(a.p, a.bt.seq, a.chunk, kWideThreads, a.mb_full);
   if (a.chunk == 0) {
     static std::atomic<uint64_t> lds_opt{0};
     allow_max_lds((const void*)k_local_wide<false>, lds_opt);
@@ -90,8 +102,10 @@ int check_local(const sfx_params& p, const sfx_batch& bt) {
 
 int launch_local(LocalArgs a, hipStream_t stream) {
   if (a.bt.batch == 0) return 0;
-  a.chunk = local_chunk(a.p, a.bt.seq);
-  const size_t lds = local_lds_bytes(a.p, a.bt.seq, a.chunk);
+  a.chunk = local_chunk(a.p, a.bt.seq, kMaxLds, kLocalThreadsDefault,
+                        &a.mb_full);
+  const size_t lds = local_lds_bytes(a.p, a.bt.seq, a.chunk,
+                                     kLocalThreadsDefault, a.mb_full);
   if (a.chunk == 0) {
     static std::atomic<uint64_t> lds_opt{0};
     allow_max_lds((const void*)k_local<false>, lds_opt);

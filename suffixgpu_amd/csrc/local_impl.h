@@ -26,6 +26,7 @@ struct LocalArgs {
   int32_t* new_counts;  // step
   StepWs ws;
   int chunk;  // 0: the whole row is staged in LDS; else streamed in chunks
+  int mb_full;  // streamed: LDS holds the match lengths of the whole row
 };
 
 struct LocalLayout {
@@ -50,13 +51,15 @@ __host__ __device__ inline int mb_bytes(int n, int nthreads) {
 __host__ __device__ inline int stream_halo(int P) { return (P + 3) & ~3; }
 
 // chunk == 0: the row (S tokens) and its match lengths live in LDS.
-// chunk > 0: LDS holds one chunk of positions, its match lengths and the
-// stream_halo(P) tokens before it.
+// chunk > 0: LDS holds one chunk of positions and the stream_halo(P)
+// tokens before it, and the match lengths of that chunk (mb_full == 0) or
+// of the whole row (mb_full == 1).
 __host__ __device__ inline LocalLayout local_layout(int S, int P, int C,
                                                     int R, int K, int nwaves,
-                                                    int chunk = 0) {
+                                                    int chunk = 0,
+                                                    int mb_full = 0) {
   const int nthreads = nwaves * kWave;
-  const int span = chunk > 0 ? chunk : S;
+  const int span = chunk > 0 && !mb_full ? chunk : S;
   LocalLayout L;
   int off = 0;
   L.row = lds_take(off, (chunk > 0 ? chunk + stream_halo(P) : S) * 4);
@@ -90,10 +93,12 @@ constexpr int kWideThreads = 1024;
 constexpr int64_t kWideMinSeq = 8192;
 
 // kStream: the row stays in HBM.  match_back is computed over chunks of
-// a.chunk positions staged through LDS, once to histogram the match
-// lengths and once more, in order, to compact the first R ends per
+// a.chunk positions staged through LDS.  With a.mb_full the match lengths
+// of the whole row stay in LDS and one ordered pass compacts them, as for
+// a row held whole; otherwise the chunks are staged once to histogram the
+// match lengths and once more, in order, to compact the first R ends per
 // candidate with the counts carried from chunk to chunk (stopping once
-// every candidate holds R); the expansion reads continuations from HBM.
+// every candidate holds R).  The expansion reads continuations from HBM.
 template <bool kStream, int NT = kLocalThreads>
 __device__ __forceinline__ void local_body(const LocalArgs& a,
                                            unsigned char* smem, int b) {
@@ -107,7 +112,9 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
   const int C = p.num_thresholds;
   const int R = p.max_occurrences;
   const int K = p.k;
-  const LocalLayout L = local_layout(S, P, C, R, K, NW, kStream ? a.chunk : 0);
+  const bool mb_full = kStream && a.mb_full;
+  const LocalLayout L = local_layout(S, P, C, R, K, NW, kStream ? a.chunk : 0,
+                                     mb_full ? 1 : 0);
   int32_t* row = (int32_t*)(smem + L.row);  // the row, or a staged chunk
   uint8_t* mbuf = (uint8_t*)(smem + L.mb);
   int32_t* pat = (int32_t*)(smem + L.pat);
@@ -215,7 +222,7 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
       const int k = i - 1 - (c0 - halo);  // row index of x(i - 1)
       int m = 0;
       while (m < P && row[k - m] == pat[m]) ++m;
-      mbuf[i - c0] = (uint8_t)m;
+      mbuf[mb_full ? i : i - c0] = (uint8_t)m;
       if (count && m > 0) atomicAdd(&hist[m], 1);
     }
   };
@@ -411,7 +418,7 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
   SFX_TRACE_POINT(3);
   // First R ascending ends per candidate (triton_kernels.py:217-243
   // semantics): one ordered pass per group of 8 candidates.
-  if (!kStream) {
+  if (!kStream || mb_full) {
     for (int g0 = 0; g0 < C; g0 += 8)
       compact_first_r<NT>(mbuf, qe, cand + g0, min(8, C - g0), R,
                           occ + g0 * R, 0, found + g0, scan, (g0 >> 3) & 1);

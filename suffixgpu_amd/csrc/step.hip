@@ -123,8 +123,10 @@ int launch_step(const sfx_params* p, const sfx_index* ix, const sfx_batch* bt,
          merge_waves_for(*p, *ix, dparts, &glds, kHalfLds) > 0);
     if (fits) cap = kHalfLds;
   }
-  a.l.chunk = local_chunk(*p, bt->seq, cap);
-  size_t lds = local_lds_bytes(*p, bt->seq, a.l.chunk);
+  a.l.chunk = local_chunk(*p, bt->seq, cap, kLocalThreadsDefault,
+                          &a.l.mb_full);
+  size_t lds = local_lds_bytes(*p, bt->seq, a.l.chunk, kLocalThreadsDefault,
+                               a.l.mb_full);
   if (global_on) {
     rc = check_global(*p, *ix, bt->batch);
     if (rc) return rc;

@@ -159,9 +159,10 @@ def _long_rows(seed, s, vocab, q_list, p):
 @pytest.mark.parametrize("vocab", [3, 1000])
 @pytest.mark.parametrize("s", [40000, 70001])
 def test_local_long_rows_streamed(gpu, vocab, s):
-    """Rows of 40K-70K tokens take the streamed path (chunks of 16384
-    positions): committed lengths of 0, 1, inside the first chunk, on and
-    just past a chunk boundary, full and past the buffer."""
+    """Rows of 40K-70K tokens take the streamed path (chunks of 16384 or
+    8192 positions, the whole row's match lengths kept in LDS):
+    committed lengths of 0, 1, inside the first chunk, on and just past a
+    chunk boundary, full and past the buffer."""
     q_list = [0, 1, 5000, 16384, 16385, 16400, 32769, s, s + 7]
     tok, nt = _long_rows(vocab * 7 + s, s, vocab, q_list, 32)
     mask = np.ones(len(q_list), bool)
@@ -170,6 +171,19 @@ def test_local_long_rows_streamed(gpu, vocab, s):
                  max_spec_factor=2.0, min_token_prob=0.1,
                  support_thresholds=backoff_thresholds(8))
     _check(gpu, g, o, nt, tok, mask)
+
+
+def test_local_rows_beyond_the_match_array(gpu):
+    """Rows of 140,000 tokens: their match lengths do not fit in LDS beside
+    the smallest chunk, so the chunks are staged twice (histogram pass,
+    then the ordered compaction with counts carried between chunks)."""
+    s = 140_000
+    q_list = [16383, 16385, 70000, s]
+    tok, nt = _long_rows(s + 11, s, 40, q_list, 32)
+    g, o = _pair(gpu, k=16, max_pattern_len=32, max_occurrences=128,
+                 max_spec_factor=2.0, min_token_prob=0.1,
+                 support_thresholds=backoff_thresholds(8))
+    _check(gpu, g, o, nt, tok, np.ones(len(q_list), bool))
 
 
 def test_local_long_rows_small_chunks(gpu):
