@@ -32,7 +32,7 @@ extern "C" {
 
 #define SFX_EINVAL (-1)
 #define SFX_MAX_CANDIDATES 32
-#define SFX_ABI_VERSION 14
+#define SFX_ABI_VERSION 15
 
 /* Drafter configuration shared by the local and global paths.
  * Mirrors the constructor arguments of SuffixGPUDrafter
@@ -82,6 +82,11 @@ typedef struct sfx_index {
                                   array (sfx_gram_build), or NULL         */
     const void* gram_alt;      /* the table of sa_key_alt's, or NULL      */
     int64_t gram_slots;        /* slots per table, a multiple of 16      */
+    const uint32_t* delta_pos;   /* delta token index of the live delta
+                                    (sfx_delta_index_build), or NULL: each
+                                    decode row then scans the delta       */
+    const uint32_t* delta_start; /* [delta_buckets + 1] its bucket starts */
+    int64_t delta_buckets;       /* a power of two, 2^10 .. 2^17          */
 } sfx_index;
 
 /* One decode step's batch (suffix_gpu/proposer.py:135-214).
@@ -269,6 +274,25 @@ int sfx_sa_build(const int32_t* text, int64_t m, int64_t n_total, void* sa,
 size_t sfx_gram_table_bytes(int64_t slots);
 int sfx_gram_build(const int32_t* keys, int64_t key_width, int64_t m,
                    void* table, int64_t slots, hipStream_t stream);
+
+/* No reference counterpart.  The delta token index: pos[0 .. D) holds the
+ * delta positions 0 .. *delta_len - 1 grouped by a hash bucket of their
+ * token (delta_bucket: Fibonacci hashing into `buckets`, a power of two
+ * from 2^10 to 2^17), ascending within a bucket, followed by the positions
+ * past the live length; start[b] (b = 0 .. buckets) is the first index of
+ * bucket b, so bucket b spans pos[start[b] .. start[b + 1]).  A decode
+ * step given it (sfx_index.delta_pos/delta_start/delta_buckets) visits
+ * only the positions in its newest pattern token's bucket instead of
+ * scanning the delta (global_index.py:465-546 computes the same match
+ * lengths over every position).  Rebuild it, on the stream the delta is
+ * written on, after every change to the delta or its length.  `workspace`
+ * (256-byte aligned, sfx_delta_index_bytes(D) bytes) holds nothing
+ * between calls.  Enqueued on `stream` with no host read. */
+size_t sfx_delta_index_bytes(int64_t delta_capacity);
+int sfx_delta_index_build(const int32_t* delta, const int64_t* delta_len,
+                          int64_t delta_capacity, uint32_t* pos,
+                          uint32_t* start, int64_t buckets, void* workspace,
+                          size_t workspace_bytes, hipStream_t stream);
 
 /* The same build in steps, for a caller that advances it from a host poll
  * loop and stops enqueueing rounds once the array is final (no reference

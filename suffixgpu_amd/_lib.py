@@ -17,7 +17,7 @@ import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libsuffixgpu_amd.so"
 MAX_CANDIDATES = 32
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -43,6 +43,7 @@ class SfxIndex(ctypes.Structure):
         ("sa_key", c_p), ("key_width", c_i64),
         ("sa_key_alt", c_p), ("key_select", c_p),
         ("gram", c_p), ("gram_alt", c_p), ("gram_slots", c_i64),
+        ("delta_pos", c_p), ("delta_start", c_p), ("delta_buckets", c_i64),
     ]
 
 
@@ -130,6 +131,9 @@ SIGNATURES = {
     "sfx_sa_keys": (c_i32, [c_p, c_p, c_i64, c_i64, c_i64, c_p, c_p, c_p]),
     "sfx_gram_table_bytes": (ctypes.c_size_t, [c_i64]),
     "sfx_gram_build": (c_i32, [c_p, c_i64, c_i64, c_p, c_i64, c_p]),
+    "sfx_delta_index_bytes": (ctypes.c_size_t, [c_i64]),
+    "sfx_delta_index_build": (c_i32, [c_p, c_p, c_i64, c_p, c_p, c_i64, c_p,
+                                      ctypes.c_size_t, c_p]),
     "sfx_sa_build": (c_i32, [c_p, c_i64, c_i64, c_p, c_i32, c_p,
                              ctypes.c_size_t, c_p]),
 }

@@ -29,7 +29,12 @@ __global__ __launch_bounds__(kGlobalThreads) void k_global(GlobalArgs a) {
 }
 
 
+int delta_parts_of(const sfx_index& ix, int64_t batch) {
+  return ix.delta_pos ? 1 : delta_parts_for(batch, ix.delta_capacity);
+}
+
 int mb_lds_bytes(const sfx_index& ix, int parts) {
+  if (ix.delta_pos) return 0;  // the indexed delta role keeps no u8 array
   const int64_t cap = delta_part_cap(ix.delta_capacity, parts);
   if (cap > kMbLdsMax) return 0;
   const int n = (int)cap;
@@ -47,7 +52,7 @@ int merge_waves_for(const sfx_params& p, const sfx_index& ix, int parts,
     const GlobalLayout L = global_layout(p.max_pattern_len, C,
                                          p.max_occurrences, p.k, nmw,
                                          mb_lds_bytes(ix, parts), 0,
-                                         dend_parts);
+                                         dend_parts, ix.delta_pos ? 1 : 0);
     if ((size_t)L.total <= cap) {
       *lds = (size_t)L.total;
       return nmw;
@@ -61,10 +66,12 @@ int delta_chunk_for(const sfx_params& p, const sfx_index& ix, int parts,
   const int P = p.max_pattern_len;
   const int halo = (P + 3) & ~3;
   const int mb = mb_lds_bytes(ix, parts);
+  const int dindex = ix.delta_pos ? 1 : 0;
   const GlobalLayout L0 = global_layout(P, p.num_caps, p.max_occurrences,
                                         p.k, nmw, mb, kDeltaChunk,
-                                        dend_parts);
+                                        dend_parts, dindex);
   *lds = (size_t)L0.total;
+  if (dindex) return kDeltaChunk;  // (no delta staging)
   // the staged words and the match bytes sit after the header
   const int64_t avail = (int64_t)cap - L0.dtok - ((mb + 15) & ~15);
   const int64_t most = (delta_part_cap(ix.delta_capacity, parts) + 255) &
@@ -104,8 +111,15 @@ int check_global(const sfx_params& p, const sfx_index& ix, int64_t batch) {
        ix.gram_slots > (1ll << 31) || ((uintptr_t)ix.gram & 255) ||
        ((uintptr_t)ix.gram_alt & 255) || (ix.gram_alt && !ix.key_select)))
     return SFX_EINVAL;
+  // the delta token index: both arrays and a bucket count of 2^10 .. 2^17
+  if ((ix.delta_pos || ix.delta_start) &&
+      (!ix.delta_pos || !ix.delta_start ||
+       ix.delta_buckets < (1ll << kDeltaBucketBitsMin) ||
+       ix.delta_buckets > (1ll << kDeltaBucketBitsMax) ||
+       (ix.delta_buckets & (ix.delta_buckets - 1))))
+    return SFX_EINVAL;
   size_t lds = 0;
-  const int parts = delta_parts_for(batch, ix.delta_capacity);
+  const int parts = delta_parts_of(ix, batch);
   if (merge_waves_for(p, ix, parts, &lds) < 1) return SFX_EINVAL;
   return 0;
 }
@@ -113,7 +127,7 @@ int check_global(const sfx_params& p, const sfx_index& ix, int64_t batch) {
 static int launch_global(GlobalArgs& a, hipStream_t stream) {
   if (a.B == 0) return 0;
   size_t lds = 0;
-  a.dparts = delta_parts_for(a.B, a.ix.delta_capacity);
+  a.dparts = delta_parts_of(a.ix, a.B);
   a.merge_waves = merge_waves_for(a.p, a.ix, a.dparts, &lds);
   a.mb_lds = mb_lds_bytes(a.ix, a.dparts);
   a.dchunk = delta_chunk_for(a.p, a.ix, a.dparts, a.merge_waves, 0,

@@ -48,6 +48,9 @@ struct GlobalLayout {
 // longer parts keep them in the workspace.
 constexpr int kDeltaChunk = 8192;
 constexpr int kMbLdsMax = (int)kDeltaMbLdsMax;
+// With the delta token index: match lengths of this many bucket entries
+// stay in LDS at a time (longer buckets are compacted chunk by chunk).
+constexpr int kDixList = 16384;
 
 __host__ __device__ inline int g_take(int& off, int bytes) {
   const int o = off;
@@ -59,11 +62,14 @@ __host__ __device__ inline int g_take(int& off, int bytes) {
 // time the block (if it arrives second) merges the row.
 // dparts > 0 (decode step): the merge side also holds every delta part's
 // end lists, copied in at the parts' join.
+// dindex: the delta role reads the delta token index; dtok then holds the
+// bucket entries' match lengths and dmb their compacted list indices.
 __host__ __device__ inline GlobalLayout global_layout(int P, int C, int R,
                                                       int K, int nmw,
                                                       int mb_lds,
                                                       int dchunk = 0,
-                                                      int dparts = 0) {
+                                                      int dparts = 0,
+                                                      int dindex = 0) {
   constexpr int NW = kGlobalThreads / kWave;
   const int Rp = (R + 3) & ~3;
   GlobalLayout L;
@@ -92,9 +98,14 @@ __host__ __device__ inline GlobalLayout global_layout(int P, int C, int R,
   L.rlen = g_take(off, C * 4);
   L.rocc = g_take(off, C * 4);
   const int ubase = off;
-  L.dtok = g_take(off, ((dchunk > 0 ? dchunk : kDeltaChunk) +
-                        ((P + 3) & ~3)) * 4);
-  L.dmb = g_take(off, mb_lds);
+  if (dindex) {
+    L.dtok = g_take(off, kDixList);
+    L.dmb = g_take(off, C * R * 4);
+  } else {
+    L.dtok = g_take(off, ((dchunk > 0 ? dchunk : kDeltaChunk) +
+                          ((P + 3) & ~3)) * 4);
+    L.dmb = g_take(off, mb_lds);
+  }
   const int delta_end = off;
   off = ubase;
   L.mpos = g_take(off, nmw * Rp * 4);
@@ -166,6 +177,205 @@ __device__ __forceinline__ void delta_part_of(const GlobalArgs& a, int part,
   int64_t dl = *a.ix.delta_len;
   dl = dl < 0 ? 0 : (dl > D ? D : dl);
   delta_part_range(dl + 1, a.dparts, part, plo, phi);
+}
+
+// The part's thresholds min(part_max, cap) per cap (lo[c]), numbered by
+// distinct value in cap order: list u serves every cap with umap[c] = u,
+// ulo[u] is its threshold and ulo[C] the number of lists.  Caps are
+// non-increasing (the drafter's cap set), so equal thresholds are adjacent
+// and wave 0 numbers the distinct ones with one ballot; any other cap
+// order takes thread 0's search.  The caller syncs the block after it.
+__device__ __forceinline__ void delta_thresholds(const int32_t* caps, int C,
+                                                 int part_max, int32_t* lo,
+                                                 int32_t* ulo,
+                                                 int32_t* umap) {
+  const int wv = threadIdx.x / kWave;
+  const int ln = lane_id();
+  if (wv == 0) {
+    const int t = ln < C ? min(part_max, caps[ln]) : 0;
+    const int tp = __shfl_up(t, 1);
+    const bool sorted = ballot(ln > 0 && ln < C && t > tp) == 0ull;
+    if (sorted) {
+      const bool fresh = ln < C && (ln == 0 || t != tp);
+      const uint64_t fm = ballot(fresh);
+      if (ln < C) {
+        const int u = rank_lt(fm) + (fresh ? 0 : -1);
+        lo[ln] = t;
+        umap[ln] = u;
+        if (fresh) ulo[u] = t;
+      }
+      if (ln == 0) ulo[C] = popc(fm);
+    } else if (ln == 0) {
+      int nu = 0;
+      for (int c = 0; c < C; ++c) {
+        const int tc = min(part_max, caps[c]);
+        lo[c] = tc;
+        int u = 0;
+        while (u < nu && ulo[u] != tc) ++u;
+        if (u == nu) ulo[nu++] = tc;
+        umap[c] = u;
+      }
+      ulo[C] = nu;
+    }
+  }
+}
+
+// ---- Delta role with the delta token index (one workgroup per row): the
+// ends i = q + 1 for the positions q in the bucket of the newest pattern
+// token rpat[0] (sfx_delta_index_build), ascending -- and end 0 when that
+// token is -1, since x(j) = -1 before position 0 -- are the only ends
+// whose match length can be nonzero.  Each entry's match length compares
+// the delta in memory with the pattern, eight tokens a step (an entry of
+// another token in the bucket stops at the first); then the same ordered
+// pass as the scan extracts the first R ends per distinct threshold from
+// the entries' match lengths, and the entries' list indices are mapped to
+// their ends (global_index.py:465-546 computes the same lengths over
+// every end).
+__device__ __forceinline__ void delta_role_indexed(const GlobalArgs& a,
+                                                   const GlobalLayout& L,
+                                                   unsigned char* smem,
+                                                   int b,
+                                                   const int32_t* rpat) {
+  constexpr int NT = kGlobalThreads;
+  constexpr int NW = NT / kWave;
+  const sfx_params& p = a.p;
+  const int tid = threadIdx.x;
+  const int wv = tid / kWave;
+  const int ln = tid % kWave;
+  const int P = p.max_pattern_len;
+  const int C = p.num_caps;
+  const int R = p.max_occurrences;
+  const int64_t D = a.ix.delta_capacity;
+  int32_t* found = (int32_t*)(smem + L.found);
+  uint32_t* scan = (uint32_t*)(smem + L.scan);
+  int32_t* red = (int32_t*)(smem + L.red);
+  int32_t* lo_lds = (int32_t*)(smem + L.lo);
+  uint8_t* lmb = (uint8_t*)(smem + L.dtok);
+  int32_t* lend = (int32_t*)(smem + L.dmb);
+  const int64_t slot = b;  // one part per row
+  int64_t dl64 = *a.ix.delta_len;
+  dl64 = dl64 < 0 ? 0 : (dl64 > D ? D : dl64);
+  const int dl = (int)dl64;  // the index covers at most 2^30 positions
+  const int hb = __builtin_ctzll((unsigned long long)a.ix.delta_buckets);
+  const int32_t r0 = rpat[0];
+  const uint32_t bk = delta_bucket(r0, hb);
+  const uint32_t s0 = a.ix.delta_start[bk];
+  const uint32_t s1 = a.ix.delta_start[bk + 1];
+  const int has0 = r0 == -1 ? 1 : 0;
+  const int n = (int)(s1 > s0 ? s1 - s0 : 0) + has0;
+  const uint32_t* dpos = a.ix.delta_pos + s0;
+  const int32_t* delta = a.ix.delta;
+  // the position q of entry j (its end is q + 1)
+  auto pos_of = [&](int j) -> int {
+    return has0 ? (j == 0 ? -1 : (int)dpos[j - 1]) : (int)dpos[j];
+  };
+  // The match length of the end after q, continuing from m leading
+  // matches: x(q - m) .. x(q - m - 3) against rpat[m ..], four independent
+  // loads a step; x(j) = -1 before position 0.
+  auto mb_from = [&](int q, int m) -> int {
+    while (m < P) {
+      int32_t x[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int j = q - m - k;
+        x[k] = j >= 0 ? delta[j] : -1;
+      }
+      int n4 = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        n4 += (n4 == k && m + k < P && x[k] == rpat[m + k]) ? 1 : 0;
+      m += n4;
+      if (n4 < 4) break;
+    }
+    return m;
+  };
+  // Match lengths of entries jb + u * NT + tid (u < 4) of [j0, j1) into
+  // lmb[j - lbase] (where below kDixList): the first four tokens of the
+  // four entries are loaded together, and only entries matching all four
+  // walk on.  Returns the largest length.
+  auto mb4 = [&](int jb, int j1, int lbase) -> int {
+    int q[4], m[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int j = jb + u * NT + tid;
+      q[u] = j < j1 ? pos_of(j) : dl;  // q >= dl: no match
+    }
+    int32_t x[4][4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int j = q[u] - k;
+        x[u][k] = q[u] >= dl ? -3 : (j >= 0 ? delta[j] : -1);
+      }
+    int mx4 = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      int n4 = 0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        n4 += (n4 == k && k < P && x[u][k] == rpat[k]) ? 1 : 0;
+      m[u] = q[u] >= dl ? 0 : n4;  // (q >= dl: an index for a longer delta)
+      if (m[u] == 4 && P > 4) m[u] = mb_from(q[u], 4);
+      const int j = jb + u * NT + tid;
+      if (j < j1 && j - lbase < kDixList) lmb[j - lbase] = (uint8_t)m[u];
+      mx4 = max(mx4, m[u]);
+    }
+    return mx4;
+  };
+  // Match lengths of the first chunk of entries (kept for the compaction
+  // when the bucket fits it) and the largest over all entries.
+  int mx = 0;
+  for (int jb = 0; jb < n; jb += 4 * NT) mx = max(mx, mb4(jb, n, 0));
+  mx = (int)wave_all_max((uint32_t)mx);
+  if (ln == 0) red[wv] = mx;
+  __syncthreads();
+  int part_max = 0;
+  for (int w = 0; w < NW; ++w) part_max = max(part_max, red[w]);
+  SFX_TRACE_POINT(2);
+  const int32_t* caps = (const int32_t*)(smem + L.caps);
+  int32_t* ulo = (int32_t*)(smem + L.ulo);
+  int32_t* umap = (int32_t*)(smem + L.umap);
+  delta_thresholds(caps, C, part_max, lo_lds, ulo, umap);
+  __syncthreads();
+  const int nu = ulo[C];
+  if (n <= kDixList) {
+    for (int g0 = 0; g0 < nu; g0 += 8)
+      compact_first_r<NT>(lmb, n, ulo + g0, min(8, nu - g0), R,
+                          lend + g0 * R, 0, found + g0, scan, (g0 >> 3) & 1);
+  } else {
+    // Chunks of entries in order, their match lengths computed again, with
+    // the kept counts carried; done once every list holds R.
+    for (int u = tid; u < nu; u += NT) found[u] = 0;
+    for (int j0 = 0; j0 < n; j0 += kDixList) {
+      const int cnt = n - j0 < kDixList ? n - j0 : kDixList;
+      __syncthreads();  // the previous chunk's compaction read lmb
+      for (int jb = j0; jb < j0 + cnt; jb += 4 * NT) mb4(jb, j0 + cnt, j0);
+      __syncthreads();
+      for (int g0 = 0; g0 < nu; g0 += 8)
+        compact_first_r<NT, true>(lmb, cnt, ulo + g0, min(8, nu - g0), R,
+                                  lend + g0 * R, j0, found + g0, scan,
+                                  (g0 >> 3) & 1);
+      __syncthreads();
+      bool open = false;
+      for (int u = 0; u < nu; ++u) open |= ulo[u] > 0 && found[u] < R;
+      if (!open) break;
+    }
+  }
+  __syncthreads();
+  SFX_TRACE_POINT(3);
+  // list indices -> ends, for the combine and the gather
+  for (int e = tid; e < nu * R; e += NT) {
+    const int u = e / R;
+    if (e - u * R < found[u])
+      ws_store(a.ws.d_end + (slot * C + u) * R + (e - u * R),
+               (int32_t)(pos_of(lend[e]) + 1));
+  }
+  for (int c = tid; c < C; c += NT) {
+    ws_store(a.ws.d_cnt + slot * C + c, lo_lds[c] > 0 ? found[umap[c]] : 0);
+    ws_store(a.ws.d_map + slot * C + c, umap[c]);
+  }
+  if (tid == 0) ws_store(a.ws.d_mx + slot, part_max);
 }
 
 // ---- Delta role, one part of the row: match_back over ends i in
@@ -279,37 +489,7 @@ __device__ __forceinline__ void delta_role(const GlobalArgs& a,
   const int32_t* caps = (const int32_t*)(smem + L.caps);
   int32_t* ulo = (int32_t*)(smem + L.ulo);
   int32_t* umap = (int32_t*)(smem + L.umap);
-  // Distinct thresholds in cap order; list u serves every cap mapped to u.
-  // Caps are non-increasing (the drafter's cap set), so equal thresholds
-  // are adjacent and wave 0 numbers the distinct ones with one ballot; any
-  // other cap order takes thread 0's search.
-  if (wv == 0) {
-    const int t = ln < C ? min(part_max, caps[ln]) : 0;
-    const int tp = __shfl_up(t, 1);
-    const bool sorted = ballot(ln > 0 && ln < C && t > tp) == 0ull;
-    if (sorted) {
-      const bool fresh = ln < C && (ln == 0 || t != tp);
-      const uint64_t fm = ballot(fresh);
-      if (ln < C) {
-        const int u = rank_lt(fm) + (fresh ? 0 : -1);
-        lo_lds[ln] = t;
-        umap[ln] = u;
-        if (fresh) ulo[u] = t;
-      }
-      if (ln == 0) ulo[C] = popc(fm);
-    } else if (ln == 0) {
-      int nu = 0;
-      for (int c = 0; c < C; ++c) {
-        const int tc = min(part_max, caps[c]);
-        lo_lds[c] = tc;
-        int u = 0;
-        while (u < nu && ulo[u] != tc) ++u;
-        if (u == nu) ulo[nu++] = tc;
-        umap[c] = u;
-      }
-      ulo[C] = nu;
-    }
-  }
+  delta_thresholds(caps, C, part_max, lo_lds, ulo, umap);
   __syncthreads();
   const int nu = ulo[C];
   for (int g0 = 0; g0 < nu; g0 += 8)
@@ -575,8 +755,10 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
   const int R = p.max_occurrences;
   const int K = p.k;
   const int Rp = (R + 3) & ~3;
-  const GlobalLayout L = global_layout(P, C, R, K, a.merge_waves, a.mb_lds,
-                                       a.dchunk, a.dend ? a.dparts : 0);
+  const bool dindex = a.ix.delta_pos != nullptr;
+  const GlobalLayout L =
+      global_layout(P, C, R, K, a.merge_waves, a.mb_lds, a.dchunk,
+                    a.dend ? a.dparts : 0, dindex ? 1 : 0);
   int32_t* rpat = (int32_t*)(smem + L.rpat);
   int64_t* lbs = (int64_t*)(smem + L.lb);
   int64_t* ubs = (int64_t*)(smem + L.ub);
@@ -598,7 +780,7 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
   // past the header the setup writes.
   const int wpat = (P + kWave - 1) / kWave;  // waves holding pattern threads
   auto stage_first_chunk = [&]() {
-    if (role > 0 && wv >= wpat) {
+    if (role > 0 && wv >= wpat && !dindex) {
       int64_t plo, phi;
       delta_part_of(a, role - 1, &plo, &phi);
       if (plo < phi)
@@ -611,7 +793,7 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
   // -3 past the start (global_index.py:493-501).
   int64_t qlen = 0;
   if (a.step) {
-    if (role > 0 && wv >= wpat) {
+    if (role > 0 && wv >= wpat && !dindex) {
       stage_first_chunk();
     } else {
       const RowState st = row_state(a.bt, b);
@@ -749,7 +931,9 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
       return;
     }
   } else {
-    if (a.mb_lds)
+    if (dindex)
+      delta_role_indexed(a, L, smem, b, rpat);
+    else if (a.mb_lds)
       delta_role<true>(a, L, smem, b, role - 1, rpat);
     else
       delta_role<false>(a, L, smem, b, role - 1, rpat);

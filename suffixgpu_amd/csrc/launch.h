@@ -76,6 +76,9 @@ size_t local_lds_bytes(const sfx_params& p, int64_t S, int chunk,
 
 int check_global(const sfx_params& p, const sfx_index& ix, int64_t batch);
 int mb_lds_bytes(const sfx_index& ix, int parts);
+// Delta workgroups per row: one with the delta token index, else
+// delta_parts_for's split of the delta.
+int delta_parts_of(const sfx_index& ix, int64_t batch);
 // Merge waves (one per cap expansion) whose layout fits `cap`, with the
 // delta parts' end lists in LDS when dend_parts > 0 (decode step).
 int merge_waves_for(const sfx_params& p, const sfx_index& ix, int parts,

@@ -1045,6 +1045,85 @@ static int doubling_round(SaWs& w, int64_t nb, int64_t m, int round,
   return sort_and_rank(w, nb, m, round, stream);
 }
 
+// ---------------------------------------------------------- delta index
+// The delta's positions grouped by a hash bucket of their token, ascending
+// within a bucket, and each bucket's first index: a decode step's delta
+// workgroup then visits only the positions whose token hashes like the
+// newest pattern token's instead of scanning the whole delta.  The
+// grouping is a stable LSD radix sort of (bucket, position) in two 9-bit
+// passes with the launches above (a stand-in state block: one list of all
+// D positions, round 0); positions at or past the live length take the
+// key `buckets`, after every real bucket.
+
+static_assert(2 * kDigitBits >= kDeltaBucketBitsMax + 1,
+              "two radix passes cover a bucket key");
+
+struct DixWs {
+  uint64_t* keyA;    // [D] bucket keys; sorted after the second pass
+  uint64_t* keyB;    // [D]
+  uint32_t* valB;    // [D]
+  uint32_t* hist;    // [512][NB]
+  uint32_t* rowsum;  // [512]
+  uint32_t* state;   // [kStateWords]
+};
+
+static size_t dix_ws_layout(int64_t D, void* base, DixWs* w) {
+  const size_t N = (size_t)(D > 0 ? D : 1);
+  const size_t NB = (N + kTile - 1) / kTile;
+  size_t off = 0;
+  char* c = (char*)base;
+  auto take = [&](size_t bytes) -> void* {
+    void* ptr = c ? (void*)(c + off) : nullptr;
+    off += ws_align(bytes);
+    return ptr;
+  };
+  DixWs s;
+  s.keyA = (uint64_t*)take(N * 8);
+  s.keyB = (uint64_t*)take(N * 8);
+  s.valB = (uint32_t*)take(N * 4);
+  s.hist = (uint32_t*)take((size_t)kRadix * NB * 4);
+  s.rowsum = (uint32_t*)take(kRadix * 4);
+  s.state = (uint32_t*)take(kStateWords * 4);
+  if (w) *w = s;
+  return off;
+}
+
+__global__ __launch_bounds__(256) void k_dix_init(
+    const int32_t* __restrict__ delta, const int64_t* __restrict__ delta_len,
+    int64_t D, int hbits, uint64_t* key, uint32_t* pos, uint32_t* state) {
+  int64_t dl = *delta_len;
+  dl = dl < 0 ? 0 : (dl > D ? D : dl);
+  const uint32_t past = 1u << hbits;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; p < D;
+       p += stride) {
+    key[p] = p < dl ? delta_bucket(delta[p], hbits) : past;
+    pos[p] = (uint32_t)p;
+  }
+  if (blockIdx.x == 0 && threadIdx.x < kStateWords)
+    state[threadIdx.x] = threadIdx.x == kLen ? (uint32_t)D : 0u;
+}
+
+// start[b] = the first sorted index whose key is at least b, b = 0 .. H.
+__global__ __launch_bounds__(256) void k_dix_start(
+    const uint64_t* __restrict__ key, int64_t D, int hbits,
+    uint32_t* start) {
+  const int64_t H = (int64_t)1 << hbits;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b <= H;
+       b += stride) {
+    int64_t lo = 0, hi = D;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (key[mid] < (uint64_t)b)
+        lo = mid + 1;
+      else
+        hi = mid;
+    }
+    start[b] = (uint32_t)lo;
+  }
+}
+
 }  // namespace sfx
 
 using namespace sfx;
@@ -1206,4 +1285,57 @@ extern "C" int sfx_sa_build_finish(int64_t m, int64_t n_total, void* sa_out,
   if (!sa_out) return SFX_EINVAL;
   if (!ws_ok(m, workspace, workspace_bytes)) return SFX_EINVAL;
   return build_finish(m, n_total, sa_out, sa_is64, workspace, stream);
+}
+
+extern "C" size_t sfx_delta_index_bytes(int64_t delta_capacity) {
+  if (delta_capacity < 1 || delta_capacity > (1ll << 30)) return 0;
+  return dix_ws_layout(delta_capacity, nullptr, nullptr);
+}
+
+extern "C" int sfx_delta_index_build(const int32_t* delta,
+                                     const int64_t* delta_len,
+                                     int64_t delta_capacity, uint32_t* pos,
+                                     uint32_t* start, int64_t buckets,
+                                     void* workspace, size_t workspace_bytes,
+                                     hipStream_t stream) {
+  const int64_t D = delta_capacity;
+  if (!delta || !delta_len || !pos || !start || !workspace) return SFX_EINVAL;
+  if (D < 1 || D > (1ll << 30)) return SFX_EINVAL;
+  if (buckets < (1ll << kDeltaBucketBitsMin) ||
+      buckets > (1ll << kDeltaBucketBitsMax) || (buckets & (buckets - 1)))
+    return SFX_EINVAL;
+  if (((uintptr_t)workspace & 255) ||
+      workspace_bytes < dix_ws_layout(D, nullptr, nullptr))
+    return SFX_EINVAL;
+  const int hbits = __builtin_ctzll((unsigned long long)buckets);
+  DixWs w;
+  dix_ws_layout(D, workspace, &w);
+  const int64_t nb = (D + kTile - 1) / kTile;
+  const unsigned gb = (unsigned)((D + 255) / 256 < 2048 ? (D + 255) / 256
+                                                         : 2048);
+  hipLaunchKernelGGL(k_dix_init, dim3(gb), dim3(256), 0, stream, delta,
+                     delta_len, D, hbits, w.keyA, pos, w.state);
+  uint64_t* keys[2] = {w.keyA, w.keyB};
+  uint32_t* vals[2] = {pos, w.valB};
+  int x = 0;
+  for (int sh = 0; sh <= hbits; sh += kDigitBits) {
+    hipLaunchKernelGGL(k_rs_hist<kRsThreads>, dim3((unsigned)nb),
+                       dim3(kRsThreads), 0, stream, keys[x], sh, w.hist, nb,
+                       w.state, 0);
+    hipLaunchKernelGGL(k_rs_rowscan<kRsThreads>, dim3(kRadix),
+                       dim3(kRsThreads), 0, stream, w.hist, nb, w.rowsum,
+                       w.state, 0);
+    hipLaunchKernelGGL(k_rs_scatter<kRsThreads>, dim3((unsigned)nb),
+                       dim3(kRsThreads), 0, stream, keys[x], vals[x],
+                       keys[x ^ 1], vals[x ^ 1], sh, w.hist, nb, w.rowsum,
+                       w.state, 0);
+    x ^= 1;
+  }
+  // two passes (keys of at most 18 bits): the sorted data is back in
+  // keyA and pos
+  const int64_t H = buckets;
+  const unsigned sb = (unsigned)((H + 256) / 256);
+  hipLaunchKernelGGL(k_dix_start, dim3(sb), dim3(256), 0, stream, w.keyA, D,
+                     hbits, start);
+  return (int)hipGetLastError();
 }

@@ -107,8 +107,7 @@ int launch_step(const sfx_params* p, const sfx_index* ix, const sfx_batch* bt,
     rc = launch_local_step(a.l, stream);
     if (rc >= 0) return rc;
   }
-  const int dparts =
-      global_on ? delta_parts_for(bt->batch, ix->delta_capacity) : 0;
+  const int dparts = global_on ? delta_parts_of(*ix, bt->batch) : 0;
   const unsigned blocks =
       (unsigned)(bt->batch * (global_on ? 2 + dparts : 1));
   // A grid larger than the CU count runs in waves of workgroups; when every

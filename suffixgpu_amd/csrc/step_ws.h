@@ -84,6 +84,14 @@ __host__ __device__ inline void delta_part_range(int64_t n, int parts, int k,
   *hi = k == parts - 1 ? n : (((k + 1) * n / parts) & ~(int64_t)15);
 }
 
+// Delta token index (sfx_delta_index_build): bucket of a token among
+// 2^hbits buckets, by Fibonacci hashing of its 32 bits.
+constexpr int kDeltaBucketBitsMin = 10;
+constexpr int kDeltaBucketBitsMax = 17;
+__host__ __device__ inline uint32_t delta_bucket(int32_t t, int hbits) {
+  return ((uint32_t)t * 0x9E3779B1u) >> (32 - hbits);
+}
+
 // Largest delta part (positions) whose match_back bytes stay in LDS;
 // longer parts use StepWs::d_mb.
 constexpr int64_t kDeltaMbLdsMax = 65540;

@@ -50,6 +50,16 @@ GRAM_SLOTS_PER_TOKEN = 3
 def gram_slots_for(capacity: int) -> int:
     n = max(1024, GRAM_SLOTS_PER_TOKEN * capacity)
     return (n + 15) // 16 * 16
+# Delta token index buckets: about four delta positions per bucket, a
+# power of two from 2^10 to 2^17; deltas above 2^30 positions are scanned.
+DELTA_INDEX_MAX = 1 << 30
+
+
+def delta_buckets_for(delta_capacity: int) -> int:
+    b = 1 << max(0, (max(1, delta_capacity // 4) - 1).bit_length())
+    return min(max(b, 1 << 10), 1 << 17)
+
+
 # Written between documents; negative, so no query token (>= 0) can match
 # it and neither matches nor continuations cross document boundaries.
 SEP_TOKEN = -2
@@ -65,7 +75,8 @@ class GlobalIndex:
                  device: torch.device | str = "cuda",
                  rebuild_stream: torch.cuda.Stream | None = None,
                  gram_slots: int | None = None,
-                 search_tables: bool = True):
+                 search_tables: bool = True,
+                 delta_index: bool = True):
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise _lib.SuffixGPUError(
@@ -94,6 +105,22 @@ class GlobalIndex:
         self.delta = torch.zeros(delta_capacity, dtype=torch.int32,
                                  device=dev)
         self.delta_len_t = torch.zeros((), dtype=torch.int64, device=dev)
+        # Delta token index (sfx_delta_index_build): the delta positions by
+        # token bucket, rebuilt after every write to the delta, so that a
+        # decode row visits only the positions of its newest token's
+        # bucket.  delta_index=False: every row scans the whole delta.
+        self.delta_buckets = 0
+        self._dix_pos = self._dix_start = self._dix_ws = None
+        if delta_index and delta_capacity <= DELTA_INDEX_MAX:
+            self.delta_buckets = delta_buckets_for(delta_capacity)
+            self._dix_pos = torch.empty(delta_capacity, dtype=torch.int32,
+                                        device=dev)
+            self._dix_start = torch.zeros(self.delta_buckets + 1,
+                                          dtype=torch.int32, device=dev)
+            self._dix_ws = torch.empty(
+                int(lib().sfx_delta_index_bytes(delta_capacity)),
+                dtype=torch.uint8, device=dev)
+            self._index_delta()
         # Two key-row buffers and n-gram range tables; the device word
         # key_select names the live pair (the step reads it), a rebuild
         # writes the other.  search_tables=False keeps neither (about
@@ -188,12 +215,17 @@ class GlobalIndex:
         return self._keys[1 - self._key_live] if self._keys else None
 
     def index_struct(self) -> _lib.SfxIndex:
+        if self._dix_pos is not None:
+            dix = (self._dix_pos.data_ptr(), self._dix_start.data_ptr(),
+                   self.delta_buckets)
+        else:
+            dix = (None, None, 0)
         if not self.search_tables:
             return _lib.SfxIndex(self.corpus.data_ptr(), self.sa.data_ptr(),
                                  self.capacity, self.delta.data_ptr(),
                                  self.delta_capacity,
                                  self.delta_len_t.data_ptr(), None, 0, None,
-                                 None, None, None, 0)
+                                 None, None, None, 0, *dix)
         return _lib.SfxIndex(self.corpus.data_ptr(), self.sa.data_ptr(),
                              self.capacity, self.delta.data_ptr(),
                              self.delta_capacity,
@@ -202,7 +234,8 @@ class GlobalIndex:
                              self._keys[1].data_ptr(),
                              self.key_select.data_ptr(),
                              self._grams[0].data_ptr(),
-                             self._grams[1].data_ptr(), self.gram_slots)
+                             self._grams[1].data_ptr(), self.gram_slots,
+                             *dix)
 
     def device_bytes(self) -> dict:
         """Device memory held by the index, by role (bytes).  With search
@@ -216,6 +249,9 @@ class GlobalIndex:
             "key_rows": sum(t.numel() * 4 for t in self._keys or ()),
             "gram_tables": sum(t.numel() for t in self._grams or ()),
             "delta": 4 * self.delta_capacity + 8,
+            "delta_index": sum(t.numel() * t.element_size() for t in (
+                self._dix_pos, self._dix_start, self._dix_ws)
+                if t is not None),
             "sa_build_workspace": ws,
             "query_workspace": qws,
         }
@@ -255,6 +291,18 @@ class GlobalIndex:
                                    self._grams[slot].data_ptr(),
                                    self.gram_slots, stream_of(self.device)),
               "n-gram table")
+
+    def _index_delta(self) -> None:
+        """Rebuild the delta token index on the current stream (after
+        every write to the delta or its device length)."""
+        if self._dix_pos is None:
+            return
+        check(lib().sfx_delta_index_build(
+            self.delta.data_ptr(), self.delta_len_t.data_ptr(),
+            self.delta_capacity, self._dix_pos.data_ptr(),
+            self._dix_start.data_ptr(), self.delta_buckets,
+            self._dix_ws.data_ptr(), self._dix_ws.numel(),
+            stream_of(self.device)), "delta index")
 
     # ------------------------------------------------------------------
     # writes (global_index.py:86-133)
@@ -299,6 +347,7 @@ class GlobalIndex:
                                      self.delta_len, stream_of(self.device)),
               "delta append")
         pending.clear()
+        self._index_delta()
 
     def _shift_delta(self, start: int) -> None:
         """Drop delta[:start]: the rest moves to the front in place and the
@@ -309,6 +358,7 @@ class GlobalIndex:
                                     self.delta_len_t.data_ptr(),
                                     stream_of(self.device)), "delta shift")
         self.delta_len = remaining
+        self._index_delta()
 
     def _make_room(self, needed: int) -> None:
         self.poll_rebuild()
@@ -660,6 +710,7 @@ class GlobalIndex:
             row_idx.data_ptr(), int(row_idx.dtype == torch.int64),
             lengths.data_ptr(), int(lengths.dtype == torch.int64), n,
             self.rebuild_threshold, stream_of(self.device)), "ingest")
+        self._index_delta()
 
     def ingest_active_device(self, keys: torch.Tensor, rows: torch.Tensor,
                              lengths: torch.Tensor, ingested: torch.Tensor,
@@ -689,6 +740,7 @@ class GlobalIndex:
             ingested.data_ptr(), ingested.numel(), int(bool(final)),
             int(chunk), int(overlap), self.rebuild_threshold,
             stream_of(self.device)), "ingest_active")
+        self._index_delta()
 
     def _ingest_header(self, words) -> dict:
         return dict(zip(_lib.INGEST_HEADER_FIELDS, (int(x) for x in words)))
@@ -903,6 +955,7 @@ class GlobalIndex:
         self.delta[:n_del].copy_(torch.from_numpy(arrays["delta"]).to(dev))
         self.delta_len = n_del
         self.delta_len_t.fill_(n_del)
+        self._index_delta()
         self.active_len = n_act
         self.active_doc_lens = deque(int(x) for x in meta["active_doc_lens"])
         self.delta_doc_lens = [int(x) for x in meta["delta_doc_lens"]]

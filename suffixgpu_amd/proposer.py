@@ -64,6 +64,7 @@ class SuffixGPUDrafter:
         parallel_paths: bool = True,
         global_search_tables: bool = True,
         global_gram_slots: int | None = None,
+        global_delta_index: bool = True,
     ):
         self.k = k
         self.device = torch.device(device)
@@ -111,7 +112,8 @@ class SuffixGPUDrafter:
                 rebuild_threshold=rebuild_threshold, device=self.device,
                 rebuild_stream=rebuild_stream,
                 search_tables=global_search_tables,
-                gram_slots=global_gram_slots)
+                gram_slots=global_gram_slots,
+                delta_index=global_delta_index)
 
     # ------------------------------------------------------------------
     def poll(self) -> None:

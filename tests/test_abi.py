@@ -186,7 +186,8 @@ int main(void) {
   F(sfx_params, alpha); F(sfx_params, thresholds); F(sfx_params, caps);
   S(sfx_index); F(sfx_index, delta_len); F(sfx_index, sa_key);
   F(sfx_index, key_width); F(sfx_index, sa_key_alt);
-  F(sfx_index, key_select);
+  F(sfx_index, key_select); F(sfx_index, gram_slots);
+  F(sfx_index, delta_pos); F(sfx_index, delta_buckets);
   S(sfx_batch); F(sfx_batch, num_tokens_is64); F(sfx_batch, sampled);
   F(sfx_batch, valid_count_is64); F(sfx_batch, mask); F(sfx_batch, limit);
   S(sfx_global_out); F(sfx_global_out, draft_score);
@@ -220,3 +221,26 @@ def test_struct_layouts_match_the_header(tmp_path):
             assert getattr(mirrors[t], f).offset == int(val), key
         else:
             assert ctypes.sizeof(mirrors[key]) == int(val), key
+
+
+def test_delta_index_build_checks_arguments_on_the_host():
+    """sfx_delta_index_build rejects a bucket count that is not a power of
+    two in 2^10 .. 2^17, a missing buffer, a misaligned or short workspace,
+    and a capacity out of range, before any launch."""
+    lib = _lib.lib()
+    d = 1 << 12
+    need = lib.sfx_delta_index_bytes(d)
+    assert need > 0 and lib.sfx_delta_index_bytes(0) == 0
+    ok = (0x100000, 0x200000, d, 0x300000, 0x400000)
+    for buckets in (1 << 9, 3 << 10, 1 << 18):
+        assert lib.sfx_delta_index_build(*ok, buckets, 0x500000, need,
+                                          None) == -1
+    assert lib.sfx_delta_index_build(*ok, 1 << 10, 0x500010, need,
+                                      None) == -1
+    assert lib.sfx_delta_index_build(*ok, 1 << 10, 0x500000, need - 1,
+                                     None) == -1
+    assert lib.sfx_delta_index_build(None, *ok[1:], 1 << 10, 0x500000, need,
+                                     None) == -1
+    assert lib.sfx_delta_index_build(0x100000, 0x200000, 0, 0x300000,
+                                     0x400000, 1 << 10, 0x500000, need,
+                                     None) == -1

@@ -205,7 +205,7 @@ def test_c4_steps_overlap_the_background_rebuild(c3, gpu):
     """The snapshot rebuild of the 2^22 index (oldest documents evicted so
     that the corpus and the delta's whole documents fit) on the rebuild
     stream, with global-on B=64 S=8192 steps of the rebuilding drafter
-    itself on the main stream meanwhile -- 40 replays of the captured step
+    itself on another stream meanwhile -- 40 replays of the captured step
     and 4 eager calls, no poll in between -- each equal to the oracle's
     step on the index as it stands before the swap (the snapshot staged,
     the delta compacted).  HIP events on both streams show the replays ran
@@ -224,38 +224,46 @@ def test_c4_steps_overlap_the_background_rebuild(c3, gpu):
     with torch.cuda.graph(graph):
         out = d.propose_with_update(nt, tok, samp)
     torch.cuda.synchronize()
-    main = torch.cuda.current_stream(gpu)
-    with torch.cuda.stream(gi.rebuild_stream):  # the stream's first use
+    # HIP maps streams onto a few hardware queues, and two streams on one
+    # queue run one after the other: the steps and the build get a fresh
+    # pair of streams, created one after the other (different queues).
+    side = torch.cuda.Stream(gpu)
+    run = torch.cuda.Stream(gpu)
+    gi.rebuild_stream = side
+    with torch.cuda.stream(side):  # the streams' first use
         torch.zeros(1, device=gpu)
+    with torch.cuda.stream(run):  # and the eager step's workspace on `run`
+        d.propose_with_update(nt, tok.clone(), samp)
     torch.cuda.synchronize()
     gi.rebuild_threshold = og.rebuild_threshold = 1
     gi.blocking_poll = False
-    # The build waits for the main stream's staging copies; holding the
-    # main stream for about 3 ms first lets the host enqueue the steps
-    # below before the build (about 2 ms) can have finished, however long
-    # the host takes.
-    t0 = torch.cuda.Event(enable_timing=True)
-    t0.record(main)
-    torch.cuda._sleep(6_000_000)
-    gi.maybe_rebuild()
-    assert gi._rebuild_event is not None
-    side_end = torch.cuda.Event(enable_timing=True)
-    side_end.record(gi.rebuild_stream)
     outs, ends = [], []
-    for i in range(44):
-        if i % 11 == 10:  # an eager call on the step's own workspace
-            res = d.propose_with_update(nt, tok, samp)
-        else:
-            graph.replay()
-            res = out
-        outs.append([t.clone() for t in res])
-        e = torch.cuda.Event(enable_timing=True)
-        e.record(main)
-        ends.append(e)
+    with torch.cuda.stream(run):
+        # The build waits for the staging copies on `run`; holding `run`
+        # first (about 20 ms) lets the host enqueue the rebuild and every
+        # step below before any of it runs, so the steps start with the
+        # build however long the host takes to enqueue them.
+        t0 = torch.cuda.Event(enable_timing=True)
+        t0.record(run)
+        torch.cuda._sleep(40_000_000)
+        gi.maybe_rebuild()
+        assert gi._rebuild_event is not None
+        side_end = torch.cuda.Event(enable_timing=True)
+        side_end.record(side)
+        for i in range(44):
+            if i % 11 == 10:  # an eager call
+                res = d.propose_with_update(nt, tok, samp)
+            else:
+                graph.replay()
+                res = out
+            outs.append([t.clone() for t in res])
+            e = torch.cuda.Event(enable_timing=True)
+            e.record(run)
+            ends.append(e)
     side_end.synchronize()
-    main.synchronize()
+    run.synchronize()
     # steps that ended before the build did ran beside it: the build was
-    # enqueued, behind the main stream's staging copies, before them all
+    # enqueued, behind the staging copies, before them all
     overlapped = sum(e.elapsed_time(side_end) > 0 for e in ends)
     assert overlapped >= 8, (overlapped, t0.elapsed_time(side_end),
                              [round(t0.elapsed_time(e), 3) for e in ends])

@@ -256,10 +256,11 @@ def test_kat_no_cross_document(gpu):
 
 
 # ------------------------------------------------------ random vs oracle
-def _load_pair(gpu, docs, delta_docs, cap, dcap, r, k=16):
+def _load_pair(gpu, docs, delta_docs, cap, dcap, r, k=16, delta_index=True):
     from suffixgpu_amd.global_index import GlobalIndex
     g = GlobalIndex(capacity=cap, delta_capacity=dcap, k=k,
-                    max_occurrences=r, rebuild_threshold=10 ** 9, device=gpu)
+                    max_occurrences=r, rebuild_threshold=10 ** 9, device=gpu,
+                    delta_index=delta_index)
     o = GlobalIndexOracle(capacity=cap, delta_capacity=dcap, k=k,
                           max_occurrences=r, rebuild_threshold=10 ** 9)
     g.load_documents([T(d, gpu) for d in docs])
@@ -358,11 +359,15 @@ def test_queries_vs_oracle(gpu, vocab):
         np.testing.assert_array_equal(N(got), exp)
 
 
+@pytest.mark.parametrize("delta_index", [False, True])
 @pytest.mark.parametrize("mode", ["small_vocab", "templates", "short"])
-def test_split_delta_vs_oracle(gpu, mode):
-    """A 2^16-token delta is scanned by several workgroups per row; their
-    lists are combined in part order.  Queries whose longest delta match
-    lies in a late part exercise the per-part threshold check."""
+def test_split_delta_vs_oracle(gpu, mode, delta_index):
+    """A 2^16-token delta, without the delta token index, is scanned by
+    several workgroups per row; their lists are combined in part order.
+    Queries whose longest delta match lies in a late part exercise the
+    per-part threshold check.  With the index each row visits its newest
+    token's bucket (over a 5-token vocabulary: buckets of thousands of
+    positions, longer than the LDS chunk)."""
     rng = np.random.default_rng({"small_vocab": 1, "templates": 2,
                                  "short": 3}[mode])
     tc = synth.TemplateCorpus(seed=9, n_templates=10)
@@ -375,8 +380,10 @@ def test_split_delta_vs_oracle(gpu, mode):
     else:
         dd = [tc.sequence(lo=20, hi=60) for _ in range(2)]
     cap = sum(len(d) + 1 for d in docs) + 11
-    g, o = _load_pair(gpu, docs, dd, cap, 1 << 16, 32, k=8)
+    g, o = _load_pair(gpu, docs, dd, cap, 1 << 16, 32, k=8,
+                      delta_index=delta_index)
     assert g.delta_len == o.delta_len
+    assert (g.delta_buckets > 0) == delta_index
     b, p = 40, 24
     q = np.zeros((b, p), I32)
     ql = np.zeros(b, np.int64)
@@ -400,6 +407,104 @@ def test_split_delta_vs_oracle(gpu, mode):
                         o.draft(q, ql, p, 8, min_token_prob=0.05,
                                 caps=caps)):
         np.testing.assert_array_equal(N(got), exp)
+
+
+def delta_bucket(t, hbits):
+    """The index's bucket of token t (Fibonacci hashing of its 32 bits)."""
+    return ((int(t) & 0xFFFFFFFF) * 0x9E3779B1 & 0xFFFFFFFF) >> (32 - hbits)
+
+
+def check_delta_index(g):
+    """The delta token index of g by its definition: bucket b lists the
+    positions p < delta_len with delta_bucket(delta[p]) == b, ascending,
+    the positions from delta_len on follow in order, and start[b] is each
+    bucket's first index."""
+    hb = g.delta_buckets.bit_length() - 1
+    dl = g.delta_len
+    delta = N(g.delta)
+    pos = N(g._dix_pos).view(np.uint32).astype(np.int64)
+    start = N(g._dix_start).view(np.uint32).astype(np.int64)
+    keys = np.array([delta_bucket(t, hb) for t in delta[:dl]], np.int64)
+    order = np.lexsort((np.arange(dl), keys))
+    np.testing.assert_array_equal(pos[:dl], order)
+    np.testing.assert_array_equal(pos[dl:], np.arange(dl, g.delta_capacity))
+    exp = np.searchsorted(keys[order], np.arange(g.delta_buckets + 1),
+                          side="left")
+    np.testing.assert_array_equal(start, exp)
+
+
+@pytest.mark.parametrize("kind", ["repeated", "colliding", "edges"])
+def test_delta_index_rows_vs_scan(gpu, kind):
+    """Queries and drafts through the delta token index equal the delta
+    scan's and the oracle's, and the index matches its definition after
+    appends and a compaction: a delta of one repeated token (a bucket
+    covering the whole delta, compacted in chunks); tokens chosen to share
+    one bucket (each row's entries mostly of other tokens); query tails
+    holding -1 (end 0 reads x(-1) = -1), separators and padding, and an
+    empty delta."""
+    from suffixgpu_amd.global_index import GlobalIndex
+    rng = np.random.default_rng({"repeated": 31, "colliding": 32,
+                                 "edges": 33}[kind])
+    tc = synth.TemplateCorpus(seed=19, n_templates=6)
+    docs = [tc.sequence(lo=64, hi=300) for _ in range(20)]
+    dcap = 1 << 15
+    hb = 13  # delta_buckets_for(2^15) = 2^13
+    if kind == "repeated":
+        dd = [np.full(int(rng.integers(3000, 9000)), 7, I32)
+              for _ in range(4)]
+        dd.append(np.concatenate([np.full(50, 7, I32),
+                                  np.array([3, 7, 7, 9], I32)]))
+    elif kind == "colliding":
+        pool = [t for t in range(1, 400000)
+                if delta_bucket(t, hb) == delta_bucket(11, hb)][:6] + [11]
+        assert len(pool) == 7
+        dd = [rng.choice(np.array(pool, I32), size=int(rng.integers(500,
+                         3000))).astype(I32) for _ in range(8)]
+    else:
+        dd = [tc.sequence(lo=100, hi=900) for _ in range(6)]
+    cap = sum(len(d) + 1 for d in docs) + 11
+    pairs = [_load_pair(gpu, docs, dd if kind != "edges" else [], cap, dcap,
+                        32, k=8, delta_index=x) for x in (True, False)]
+    (gi, o), (gs, _) = pairs
+    assert gi.delta_buckets == 1 << hb and gs.delta_buckets == 0
+    check_delta_index(gi)
+    b, p = 48, 20
+    q = np.zeros((b, p), I32)
+    ql = np.zeros(b, np.int64)
+    src_all = dd if dd else docs
+    for i in range(b):
+        src = src_all[i % len(src_all)]
+        n = int(rng.integers(1, min(len(src), p) + 1))
+        st = int(rng.integers(0, len(src) - n + 1))
+        q[i, :n] = src[st:st + n]
+        ql[i] = n
+        if kind == "edges" and i % 3 == 0:
+            q[i, n - 1 - int(rng.integers(0, min(n, 3)))] = (-1, -2, PAD)[
+                (i // 3) % 3]
+        if kind == "edges" and i % 12 == 0:
+            q[i, :n] = -1  # a tail of -1s matches before position 0
+    caps = np.array([20, 10, 5, 3, 2, 1], np.int64)
+    for step in range(2):
+        if step == 1:
+            # more documents, then drop the oldest: both rebuild the index
+            more = [tc.sequence(lo=200, hi=600) for _ in range(3)]
+            for g in (gi, gs):
+                g.append_documents([T(d, gpu) for d in more])
+                g._drop_oldest_docs(1)
+            o.append_documents(more)
+            o._drop_oldest_docs(1)
+            gpu_state_equal(gi, o)
+            check_delta_index(gi)
+        tq, tl, tc_ = T(q, gpu), T(ql, gpu), T(caps, gpu)
+        exp = o._query_backoff(q, ql, p, caps)
+        for g in (gi, gs):
+            for got, e in zip(g._query_backoff(tq, tl, p, tc_), exp):
+                np.testing.assert_array_equal(N(got), e)
+        exp = o.draft(q, ql, p, 8, min_token_prob=0.05, caps=caps)
+        for g in (gi, gs):
+            for got, e in zip(g.draft(tq, tl, p, 8, min_token_prob=0.05,
+                                      caps=tc_), exp):
+                np.testing.assert_array_equal(N(got), e)
 
 
 @pytest.mark.parametrize("hint", [12, 1, 3])
