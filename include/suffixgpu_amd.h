@@ -82,10 +82,11 @@ typedef struct sfx_index {
                                   array (sfx_gram_build), or NULL         */
     const void* gram_alt;      /* the table of sa_key_alt's, or NULL      */
     int64_t gram_slots;        /* slots per table, a multiple of 16      */
-    const uint32_t* delta_pos;   /* delta token index of the live delta
-                                    (sfx_delta_index_build), or NULL: each
-                                    decode row then scans the delta       */
-    const uint32_t* delta_start; /* [delta_buckets + 1] its bucket starts */
+    const int32_t* delta_entries; /* delta token index of the live delta
+                                     (sfx_delta_index_build), 16-byte
+                                     aligned, or NULL: each decode row then
+                                     scans the delta                     */
+    const uint32_t* delta_start;  /* [delta_buckets + 1] its bucket starts */
     int64_t delta_buckets;       /* a power of two, 2^10 .. 2^17          */
 } sfx_index;
 
@@ -275,22 +276,24 @@ size_t sfx_gram_table_bytes(int64_t slots);
 int sfx_gram_build(const int32_t* keys, int64_t key_width, int64_t m,
                    void* table, int64_t slots, hipStream_t stream);
 
-/* No reference counterpart.  The delta token index: pos[0 .. D) holds the
- * delta positions 0 .. *delta_len - 1 grouped by a hash bucket of their
- * token (delta_bucket: Fibonacci hashing into `buckets`, a power of two
- * from 2^10 to 2^17), ascending within a bucket, followed by the positions
- * past the live length; start[b] (b = 0 .. buckets) is the first index of
- * bucket b, so bucket b spans pos[start[b] .. start[b + 1]).  A decode
- * step given it (sfx_index.delta_pos/delta_start/delta_buckets) visits
- * only the positions in its newest pattern token's bucket instead of
- * scanning the delta (global_index.py:465-546 computes the same match
- * lengths over every position).  Rebuild it, on the stream the delta is
- * written on, after every change to the delta or its length.  `workspace`
- * (256-byte aligned, sfx_delta_index_bytes(D) bytes) holds nothing
- * between calls.  Enqueued on `stream` with no host read. */
+/* No reference counterpart.  The delta token index: entries[0 .. D), four
+ * int32 each {q, x(q), x(q - 1), x(q - 2)} (x = -1 before position 0),
+ * hold the delta positions q = 0 .. *delta_len - 1 grouped by a hash
+ * bucket of their token x(q) (delta_bucket: Fibonacci hashing into
+ * `buckets`, a power of two from 2^10 to 2^17), ascending within a
+ * bucket, followed by the positions past the live length; start[b]
+ * (b = 0 .. buckets) is the first entry of bucket b, so bucket b spans
+ * entries[start[b] .. start[b + 1]).  A decode step given it
+ * (sfx_index.delta_entries/delta_start/delta_buckets) visits only the
+ * entries in its newest pattern token's bucket instead of scanning the
+ * delta (global_index.py:465-546 computes the same match lengths over
+ * every position).  Rebuild it, on the stream the delta is written on,
+ * after every change to the delta or its length.  `entries` is 16-byte
+ * aligned; `workspace` (256-byte aligned, sfx_delta_index_bytes(D) bytes)
+ * holds nothing between calls.  Enqueued on `stream` with no host read. */
 size_t sfx_delta_index_bytes(int64_t delta_capacity);
 int sfx_delta_index_build(const int32_t* delta, const int64_t* delta_len,
-                          int64_t delta_capacity, uint32_t* pos,
+                          int64_t delta_capacity, int32_t* entries,
                           uint32_t* start, int64_t buckets, void* workspace,
                           size_t workspace_bytes, hipStream_t stream);
 

@@ -43,7 +43,8 @@ class SfxIndex(ctypes.Structure):
         ("sa_key", c_p), ("key_width", c_i64),
         ("sa_key_alt", c_p), ("key_select", c_p),
         ("gram", c_p), ("gram_alt", c_p), ("gram_slots", c_i64),
-        ("delta_pos", c_p), ("delta_start", c_p), ("delta_buckets", c_i64),
+        ("delta_entries", c_p), ("delta_start", c_p),
+        ("delta_buckets", c_i64),
     ]
 
 

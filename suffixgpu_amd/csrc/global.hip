@@ -30,11 +30,11 @@ __global__ __launch_bounds__(kGlobalThreads) void k_global(GlobalArgs a) {
 
 
 int delta_parts_of(const sfx_index& ix, int64_t batch) {
-  return ix.delta_pos ? 1 : delta_parts_for(batch, ix.delta_capacity);
+  return ix.delta_entries ? 1 : delta_parts_for(batch, ix.delta_capacity);
 }
 
 int mb_lds_bytes(const sfx_index& ix, int parts) {
-  if (ix.delta_pos) return 0;  // the indexed delta role keeps no u8 array
+  if (ix.delta_entries) return 0;  // the indexed delta role keeps no u8 array
   const int64_t cap = delta_part_cap(ix.delta_capacity, parts);
   if (cap > kMbLdsMax) return 0;
   const int n = (int)cap;
@@ -52,7 +52,7 @@ int merge_waves_for(const sfx_params& p, const sfx_index& ix, int parts,
     const GlobalLayout L = global_layout(p.max_pattern_len, C,
                                          p.max_occurrences, p.k, nmw,
                                          mb_lds_bytes(ix, parts), 0,
-                                         dend_parts, ix.delta_pos ? 1 : 0);
+                                         dend_parts, ix.delta_entries ? 1 : 0);
     if ((size_t)L.total <= cap) {
       *lds = (size_t)L.total;
       return nmw;
@@ -66,7 +66,7 @@ int delta_chunk_for(const sfx_params& p, const sfx_index& ix, int parts,
   const int P = p.max_pattern_len;
   const int halo = (P + 3) & ~3;
   const int mb = mb_lds_bytes(ix, parts);
-  const int dindex = ix.delta_pos ? 1 : 0;
+  const int dindex = ix.delta_entries ? 1 : 0;
   const GlobalLayout L0 = global_layout(P, p.num_caps, p.max_occurrences,
                                         p.k, nmw, mb, kDeltaChunk,
                                         dend_parts, dindex);
@@ -112,11 +112,12 @@ int check_global(const sfx_params& p, const sfx_index& ix, int64_t batch) {
        ((uintptr_t)ix.gram_alt & 255) || (ix.gram_alt && !ix.key_select)))
     return SFX_EINVAL;
   // the delta token index: both arrays and a bucket count of 2^10 .. 2^17
-  if ((ix.delta_pos || ix.delta_start) &&
-      (!ix.delta_pos || !ix.delta_start ||
+  if ((ix.delta_entries || ix.delta_start) &&
+      (!ix.delta_entries || !ix.delta_start ||
        ix.delta_buckets < (1ll << kDeltaBucketBitsMin) ||
        ix.delta_buckets > (1ll << kDeltaBucketBitsMax) ||
-       (ix.delta_buckets & (ix.delta_buckets - 1))))
+       (ix.delta_buckets & (ix.delta_buckets - 1)) ||
+       ((uintptr_t)ix.delta_entries & 15)))
     return SFX_EINVAL;
   size_t lds = 0;
   const int parts = delta_parts_of(ix, batch);

@@ -263,11 +263,12 @@ __device__ __forceinline__ void delta_role_indexed(const GlobalArgs& a,
   const uint32_t s1 = a.ix.delta_start[bk + 1];
   const int has0 = r0 == -1 ? 1 : 0;
   const int n = (int)(s1 > s0 ? s1 - s0 : 0) + has0;
-  const uint32_t* dpos = a.ix.delta_pos + s0;
+  const int4* ent = reinterpret_cast<const int4*>(a.ix.delta_entries) + s0;
   const int32_t* delta = a.ix.delta;
-  // the position q of entry j (its end is q + 1)
-  auto pos_of = [&](int j) -> int {
-    return has0 ? (j == 0 ? -1 : (int)dpos[j - 1]) : (int)dpos[j];
+  // Entry j: {q, x(q), x(q - 1), x(q - 2)} for the end q + 1; entry 0 is
+  // the end 0 (q = -1) when has0.
+  auto entry = [&](int j) -> int4 {
+    return has0 ? (j == 0 ? make_int4(-1, -1, -1, -1) : ent[j - 1]) : ent[j];
   };
   // The match length of the end after q, continuing from m leading
   // matches: x(q - m) .. x(q - m - 3) against rpat[m ..], four independent
@@ -289,37 +290,32 @@ __device__ __forceinline__ void delta_role_indexed(const GlobalArgs& a,
     }
     return m;
   };
-  // Match lengths of entries jb + u * NT + tid (u < 4) of [j0, j1) into
-  // lmb[j - lbase] (where below kDixList): the first four tokens of the
-  // four entries are loaded together, and only entries matching all four
-  // walk on.  Returns the largest length.
+  // Match lengths of entries jb + u * NT + tid (u < 4) of [.., j1) into
+  // lmb[j - lbase] (where below kDixList): the four entries -- position
+  // and first three tokens each -- are loaded together, and only entries
+  // matching all three walk on in the delta.  Returns the largest length.
   auto mb4 = [&](int jb, int j1, int lbase) -> int {
-    int q[4], m[4];
+    int4 e[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int j = jb + u * NT + tid;
-      q[u] = j < j1 ? pos_of(j) : dl;  // q >= dl: no match
+      e[u] = j < j1 ? entry(j) : make_int4(dl, 0, 0, 0);
     }
-    int32_t x[4][4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int j = q[u] - k;
-        x[u][k] = q[u] >= dl ? -3 : (j >= 0 ? delta[j] : -1);
-      }
     int mx4 = 0;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      int n4 = 0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        n4 += (n4 == k && k < P && x[u][k] == rpat[k]) ? 1 : 0;
-      m[u] = q[u] >= dl ? 0 : n4;  // (q >= dl: an index for a longer delta)
-      if (m[u] == 4 && P > 4) m[u] = mb_from(q[u], 4);
+      // (q >= dl: past the delta, or an index for a longer delta)
+      int m = e[u].x >= dl
+                  ? 0
+                  : (e[u].y != r0 ? 0
+                                  : (P < 2 || e[u].z != rpat[1]
+                                         ? 1
+                                         : (P < 3 || e[u].w != rpat[2] ? 2
+                                                                       : 3)));
+      if (m == 3 && P > 3) m = mb_from(e[u].x, 3);
       const int j = jb + u * NT + tid;
-      if (j < j1 && j - lbase < kDixList) lmb[j - lbase] = (uint8_t)m[u];
-      mx4 = max(mx4, m[u]);
+      if (j < j1 && j - lbase < kDixList) lmb[j - lbase] = (uint8_t)m;
+      mx4 = max(mx4, m);
     }
     return mx4;
   };
@@ -369,7 +365,7 @@ __device__ __forceinline__ void delta_role_indexed(const GlobalArgs& a,
     const int u = e / R;
     if (e - u * R < found[u])
       ws_store(a.ws.d_end + (slot * C + u) * R + (e - u * R),
-               (int32_t)(pos_of(lend[e]) + 1));
+               entry(lend[e]).x + 1);
   }
   for (int c = tid; c < C; c += NT) {
     ws_store(a.ws.d_cnt + slot * C + c, lo_lds[c] > 0 ? found[umap[c]] : 0);
@@ -755,7 +751,7 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
   const int R = p.max_occurrences;
   const int K = p.k;
   const int Rp = (R + 3) & ~3;
-  const bool dindex = a.ix.delta_pos != nullptr;
+  const bool dindex = a.ix.delta_entries != nullptr;
   const GlobalLayout L =
       global_layout(P, C, R, K, a.merge_waves, a.mb_lds, a.dchunk,
                     a.dend ? a.dparts : 0, dindex ? 1 : 0);

@@ -1061,6 +1061,7 @@ static_assert(2 * kDigitBits >= kDeltaBucketBitsMax + 1,
 struct DixWs {
   uint64_t* keyA;    // [D] bucket keys; sorted after the second pass
   uint64_t* keyB;    // [D]
+  uint32_t* pos;     // [D] positions; sorted after the second pass
   uint32_t* valB;    // [D]
   uint32_t* hist;    // [512][NB]
   uint32_t* rowsum;  // [512]
@@ -1080,6 +1081,7 @@ static size_t dix_ws_layout(int64_t D, void* base, DixWs* w) {
   DixWs s;
   s.keyA = (uint64_t*)take(N * 8);
   s.keyB = (uint64_t*)take(N * 8);
+  s.pos = (uint32_t*)take(N * 4);
   s.valB = (uint32_t*)take(N * 4);
   s.hist = (uint32_t*)take((size_t)kRadix * NB * 4);
   s.rowsum = (uint32_t*)take(kRadix * 4);
@@ -1102,6 +1104,21 @@ __global__ __launch_bounds__(256) void k_dix_init(
   }
   if (blockIdx.x == 0 && threadIdx.x < kStateWords)
     state[threadIdx.x] = threadIdx.x == kLen ? (uint32_t)D : 0u;
+}
+
+// Entry j of the index: its position q and the tokens x(q), x(q - 1),
+// x(q - 2) (-1 before position 0), so a row's first test of an entry
+// needs no load that depends on the position.
+__global__ __launch_bounds__(256) void k_dix_entries(
+    const uint32_t* __restrict__ pos, const int32_t* __restrict__ delta,
+    int64_t D, int4* ent) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; j < D;
+       j += stride) {
+    const int64_t q = pos[j];
+    ent[j] = make_int4((int32_t)q, delta[q], q >= 1 ? delta[q - 1] : -1,
+                       q >= 2 ? delta[q - 2] : -1);
+  }
 }
 
 // start[b] = the first sorted index whose key is at least b, b = 0 .. H.
@@ -1294,12 +1311,14 @@ extern "C" size_t sfx_delta_index_bytes(int64_t delta_capacity) {
 
 extern "C" int sfx_delta_index_build(const int32_t* delta,
                                      const int64_t* delta_len,
-                                     int64_t delta_capacity, uint32_t* pos,
+                                     int64_t delta_capacity, int32_t* entries,
                                      uint32_t* start, int64_t buckets,
                                      void* workspace, size_t workspace_bytes,
                                      hipStream_t stream) {
   const int64_t D = delta_capacity;
-  if (!delta || !delta_len || !pos || !start || !workspace) return SFX_EINVAL;
+  if (!delta || !delta_len || !entries || !start || !workspace)
+    return SFX_EINVAL;
+  if ((uintptr_t)entries & 15) return SFX_EINVAL;
   if (D < 1 || D > (1ll << 30)) return SFX_EINVAL;
   if (buckets < (1ll << kDeltaBucketBitsMin) ||
       buckets > (1ll << kDeltaBucketBitsMax) || (buckets & (buckets - 1)))
@@ -1314,9 +1333,9 @@ extern "C" int sfx_delta_index_build(const int32_t* delta,
   const unsigned gb = (unsigned)((D + 255) / 256 < 2048 ? (D + 255) / 256
                                                          : 2048);
   hipLaunchKernelGGL(k_dix_init, dim3(gb), dim3(256), 0, stream, delta,
-                     delta_len, D, hbits, w.keyA, pos, w.state);
+                     delta_len, D, hbits, w.keyA, w.pos, w.state);
   uint64_t* keys[2] = {w.keyA, w.keyB};
-  uint32_t* vals[2] = {pos, w.valB};
+  uint32_t* vals[2] = {w.pos, w.valB};
   int x = 0;
   for (int sh = 0; sh <= hbits; sh += kDigitBits) {
     hipLaunchKernelGGL(k_rs_hist<kRsThreads>, dim3((unsigned)nb),
@@ -1333,6 +1352,8 @@ extern "C" int sfx_delta_index_build(const int32_t* delta,
   }
   // two passes (keys of at most 18 bits): the sorted data is back in
   // keyA and pos
+  hipLaunchKernelGGL(k_dix_entries, dim3(gb), dim3(256), 0, stream, w.pos,
+                     delta, D, reinterpret_cast<int4*>(entries));
   const int64_t H = buckets;
   const unsigned sb = (unsigned)((H + 256) / 256);
   hipLaunchKernelGGL(k_dix_start, dim3(sb), dim3(256), 0, stream, w.keyA, D,

@@ -33,18 +33,23 @@ __global__ __launch_bounds__(kGlobalThreads) void k_step(StepArgs a) {
     local_body<kStream>(a.l, smem, blockIdx.x);
     return;
   }
-  // Blocks are ordered by role, longest first: local, SA, then the delta
-  // parts (role 0: SA, 1..dparts: delta parts, per - 1: local).  A grid
-  // beyond the workgroups that run at once finishes in waves, and so the
-  // longest roles start at once while the shorter delta parts fill the
-  // slots they free: B = 256, S = 16384 with two delta parts measured
-  // 112-115 us with blocks ordered row by row, 94-97 us so.  At B = 64
-  // (one wave) the two orders measured the same within 0.3 us.
+  // Blocks are ordered by role (role 0: SA, 1..dparts: delta parts,
+  // per - 1: local): local, then the delta parts, then SA.  A grid beyond
+  // the workgroups that run at once finishes in waves, so the order
+  // decides which roles start at once.  With the delta token index (one
+  // delta workgroup per row, whose bucket walk ends with the delta
+  // expansion) B = 256, S = 16384 with a full 2^16 delta measured
+  // 48.7-49.5 us with SA second and 42.4-43.3 us with the delta second.
+  // (Scanning the delta, two parts per row, SA second had measured 94-97
+  // us and row by row 112-115 us.)  At B = 64 (one wave) the orders
+  // measured the same within 0.3 us.  The order is a fixed function of
+  // the block index: an order chosen by a kernel argument made the
+  // compiler spill the streamed variant to scratch.
   const int per = 2 + a.g.dparts;
   const int B = (int)a.g.B;
   const int slot = (int)(blockIdx.x / B);
   const int b = (int)(blockIdx.x % B);
-  const int role = slot == 0 ? per - 1 : slot - 1;
+  const int role = slot == 0 ? per - 1 : (slot == per - 1 ? 0 : slot);
   if (role == per - 1)
     local_body<kStream>(a.l, smem, b);
   else

@@ -110,11 +110,12 @@ class GlobalIndex:
         # decode row visits only the positions of its newest token's
         # bucket.  delta_index=False: every row scans the whole delta.
         self.delta_buckets = 0
-        self._dix_pos = self._dix_start = self._dix_ws = None
+        self._dix_ent = self._dix_start = self._dix_ws = None
         if delta_index and delta_capacity <= DELTA_INDEX_MAX:
             self.delta_buckets = delta_buckets_for(delta_capacity)
-            self._dix_pos = torch.empty(delta_capacity, dtype=torch.int32,
-                                        device=dev)
+            # {q, x(q), x(q - 1), x(q - 2)} per entry
+            self._dix_ent = torch.empty((delta_capacity, 4),
+                                        dtype=torch.int32, device=dev)
             self._dix_start = torch.zeros(self.delta_buckets + 1,
                                           dtype=torch.int32, device=dev)
             self._dix_ws = torch.empty(
@@ -215,8 +216,8 @@ class GlobalIndex:
         return self._keys[1 - self._key_live] if self._keys else None
 
     def index_struct(self) -> _lib.SfxIndex:
-        if self._dix_pos is not None:
-            dix = (self._dix_pos.data_ptr(), self._dix_start.data_ptr(),
+        if self._dix_ent is not None:
+            dix = (self._dix_ent.data_ptr(), self._dix_start.data_ptr(),
                    self.delta_buckets)
         else:
             dix = (None, None, 0)
@@ -250,7 +251,7 @@ class GlobalIndex:
             "gram_tables": sum(t.numel() for t in self._grams or ()),
             "delta": 4 * self.delta_capacity + 8,
             "delta_index": sum(t.numel() * t.element_size() for t in (
-                self._dix_pos, self._dix_start, self._dix_ws)
+                self._dix_ent, self._dix_start, self._dix_ws)
                 if t is not None),
             "sa_build_workspace": ws,
             "query_workspace": qws,
@@ -295,11 +296,11 @@ class GlobalIndex:
     def _index_delta(self) -> None:
         """Rebuild the delta token index on the current stream (after
         every write to the delta or its device length)."""
-        if self._dix_pos is None:
+        if self._dix_ent is None:
             return
         check(lib().sfx_delta_index_build(
             self.delta.data_ptr(), self.delta_len_t.data_ptr(),
-            self.delta_capacity, self._dix_pos.data_ptr(),
+            self.delta_capacity, self._dix_ent.data_ptr(),
             self._dix_start.data_ptr(), self.delta_buckets,
             self._dix_ws.data_ptr(), self._dix_ws.numel(),
             stream_of(self.device)), "delta index")

@@ -187,7 +187,7 @@ int main(void) {
   S(sfx_index); F(sfx_index, delta_len); F(sfx_index, sa_key);
   F(sfx_index, key_width); F(sfx_index, sa_key_alt);
   F(sfx_index, key_select); F(sfx_index, gram_slots);
-  F(sfx_index, delta_pos); F(sfx_index, delta_buckets);
+  F(sfx_index, delta_entries); F(sfx_index, delta_buckets);
   S(sfx_batch); F(sfx_batch, num_tokens_is64); F(sfx_batch, sampled);
   F(sfx_batch, valid_count_is64); F(sfx_batch, mask); F(sfx_batch, limit);
   S(sfx_global_out); F(sfx_global_out, draft_score);
@@ -225,13 +225,17 @@ def test_struct_layouts_match_the_header(tmp_path):
 
 def test_delta_index_build_checks_arguments_on_the_host():
     """sfx_delta_index_build rejects a bucket count that is not a power of
-    two in 2^10 .. 2^17, a missing buffer, a misaligned or short workspace,
-    and a capacity out of range, before any launch."""
+    two in 2^10 .. 2^17, a missing buffer, misaligned entries, a
+    misaligned or short workspace, and a capacity out of range, before any
+    launch."""
     lib = _lib.lib()
     d = 1 << 12
     need = lib.sfx_delta_index_bytes(d)
     assert need > 0 and lib.sfx_delta_index_bytes(0) == 0
     ok = (0x100000, 0x200000, d, 0x300000, 0x400000)
+    assert lib.sfx_delta_index_build(0x100000, 0x200000, d, 0x300008,
+                                     0x400000, 1 << 10, 0x500000, need,
+                                     None) == -1  # entries 16-byte aligned
     for buckets in (1 << 9, 3 << 10, 1 << 18):
         assert lib.sfx_delta_index_build(*ok, buckets, 0x500000, need,
                                           None) == -1

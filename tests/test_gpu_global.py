@@ -417,12 +417,17 @@ def delta_bucket(t, hbits):
 def check_delta_index(g):
     """The delta token index of g by its definition: bucket b lists the
     positions p < delta_len with delta_bucket(delta[p]) == b, ascending,
+    each with the tokens x(p), x(p - 1), x(p - 2) (-1 before position 0);
     the positions from delta_len on follow in order, and start[b] is each
     bucket's first index."""
     hb = g.delta_buckets.bit_length() - 1
     dl = g.delta_len
     delta = N(g.delta)
-    pos = N(g._dix_pos).view(np.uint32).astype(np.int64)
+    ent = N(g._dix_ent).astype(np.int64)
+    pos = ent[:, 0]
+    padded = np.concatenate([[-1, -1], delta.astype(np.int64)])
+    for k in range(3):
+        np.testing.assert_array_equal(ent[:, 1 + k], padded[pos + 2 - k])
     start = N(g._dix_start).view(np.uint32).astype(np.int64)
     keys = np.array([delta_bucket(t, hb) for t in delta[:dl]], np.int64)
     order = np.lexsort((np.arange(dl), keys))
