@@ -59,11 +59,14 @@ typedef struct sfx_params {
  * first key_width tokens of the suffix at sa[r] (-1 past the end), built
  * by sfx_sa_keys() with every suffix array; NULL disables it.
  *
- * The key rows may be double-buffered: with key_select != NULL the kernels
- * read the device word *key_select when they run and take sa_key_alt when
- * it is nonzero, sa_key otherwise.  A rebuild writes the idle buffer and
- * sfx_index_swap() flips the word, so a swap copies no key rows and graphs
- * captured over this struct follow the live buffer. */
+ * With key_select != NULL the kernels read the device word *key_select
+ * when they run and take sa_key_alt and gram_alt when it is nonzero, sa_key
+ * and gram otherwise; a NULL second buffer means none (the search then
+ * compares through sa and corpus, exact and slower).  Double buffers let a
+ * rebuild write the idle pair and sfx_index_swap() flip the word; single
+ * buffers let the swap set the word while the new array's key rows and
+ * table are written, and a later sfx_index_swap() with capacity 0 clear
+ * it.  Either way graphs captured over this struct follow the word. */
 typedef struct sfx_index {
     const int32_t* corpus;    /* [capacity] PAD-filled ring               */
     const int32_t* sa;        /* [capacity] suffix array of corpus        */
@@ -75,9 +78,10 @@ typedef struct sfx_index {
                                  aligned                                 */
     int64_t key_width;        /* 4..32, a multiple of 4                   */
     const int32_t* sa_key_alt; /* second key-row buffer (same layout) or
-                                  NULL                                   */
-    const int32_t* key_select; /* device int32 selecting sa_key_alt when
-                                  nonzero, or NULL (sa_key is live)      */
+                                  NULL (none while selected)             */
+    const int32_t* key_select; /* device int32 selecting sa_key_alt and
+                                  gram_alt when nonzero, or NULL (sa_key
+                                  and gram are live)                     */
     const void* gram;          /* n-gram range table of sa_key's suffix
                                   array (sfx_gram_build), or NULL         */
     const void* gram_alt;      /* the table of sa_key_alt's, or NULL      */
@@ -339,8 +343,8 @@ int sfx_sa_build_finish(int64_t m, int64_t n_total, void* sa, int32_t sa_is64,
  * rebuild into the live buffers (corpus, sa: capacity int32 each), one
  * launch, so graphs captured over the live buffers keep their pointers.
  * The key rows are not copied: when key_select is not NULL the same launch
- * stores key_select_value there (sfx_index.key_select picks the buffer the
- * rebuild wrote). */
+ * stores key_select_value there (sfx_index.key_select picks the buffers
+ * the steps read); capacity 0 stores only the word. */
 int sfx_index_swap(int32_t* corpus, int32_t* sa, const int32_t* new_corpus,
                    const int32_t* new_sa, int64_t capacity,
                    int32_t* key_select, int32_t key_select_value,

@@ -100,9 +100,9 @@ int check_global(const sfx_params& p, const sfx_index& ix, int64_t batch) {
       (ix.key_width < 4 || ix.key_width > 32 || (ix.key_width & 3) ||
        ((uintptr_t)ix.sa_key & 15)))
     return SFX_EINVAL;
-  // A selector needs both key buffers, with the same alignment rule.
-  if (ix.key_select &&
-      (!ix.sa_key || !ix.sa_key_alt || ((uintptr_t)ix.sa_key_alt & 15)))
+  // A selector needs the first key buffer; the second (NULL: none while
+  // the selector is set) follows the same alignment rule.
+  if (ix.key_select && (!ix.sa_key || ((uintptr_t)ix.sa_key_alt & 15)))
     return SFX_EINVAL;
   // n-gram tables: a power-of-two slot count of at least one bucket,
   // 256-byte aligned tables, the second one only with a selector

@@ -724,15 +724,16 @@ __device__ __forceinline__ void source_expand(
 }
 
 // The key rows the index's selector word names (sfx_index.key_select).
+// A nonzero selector names the second buffer, which may be NULL: no key
+// rows while they are being rebuilt.
 __device__ __forceinline__ const int32_t* live_keys(const sfx_index& ix) {
-  if (ix.key_select && ix.sa_key_alt && *ix.key_select != 0)
-    return ix.sa_key_alt;
+  if (ix.key_select && *ix.key_select != 0) return ix.sa_key_alt;
   return ix.sa_key;
 }
 
 // The n-gram range table of the live suffix array, or NULL.
 __device__ __forceinline__ const void* live_gram(const sfx_index& ix) {
-  if (ix.key_select && ix.gram_alt && *ix.key_select != 0) return ix.gram_alt;
+  if (ix.key_select && *ix.key_select != 0) return ix.gram_alt;
   return ix.gram;
 }
 

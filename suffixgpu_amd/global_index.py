@@ -122,45 +122,40 @@ class GlobalIndex:
                 int(lib().sfx_delta_index_bytes(delta_capacity)),
                 dtype=torch.uint8, device=dev)
             self._index_delta()
-        # Two key-row buffers and n-gram range tables; the device word
-        # key_select names the live pair (the step reads it), a rebuild
-        # writes the other.  search_tables=False keeps neither (about
-        # 260 bytes per corpus position less) and releases the build
-        # workspace between builds: searches then compare through the
-        # suffix array and the corpus, exact but slower.
+        # One key-row buffer and one n-gram range table, of the live
+        # suffix array.  A swap brings in a new array with the device word
+        # key_select set (the steps then search through the suffix array
+        # and the corpus, exact but slower: the selector names no second
+        # buffer) and the rebuild stream writes the new rows and table; the
+        # next poll clears the word once they are done.  search_tables=
+        # False keeps neither (about 130 bytes per corpus position less)
+        # and releases the build workspace between builds.
         self.search_tables = bool(search_tables)
         self._keys = None
-        self._grams = None
+        self._gram = None
         self.gram_slots = 0
         self.key_select = None
         if self.search_tables:
-            self._keys = [torch.empty(capacity * KEY_WIDTH,
-                                      dtype=torch.int32, device=dev)
-                          for _ in range(2)]
+            self._keys = torch.empty(capacity * KEY_WIDTH, dtype=torch.int32,
+                                     device=dev)
             # gram_slots (a multiple of 16) overrides the table size; a
-            # table too small for the corpus marks itself unusable and
-            # searches span the whole suffix array instead.
+            # table too small for the corpus keeps the run lengths that
+            # fit (possibly none).
             self.gram_slots = gram_slots or gram_slots_for(capacity)
-            # Each table's buffer: the table, then each rank's first four
-            # tokens (written with the key rows, read by the table build).
-            # The idle buffer also lends its table region to the suffix
-            # array build as workspace: a build's table is written only
-            # once the host has seen its suffix array is final.
-            tbytes = int(lib().sfx_gram_table_bytes(self.gram_slots))
-            self._gram_bytes = max(tbytes,
-                                   sa_workspace_bytes(capacity) + 255) \
-                // 256 * 256
-            gbytes = self._gram_bytes + 16 * capacity
-            self._grams = [torch.zeros(gbytes, dtype=torch.uint8,
-                                       device=dev) for _ in range(2)]
+            self._gram = torch.zeros(
+                int(lib().sfx_gram_table_bytes(self.gram_slots)),
+                dtype=torch.uint8, device=dev)
             self.key_select = torch.zeros(1, dtype=torch.int32, device=dev)
-        self._key_live = 0
-        # Per buffer: ranks from this one on hold padding-suffix rows (the
-        # suffix array is the identity there and the corpus PAD), so the
-        # next build into it rewrites only the rows below max(m, this).
-        self._key_rows = [capacity, capacity]
-        self._build_keys(self.corpus, self.sa, self._key_live, 0)
+        # Ranks from this one on hold padding-suffix rows (the suffix array
+        # is the identity there and the corpus PAD), so the next key build
+        # rewrites only the rows below max(m, this).
+        self._key_rows = capacity
+        # the background build of the live array's key rows and table:
+        # its event on the rebuild stream until a poll has cleared the
+        # selector
+        self._tables_event = None
         self._sa_ws: torch.Tensor | None = None
+        self._build_tables(0)
         self._query_ws: dict = {}
 
         self.active_len = 0
@@ -207,13 +202,15 @@ class GlobalIndex:
     # ------------------------------------------------------------------
     @property
     def sa_key(self) -> torch.Tensor | None:
-        """Key rows of the live suffix array ([capacity * 32] int32)."""
-        return self._keys[self._key_live] if self._keys else None
+        """Key rows of the live suffix array ([capacity * 32] int32); being
+        rewritten while tables_pending."""
+        return self._keys
 
     @property
-    def staging_sa_key(self) -> torch.Tensor | None:
-        """Key rows a rebuild writes (the idle buffer)."""
-        return self._keys[1 - self._key_live] if self._keys else None
+    def tables_pending(self) -> bool:
+        """The live array's key rows and table are still being built (the
+        steps search without them)."""
+        return self._tables_event is not None
 
     def index_struct(self) -> _lib.SfxIndex:
         if self._dix_ent is not None:
@@ -231,24 +228,19 @@ class GlobalIndex:
                              self.capacity, self.delta.data_ptr(),
                              self.delta_capacity,
                              self.delta_len_t.data_ptr(),
-                             self._keys[0].data_ptr(), KEY_WIDTH,
-                             self._keys[1].data_ptr(),
+                             self._keys.data_ptr(), KEY_WIDTH, None,
                              self.key_select.data_ptr(),
-                             self._grams[0].data_ptr(),
-                             self._grams[1].data_ptr(), self.gram_slots,
+                             self._gram.data_ptr(), None, self.gram_slots,
                              *dix)
 
     def device_bytes(self) -> dict:
-        """Device memory held by the index, by role (bytes).  With search
-        tables the suffix-array build workspace lies inside the idle
-        table's buffer (counted under gram_tables)."""
-        ws = (self._sa_ws.numel() if self._sa_ws is not None
-              and not self.search_tables else 0)
+        """Device memory held by the index, by role (bytes)."""
+        ws = self._sa_ws.numel() if self._sa_ws is not None else 0
         qws = sum(t.numel() for t in self._query_ws.values())
         return {
             "corpus_sa": 4 * 4 * self.capacity,  # live + staging, int32
-            "key_rows": sum(t.numel() * 4 for t in self._keys or ()),
-            "gram_tables": sum(t.numel() for t in self._grams or ()),
+            "key_rows": 4 * self._keys.numel() if self.search_tables else 0,
+            "gram_tables": self._gram.numel() if self.search_tables else 0,
             "delta": 4 * self.delta_capacity + 8,
             "delta_index": sum(t.numel() * t.element_size() for t in (
                 self._dix_ent, self._dix_start, self._dix_ws)
@@ -257,41 +249,66 @@ class GlobalIndex:
             "query_workspace": qws,
         }
 
-    def _build_keys(self, corpus, sa, slot: int, m: int,
-                    table: bool = True) -> None:
-        """Key rows (and, with `table`, the n-gram range table) of
-        (corpus, sa) into buffer pair `slot` (0 or 1), on the current
-        stream.  Ranks from m on are the padding suffixes (sa the identity,
-        corpus PAD): their rows are rewritten only where the buffer's
+    def _build_tables(self, m: int) -> None:
+        """Key rows and n-gram range table of the live suffix array (m
+        ranks hold real suffixes) on the current stream.  Ranks from m on
+        are the padding suffixes: their rows are rewritten only where the
         previous build had real ones, and they hold no run of real tokens
-        for the table."""
+        for the table.  The key-row launch also writes each rank's first
+        four tokens compactly into the build workspace (dead between
+        builds), from which the table is built."""
         if not self.search_tables:
             return
-        keys = self._keys[slot]
         st = stream_of(self.device)
-        rows = max(m, self._key_rows[slot])
-        # each rank's first four tokens, written compactly by the same
-        # launch after the table in its buffer, for the table build
-        first4 = self._first4(slot) if m > 0 else None
-        check(lib().sfx_sa_keys(corpus.data_ptr(), sa.data_ptr(),
+        rows = max(m, self._key_rows)
+        ws = self._sa_workspace() if m > 0 else None
+        first4 = ws.data_ptr() if m > 0 else None
+        check(lib().sfx_sa_keys(self.corpus.data_ptr(), self.sa.data_ptr(),
                                 self.capacity, rows, KEY_WIDTH,
-                                keys.data_ptr(), first4, st), "SA key rows")
-        self._key_rows[slot] = m
-        if table:
-            self._build_table(slot, m)
+                                self._keys.data_ptr(), first4, st),
+              "SA key rows")
+        self._key_rows = m
+        src = first4 if m > 0 else self._keys.data_ptr()
+        check(lib().sfx_gram_build(src, 4 if m > 0 else KEY_WIDTH, m,
+                                   self._gram.data_ptr(), self.gram_slots,
+                                   st), "n-gram table")
 
-    def _first4(self, slot: int) -> int:
-        return self._grams[slot].data_ptr() + self._gram_bytes
+    def _swap_tables(self, m: int, sync: bool) -> None:
+        """After a swap (selector set): build the new array's key rows and
+        table, on the rebuild stream (cleared by a later poll) or, with
+        `sync` or no rebuild stream, on the current one (cleared now)."""
+        if not self.search_tables:
+            return
+        if sync or self.rebuild_stream is None:
+            self._build_tables(m)
+            self._clear_selector()
+            return
+        self.rebuild_stream.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(self.rebuild_stream):
+            self._build_tables(m)
+        ev = torch.cuda.Event()
+        ev.record(self.rebuild_stream)
+        self._tables_event = ev
 
-    def _build_table(self, slot: int, m: int) -> None:
-        """The n-gram range table of buffer pair `slot` from the first
-        four tokens its key-row launch wrote (m ranks), on the current
-        stream."""
-        first4 = self._first4(slot) if m > 0 else self._keys[slot].data_ptr()
-        check(lib().sfx_gram_build(first4, 4 if m > 0 else KEY_WIDTH, m,
-                                   self._grams[slot].data_ptr(),
-                                   self.gram_slots, stream_of(self.device)),
-              "n-gram table")
+    def _clear_selector(self) -> None:
+        check(lib().sfx_index_swap(None, None, None, None, 0,
+                                   self.key_select.data_ptr(), 0,
+                                   stream_of(self.device)), "tables live")
+
+    def poll_tables(self, wait: bool = False) -> None:
+        """Clear the selector once the key rows and table of the live
+        array are built (the current stream waits for their event first),
+        so later steps use them again."""
+        ev = self._tables_event
+        if ev is None:
+            return
+        if wait:
+            ev.synchronize()
+        elif not ev.query():
+            return
+        torch.cuda.current_stream(self.device).wait_event(ev)
+        self._clear_selector()
+        self._tables_event = None
 
     def _index_delta(self) -> None:
         """Rebuild the delta token index on the current stream (after
@@ -465,15 +482,16 @@ class GlobalIndex:
             self._finish_swap(n_new, new_doc_lens)
 
     def _sa_workspace(self) -> torch.Tensor:
-        """The suffix-array build workspace: the table region of the idle
-        buffer pair with search tables (nothing reads it until the build's
-        own table is written there), else an allocation of its own."""
-        need = sa_workspace_bytes(self.capacity)
-        if self.search_tables:
-            self._sa_ws = self._grams[1 - self._key_live][:max(need, 1)]
-        elif self._sa_ws is None or self._sa_ws.numel() < need:
+        """The suffix-array build workspace (also where the table build
+        finds each rank's first four tokens).  Work enqueued on another
+        stream than a pending table build's waits for it first."""
+        need = max(sa_workspace_bytes(self.capacity), 16 * self.capacity)
+        if self._sa_ws is None or self._sa_ws.numel() < need:
             self._sa_ws = torch.empty(max(need, 1), dtype=torch.uint8,
                                       device=self.device)
+        if self._tables_event is not None:
+            torch.cuda.current_stream(self.device).wait_event(
+                self._tables_event)
         return self._sa_ws
 
     def _build_staging_sa(self, dst: torch.Tensor, m: int) -> None:
@@ -483,8 +501,6 @@ class GlobalIndex:
                                  self.staging_sa.data_ptr(), 0,
                                  ws.data_ptr(), ws.numel(),
                                  stream_of(self.device)), "SA rebuild")
-        # (the workspace is dead once the build wrote staging_sa)
-        self._build_keys(dst, self.staging_sa, 1 - self._key_live, m)
 
     # Background builds, enqueued on the current (rebuild) stream.
     def _staged_build_begin(self, dst: torch.Tensor, m: int) -> None:
@@ -513,17 +529,14 @@ class GlobalIndex:
         self._flag_host.copy_(state_view(self._sa_ws, m), non_blocking=True)
 
     def _staged_build_finish(self, dst: torch.Tensor, m: int) -> None:
-        """The output and key rows, speculatively (the host has not seen
-        whether the array is final yet); the table only once it has, as
-        the workspace may still be needed for more rounds."""
+        """The output, speculatively (the host has not seen whether the
+        array is final yet)."""
         ws = self._sa_ws
         check(lib().sfx_sa_build_finish(m, self.capacity,
                                         self.staging_sa.data_ptr(), 0,
                                         ws.data_ptr(), ws.numel(),
                                         stream_of(self.device)),
               "SA rebuild")
-        self._build_keys(dst, self.staging_sa, 1 - self._key_live, m,
-                         table=False)
 
     def _staged_build_check(self) -> bool:
         """After the build's event: True when the staged output is final;
@@ -537,17 +550,15 @@ class GlobalIndex:
             return True
         m, nxt = self._build_state
         self._build_state = None
-        if nxt is None:
-            return True  # the table of a final array is built
         if m <= 1:
-            return self._staged_table(m)  # nothing to sort
+            return True  # nothing to sort
         state = BuildState.of(self._flag_host.tolist())
         L = lib()
         total = int(L.sfx_sa_build_rounds_total(m))
         if state.done:
             self.sa_round_hint = state.needed + 2
             self.sa_radix_hint = state.radix_mask & ~1
-            return self._staged_table(m)
+            return True
         if state.stalled:
             nxt, radix = state.stalled, 1 << state.stalled
         elif nxt > total:
@@ -555,7 +566,7 @@ class GlobalIndex:
             # have raised the flag, so the array is final as it stands.
             self.sa_round_hint = total
             self.sa_radix_hint = state.radix_mask & ~1
-            return self._staged_table(m)
+            return True
         else:
             radix = 0
         self.rebuild_stream.wait_stream(torch.cuda.current_stream(self.device))
@@ -571,22 +582,6 @@ class GlobalIndex:
         self._rebuild_event = event
         return False
 
-    def _staged_table(self, m: int) -> bool:
-        """The suffix array of a background build is final: with search
-        tables, enqueue its n-gram table (over the workspace, dead now) on
-        the rebuild stream under a new event and report the build as not
-        done yet; else it is done."""
-        if not self.search_tables:
-            return True
-        self.rebuild_stream.wait_stream(torch.cuda.current_stream(self.device))
-        with torch.cuda.stream(self.rebuild_stream):
-            self._build_table(1 - self._key_live, m)
-        self._build_state = (m, None)
-        event = torch.cuda.Event()
-        event.record(self.rebuild_stream)
-        self._rebuild_event = event
-        return False
-
     def _count_docs_within(self, tokens: int) -> int:
         acc = 0
         count = 0
@@ -597,18 +592,24 @@ class GlobalIndex:
             count += 1
         return count
 
-    def _finish_swap(self, n_new: int, new_doc_lens: deque[int]) -> None:
+    def _finish_swap(self, n_new: int, new_doc_lens: deque[int],
+                     sync_tables: bool = False) -> None:
         # Ring and suffix array are copied into the live tensors (captured
-        # graphs hold their pointers); the key rows switch buffers by the
-        # selector word, in the same launch.
-        live = 1 - self._key_live
+        # graphs hold their pointers) and the selector set in the same
+        # launch: the steps search without key rows and table until the
+        # new array's are built.  A table build still pending reads the
+        # live arrays: the swap waits for it.
+        if self._tables_event is not None:
+            torch.cuda.current_stream(self.device).wait_event(
+                self._tables_event)
+            self._tables_event = None
         check(lib().sfx_index_swap(
             self.corpus.data_ptr(), self.sa.data_ptr(),
             self.staging_corpus.data_ptr(), self.staging_sa.data_ptr(),
             self.capacity,
             self.key_select.data_ptr() if self.search_tables else None,
-            live, stream_of(self.device)), "swap")
-        self._key_live = live
+            1, stream_of(self.device)), "swap")
+        self._swap_tables(min(n_new + 1, self.capacity), sync_tables)
         self.swap_count += 1
         self.active_len = n_new
         if new_doc_lens is not None:  # None: the device keeps them
@@ -644,6 +645,7 @@ class GlobalIndex:
             if self._ing_event.query():
                 self._ing_event = None
                 self._read_ingest_mirror()
+        self.poll_tables(wait=self.blocking_poll)
         ev = self._rebuild_event
         if ev is None:
             return
@@ -960,7 +962,12 @@ class GlobalIndex:
         self.active_len = n_act
         self.active_doc_lens = deque(int(x) for x in meta["active_doc_lens"])
         self.delta_doc_lens = [int(x) for x in meta["delta_doc_lens"]]
-        self._build_keys(self.corpus, self.sa, self._key_live, m)
+        if self._tables_event is not None:
+            self._tables_event.synchronize()
+            self._tables_event = None
+        self._build_tables(m)
+        if self.search_tables:
+            self._clear_selector()
 
     @classmethod
     def from_file(cls, path, device="cuda",
@@ -1000,7 +1007,7 @@ class GlobalIndex:
             dst[off + d.shape[0]] = SEP_TOKEN
             off += d.shape[0] + 1
         self._build_staging_sa(dst, min(n + 1, self.capacity))
-        self._finish_swap(n, deque(lens))
+        self._finish_swap(n, deque(lens), sync_tables=True)
 
     # ------------------------------------------------------------------
     # queries (global_index.py:257-553)

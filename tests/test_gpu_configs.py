@@ -55,6 +55,7 @@ def index_equal(gi, og) -> None:
     np.testing.assert_array_equal(N(gi.delta)[:gi.delta_len],
                                   og.delta[:og.delta_len])
     assert int(gi.delta_len_t.item()) == gi.delta_len
+    gi.poll_tables(wait=True)  # rows of a swap built on the rebuild stream
     keys_by_definition(gi.corpus, gi.sa, gi.sa_key)
 
 

@@ -34,6 +34,8 @@ def key_arrays_equal(gi):
     if gi.sa_key is None:
         assert not gi.search_tables
         return
+    gi.poll_tables(wait=True)  # rows of a swap built on the rebuild stream
+    assert not gi.tables_pending
     corpus, sa = N(gi.corpus), N(gi.sa).astype(np.int64)
     n, kw = corpus.shape[0], 32
     pos = sa[:, None] + np.arange(kw)[None, :]
@@ -763,7 +765,7 @@ def gpu_gram_table(g):
     min(count, 16) slots are filled.  Entries are keyed (k, t0, t1, t2,
     t3), tokens past k 0; kmax is the longest length whose runs are all
     stored."""
-    raw = N(g._grams[g._key_live])
+    raw = N(g._gram)
     slots_n = g.gram_slots
     nb = slots_n // 16
     cbytes = (nb * 4 + 255) // 256 * 256
