@@ -1134,10 +1134,13 @@ def summarize_api(trace_dir: str) -> dict:
              == SYNC_CHECK_STEPS]
     replay = [s for s in sections
               if s["calls"].get("hipGraphLaunch", 0) == SYNC_CHECK_STEPS]
-    # The last section: the device harvests (three launches each).
+    # The last section: the device harvests (three ingest launches each,
+    # then the nine of the delta token index's rebuild).
     harvest = [s for s in sections
-               if s["calls"].get("hipLaunchKernel", 0)
-               == 3 * SYNC_CHECK_STEPS]
+               if s["calls"].get("hipLaunchKernel", 0) >= 3 * SYNC_CHECK_STEPS
+               and s["calls"].get("hipLaunchKernel", 0)
+               % SYNC_CHECK_STEPS == 0
+               and not s["calls"].get("hipGraphLaunch", 0)]
     return {"steps_per_section": SYNC_CHECK_STEPS,
             "eager_steps": eager[-1] if eager else None,
             "graph_replays": replay[-1] if replay else None,
