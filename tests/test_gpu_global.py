@@ -549,6 +549,88 @@ def test_async_rebuild_blocking_poll(gpu, hint):
     gpu_state_equal(g, o)
 
 
+def test_queries_while_the_swapped_tables_are_built(gpu):
+    """After a background rebuild swaps in, the steps before the next poll
+    find the selector set (the swap sets it on their stream) and search
+    without key rows and table; the poll after the tables' event clears it.
+    Queries and drafts equal the oracle's in both windows, and the rebuilt
+    key rows and table equal their definition."""
+    from suffixgpu_amd.global_index import GlobalIndex
+    rng = np.random.default_rng(41)
+    tc = synth.TemplateCorpus(seed=23, n_templates=6)
+    side = torch.cuda.Stream(gpu)
+    kw = dict(capacity=1 << 15, delta_capacity=1 << 13, k=8,
+              max_occurrences=16, rebuild_threshold=1 << 30)
+    g = GlobalIndex(device=gpu, rebuild_stream=side, **kw)
+    o = GlobalIndexOracle(async_rebuild=True, **kw)
+    docs = [tc.sequence(lo=200, hi=600) for _ in range(20)]
+    g.load_documents([T(d, gpu) for d in docs])
+    o.load_documents(docs)
+    dd = [tc.sequence(lo=200, hi=900) for _ in range(8)]
+    g.append_documents([T(d, gpu) for d in dd])
+    o.append_documents(dd)
+    g.rebuild_threshold = o.rebuild_threshold = 1
+    g.blocking_poll = True
+    g.maybe_rebuild()
+    o.maybe_rebuild()
+    g.poll_rebuild()  # swaps; the tables are built on `side`
+    o.poll_rebuild()
+    assert g._rebuild_event is None and o._rebuild_event is None
+    assert g.tables_pending and int(g.key_select.item()) == 1
+    b, p = 32, 24
+    q = np.zeros((b, p), I32)
+    ql = np.zeros(b, np.int64)
+    src_all = docs + dd
+    for i in range(b):
+        src = src_all[int(rng.integers(0, len(src_all)))]
+        n = int(rng.integers(1, min(len(src), p) + 1))
+        st = int(rng.integers(0, len(src) - n + 1))
+        q[i, :n] = src[st:st + n]
+        ql[i] = n
+    caps = np.array([24, 12, 6, 3, 2], np.int64)
+    tq, tl, tc_ = T(q, gpu), T(ql, gpu), T(caps, gpu)
+    for pending in (True, False):
+        if not pending:
+            g.poll_rebuild()  # waits for the tables' event, clears the word
+            assert not g.tables_pending and int(g.key_select.item()) == 0
+        for got, e in zip(g._query_backoff(tq, tl, p, tc_),
+                          o._query_backoff(q, ql, p, caps)):
+            np.testing.assert_array_equal(N(got), e)
+        for got, e in zip(g.draft(tq, tl, p, 8, min_token_prob=0.05,
+                                  caps=tc_),
+                          o.draft(q, ql, p, 8, min_token_prob=0.05,
+                                  caps=caps)):
+            np.testing.assert_array_equal(N(got), e)
+    gpu_state_equal(g, o)
+    kmax, tab = gpu_gram_table(g)
+    assert kmax == 4
+    assert tab == gram_runs(N(g.corpus), N(g.sa))
+
+
+@pytest.mark.parametrize("dcap", [400, 4097])
+def test_delta_index_at_odd_capacities(gpu, dcap):
+    """The delta token index by its definition at a capacity below the
+    smallest bucket count (400: 1024 buckets) and one just past a radix
+    tile (4097), after appends, a drop and a rebuild's compaction."""
+    from suffixgpu_amd.global_index import GlobalIndex
+    rng = np.random.default_rng(dcap)
+    g = GlobalIndex(capacity=1 << 14, delta_capacity=dcap, k=4,
+                    max_occurrences=8, rebuild_threshold=1 << 30,
+                    device=gpu)
+    for step in range(6):
+        docs = [rng.integers(0, 50, size=int(rng.integers(1, dcap // 3)))
+                .astype(I32) for _ in range(3)]
+        g.append_documents([T(d, gpu) for d in docs])
+        torch.cuda.synchronize()
+        check_delta_index(g)
+        if step == 3:
+            g.rebuild_threshold = 1
+            g.maybe_rebuild()  # synchronous: the delta is compacted
+            g.rebuild_threshold = 1 << 30
+            torch.cuda.synchronize()
+            check_delta_index(g)
+
+
 def test_round_hint_follows_the_last_build(gpu):
     """The background rebuild's first chunk of doubling rounds is sized
     from the rounds the previous build needed, with the radix path for the
