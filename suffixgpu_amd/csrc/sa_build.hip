@@ -61,11 +61,19 @@ constexpr uint32_t kJustFinished = 0xfffffffeu;
 // state[] words: [0] done, [1] global list length, [2] round that found no
 // group left, [3] / [4] least / largest token other than PAD (INT32_MAX),
 // [5] h of round 1, [7] round that stalled (0: none), [8] bit r set when
-// round r took the global path, [16 + r] largest group entering round r.
+// round r took the global path, [16 + r] largest group entering round r,
+// [64 + r] h of round r (the prefix length its groups share).
 constexpr int kDone = 0, kLen = 1, kFoundNone = 2, kTokLo = 3, kTokHi = 4,
-              kH0 = 5, kStalled = 7, kGlobalMask = 8, kMaxGrp = 16;
-constexpr int kStateWords = 64;
-static_assert(kMaxGrp + 33 <= kStateWords, "a round word per doubling");
+              kH0 = 5, kStalled = 7, kGlobalMask = 8, kMaxGrp = 16,
+              kHRound = 64;
+constexpr int kStateWords = 128;
+static_assert(kMaxGrp + 33 <= kHRound, "a round word per doubling");
+static_assert(kHRound + 33 <= kStateWords, "an h word per doubling");
+// A round whose groups all fit the local part sorts them by the ranks at
+// i + h and i + 2h (h -> 3h) when both fit one 64-bit key beside the
+// bitonic sort's chunk and lane fields: ranks + 1 below 2^26.
+constexpr int kTripleBits = 26;
+constexpr int64_t kTripleMaxM = (1ll << kTripleBits) - 2;
 static_assert(kCap <= kPosTile, "a group spans at most two tiles");
 
 struct SaWs {
@@ -229,7 +237,7 @@ __global__ __launch_bounds__(256) void k_sa_init(const int32_t* text,
     if (i == kLen) v = (uint32_t)n;
     if (i == kTokLo) v = (uint32_t)tlo;
     if (i == kTokHi) v = (uint32_t)thi;
-    if (i == kH0) v = pairs ? 2u : 1u;
+    if (i == kH0 || i == kHRound + 1) v = pairs ? 2u : 1u;
     if (i == kGlobalMask) v = 1u;  // round 0 is a radix round
     state[i] = v;
   }
@@ -606,7 +614,7 @@ __global__ __launch_bounds__(NT) void k_pos_gather(
   constexpr int kSpan = kTile / NW;
   constexpr int kSteps = kSpan / kWave;
   if (radix_idle(state, round)) return;
-  const int64_t h = (int64_t)state[kH0] << (round - 1);
+  const int64_t h = state[kHRound + round];
   const int64_t base = (int64_t)blockIdx.x * kTile;
   __shared__ uint32_t scnt[NW];
   __shared__ uint32_t ored[NW];
@@ -691,20 +699,29 @@ __device__ __forceinline__ uint32_t lane_next(uint32_t v) {
                                                0xf, false);
 }
 
+__device__ __forceinline__ uint64_t lane_prev64(uint64_t v) {
+  return ((uint64_t)lane_prev((uint32_t)(v >> 32)) << 32) |
+         lane_prev((uint32_t)v);
+}
+__device__ __forceinline__ uint64_t lane_next64(uint64_t v) {
+  return ((uint64_t)lane_next((uint32_t)(v >> 32)) << 32) |
+         lane_next((uint32_t)v);
+}
+
 __device__ __forceinline__ uint64_t lanes_le(int ln) {
   return ln == kWave - 1 ? ~0ull : (2ull << ln) - 1;
 }
 
 // Entries of c[0 .. len) (ascending, len <= 64) below key, or at most key
 // when `incl`.
-__device__ __forceinline__ int count_below(const uint32_t* c, int len,
-                                           uint32_t key, bool incl) {
+__device__ __forceinline__ int count_below(const uint64_t* c, int len,
+                                           uint64_t key, bool incl) {
   int at = 0;
 #pragma unroll
   for (int step = kWave; step >= 1; step >>= 1) {
     const int q = at + step;
     if (q <= len) {
-      const uint32_t v = c[q - 1];
+      const uint64_t v = c[q - 1];
       if (incl ? v <= key : v < key) at = q;
     }
   }
@@ -764,10 +781,17 @@ __global__ __launch_bounds__(NT) void k_sa_local(
   // a resumed round clears its stall mark before its radix launches
   if (stalled != 0 && blockIdx.x == 0 && threadIdx.x == 0)
     state[kStalled] = 0;
-  __shared__ uint32_t sk[kSlots];  // sorted keys, chunk by chunk
+  const int64_t h = state[kHRound + round];
+  // Every group fits this launch: sort by (rank[i + h], rank[i + 2h]) and
+  // the round triples h; a round with a radix part doubles it.
+  const bool triple = mg <= (uint32_t)kCap && m <= kTripleMaxM;
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    const int64_t hn = triple ? 3 * h : 2 * h;
+    state[kHRound + round + 1] = (uint32_t)(hn < 0x7fffffff ? hn : 0x7fffffff);
+  }
+  __shared__ uint64_t sk[kSlots];  // sorted keys, chunk by chunk
   __shared__ uint32_t gmax[NW];
   __shared__ uint32_t skip_out;
-  const int64_t h = (int64_t)state[kH0] << (round - 1);
   const int64_t b = blockIdx.x;
   const int64_t ts = b * kPosTile;
   const int64_t te = min(ts + (int64_t)kPosTile, m);
@@ -785,7 +809,8 @@ __global__ __launch_bounds__(NT) void k_sa_local(
   // The first `skip` positions belong to a group the tile before owns
   // (its workgroup rewrites them meanwhile): they are not read as ours.
   const int skip = (int)skip_cur[b];
-  uint32_t g[kW], iv[kW], sz[kW], kv[kW];
+  uint32_t g[kW], iv[kW], sz[kW];
+  uint64_t kv[kW];
 #pragma unroll
   for (int k = 0; k < kW; ++k) {
     const int slot = (wv + k * NW) * kWave + ln;
@@ -808,7 +833,14 @@ __global__ __launch_bounds__(NT) void k_sa_local(
     // owned: a group whose head lies in the tile
     if (g[k] < kJustFinished && g[k] >= (uint32_t)ts && g[k] < (uint32_t)te) {
       sz[k] = gsz[g[k]];
-      if ((int64_t)iv[k] + h < m) kv[k] = rank_cur[iv[k] + h] + 1;
+      const int64_t i1 = (int64_t)iv[k] + h;
+      uint64_t k2 = i1 < m ? (uint64_t)rank_cur[i1] + 1 : 0;
+      if (triple) {
+        const int64_t i2 = i1 + h;
+        const uint64_t k3 = i2 < m ? (uint64_t)rank_cur[i2] + 1 : 0;
+        k2 = (k2 << kTripleBits) | k3;
+      }
+      kv[k] = k2;
     } else {
       g[k] = kFinished;
     }
@@ -836,22 +868,23 @@ __global__ __launch_bounds__(NT) void k_sa_local(
     const int c0 = kWave - 1 - __builtin_clzll(le);
     const uint64_t after = starts & ~lanes_le(ln);
     const int c1 = after ? __builtin_ctzll(after) : kWave;
-    uint32_t ke = act ? kv[k] : 0u;
+    uint64_t ke = act ? kv[k] : 0ull;
     int from = ln;  // the lane this lane's element came from
     // Most groups keep their order (keys equal or already ascending):
     // the sort runs only for a window with a descent inside a chunk.
-    const uint32_t kin = lane_prev(ke);
+    // (chunk index: 6 bits, key: at most 52, lane: 6)
+    const uint64_t kin = lane_prev64(ke);
     if (ballot(ln > c0 && kin > ke)) {
-      const uint64_t key64 = ((uint64_t)(popc(le) - 1) << 37) |
-                             ((uint64_t)ke << 6) | (uint64_t)ln;
+      const uint64_t key64 = ((uint64_t)(popc(le) - 1) << 58) | (ke << 6) |
+                             (uint64_t)ln;
       const uint64_t sorted = wave_sort_u64(key64);
-      ke = (uint32_t)(sorted >> 6) & 0x7fffffffu;
+      ke = (sorted >> 6) & ((1ull << 52) - 1);
       from = (int)(sorted & (kWave - 1));
       iv[k] = (uint32_t)__shfl((int)iv[k], from);
     }
     sk[base + ln] = ke;
-    const uint32_t kprev = lane_prev(ke);
-    const uint32_t knext = lane_next(ke);
+    const uint64_t kprev = lane_prev64(ke);
+    const uint64_t knext = lane_next64(ke);
     const bool eqprev = ln > c0 && kprev == ke;
     const bool eqnext = ln + 1 < c1 && knext == ke;
     const uint64_t rs = ballot(!eqprev) & lanes_le(ln);
@@ -874,7 +907,7 @@ __global__ __launch_bounds__(NT) void k_sa_local(
     const uint32_t osz = gs[k] >> 16;  // the old group's size
     const uint32_t oh = (uint32_t)(ts + g0);  // and head
     const int g1 = min(g0 + (int)osz, n);
-    const uint32_t ke = sk[base + ln];
+    const uint64_t ke = sk[base + ln];
     int stable = (int)(own[k] & 0xff);
     int lt = (int)((own[k] >> 8) & 0xff);
     int leq = (int)((own[k] >> 16) & 0xff);
@@ -883,7 +916,7 @@ __global__ __launch_bounds__(NT) void k_sa_local(
       if (w2 == w) continue;
       const int a0 = max(g0, w2 * kWave);
       const int len = min(g1, w2 * kWave + kWave) - a0;
-      const uint32_t lo_k = sk[a0], hi_k = sk[a0 + len - 1];
+      const uint64_t lo_k = sk[a0], hi_k = sk[a0 + len - 1];
       int l2, e2;
       if (ke < lo_k) {
         l2 = e2 = 0;
