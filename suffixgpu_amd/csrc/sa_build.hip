@@ -216,9 +216,12 @@ __global__ __launch_bounds__(256) void k_sa_range(const int32_t* text,
 // past the end; pair keys need span + 2 < 2^kPairBits.
 constexpr int kPairBits = 18;
 
+// vb > 0: the key carries the position in its low vb bits (no value or
+// position arrays); 0: key, value and position arrays.
 __global__ __launch_bounds__(256) void k_sa_init(const int32_t* text,
                                                  int64_t n, uint64_t* key,
                                                  uint32_t* val, uint32_t* pos,
+                                                 int vb,
                                                  const int32_t* part_lo,
                                                  const int32_t* part_hi,
                                                  int nparts, uint32_t* skip0,
@@ -247,6 +250,7 @@ __global__ __launch_bounds__(256) void k_sa_init(const int32_t* text,
     skip1[e] = 0;
   }
   if (i >= n) return;
+  uint64_t k;
   if (pairs) {
     auto code = [&](int64_t j) -> uint64_t {
       if (j >= n) return 0;
@@ -254,12 +258,17 @@ __global__ __launch_bounds__(256) void k_sa_init(const int32_t* text,
       return t == INT32_MAX ? (uint64_t)span + 1
                             : (uint64_t)((int64_t)t - tlo + 1);
     };
-    key[i] = (code(i) << kPairBits) | code(i + 1);
+    k = (code(i) << kPairBits) | code(i + 1);
   } else {
-    key[i] = (uint64_t)((uint32_t)text[i] ^ 0x80000000u);
+    k = (uint64_t)((uint32_t)text[i] ^ 0x80000000u);
   }
-  val[i] = (uint32_t)i;
-  pos[i] = (uint32_t)i;
+  if (vb > 0) {
+    key[i] = (k << vb) | (uint64_t)i;
+  } else {
+    key[i] = k;
+    val[i] = (uint32_t)i;
+    pos[i] = (uint32_t)i;
+  }
 }
 
 // Lanes of the wave holding the same digit as the calling lane.
@@ -362,7 +371,7 @@ __global__ __launch_bounds__(NT) void k_rs_rowscan(
 // offset, and then each wave places its elements step by step with a
 // nine-ballot digit match, advancing only its own offsets: three barriers
 // per tile.
-template <int NT>
+template <int NT, bool kVal = true>
 __global__ __launch_bounds__(NT) void k_rs_scatter(
     const uint64_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint64_t* __restrict__ kout, uint32_t* __restrict__ vout, int sh,
@@ -389,7 +398,7 @@ __global__ __launch_bounds__(NT) void k_rs_scatter(
   for (int s = 0; s < kSteps; ++s) {
     const int64_t idx = wbase + s * kWave + ln;
     k[s] = idx < A ? kin[idx] : 0;
-    v[s] = idx < A ? vin[idx] : 0;
+    v[s] = kVal && idx < A ? vin[idx] : 0;
   }
   for (int e = tid; e < NW * kRadix; e += NT) (&woff[0][0])[e] = 0;
   // Digit d's first output slot: the totals of the digits below it.
@@ -426,7 +435,7 @@ __global__ __launch_bounds__(NT) void k_rs_scatter(
     if (act) {
       const uint32_t p = woff[wv][d] + (uint32_t)rk;
       kout[p] = k[s];
-      vout[p] = v[s];
+      if (kVal) vout[p] = v[s];
     }
     wave_lds_sync();  // every lane has read its offset
     if (act && rk == 0) woff[wv][d] += (uint32_t)popc(peers[s]);
@@ -439,16 +448,18 @@ __global__ __launch_bounds__(NT) void k_rs_scatter(
 // from slot t-1's; the group's head is pos[start] (pos ascends with t, so
 // the head of slot t is the largest start position at or before t).  Wave
 // w of a tile owns slots base + w*1024 .. +1024, 64 consecutive per step.
+// vb > 0 (the token round's packed keys): the key above its low vb bits is
+// the sort key, the low bits the value, and pos[t] = t.
 
 __device__ __forceinline__ bool starts_group(const uint64_t* key, int64_t t,
-                                             uint64_t kt) {
-  return t == 0 || key[t - 1] != kt;
+                                             uint64_t kt, int vb) {
+  return t == 0 || (key[t - 1] >> vb) != kt;
 }
 
 template <int NT>
 __global__ __launch_bounds__(NT) void k_grp_reduce(
     const uint64_t* __restrict__ key, const uint32_t* __restrict__ pos,
-    uint32_t* blkmax, const uint32_t* state, int round) {
+    int vb, uint32_t* blkmax, const uint32_t* state, int round) {
   constexpr int NW = NT / kWave;
   constexpr int kSpan = kTile / NW;
   if (radix_idle(state, round)) return;
@@ -464,8 +475,9 @@ __global__ __launch_bounds__(NT) void k_grp_reduce(
   for (int s = 0; s < kSpan / kWave; ++s) {
     const int64_t t = wbase + s * kWave + ln;
     if (t < A) {
-      const uint64_t kt = key[t];
-      if (starts_group(key, t, kt)) mx = max(mx, pos[t]);
+      const uint64_t kt = key[t] >> vb;
+      if (starts_group(key, t, kt, vb))
+        mx = max(mx, vb ? (uint32_t)t : pos[t]);
     }
   }
   mx = (uint32_t)wave_max_i32((int)mx);
@@ -490,7 +502,8 @@ __global__ __launch_bounds__(NT) void k_grp_reduce(
 template <int NT>
 __global__ __launch_bounds__(NT) void k_grp_rank(
     const uint64_t* __restrict__ key, const uint32_t* __restrict__ val,
-    const uint32_t* __restrict__ pos, const uint32_t* __restrict__ blkmax,
+    const uint32_t* __restrict__ pos, int vb,
+    const uint32_t* __restrict__ blkmax,
     uint32_t* __restrict__ rank_next, uint32_t* __restrict__ sa,
     uint32_t* __restrict__ gp, uint32_t* __restrict__ gsz,
     uint32_t* __restrict__ skip_next, uint32_t* state, int round) {
@@ -522,10 +535,10 @@ __global__ __launch_bounds__(NT) void k_grp_rank(
     const int64_t t = wbase + s * kWave + ln;
     st[s] = 0;
     if (t < A) {
-      const uint64_t kt = key[t];
-      const bool first = starts_group(key, t, kt);
-      const bool last = t + 1 == A || key[t + 1] != kt;
-      if (first) st[s] = pos[t];
+      const uint64_t kt = key[t] >> vb;
+      const bool first = starts_group(key, t, kt, vb);
+      const bool last = t + 1 == A || (key[t + 1] >> vb) != kt;
+      if (first) st[s] = vb ? (uint32_t)t : pos[t];
       single |= (uint32_t)(first && last) << s;
       lastb |= (uint32_t)last << s;
     }
@@ -545,8 +558,9 @@ __global__ __launch_bounds__(NT) void k_grp_rank(
     run = max(run, (uint32_t)__builtin_amdgcn_readlane((int)head, kWave - 1));
     const bool fin = (single >> s) & 1u;
     if (t < A) {
-      const uint32_t i = val[t];
-      const uint32_t p = pos[t];
+      const uint32_t i =
+          vb ? (uint32_t)(key[t] & ((1ull << vb) - 1)) : val[t];
+      const uint32_t p = vb ? (uint32_t)t : pos[t];
       rank_next[i] = head;
       sa[p] = i;
       gp[p] = fin ? kJustFinished : head;
@@ -1024,34 +1038,50 @@ static int round_bits(int64_t m) {
   return bits_for((uint64_t)(m - 1) * (uint64_t)(m + 1) + (uint64_t)m);
 }
 
+// Low bits of the token round's keys that hold the position (0: the
+// round keeps separate value and position arrays): the 36-bit token key
+// sits above them when both fit 64 bits.
+static int token_round_vb(int64_t m) {
+  const int vb = bits_for((uint64_t)(m > 1 ? m - 1 : 1));
+  return 2 * kPairBits + vb <= 64 ? vb : 0;
+}
+
 // LSD radix sort of round r's list (written to keyA / valA) by the low
-// `nbits` bits of its keys, then the group heads of the sorted order.
+// `nbits` bits of its keys (above the vb value bits of the token round's
+// packed keys), then the group heads of the sorted order.
 static int sort_and_rank(SaWs& w, int64_t nb, int64_t m, int round,
                          hipStream_t stream) {
+  const int vb = round == 0 ? token_round_vb(m) : 0;
   const int nbits = round == 0 ? 2 * kPairBits : round_bits(m);
   uint64_t* keys[2] = {w.keyA, w.keyB};
   uint32_t* vals[2] = {w.valA, w.valB};
   int x = 0;
-  for (int sh = 0; sh < nbits; sh += kDigitBits) {
+  for (int sh = vb; sh < vb + nbits; sh += kDigitBits) {
     hipLaunchKernelGGL(k_rs_hist<kRsThreads>, dim3((unsigned)nb),
                        dim3(kRsThreads), 0, stream, keys[x], sh, w.hist, nb,
                        w.state, round);
     hipLaunchKernelGGL(k_rs_rowscan<kRsThreads>, dim3(kRadix),
                        dim3(kRsThreads), 0, stream, w.hist, nb, w.rowsum,
                        w.state, round);
-    hipLaunchKernelGGL(k_rs_scatter<kRsThreads>, dim3((unsigned)nb),
-                       dim3(kRsThreads), 0, stream, keys[x], vals[x],
-                       keys[x ^ 1], vals[x ^ 1], sh, w.hist, nb, w.rowsum,
-                       w.state, round);
+    if (vb)
+      hipLaunchKernelGGL((k_rs_scatter<kRsThreads, false>),
+                         dim3((unsigned)nb), dim3(kRsThreads), 0, stream,
+                         keys[x], nullptr, keys[x ^ 1], nullptr, sh, w.hist,
+                         nb, w.rowsum, w.state, round);
+    else
+      hipLaunchKernelGGL(k_rs_scatter<kRsThreads>, dim3((unsigned)nb),
+                         dim3(kRsThreads), 0, stream, keys[x], vals[x],
+                         keys[x ^ 1], vals[x ^ 1], sh, w.hist, nb, w.rowsum,
+                         w.state, round);
     x ^= 1;
   }
   const int nx = (round + 1) & 1;
   hipLaunchKernelGGL(k_grp_reduce<kRsThreads>, dim3((unsigned)nb),
-                     dim3(kRsThreads), 0, stream, keys[x], w.pos, w.blkmax,
-                     w.state, round);
+                     dim3(kRsThreads), 0, stream, keys[x], w.pos, vb,
+                     w.blkmax, w.state, round);
   hipLaunchKernelGGL(k_grp_rank<kRsThreads>, dim3((unsigned)nb),
                      dim3(kRsThreads), 0, stream, keys[x], vals[x], w.pos,
-                     w.blkmax, w.rank[nx], w.sa, w.gp, w.gsz, w.skip[nx],
+                     vb, w.blkmax, w.rank[nx], w.sa, w.gp, w.gsz, w.skip[nx],
                      w.state, round);
   return (int)hipGetLastError();
 }
@@ -1245,7 +1275,8 @@ int build_begin(const int32_t* text, int64_t m, void* workspace,
   hipLaunchKernelGGL(k_sa_range, dim3((unsigned)parts), dim3(256), 0, stream,
                      text, m, plo, phi);
   hipLaunchKernelGGL(k_sa_init, dim3(eb), dim3(256), 0, stream, text, m,
-                     w.keyA, w.valA, w.pos, plo, phi, parts, w.skip[0],
+                     w.keyA, w.valA, w.pos, token_round_vb(m), plo, phi,
+                     parts, w.skip[0],
                      w.skip[1], (m + kPosTile - 1) / kPosTile, w.state);
   return sort_and_rank(w, nb, m, 0, stream);
 }
