@@ -776,10 +776,36 @@ __global__ __launch_bounds__(NT) void k_sa_local(
   constexpr int NW = NT / kWave;
   constexpr int kW = kSlots / kWave / NW;  // windows per wave
   static_assert(kSlots % (kWave * NW) == 0, "windows per wave");
-  if (state[kDone]) return;
+  static_assert(kPosTile % (kWave * NW) == 0, "tile windows per wave");
+  const int64_t b = blockIdx.x;
+  const int64_t ts = b * kPosTile;
+  const int wv = threadIdx.x / kWave;
+  const int ln = lane_id();
+  // The tile's group marks and suffixes are read before the state and skip
+  // words are known, so all of them share one round trip; the slots the
+  // skip words and the marks exclude are dropped below.  Slot
+  // (wv + k * NW) * 64 + ln lies in the tile for k < kWT.
+  constexpr int kWT = kPosTile / kWave / NW;
+  uint32_t gt[kWT], st[kWT];
+#pragma unroll
+  for (int k = 0; k < kWT; ++k) {
+    const int64_t p = ts + (wv + k * NW) * kWave + ln;
+    gt[k] = p < m ? gp[p] : kFinished;
+    st[k] = p < m ? sa[p] : 0u;
+  }
+  // every word the launch decides on, loaded at once
+  const uint32_t done = state[kDone];
   const uint32_t stalled = state[kStalled];
-  if (stalled != 0 && stalled < (uint32_t)round) return;
   const uint32_t mg = state[kMaxGrp + round];
+  const int64_t h = state[kHRound + round];
+  const int skip = (int)skip_cur[b];
+  const uint32_t sn = b + 1 < nl ? skip_cur[b + 1] : 0u;
+  // (kept together: the compiler would otherwise sink each load to its
+  // first use past the early returns, one round trip each)
+  asm volatile("" ::"s"(done), "s"(stalled), "s"(mg), "s"((uint32_t)h),
+               "s"(skip), "s"(sn));
+  if (done) return;
+  if (stalled != 0 && stalled < (uint32_t)round) return;
   if (mg == 0) {
     if (blockIdx.x == 0 && threadIdx.x == 0) {
       state[kDone] = 1;
@@ -795,7 +821,6 @@ __global__ __launch_bounds__(NT) void k_sa_local(
   // a resumed round clears its stall mark before its radix launches
   if (stalled != 0 && blockIdx.x == 0 && threadIdx.x == 0)
     state[kStalled] = 0;
-  const int64_t h = state[kHRound + round];
   // Every group fits this launch: sort by (rank[i + h], rank[i + 2h]) and
   // the round triples h; a round with a radix part doubles it.
   const bool triple = mg <= (uint32_t)kCap && m <= kTripleMaxM;
@@ -806,34 +831,35 @@ __global__ __launch_bounds__(NT) void k_sa_local(
   __shared__ uint64_t sk[kSlots];  // sorted keys, chunk by chunk
   __shared__ uint32_t gmax[NW];
   __shared__ uint32_t skip_out;
-  const int64_t b = blockIdx.x;
-  const int64_t ts = b * kPosTile;
   const int64_t te = min(ts + (int64_t)kPosTile, m);
   if (threadIdx.x == 0) skip_out = 0;
   // slots cover [ts, ts + n): the tile and the tail of the group that
   // runs on into the next tile (its skip word; a run of kCap or more
   // belongs to a group above kCap, not sorted here)
-  const uint32_t sn = b + 1 < nl ? skip_cur[b + 1] : 0u;
   const uint32_t ext = sn < (uint32_t)kCap ? sn : 0u;
   const int n = (int)(min(m, te + (int64_t)ext) - ts);
-  const int wv = threadIdx.x / kWave;
-  const int ln = lane_id();
 
-  // 1. loads: gp, then sa where unfinished, then the group's size and key
-  // The first `skip` positions belong to a group the tile before owns
-  // (its workgroup rewrites them meanwhile): they are not read as ours.
-  const int skip = (int)skip_cur[b];
+  // 1. loads: gp and sa (the tile's above, the extension's here), then
+  // the group's size and key.  The first `skip` positions belong to a
+  // group the tile before owns (its workgroup rewrites them meanwhile):
+  // what was read of them is dropped.
   uint32_t g[kW], iv[kW], sz[kW];
   uint64_t kv[kW];
 #pragma unroll
   for (int k = 0; k < kW; ++k) {
     const int slot = (wv + k * NW) * kWave + ln;
-    g[k] = slot < n && slot >= skip ? gp[ts + slot] : kFinished;
+    if (k < kWT)
+      g[k] = slot < n && slot >= skip ? gt[k] : kFinished;
+    else
+      g[k] = slot < n && slot >= skip ? gp[ts + slot] : kFinished;
   }
 #pragma unroll
   for (int k = 0; k < kW; ++k) {
     const int slot = (wv + k * NW) * kWave + ln;
-    iv[k] = g[k] != kFinished ? sa[ts + slot] : 0u;
+    if (k < kWT)
+      iv[k] = g[k] != kFinished ? st[k] : 0u;
+    else
+      iv[k] = g[k] != kFinished ? sa[ts + slot] : 0u;
   }
 #pragma unroll
   for (int k = 0; k < kW; ++k) {
