@@ -271,6 +271,10 @@ __global__ __launch_bounds__(256) void k_sa_init(const int32_t* text,
   }
 }
 
+__device__ __forceinline__ uint64_t lanes_le(int ln) {
+  return ln == kWave - 1 ? ~0ull : (2ull << ln) - 1;
+}
+
 // Lanes of the wave holding the same digit as the calling lane.
 __device__ __forceinline__ uint64_t match_digit(bool act, uint32_t d) {
   uint64_t peers = ballot(act);
@@ -585,45 +589,62 @@ __global__ __launch_bounds__(NT) void k_grp_rank(
 
 // ------------------------------------------------------- radix part
 // The suffixes of a round's groups of more than kCap.  k_pos_count: per
-// tile of SA positions, how many lie in such a group (tcnt[]).  It runs
-// after the round's local launch, which changed only groups of at most
-// kCap.
+// tile of SA positions, how many lie in such a group (tcnt[]) and how many
+// of them are a group's head (hcnt[]).  It runs after the round's local
+// launch, which changed only groups of at most kCap.
 __device__ __forceinline__ bool in_big_group(const uint32_t* gsz, uint32_t g) {
   return g < kJustFinished && gsz[g] > (uint32_t)kCap;
+}
+
+// Groups of more than kCap among m suffixes, at most (and at least 1).
+__host__ __device__ inline int64_t big_groups_max(int64_t m) {
+  const int64_t n = m / (kCap + 1);
+  return n > 1 ? n : 1;
 }
 
 template <int NT>
 __global__ __launch_bounds__(NT) void k_pos_count(
     const uint32_t* __restrict__ gp, const uint32_t* __restrict__ gsz,
-    uint32_t* __restrict__ tcnt, int64_t m, const uint32_t* state,
-    int round) {
+    uint32_t* __restrict__ tcnt, uint32_t* __restrict__ hcnt, int64_t m,
+    const uint32_t* state, int round) {
   if (radix_idle(state, round)) return;
   __shared__ uint32_t red[NT / kWave];
   const int64_t base = (int64_t)blockIdx.x * kTile;
-  uint32_t c = 0;
+  uint32_t c = 0, hc = 0;
 #pragma unroll
   for (int s = 0; s < kTile / NT; ++s) {
     const int64_t p = base + s * NT + threadIdx.x;
-    if (p < m) c += in_big_group(gsz, gp[p]);
+    if (p < m) {
+      const uint32_t g = gp[p];
+      const bool big = in_big_group(gsz, g);
+      c += big;
+      hc += big && g == (uint32_t)p;
+    }
   }
-  uint32_t tot;
+  uint32_t tot, htot;
   block_exscan1<NT>(c, red, &tot);
-  if (threadIdx.x == 0) tcnt[blockIdx.x] = tot;
+  block_exscan1<NT>(hc, red, &htot);
+  if (threadIdx.x == 0) {
+    tcnt[blockIdx.x] = tot;
+    hcnt[blockIdx.x] = htot;
+  }
 }
 
 // The round's list: the SA positions of its groups of more than kCap in
-// order, keyed head * (m + 1) + (rank[i + h] + 1, or 0 past the end) with
-// i = sa[p].
-// Each block sums the earlier tiles' counts for its output offset; block 0
-// also sums them all: the list length (state[kLen]).
+// order, keyed q * (m + 1) + (rank[i + h] + 1, or 0 past the end) with
+// i = sa[p] and q the group's ordinal among those groups (its head's: the
+// list is in SA order, so q + 1 counts the heads at or before p; below
+// big_groups_max(m), so the key takes fewer bits than the head would).
+// Each block sums the earlier tiles' counts for its output offset and
+// ordinal base; block 0 also sums them all: the list length (state[kLen]).
 template <int NT>
 __global__ __launch_bounds__(NT) void k_pos_gather(
     const uint32_t* __restrict__ gp, const uint32_t* __restrict__ gsz,
     const uint32_t* __restrict__ sa,
     const uint32_t* __restrict__ rank_cur, const uint32_t* __restrict__ tcnt,
-    int64_t m, int64_t nb, int round, uint64_t* __restrict__ key,
-    uint32_t* __restrict__ val, uint32_t* __restrict__ pos,
-    uint32_t* state) {
+    const uint32_t* __restrict__ hcnt, int64_t m, int64_t nb, int round,
+    uint64_t* __restrict__ key, uint32_t* __restrict__ val,
+    uint32_t* __restrict__ pos, uint32_t* state) {
   constexpr int NW = NT / kWave;
   constexpr int kSpan = kTile / NW;
   constexpr int kSteps = kSpan / kWave;
@@ -631,12 +652,19 @@ __global__ __launch_bounds__(NT) void k_pos_gather(
   const int64_t h = state[kHRound + round];
   const int64_t base = (int64_t)blockIdx.x * kTile;
   __shared__ uint32_t scnt[NW];
+  __shared__ uint32_t shcnt[NW];
   __shared__ uint32_t ored[NW];
+  __shared__ uint32_t hbase;
   {
     const int64_t upto = blockIdx.x == 0 ? nb : (int64_t)blockIdx.x;
-    uint32_t c = 0;
-    for (int64_t t = threadIdx.x; t < upto; t += NT) c += tcnt[t];
-    uint32_t tot;
+    uint32_t c = 0, hc = 0;
+    for (int64_t t = threadIdx.x; t < upto; t += NT) {
+      c += tcnt[t];
+      hc += (int64_t)t < (int64_t)blockIdx.x ? hcnt[t] : 0u;
+    }
+    uint32_t tot, htot;
+    block_exscan1<NT>(hc, ored, &htot);
+    if (threadIdx.x == 0) hbase = htot;
     block_exscan1<NT>(c, ored, &tot);
     if (blockIdx.x == 0) {
       if (threadIdx.x == 0) {
@@ -652,34 +680,46 @@ __global__ __launch_bounds__(NT) void k_pos_gather(
   const int ln = lane_id();
   const int64_t wbase = base + (int64_t)wv * kSpan;
   uint32_t gv[kSteps];
-  uint32_t cnt = 0;
+  uint32_t cnt = 0, hcn = 0;
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
     const int64_t p = wbase + s * kWave + ln;
     gv[s] = p < m ? gp[p] : kFinished;
     if (!in_big_group(gsz, gv[s])) gv[s] = kFinished;
     cnt += (uint32_t)popc(ballot(gv[s] != kFinished));
+    hcn += (uint32_t)popc(ballot(gv[s] == (uint32_t)p));
   }
-  if (ln == 0) scnt[wv] = cnt;
+  if (ln == 0) {
+    scnt[wv] = cnt;
+    shcnt[wv] = hcn;
+  }
   __syncthreads();
   uint32_t out = ored[0];
-  for (int w = 0; w < wv; ++w) out += scnt[w];
+  uint32_t hrun = hbase;
+  for (int w = 0; w < wv; ++w) {
+    out += scnt[w];
+    hrun += shcnt[w];
+  }
   const uint64_t M1 = (uint64_t)m + 1;
 #pragma unroll
   for (int s = 0; s < kSteps; ++s) {
     const int64_t p = wbase + s * kWave + ln;
     const bool a = gv[s] != kFinished;
     const uint64_t bm = ballot(a);
+    const uint64_t hm = ballot(a && gv[s] == (uint32_t)p);
     if (a) {
       const uint32_t o = out + (uint32_t)rank_lt(bm);
+      // heads at or before p in this step, then the group's ordinal
+      const uint32_t q = hrun + (uint32_t)popc(hm & lanes_le(ln)) - 1u;
       const uint32_t i = sa[p];
       const uint64_t k2 =
           (int64_t)i + h < m ? (uint64_t)rank_cur[i + h] + 1 : 0;
-      key[o] = (uint64_t)gv[s] * M1 + k2;
+      key[o] = (uint64_t)q * M1 + k2;
       val[o] = i;
       pos[o] = (uint32_t)p;
     }
     out += (uint32_t)popc(bm);
+    hrun += (uint32_t)popc(hm);
   }
 }
 
@@ -722,9 +762,6 @@ __device__ __forceinline__ uint64_t lane_next64(uint64_t v) {
          lane_next((uint32_t)v);
 }
 
-__device__ __forceinline__ uint64_t lanes_le(int ln) {
-  return ln == kWave - 1 ? ~0ull : (2ull << ln) - 1;
-}
 
 // Entries of c[0 .. len) (ascending, len <= 64) below key, or at most key
 // when `incl`.
@@ -1059,9 +1096,11 @@ static int passes_of(int nbits) {
   return (nbits + kDigitBits - 1) / kDigitBits;
 }
 
-// Key bits of a doubling round: head * (m + 1) + k2 with head < m, k2 <= m.
+// Key bits of a doubling round's radix part: q * (m + 1) + k2 with the
+// group ordinal q < big_groups_max(m), k2 <= m.
 static int round_bits(int64_t m) {
-  return bits_for((uint64_t)(m - 1) * (uint64_t)(m + 1) + (uint64_t)m);
+  return bits_for((uint64_t)(big_groups_max(m) - 1) * (uint64_t)(m + 1) +
+                  (uint64_t)m);
 }
 
 // Low bits of the token round's keys that hold the position (0: the
@@ -1124,13 +1163,14 @@ static int doubling_round(SaWs& w, int64_t nb, int64_t m, int round,
                      w.rank[cur], w.rank[nx], w.skip[cur], w.skip[nx], m, nl,
                      round, global_path, w.state);
   if (!global_path) return (int)hipGetLastError();
+  // (blkmax holds the head counts until the group-head pass needs it)
   hipLaunchKernelGGL(k_pos_count<kRsThreads>, dim3((unsigned)nb),
-                     dim3(kRsThreads), 0, stream, w.gp, w.gsz, w.tcnt, m,
-                     w.state, round);
+                     dim3(kRsThreads), 0, stream, w.gp, w.gsz, w.tcnt,
+                     w.blkmax, m, w.state, round);
   hipLaunchKernelGGL(k_pos_gather<kRsThreads>, dim3((unsigned)nb),
                      dim3(kRsThreads), 0, stream, w.gp, w.gsz, w.sa,
-                     w.rank[cur], w.tcnt, m, nb, round, w.keyA, w.valA,
-                     w.pos, w.state);
+                     w.rank[cur], w.tcnt, w.blkmax, m, nb, round, w.keyA,
+                     w.valA, w.pos, w.state);
   return sort_and_rank(w, nb, m, round, stream);
 }
 
