@@ -163,9 +163,10 @@ __device__ __forceinline__ uint32_t block_exscan1(uint32_t v, uint32_t* red,
   return before + inc - v;
 }
 
-// Block-wide least and largest of one int32 per thread (all threads).
+// Block-wide least and largest of one int32 per thread (all NT threads).
+template <int NT>
 __device__ __forceinline__ void block_minmax(int32_t& lo, int32_t& hi,
-                                             int32_t (*red)[256 / kWave]) {
+                                             int32_t (*red)[NT / kWave]) {
   lo = ~wave_max_i32(~lo);  // ~ reverses the signed order, no overflow
   hi = wave_max_i32(hi);
   const int wv = threadIdx.x / kWave;
@@ -174,19 +175,21 @@ __device__ __forceinline__ void block_minmax(int32_t& lo, int32_t& hi,
     red[1][wv] = hi;
   }
   __syncthreads();
-  for (int w = 0; w < 256 / kWave; ++w) {
+  for (int w = 0; w < NT / kWave; ++w) {
     lo = red[0][w] < lo ? red[0][w] : lo;
     hi = red[1][w] > hi ? red[1][w] : hi;
   }
 }
 
 // Least and largest token of the text, PAD (INT32_MAX) left out, per
-// block (part_lo / part_hi, gridDim.x <= 256 entries each).
-__global__ __launch_bounds__(256) void k_sa_range(const int32_t* text,
-                                                  int64_t n,
-                                                  int32_t* part_lo,
-                                                  int32_t* part_hi) {
-  __shared__ int32_t red[2][256 / kWave];
+// block (part_lo / part_hi, gridDim.x <= kInitParts entries each).
+constexpr int kRangeThreads = 1024;
+constexpr int kInitThreads = 1024;
+constexpr int kInitParts = 256;  // partials k_sa_init reduces
+
+__global__ __launch_bounds__(kRangeThreads) void k_sa_range(
+    const int32_t* text, int64_t n, int32_t* part_lo, int32_t* part_hi) {
+  __shared__ int32_t red[2][kRangeThreads / kWave];
   constexpr int kUnroll = 8;
   int32_t lo = INT32_MAX, hi = INT32_MIN;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -205,11 +208,15 @@ __global__ __launch_bounds__(256) void k_sa_range(const int32_t* text,
         hi = t[u] > hi ? t[u] : hi;
       }
   }
-  block_minmax(lo, hi, red);
+  block_minmax<kRangeThreads>(lo, hi, red);
   if (threadIdx.x == 0) {
     part_lo[blockIdx.x] = lo;
     part_hi[blockIdx.x] = hi;
   }
+}
+
+__device__ __forceinline__ uint32_t digit_of(uint64_t k, int sh) {
+  return (uint32_t)(k >> sh) & (kRadix - 1u);
 }
 
 // Tokens of the pair keys: 1 + t - least, PAD after every other token, 0
@@ -217,57 +224,92 @@ __global__ __launch_bounds__(256) void k_sa_range(const int32_t* text,
 constexpr int kPairBits = 18;
 
 // vb > 0: the key carries the position in its low vb bits (no value or
-// position arrays); 0: key, value and position arrays.
-__global__ __launch_bounds__(256) void k_sa_init(const int32_t* text,
-                                                 int64_t n, uint64_t* key,
-                                                 uint32_t* val, uint32_t* pos,
-                                                 int vb,
-                                                 const int32_t* part_lo,
-                                                 const int32_t* part_hi,
-                                                 int nparts, uint32_t* skip0,
-                                                 uint32_t* skip1, int64_t nl,
-                                                 uint32_t* state) {
-  __shared__ int32_t red[2][256 / kWave];
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+// position arrays); 0: key, value and position arrays.  Each thread keys
+// kInitItems consecutive positions, so a block keys one radix tile, and
+// the block also writes that tile's digit counts for the first radix pass
+// (digit at bit vb) to hist[d * nb + tile].
+constexpr int kInitItems = 4;
+static_assert(kInitThreads * kInitItems == kTile, "a block per radix tile");
+
+__global__ __launch_bounds__(kInitThreads) void k_sa_init(
+    const int32_t* text, int64_t n, uint64_t* key, uint32_t* val,
+    uint32_t* pos, int vb, const int32_t* part_lo, const int32_t* part_hi,
+    int nparts, uint32_t* skip0, uint32_t* skip1, int64_t nl,
+    uint32_t* hist, int64_t nb, uint32_t* state) {
+  __shared__ int32_t red[2][kInitThreads / kWave];
+  __shared__ uint32_t hcnt[kRadix];
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (int d = threadIdx.x; d < kRadix; d += kInitThreads) hcnt[d] = 0;
   int32_t tlo = (int)threadIdx.x < nparts ? part_lo[threadIdx.x] : INT32_MAX;
   int32_t thi = (int)threadIdx.x < nparts ? part_hi[threadIdx.x] : INT32_MIN;
-  block_minmax(tlo, thi, red);
+  block_minmax<kInitThreads>(tlo, thi, red);
   // thi < tlo: the text is all PAD
   const int64_t span = thi < tlo ? 0 : (int64_t)thi - (int64_t)tlo + 1;
   const bool pairs = span + 2 < ((int64_t)1 << kPairBits);
-  if (i < kStateWords) {
+  if (tid < kStateWords) {
     uint32_t v = 0;
-    if (i == kLen) v = (uint32_t)n;
-    if (i == kTokLo) v = (uint32_t)tlo;
-    if (i == kTokHi) v = (uint32_t)thi;
-    if (i == kH0 || i == kHRound + 1) v = pairs ? 2u : 1u;
-    if (i == kGlobalMask) v = 1u;  // round 0 is a radix round
-    state[i] = v;
+    if (tid == kLen) v = (uint32_t)n;
+    if (tid == kTokLo) v = (uint32_t)tlo;
+    if (tid == kTokHi) v = (uint32_t)thi;
+    if (tid == kH0 || tid == kHRound + 1) v = pairs ? 2u : 1u;
+    if (tid == kGlobalMask) v = 1u;  // round 0 is a radix round
+    state[tid] = v;
   }
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t e = i; e <= nl; e += stride) {
+  for (int64_t e = tid; e <= nl; e += stride) {
     skip0[e] = 0;
     skip1[e] = 0;
   }
-  if (i >= n) return;
-  uint64_t k;
-  if (pairs) {
-    auto code = [&](int64_t j) -> uint64_t {
-      if (j >= n) return 0;
-      const int32_t t = text[j];
-      return t == INT32_MAX ? (uint64_t)span + 1
-                            : (uint64_t)((int64_t)t - tlo + 1);
-    };
-    k = (code(i) << kPairBits) | code(i + 1);
-  } else {
-    k = (uint64_t)((uint32_t)text[i] ^ 0x80000000u);
+  // Every thread passes both barriers below (a thread past n keys
+  // nothing): a barrier in divergent code would pair up wrongly.
+  const int64_t i0 = tid * kInitItems;
+  // tokens i0 .. i0 + kInitItems (the last one: the pair partner)
+  int32_t t[kInitItems + 1];
+#pragma unroll
+  for (int j = 0; j <= kInitItems; ++j)
+    t[j] = i0 + j < n ? text[i0 + j] : 0;
+  auto code = [&](int j) -> uint64_t {
+    if (i0 + j >= n) return 0;
+    return t[j] == INT32_MAX ? (uint64_t)span + 1
+                             : (uint64_t)((int64_t)t[j] - tlo + 1);
+  };
+  uint64_t k[kInitItems];
+#pragma unroll
+  for (int j = 0; j < kInitItems; ++j) {
+    k[j] = pairs ? (code(j) << kPairBits) | code(j + 1)
+                 : (uint64_t)((uint32_t)t[j] ^ 0x80000000u);
+    if (vb > 0) k[j] = (k[j] << vb) | (uint64_t)(i0 + j);
   }
-  if (vb > 0) {
-    key[i] = (k << vb) | (uint64_t)i;
+  __syncthreads();  // the counters are cleared
+#pragma unroll
+  for (int j = 0; j < kInitItems; ++j)
+    if (i0 + j < n) atomicAdd(&hcnt[digit_of(k[j], vb)], 1u);
+  __syncthreads();
+  if (threadIdx.x < kRadix)
+    hist[(int64_t)threadIdx.x * nb + blockIdx.x] = hcnt[threadIdx.x];
+  if (i0 >= n) return;
+  if (i0 + kInitItems <= n) {
+    // key, val and pos are 256-byte aligned workspace arrays
+    static_assert(kInitItems == 4, "two 16-byte key stores");
+    reinterpret_cast<ulonglong2*>(key + i0)[0] = make_ulonglong2(k[0], k[1]);
+    reinterpret_cast<ulonglong2*>(key + i0)[1] = make_ulonglong2(k[2], k[3]);
+    if (vb == 0) {
+      const uint32_t p = (uint32_t)i0;
+      const uint4 ix = make_uint4(p, p + 1, p + 2, p + 3);
+      *reinterpret_cast<uint4*>(val + i0) = ix;
+      *reinterpret_cast<uint4*>(pos + i0) = ix;
+    }
   } else {
-    key[i] = k;
-    val[i] = (uint32_t)i;
-    pos[i] = (uint32_t)i;
+#pragma unroll
+    for (int j = 0; j < kInitItems; ++j) {
+      if (i0 + j < n) {
+        key[i0 + j] = k[j];
+        if (vb == 0) {
+          val[i0 + j] = (uint32_t)(i0 + j);
+          pos[i0 + j] = (uint32_t)(i0 + j);
+        }
+      }
+    }
   }
 }
 
@@ -287,9 +329,6 @@ __device__ __forceinline__ uint64_t match_digit(bool act, uint32_t d) {
   return peers;
 }
 
-__device__ __forceinline__ uint32_t digit_of(uint64_t k, int sh) {
-  return (uint32_t)(k >> sh) & (kRadix - 1u);
-}
 
 // ---------------------------------------------------------------- radix
 // The passes run NT threads per 4096-element tile.  With about one active
@@ -1081,9 +1120,24 @@ __global__ __launch_bounds__(256) void k_rank_keys4(const int32_t* corpus,
 template <typename T>
 __global__ __launch_bounds__(256) void k_sa_out(const uint32_t* sa, int64_t m,
                                                 int64_t n_total, T* out) {
-  const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (j >= n_total) return;
-  out[j] = j < m ? (T)sa[j] : (T)j;
+  // four outputs per thread; sa is a 256-byte aligned workspace array
+  const int64_t j0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (j0 >= n_total) return;
+  uint32_t v[4];
+  if (j0 + 4 <= m) {
+    const uint4 q = *reinterpret_cast<const uint4*>(sa + j0);
+    v[0] = q.x;
+    v[1] = q.y;
+    v[2] = q.z;
+    v[3] = q.w;
+  } else {
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      v[u] = j0 + u < m ? sa[j0 + u] : (uint32_t)(j0 + u);
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u)
+    if (j0 + u < n_total) out[j0 + u] = (T)v[u];
 }
 
 static int bits_for(uint64_t maxval) {
@@ -1122,9 +1176,11 @@ static int sort_and_rank(SaWs& w, int64_t nb, int64_t m, int round,
   uint32_t* vals[2] = {w.valA, w.valB};
   int x = 0;
   for (int sh = vb; sh < vb + nbits; sh += kDigitBits) {
-    hipLaunchKernelGGL(k_rs_hist<kRsThreads>, dim3((unsigned)nb),
-                       dim3(kRsThreads), 0, stream, keys[x], sh, w.hist, nb,
-                       w.state, round);
+    // (the token round's first counts come from k_sa_init)
+    if (round > 0 || sh > vb)
+      hipLaunchKernelGGL(k_rs_hist<kRsThreads>, dim3((unsigned)nb),
+                         dim3(kRsThreads), 0, stream, keys[x], sh, w.hist, nb,
+                         w.state, round);
     hipLaunchKernelGGL(k_rs_rowscan<kRsThreads>, dim3(kRadix),
                        dim3(kRsThreads), 0, stream, w.hist, nb, w.rowsum,
                        w.state, round);
@@ -1306,7 +1362,7 @@ namespace {
 
 int launch_out(const uint32_t* sa, int64_t m, int64_t n_total, void* sa_out,
                int32_t sa_is64, hipStream_t stream) {
-  const unsigned out_blocks = (unsigned)((n_total + 255) / 256);
+  const unsigned out_blocks = (unsigned)((n_total + 1023) / 1024);
   if (sa_is64)
     hipLaunchKernelGGL(k_sa_out<int64_t>, dim3(out_blocks), dim3(256), 0,
                        stream, sa, m, n_total, (int64_t*)sa_out);
@@ -1333,17 +1389,19 @@ int build_begin(const int32_t* text, int64_t m, void* workspace,
   SaWs w;
   sa_ws_layout(m, workspace, &w);
   const int64_t nb = (m + kTile - 1) / kTile;
-  const unsigned eb = (unsigned)((m + 255) / 256);
+  const unsigned eb = (unsigned)((m + kInitThreads * kInitItems - 1) /
+                                 (kInitThreads * kInitItems));
   // per-block token ranges in the per-tile arrays, unused until round 1
-  const int parts = (int)(nb < 256 ? nb : 256);
+  const int64_t rb = (m + kRangeThreads * 8 - 1) / (kRangeThreads * 8);
+  const int parts = (int)(rb < kInitParts ? rb : kInitParts);
   int32_t* plo = reinterpret_cast<int32_t*>(w.tcnt);
   int32_t* phi = reinterpret_cast<int32_t*>(w.blkmax);
-  hipLaunchKernelGGL(k_sa_range, dim3((unsigned)parts), dim3(256), 0, stream,
-                     text, m, plo, phi);
-  hipLaunchKernelGGL(k_sa_init, dim3(eb), dim3(256), 0, stream, text, m,
-                     w.keyA, w.valA, w.pos, token_round_vb(m), plo, phi,
-                     parts, w.skip[0],
-                     w.skip[1], (m + kPosTile - 1) / kPosTile, w.state);
+  hipLaunchKernelGGL(k_sa_range, dim3((unsigned)parts), dim3(kRangeThreads),
+                     0, stream, text, m, plo, phi);
+  hipLaunchKernelGGL(k_sa_init, dim3(eb), dim3(kInitThreads), 0, stream, text,
+                     m, w.keyA, w.valA, w.pos, token_round_vb(m), plo, phi,
+                     parts, w.skip[0], w.skip[1], (m + kPosTile - 1) / kPosTile,
+                     w.hist, nb, w.state);
   return sort_and_rank(w, nb, m, 0, stream);
 }
 
