@@ -410,10 +410,12 @@ __global__ __launch_bounds__(NT) void k_rs_rowscan(
 // Stable scatter of one tile.  Wave w owns the tile's contiguous span
 // base + w * kTile / NW .. + kTile / NW, 64 consecutive elements per step,
 // so the element order is (wave, step, lane).  The waves first count their
-// digits (LDS atomics), one scan gives every (wave, digit) its output
-// offset, and then each wave places its elements step by step with a
-// nine-ballot digit match, advancing only its own offsets: three barriers
-// per tile.
+// digits (LDS atomics); one scan over the digits gives each digit's first
+// slot in the tile and each (wave, digit) its slot, and each wave places
+// its elements into LDS step by step (a nine-ballot digit match) in digit
+// order.  The tile is then written out from LDS by consecutive threads, so
+// each store instruction writes the runs of a few digits contiguously
+// instead of up to 64 scattered words.  Four barriers per tile.
 template <int NT, bool kVal = true>
 __global__ __launch_bounds__(NT) void k_rs_scatter(
     const uint64_t* __restrict__ kin, const uint32_t* __restrict__ vin,
@@ -429,11 +431,15 @@ __global__ __launch_bounds__(NT) void k_rs_scatter(
   const int64_t base = (int64_t)blockIdx.x * kTile;
   if (base >= A) return;
   __shared__ uint32_t woff[NW][kRadix];
+  __shared__ uint32_t gdelta[kRadix];  // global slot - tile slot, per digit
+  __shared__ uint64_t sk[kTile];
+  __shared__ uint32_t sv[kVal ? kTile : 1];
   __shared__ uint32_t red[NW];
   const int tid = threadIdx.x;
   const int wv = tid / kWave;
   const int ln = lane_id();
   const int64_t wbase = base + (int64_t)wv * kSpan;
+  const int nvalid = (int)(A - base < kTile ? A - base : kTile);
   uint64_t k[kSteps];
   uint32_t v[kSteps];
   uint64_t peers[kSteps];  // lanes of the same step holding the same digit
@@ -460,8 +466,17 @@ __global__ __launch_bounds__(NT) void k_rs_scatter(
       atomicAdd(&woff[wv][d], (uint32_t)popc(peers[s]));
   }
   __syncthreads();
+  // thread d: the tile's count of digit d, then its first tile slot
+  uint32_t cnt = 0;
   if (tid < kRadix) {
-    uint32_t run = dbase + hist[(int64_t)tid * nb + blockIdx.x];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) cnt += woff[w][tid];
+  }
+  uint32_t ttot;
+  const uint32_t ls = block_exscan1<NT>(cnt, red, &ttot);
+  if (tid < kRadix) {
+    gdelta[tid] = dbase + hist[(int64_t)tid * nb + blockIdx.x] - ls;
+    uint32_t run = ls;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
       const uint32_t c = woff[w][tid];
@@ -477,12 +492,23 @@ __global__ __launch_bounds__(NT) void k_rs_scatter(
     const int rk = rank_lt(peers[s]);
     if (act) {
       const uint32_t p = woff[wv][d] + (uint32_t)rk;
-      kout[p] = k[s];
-      if (kVal) vout[p] = v[s];
+      sk[p] = k[s];
+      if (kVal) sv[p] = v[s];
     }
     wave_lds_sync();  // every lane has read its offset
     if (act && rk == 0) woff[wv][d] += (uint32_t)popc(peers[s]);
     wave_lds_sync();
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kTile / NT; ++i) {
+    const int j = tid + i * NT;
+    if (j < nvalid) {
+      const uint64_t kk = sk[j];
+      const uint32_t p = gdelta[digit_of(kk, sh)] + (uint32_t)j;
+      kout[p] = kk;
+      if (kVal) vout[p] = sv[j];
+    }
   }
 }
 
