@@ -67,6 +67,10 @@ constexpr int kDone = 0, kLen = 1, kFoundNone = 2, kTokLo = 3, kTokHi = 4,
               kH0 = 5, kStalled = 7, kGlobalMask = 8, kMaxGrp = 16,
               kHRound = 64;
 constexpr int kStateWords = 128;
+// Group sizes above this are recorded per local tile (tmax) to order the
+// next round's tiles; kOrderClasses size classes (see k_sa_order).
+constexpr uint32_t kOrderMin = 32;
+constexpr int kOrderClasses = 33;
 static_assert(kMaxGrp + 33 <= kHRound, "a round word per doubling");
 static_assert(kHRound + 33 <= kStateWords, "an h word per doubling");
 // A round whose groups all fit the local part sorts them by the ranks at
@@ -93,6 +97,11 @@ struct SaWs {
   uint32_t* blkmax;   // [NB] last group start per tile
   uint32_t* skip[2];  // [NL + 1] leading positions of a local tile owned
                       // by the tile before; round r reads skip[r & 1]
+  uint32_t* tmax[2];  // [NL + 1] largest group (above kOrderMin) headed in
+                      // a local tile, as the token round's and the radix
+                      // parts' group-head passes record them; round r's
+                      // tile order reads tmax[r & 1]
+  uint32_t* order;    // [NL] the local tiles, largest groups first
   uint32_t* state;    // the state[] words above
 };
 
@@ -124,6 +133,9 @@ static size_t sa_ws_layout(int64_t n, void* base, SaWs* w) {
   s.blkmax = (uint32_t*)take(NB * 4);
   s.skip[0] = (uint32_t*)take((NL + 1) * 4);
   s.skip[1] = (uint32_t*)take((NL + 1) * 4);
+  s.tmax[0] = (uint32_t*)take((NL + 1) * 4);
+  s.tmax[1] = (uint32_t*)take((NL + 1) * 4);
+  s.order = (uint32_t*)take(NL * 4);
   s.state = (uint32_t*)take(kStateWords * 4);
   if (w) *w = s;
   return off;
@@ -234,8 +246,9 @@ static_assert(kInitThreads * kInitItems == kTile, "a block per radix tile");
 __global__ __launch_bounds__(kInitThreads) void k_sa_init(
     const int32_t* text, int64_t n, uint64_t* key, uint32_t* val,
     uint32_t* pos, int vb, const int32_t* part_lo, const int32_t* part_hi,
-    int nparts, uint32_t* skip0, uint32_t* skip1, int64_t nl,
-    uint32_t* hist, int64_t nb, uint32_t* state) {
+    int nparts, uint32_t* skip0, uint32_t* skip1, uint32_t* tmax0,
+    uint32_t* tmax1, int64_t nl, uint32_t* hist, int64_t nb,
+    uint32_t* state) {
   __shared__ int32_t red[2][kInitThreads / kWave];
   __shared__ uint32_t hcnt[kRadix];
   const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -259,6 +272,8 @@ __global__ __launch_bounds__(kInitThreads) void k_sa_init(
   for (int64_t e = tid; e <= nl; e += stride) {
     skip0[e] = 0;
     skip1[e] = 0;
+    tmax0[e] = 0;
+    tmax1[e] = 0;
   }
   // Every thread passes both barriers below (a thread past n keys
   // nothing): a barrier in divergent code would pair up wrongly.
@@ -575,7 +590,8 @@ __global__ __launch_bounds__(NT) void k_grp_rank(
     const uint32_t* __restrict__ blkmax,
     uint32_t* __restrict__ rank_next, uint32_t* __restrict__ sa,
     uint32_t* __restrict__ gp, uint32_t* __restrict__ gsz,
-    uint32_t* __restrict__ skip_next, uint32_t* state, int round) {
+    uint32_t* __restrict__ skip_next, uint32_t* __restrict__ tmax_next,
+    uint32_t* state, int round) {
   constexpr int NW = NT / kWave;
   constexpr int kSpan = kTile / NW;
   constexpr int kSteps = kSpan / kWave;
@@ -639,6 +655,7 @@ __global__ __launch_bounds__(NT) void k_grp_rank(
         big = max(big, size);
         const uint32_t c = p / kPosTile;
         if (head / kPosTile < c) skip_next[c] = p + 1 - c * kPosTile;
+        if (size > kOrderMin) atomicMax(&tmax_next[head / kPosTile], size);
       }
     }
   }
@@ -788,6 +805,62 @@ __global__ __launch_bounds__(NT) void k_pos_gather(
   }
 }
 
+// ------------------------------------------------------------ tile order
+// A local round's workgroups take its tiles largest group first: a tile
+// with a group of hundreds of suffixes takes several times as long as one
+// of small groups, and when the large ones start last they set the
+// round's end.  order[] lists the tiles by the size class of their
+// largest group (tmax, recorded by the previous round for groups above
+// kOrderMin), largest first; within a class in any order (every tile's
+// result is the same whichever workgroup takes it and when).  Only rounds
+// with a radix part are ordered: the groups above the cap that make the
+// radix part are recorded by the group-head pass of the round before (the
+// token round for round 1), and the order kernel clears the other tmax
+// buffer for this round's radix part.
+
+__device__ __forceinline__ int order_class(uint32_t t) {
+  // 0 for tmax <= kOrderMin, else 1 + floor(log2(t)) - 5
+  return t <= kOrderMin ? 0 : 32 - __builtin_clz(t) - 5;
+}
+
+// Workgroups are handed to the 8 XCDs in turn (workgroup b to XCD b % 8),
+// and a tile stays with its XCD from round to round when workgroup b takes
+// tile b, so the XCD's L2 still holds what the round before wrote of it.
+// The order keeps that: workgroup b takes a tile t = b mod 8, the largest
+// group first among those tiles.
+constexpr int kXcds = 8;
+
+template <int NT>
+__global__ __launch_bounds__(NT) void k_sa_order(
+    const uint32_t* __restrict__ tmax, uint32_t* __restrict__ tmax_next,
+    uint32_t* __restrict__ order, int64_t nl, const uint32_t* state) {
+  if (state[kDone]) return;
+  // cleared for the round's radix part, which records its groups there
+  for (int64_t t = threadIdx.x; t <= nl; t += NT) tmax_next[t] = 0;
+  __shared__ uint32_t cnt[kXcds][kOrderClasses];
+  __shared__ uint32_t cur[kXcds][kOrderClasses];
+  for (int c = threadIdx.x; c < kXcds * kOrderClasses; c += NT)
+    (&cnt[0][0])[c] = 0;
+  __syncthreads();
+  for (int64_t t = threadIdx.x; t < nl; t += NT)
+    atomicAdd(&cnt[t % kXcds][order_class(tmax[t])], 1u);
+  __syncthreads();
+  if (threadIdx.x < kXcds) {
+    const int x = threadIdx.x;
+    uint32_t run = 0;
+    for (int c = kOrderClasses - 1; c >= 0; --c) {
+      cur[x][c] = run;
+      run += cnt[x][c];
+    }
+  }
+  __syncthreads();
+  for (int64_t t = threadIdx.x; t < nl; t += NT) {
+    const int x = (int)(t % kXcds);
+    const uint32_t r = atomicAdd(&cur[x][order_class(tmax[t])], 1u);
+    order[(int64_t)r * kXcds + x] = (uint32_t)t;
+  }
+}
+
 // -------------------------------------------------------- local rounds
 // Ascending sort of one u64 per lane across the wave (bitonic network).
 __device__ __forceinline__ uint64_t wave_sort_u64(uint64_t v) {
@@ -873,13 +946,14 @@ __global__ __launch_bounds__(NT) void k_sa_local(
     uint32_t* __restrict__ gp, uint32_t* __restrict__ gsz,
     uint32_t* __restrict__ sa, const uint32_t* __restrict__ rank_cur,
     uint32_t* __restrict__ rank_next, const uint32_t* __restrict__ skip_cur,
-    uint32_t* __restrict__ skip_next, int64_t m, int64_t nl, int round,
-    int global_follows, uint32_t* state) {
+    uint32_t* __restrict__ skip_next, const uint32_t* __restrict__ order,
+    int64_t m, int64_t nl, int round, int global_follows, uint32_t* state) {
   constexpr int NW = NT / kWave;
   constexpr int kW = kSlots / kWave / NW;  // windows per wave
   static_assert(kSlots % (kWave * NW) == 0, "windows per wave");
   static_assert(kPosTile % (kWave * NW) == 0, "tile windows per wave");
-  const int64_t b = blockIdx.x;
+  // this workgroup's tile (order: NULL for tile = workgroup)
+  const int64_t b = order ? (int64_t)order[blockIdx.x] : (int64_t)blockIdx.x;
   const int64_t ts = b * kPosTile;
   const int wv = threadIdx.x / kWave;
   const int ln = lane_id();
@@ -1229,7 +1303,7 @@ static int sort_and_rank(SaWs& w, int64_t nb, int64_t m, int round,
   hipLaunchKernelGGL(k_grp_rank<kRsThreads>, dim3((unsigned)nb),
                      dim3(kRsThreads), 0, stream, keys[x], vals[x], w.pos,
                      vb, w.blkmax, w.rank[nx], w.sa, w.gp, w.gsz, w.skip[nx],
-                     w.state, round);
+                     w.tmax[nx], w.state, round);
   return (int)hipGetLastError();
 }
 
@@ -1240,10 +1314,18 @@ static int doubling_round(SaWs& w, int64_t nb, int64_t m, int round,
                           int global_path, hipStream_t stream) {
   const int cur = round & 1, nx = (round + 1) & 1;
   const int64_t nl = (m + kPosTile - 1) / kPosTile;
+  // A round enqueued with its radix part has groups above the cap, and
+  // groups of up to the cap beside them: its tiles go largest group first.
+  // (In rounds of small groups only the order cost more than it saved:
+  // 45-60 us rounds went 15-20 us slower on the template corpus.)
+  if (global_path)
+    hipLaunchKernelGGL(k_sa_order<1024>, dim3(1), dim3(1024), 0, stream,
+                       w.tmax[cur], w.tmax[nx], w.order, nl, w.state);
   hipLaunchKernelGGL(k_sa_local<kSaLocalThreads>, dim3((unsigned)nl),
                      dim3(kSaLocalThreads), 0, stream, w.gp, w.gsz, w.sa,
-                     w.rank[cur], w.rank[nx], w.skip[cur], w.skip[nx], m, nl,
-                     round, global_path, w.state);
+                     w.rank[cur], w.rank[nx], w.skip[cur], w.skip[nx],
+                     global_path ? w.order : nullptr, m, nl, round,
+                     global_path, w.state);
   if (!global_path) return (int)hipGetLastError();
   // (blkmax holds the head counts until the group-head pass needs it)
   hipLaunchKernelGGL(k_pos_count<kRsThreads>, dim3((unsigned)nb),
@@ -1426,8 +1508,8 @@ int build_begin(const int32_t* text, int64_t m, void* workspace,
                      0, stream, text, m, plo, phi);
   hipLaunchKernelGGL(k_sa_init, dim3(eb), dim3(kInitThreads), 0, stream, text,
                      m, w.keyA, w.valA, w.pos, token_round_vb(m), plo, phi,
-                     parts, w.skip[0], w.skip[1], (m + kPosTile - 1) / kPosTile,
-                     w.hist, nb, w.state);
+                     parts, w.skip[0], w.skip[1], w.tmax[0], w.tmax[1],
+                     (m + kPosTile - 1) / kPosTile, w.hist, nb, w.state);
   return sort_and_rank(w, nb, m, 0, stream);
 }
 
