@@ -982,7 +982,7 @@ PMC_COPY_ELEMS = 1 << 26
 PMC_STEP_LAUNCHES = 10
 PMC_SA_BUILDS = 2
 # kernels of one suffix-array build (csrc/sa_build.hip)
-SA_BUILD_KERNELS = ("k_sa_", "k_rs_", "k_grp_")
+SA_BUILD_KERNELS = ("k_sa_", "k_rs_", "k_grp_", "k_pos_")
 # what a rebuild adds after the suffix array: key rows, n-gram table
 TABLE_KERNELS = ("k_rank_keys", "k_gram_")
 

@@ -957,17 +957,18 @@ __global__ __launch_bounds__(NT) void k_sa_local(
   const int64_t ts = b * kPosTile;
   const int wv = threadIdx.x / kWave;
   const int ln = lane_id();
-  // The tile's group marks and suffixes are read before the state and skip
-  // words are known, so all of them share one round trip; the slots the
-  // skip words and the marks exclude are dropped below.  Slot
-  // (wv + k * NW) * 64 + ln lies in the tile for k < kWT.
+  // The tile's group marks are read before the state and skip words are
+  // known, so they share one round trip; the slots the skip words exclude
+  // are dropped below.  (The suffixes are read only where a mark says
+  // unfinished: reading them with the marks cost 16 MB more per round at
+  // 2^22 tokens, and a round after the array is final reads the marks
+  // alone.)  Slot (wv + k * NW) * 64 + ln lies in the tile for k < kWT.
   constexpr int kWT = kPosTile / kWave / NW;
-  uint32_t gt[kWT], st[kWT];
+  uint32_t gt[kWT];
 #pragma unroll
   for (int k = 0; k < kWT; ++k) {
     const int64_t p = ts + (wv + k * NW) * kWave + ln;
     gt[k] = p < m ? gp[p] : kFinished;
-    st[k] = p < m ? sa[p] : 0u;
   }
   // every word the launch decides on, loaded at once
   const uint32_t done = state[kDone];
@@ -1015,10 +1016,10 @@ __global__ __launch_bounds__(NT) void k_sa_local(
   const uint32_t ext = sn < (uint32_t)kCap ? sn : 0u;
   const int n = (int)(min(m, te + (int64_t)ext) - ts);
 
-  // 1. loads: gp and sa (the tile's above, the extension's here), then
-  // the group's size and key.  The first `skip` positions belong to a
-  // group the tile before owns (its workgroup rewrites them meanwhile):
-  // what was read of them is dropped.
+  // 1. loads: gp (the tile's above, the extension's here), then sa where
+  // unfinished, then the group's size and key.  The first `skip` positions
+  // belong to a group the tile before owns (its workgroup rewrites them
+  // meanwhile): what was read of them is dropped.
   uint32_t g[kW], iv[kW], sz[kW];
   uint64_t kv[kW];
 #pragma unroll
@@ -1032,10 +1033,7 @@ __global__ __launch_bounds__(NT) void k_sa_local(
 #pragma unroll
   for (int k = 0; k < kW; ++k) {
     const int slot = (wv + k * NW) * kWave + ln;
-    if (k < kWT)
-      iv[k] = g[k] != kFinished ? st[k] : 0u;
-    else
-      iv[k] = g[k] != kFinished ? sa[ts + slot] : 0u;
+    iv[k] = g[k] != kFinished ? sa[ts + slot] : 0u;
   }
 #pragma unroll
   for (int k = 0; k < kW; ++k) {
