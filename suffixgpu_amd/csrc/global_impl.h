@@ -38,8 +38,8 @@ struct GlobalArgs {
 struct GlobalLayout {
   int rpat, lb, ub, found, scan, red, misc, lo, ulo, umap, dlen, dcnt, dpc,
       dmap,
-      sal, sas, sae, caps, dtok, dmb, mpos, mcache, mA, mH, dend, chain, nv,
-      score, rlen, rocc, total;
+      sal, sas, sae, caps, pre, dtok, dmb, mpos, mcache, mA, mH, dend, chain,
+      nv, score, rlen, rocc, total;
 };
 
 // Delta tokens staged per chunk, at least (after a halo of P rounded up to
@@ -92,6 +92,7 @@ __host__ __device__ inline GlobalLayout global_layout(int P, int C, int R,
   L.sas = g_take(off, C * 4);
   L.sae = g_take(off, C * 4);
   L.caps = g_take(off, C * 4);
+  L.pre = g_take(off, C * 4);
   L.chain = g_take(off, C * K * 4);
   L.nv = g_take(off, C * 4);
   L.score = g_take(off, C * 4);
@@ -575,14 +576,16 @@ __device__ __forceinline__ int32_t sa_sample(const GlobalArgs& a, int64_t s,
 // gathered into LDS -- tokens in range, not PAD, not negative, else -1
 // (:443-463) -- optionally copied to cont_out [R, K], then (expand) the
 // majority-vote expansion into chain_out.
+// slot: the wave whose LDS areas hold the block (-1: the calling wave's);
+// gathered: the block is already there (an early gather), only expand.
 __device__ __forceinline__ ExpandResult gather_expand(
     const GlobalArgs& a, const GlobalLayout& L, unsigned char* smem, int b,
     int c, int src, int len, int occ, int64_t sa_s, int64_t ilen,
     const int32_t* dpc, int32_t* cont_out, bool expand, int32_t* chain_out,
-    const int32_t* dend = nullptr) {
+    const int32_t* dend = nullptr, int slot = -1, bool gathered = false) {
   const sfx_params& p = a.p;
   const int ln = lane_id();
-  const int wv = threadIdx.x / kWave;
+  const int wv = slot >= 0 ? slot : (int)(threadIdx.x / kWave);
   const int R = p.max_occurrences;
   const int K = p.k;
   const int Rp = (R + 3) & ~3;
@@ -593,56 +596,59 @@ __device__ __forceinline__ ExpandResult gather_expand(
   // delta: each part's list index for this cap, read with the parts'
   // counts by delta_combine (one dependent load per hit here)
   const int32_t* dmap = (const int32_t*)(smem + L.dmap) + c * kMaxDeltaParts;
-  for (int r = ln; r < occ; r += kWave) {
-    int32_t pos;
-    if (src == 1) {
-      pos = sa_sample(a, sa_s, ilen, r);
-    } else {
-      int k = 0, rr = r;
-      while (k < a.dparts - 1 && rr >= dpc[c * kMaxDeltaParts + k]) {
-        rr -= dpc[c * kMaxDeltaParts + k];
-        ++k;
-      }
-      const int m = dmap[k];
-      const int64_t slot = (int64_t)b * a.dparts + k;
-      // the end lists: copied into LDS at the parts' join (dend), or read
-      // from the workspace
-      const int32_t end_r =
-          dend ? dend[(k * p.num_caps + m) * R + rr]
-               : a.ws.d_end[(slot * p.num_caps + m) * R + rr];
-      const int64_t e = (int64_t)end_r - len;
-      pos = (int32_t)(e < 0 ? 0 : e);
-    }
-    mpos[r] = pos;
-  }
-  wave_lds_sync();
-  SFX_TRACE_POINT(10);
-  const int32_t* srcbuf = src == 1 ? a.ix.corpus : a.ix.delta;
-  const int64_t nbuf = src == 1 ? N : D;
-  int64_t slen = N;
-  if (src == 2) {
-    slen = *a.ix.delta_len;
-    slen = slen < 0 ? 0 : (slen > D ? D : slen);
-  }
-  // One occurrence row per lane: its K tokens are independent loads.  Rows
-  // are K + 1 words apart in LDS (an odd stride), so the lanes' reads and
-  // writes of one depth fall in distinct banks.
   const int Kp = K + 1;
-  for (int r = ln; r < occ; r += kWave) {
-    const int64_t base = (int64_t)mpos[r] + len;
-    int32_t* dst = mcache + r * Kp;
-    for (int j0 = 0; j0 < K; j0 += 16) {
-      int32_t v[16];
-#pragma unroll
-      for (int u = 0; u < 16; ++u) {
-        const int64_t idx = base + j0 + u;
-        v[u] = -1;
-        if (j0 + u < K && idx < slen && idx >= 0)
-          v[u] = srcbuf[idx < nbuf - 1 ? idx : nbuf - 1];
+  if (!gathered) {
+    for (int r = ln; r < occ; r += kWave) {
+      int32_t pos;
+      if (src == 1) {
+        pos = sa_sample(a, sa_s, ilen, r);
+      } else {
+        int k = 0, rr = r;
+        while (k < a.dparts - 1 && rr >= dpc[c * kMaxDeltaParts + k]) {
+          rr -= dpc[c * kMaxDeltaParts + k];
+          ++k;
+        }
+        const int m = dmap[k];
+        const int64_t slot = (int64_t)b * a.dparts + k;
+        // the end lists: copied into LDS at the parts' join (dend), or read
+        // from the workspace
+        const int32_t end_r =
+            dend ? dend[(k * p.num_caps + m) * R + rr]
+                 : a.ws.d_end[(slot * p.num_caps + m) * R + rr];
+        const int64_t e = (int64_t)end_r - len;
+        pos = (int32_t)(e < 0 ? 0 : e);
       }
+      mpos[r] = pos;
+    }
+    wave_lds_sync();
+    SFX_TRACE_POINT(10);
+    const int32_t* srcbuf = src == 1 ? a.ix.corpus : a.ix.delta;
+    const int64_t nbuf = src == 1 ? N : D;
+    int64_t slen = N;
+    if (src == 2) {
+      slen = *a.ix.delta_len;
+      slen = slen < 0 ? 0 : (slen > D ? D : slen);
+    }
+    // One occurrence row per lane: its K tokens are independent loads.  Rows
+    // are K + 1 words apart in LDS (an odd stride), so the lanes' reads and
+    // writes of one depth fall in distinct banks.
+    for (int r = ln; r < occ; r += kWave) {
+      const int64_t base = (int64_t)mpos[r] + len;
+      int32_t* dst = mcache + r * Kp;
+      for (int j0 = 0; j0 < K; j0 += 16) {
+        int32_t v[16];
 #pragma unroll
-      for (int u = 0; u < 16; ++u)
-        if (j0 + u < K) dst[j0 + u] = (v[u] != kPad && v[u] >= 0) ? v[u] : -1;
+        for (int u = 0; u < 16; ++u) {
+          const int64_t idx = base + j0 + u;
+          v[u] = -1;
+          if (j0 + u < K && idx < slen && idx >= 0)
+            v[u] = srcbuf[idx < nbuf - 1 ? idx : nbuf - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+          if (j0 + u < K)
+            dst[j0 + u] = (v[u] != kPad && v[u] >= 0) ? v[u] : -1;
+      }
     }
   }
   wave_lds_sync();
@@ -674,7 +680,8 @@ __device__ __forceinline__ void source_expand(
     const GlobalArgs& a, const GlobalLayout& L, unsigned char* smem, int b,
     int src, const int32_t* lens, const int32_t* aux0, const int32_t* aux1,
     const int32_t* dpc, int32_t* nv_out, float* score_out,
-    int32_t* chain_out, const int32_t* needed = nullptr) {
+    int32_t* chain_out, const int32_t* needed = nullptr,
+    const int32_t* pre = nullptr) {
   const sfx_params& p = a.p;
   const int C = p.num_caps;
   const int R = p.max_occurrences;
@@ -708,7 +715,8 @@ __device__ __forceinline__ void source_expand(
                          nullptr, true, chain + c * K,
                          src == 2 && a.dend
                              ? (const int32_t*)(smem + L.dend)
-                             : nullptr);
+                             : nullptr,
+                         -1, pre && pre[c] == len);
     }
     wave_lds_sync();  // lane 0 wrote the chain
     for (int cc = c; cc < end; ++cc) {
@@ -738,6 +746,9 @@ __device__ __forceinline__ const void* live_gram(const sfx_index& ix) {
 }
 
 // role 0: SA search; role 1 .. dparts: delta part role - 1.
+// kEarly: the decode step's SA workgroup may gather short caps' blocks
+// early (off in the streamed step kernel, which it pushed into scratch).
+template <bool kEarly = true>
 __device__ __forceinline__ void global_body(const GlobalArgs& a,
                                             unsigned char* smem, int b,
                                             int role) {
@@ -880,6 +891,45 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
         ubs[l - 1] = hi;
       }
     }
+    // Early gathers (decode step).  With one length per search group,
+    // wave 0's groups search lengths 1 .. 4, which the n-gram table
+    // answers with one lookup, and wave 0 then waits for the longest
+    // searches.  Meanwhile it gathers the continuation blocks of the caps
+    // whose candidate it already knows (cap <= the table's longest run
+    // length) into the LDS areas of the waves that will expand them: wave
+    // c for the run of equal candidate lengths that cap c heads.  A cap
+    // whose run head it cannot know yet (the cap before lies beyond the
+    // table) is gathered as if it were one; pre[c] is the length gathered
+    // for cap c, -1 for none.
+    int32_t* pre = (int32_t*)(smem + L.pre);
+    const int nmw = a.merge_waves;
+    const bool early = kEarly && a.step && gram && ngroups >= P;
+    if (early && wv == 0) {
+      wave_lds_sync();  // this wave's groups wrote lengths 1 .. 4
+      int prev = -1;  // candidate length of cap c - 1, if known
+      for (int c = 0; c < C; ++c) {
+        const int cap = p.caps[c];
+        int best = -1;
+        if (cap <= kg) {
+          const int l = ln + 1;
+          const bool f = l <= kg && l <= cap && l <= plen &&
+                         ubs[l - 1] > lbs[l - 1];
+          const uint64_t m = ballot(f);
+          best = m ? 64 - __builtin_clzll(m) : 0;
+        }
+        int got = -1;
+        if (best > 0 && c < nmw && best != prev) {
+          const int64_t s0 = lbs[best - 1];
+          const int64_t ilen = ubs[best - 1] - s0;
+          gather_expand(a, L, smem, b, c, 1, best, (int)(ilen < R ? ilen : R),
+                        s0, ilen, nullptr, nullptr, false, nullptr, nullptr, c,
+                        false);
+          got = best;
+        }
+        if (ln == 0) pre[c] = got;
+        prev = best;
+      }
+    }
     __syncthreads();
     SFX_TRACE_POINT(2);
     // Each cap takes its longest non-empty interval (sa_search.py:
@@ -921,7 +971,8 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
       // delta and local workgroups are still running.
       __syncthreads();
       source_expand(a, L, smem, b, 1, sal, sas, sae, nullptr,
-                    a.ws.sa_nv, a.ws.sa_score, a.ws.sa_chain);
+                    a.ws.sa_nv, a.ws.sa_score, a.ws.sa_chain, nullptr,
+                    early ? pre : nullptr);
       SFX_TRACE_POINT(4);
       if (block_arrive(a.ws.pick + b, 3u, misc + 1))
         final_pick(p, a.ws, b, a.draft, a.num_valid, misc + 4);

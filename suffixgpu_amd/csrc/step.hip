@@ -53,7 +53,7 @@ __global__ __launch_bounds__(kGlobalThreads) void k_step(StepArgs a) {
   if (role == per - 1)
     local_body<kStream>(a.l, smem, b);
   else
-    global_body(a.g, smem, b, role);
+    global_body<!kStream>(a.g, smem, b, role);
 }
 
 }  // namespace sfx
