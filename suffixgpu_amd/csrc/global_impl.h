@@ -937,8 +937,9 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
     int32_t* sal = (int32_t*)(smem + L.sal);
     int32_t* sas = (int32_t*)(smem + L.sas);
     int32_t* sae = (int32_t*)(smem + L.sae);
+    const int32_t* capl = (const int32_t*)(smem + L.caps);  // LDS copy
     for (int c = wv; c < C; c += NW) {
-      const int cap = p.caps[c];
+      const int cap = capl[c];
       int best = 0;
       for (int base = 1; base <= P; base += kWave) {
         const int l = base + ln;
@@ -961,9 +962,11 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
         if (a.step)
           ws_store(a.ws.sa_known + (int64_t)b * SFX_MAX_CANDIDATES + c,
                    best + 1);
-        if (a.out.sa_len) a.out.sa_len[(int64_t)b * C + c] = best;
-        if (a.out.sa_start) a.out.sa_start[(int64_t)b * C + c] = s0;
-        if (a.out.sa_end) a.out.sa_end[(int64_t)b * C + c] = e0;
+        if (!a.step) {  // query outputs (none in a decode step)
+          if (a.out.sa_len) a.out.sa_len[(int64_t)b * C + c] = best;
+          if (a.out.sa_start) a.out.sa_start[(int64_t)b * C + c] = s0;
+          if (a.out.sa_end) a.out.sa_end[(int64_t)b * C + c] = e0;
+        }
       }
     }
     if (a.step) {
