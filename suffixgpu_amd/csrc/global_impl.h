@@ -747,9 +747,10 @@ __device__ __forceinline__ const void* live_gram(const sfx_index& ix) {
 
 // role 0: SA search; role 1 .. dparts: delta part role - 1.
 // kEarly: the decode step's SA workgroup may gather short caps' blocks
-// early.  Off in the streamed step kernel (grids of B >= 171 that run in
-// waves, two workgroups per CU): there it measured slower, the B=256
-// S=16384 decode loop's replay p50 50.4-51.0 -> 53.4-54.4 us.
+// early.  Off in the streamed step kernel (rows beyond the LDS layout, as
+// in the B=256 S=16384 decode loop, whose grid runs in waves with two
+// workgroups per CU): there it measured slower, the loop's replay p50
+// 50.4-51.0 -> 53.4-54.4 us.
 template <bool kEarly = true>
 __device__ __forceinline__ void global_body(const GlobalArgs& a,
                                             unsigned char* smem, int b,
