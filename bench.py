@@ -189,11 +189,13 @@ def time_sa_builds(w, dev, side):
         build_ms[name] = (min(times), mm)
         log(f"SA build {name}: m={mm} {min(times):.2f} ms")
         # As the index's background rebuild runs it at steady state: the
-        # rounds the previous build needed plus a margin of 2, with the
-        # radix path for the rounds that took it, then the output (the
-        # device confirms the array is final).
+        # rounds the previous build needed plus a margin of 2 (flagged as
+        # expected to find the array final), with the radix path for the
+        # rounds that took it, then the output (the device confirms the
+        # array is final).
         prev = read_build_state(ws, mm)
         final, rounds, radix = prev.done, prev.needed + 2, prev.radix_mask & ~1
+        fin = prev.needed + 1
         times = []
         for rep in range(3):
             torch.cuda.synchronize()
@@ -202,7 +204,8 @@ def time_sa_builds(w, dev, side):
             e1 = torch.cuda.Event(enable_timing=True)
             with torch.cuda.stream(side):
                 e0.record(side)
-                build_suffix_array_rounds(text, mm, out, ws, rounds, radix)
+                build_suffix_array_rounds(text, mm, out, ws, rounds, radix,
+                                          fin)
                 e1.record(side)
             e1.synchronize()
             times.append(e0.elapsed_time(e1))
@@ -545,8 +548,9 @@ def cold_step_p50(graph, dev, reps: int = 40) -> float:
 
 def concurrent_rebuild(graph, w, dev, rounds: int, radix: int) -> dict:
     """A 4.19M-token SA rebuild (as the index's background rebuild runs
-    it: ``rounds`` doubling rounds, the radix path for those in the mask
-    ``radix``) enqueued on a side stream while the
+    it: ``rounds`` doubling rounds, the last two flagged as the margin, the
+    radix path for those in the mask ``radix``) enqueued on a side stream
+    while the
     captured step replays on the main stream: build time, decode steps
     completed before the build's end event, and the step p50 meanwhile."""
     import torch
@@ -572,7 +576,8 @@ def concurrent_rebuild(graph, w, dev, rounds: int, radix: int) -> dict:
     b1 = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(side):
         b0.record(side)
-        build_suffix_array_rounds(text, m, out, ws, rounds, radix)
+        build_suffix_array_rounds(text, m, out, ws, rounds, radix,
+                                  rounds - 1)
         b1.record(side)
     ends = []
     starts = []
@@ -1028,7 +1033,8 @@ def pmc_workload(d, w, dev) -> int:
                        device=dev)
     st = _lib.stream_of(dev)
     for _ in range(PMC_SA_BUILDS):
-        build_suffix_array_rounds(text, m, out, ws, needed + 2, radix)
+        build_suffix_array_rounds(text, m, out, ws, needed + 2, radix,
+                                  needed + 1)
         # the key rows and n-gram table the index builds after it
         _lib.check(L.sfx_sa_keys(text.data_ptr(), out.data_ptr(), CAPACITY,
                                  m, KEY_WIDTH, keys.data_ptr(),

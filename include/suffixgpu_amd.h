@@ -311,11 +311,18 @@ int sfx_delta_index_build(const int32_t* delta, const int64_t* delta_len,
  *             once).  A round sorts its unsorted groups of at most
  *             sfx_sa_group_cap() suffixes inside workgroups (one launch)
  *             and its larger groups by radix launches, which are
- *             enqueued only when global_path is 1.  With global_path 0 a
- *             round that has a larger group marks the build stalled at
- *             that round and every later launch returns; enqueueing
- *             rounds again from the stalled round with global_path 1
- *             resumes the build;
+ *             enqueued only when flags has SFX_SA_ROUNDS_RADIX.  Without
+ *             it a round that has a larger group marks the build stalled
+ *             at that round and every later launch returns; enqueueing
+ *             rounds again from the stalled round with SFX_SA_ROUNDS_RADIX
+ *             resumes the build.  SFX_SA_ROUNDS_EXPECT_FINAL tells the
+ *             rounds that the caller expects the array to be final before
+ *             them (a rebuild's margin rounds past the rounds the same
+ *             text needed before): each of their launches reads the state
+ *             words before its tile, so a round with nothing to do reads
+ *             64 bytes per workgroup instead of 16 KB, and one with work
+ *             starts a memory round trip later.  Results never depend on
+ *             it.  Other flag bits are rejected (SFX_EINVAL);
  *   finish -- sa[0:m] from the workspace, sa[m:n_total] the identity.
  * The workspace's u32 state block at sfx_sa_build_flag_offset(m) (64
  * bytes to copy) holds [0] nonzero once the array is final, [2] the round
@@ -332,8 +339,10 @@ int64_t sfx_sa_build_flag_offset(int64_t m);
 int sfx_sa_group_cap(void);
 int sfx_sa_build_begin(const int32_t* text, int64_t m, void* workspace,
                        size_t workspace_bytes, hipStream_t stream);
+#define SFX_SA_ROUNDS_RADIX 1
+#define SFX_SA_ROUNDS_EXPECT_FINAL 2
 int sfx_sa_build_rounds(int64_t m, int32_t first, int32_t count,
-                        int32_t global_path, void* workspace,
+                        int32_t flags, void* workspace,
                         size_t workspace_bytes, hipStream_t stream);
 int sfx_sa_build_finish(int64_t m, int64_t n_total, void* sa, int32_t sa_is64,
                         void* workspace, size_t workspace_bytes,

@@ -187,6 +187,9 @@ EINVAL = -1
 ENOSCRATCH = -2
 NOALLOC_SCRATCH_BYTES = 16 << 20
 NOALLOC_MAX_ROWS = 4096
+# flags of sfx_sa_build_rounds
+SA_ROUNDS_RADIX = 1
+SA_ROUNDS_EXPECT_FINAL = 2
 INGEST_MAX_DOCS = 4096
 # sfx_ingest_header, in order (int64 each)
 INGEST_HEADER_FIELDS = (

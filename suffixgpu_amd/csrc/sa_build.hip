@@ -91,7 +91,7 @@ struct SaWs {
   uint32_t* sa;       // [m] current suffix order
   uint32_t* gp;       // [m] group head of SA position p, or a finished mark
   uint32_t* gsz;      // [m] size of the group headed at p
-  uint32_t* hist;     // [512][NB] digit counts per tile, then offsets
+  uint32_t* hist;     // [NB][512] digit counts per tile, then offsets
   uint32_t* rowsum;   // [512] digit totals
   uint32_t* tcnt;     // [NB] unfinished positions per tile
   uint32_t* blkmax;   // [NB] last group start per tile
@@ -235,11 +235,46 @@ __device__ __forceinline__ uint32_t digit_of(uint64_t k, int sh) {
 // past the end; pair keys need span + 2 < 2^kPairBits.
 constexpr int kPairBits = 18;
 
+// The token round's sort key of position i (below the vb position bits):
+// with `pairs`, code(t[i]) << kPairBits | code(t[i + 1]), code(t) = 1 +
+// t - lo, span + 1 for PAD, 0 past the end; else t[i] in signed order.
+struct TokenCoding {
+  int32_t lo;
+  int64_t span;
+  bool pairs;
+};
+
+__device__ __forceinline__ TokenCoding token_coding(int32_t lo, int32_t hi) {
+  TokenCoding c;
+  c.lo = lo;
+  // hi < lo: the text is all PAD
+  c.span = hi < lo ? 0 : (int64_t)hi - (int64_t)lo + 1;
+  c.pairs = c.span + 2 < ((int64_t)1 << kPairBits);
+  return c;
+}
+
+__device__ __forceinline__ uint64_t token_code(const TokenCoding& c,
+                                               int32_t t, bool in_text) {
+  if (!in_text) return 0;
+  return t == INT32_MAX ? (uint64_t)c.span + 1
+                        : (uint64_t)((int64_t)t - c.lo + 1);
+}
+
+__device__ __forceinline__ uint64_t token_key(const TokenCoding& c,
+                                              int32_t t0, int32_t t1,
+                                              bool t1_in_text) {
+  return c.pairs ? (token_code(c, t0, true) << kPairBits) |
+                       token_code(c, t1, t1_in_text)
+                 : (uint64_t)((uint32_t)t0 ^ 0x80000000u);
+}
+
 // vb > 0: the key carries the position in its low vb bits (no value or
-// position arrays); 0: key, value and position arrays.  Each thread keys
-// kInitItems consecutive positions, so a block keys one radix tile, and
-// the block also writes that tile's digit counts for the first radix pass
-// (digit at bit vb) to hist[d * nb + tile].
+// position arrays), and the token round's first scatter computes the keys
+// from the text itself, so none are written here; vb = 0: key, value and
+// position arrays.  Each thread keys kInitItems consecutive positions, so
+// a block keys one radix tile, and the block also writes that tile's
+// digit counts for the first radix pass (digit at bit vb) to
+// hist[tile * 512 + d].
 constexpr int kInitItems = 4;
 static_assert(kInitThreads * kInitItems == kTile, "a block per radix tile");
 
@@ -256,9 +291,8 @@ __global__ __launch_bounds__(kInitThreads) void k_sa_init(
   int32_t tlo = (int)threadIdx.x < nparts ? part_lo[threadIdx.x] : INT32_MAX;
   int32_t thi = (int)threadIdx.x < nparts ? part_hi[threadIdx.x] : INT32_MIN;
   block_minmax<kInitThreads>(tlo, thi, red);
-  // thi < tlo: the text is all PAD
-  const int64_t span = thi < tlo ? 0 : (int64_t)thi - (int64_t)tlo + 1;
-  const bool pairs = span + 2 < ((int64_t)1 << kPairBits);
+  const TokenCoding tc = token_coding(tlo, thi);
+  const bool pairs = tc.pairs;
   if (tid < kStateWords) {
     uint32_t v = 0;
     if (tid == kLen) v = (uint32_t)n;
@@ -283,16 +317,10 @@ __global__ __launch_bounds__(kInitThreads) void k_sa_init(
 #pragma unroll
   for (int j = 0; j <= kInitItems; ++j)
     t[j] = i0 + j < n ? text[i0 + j] : 0;
-  auto code = [&](int j) -> uint64_t {
-    if (i0 + j >= n) return 0;
-    return t[j] == INT32_MAX ? (uint64_t)span + 1
-                             : (uint64_t)((int64_t)t[j] - tlo + 1);
-  };
   uint64_t k[kInitItems];
 #pragma unroll
   for (int j = 0; j < kInitItems; ++j) {
-    k[j] = pairs ? (code(j) << kPairBits) | code(j + 1)
-                 : (uint64_t)((uint32_t)t[j] ^ 0x80000000u);
+    k[j] = token_key(tc, t[j], t[j + 1], i0 + j + 1 < n);
     if (vb > 0) k[j] = (k[j] << vb) | (uint64_t)(i0 + j);
   }
   __syncthreads();  // the counters are cleared
@@ -301,28 +329,24 @@ __global__ __launch_bounds__(kInitThreads) void k_sa_init(
     if (i0 + j < n) atomicAdd(&hcnt[digit_of(k[j], vb)], 1u);
   __syncthreads();
   if (threadIdx.x < kRadix)
-    hist[(int64_t)threadIdx.x * nb + blockIdx.x] = hcnt[threadIdx.x];
-  if (i0 >= n) return;
+    hist[(int64_t)blockIdx.x * kRadix + threadIdx.x] = hcnt[threadIdx.x];
+  if (i0 >= n || vb > 0) return;
   if (i0 + kInitItems <= n) {
     // key, val and pos are 256-byte aligned workspace arrays
     static_assert(kInitItems == 4, "two 16-byte key stores");
     reinterpret_cast<ulonglong2*>(key + i0)[0] = make_ulonglong2(k[0], k[1]);
     reinterpret_cast<ulonglong2*>(key + i0)[1] = make_ulonglong2(k[2], k[3]);
-    if (vb == 0) {
-      const uint32_t p = (uint32_t)i0;
-      const uint4 ix = make_uint4(p, p + 1, p + 2, p + 3);
-      *reinterpret_cast<uint4*>(val + i0) = ix;
-      *reinterpret_cast<uint4*>(pos + i0) = ix;
-    }
+    const uint32_t p = (uint32_t)i0;
+    const uint4 ix = make_uint4(p, p + 1, p + 2, p + 3);
+    *reinterpret_cast<uint4*>(val + i0) = ix;
+    *reinterpret_cast<uint4*>(pos + i0) = ix;
   } else {
 #pragma unroll
     for (int j = 0; j < kInitItems; ++j) {
       if (i0 + j < n) {
         key[i0 + j] = k[j];
-        if (vb == 0) {
-          val[i0 + j] = (uint32_t)(i0 + j);
-          pos[i0 + j] = (uint32_t)(i0 + j);
-        }
+        val[i0 + j] = (uint32_t)(i0 + j);
+        pos[i0 + j] = (uint32_t)(i0 + j);
       }
     }
   }
@@ -396,30 +420,77 @@ __global__ __launch_bounds__(NT) void k_rs_hist(
     uint32_t sum = 0;
 #pragma unroll
     for (int w = 0; w < kRsHists; ++w) sum += h[w][tid];
-    hist[(int64_t)tid * nb + blockIdx.x] = sum;
+    hist[(int64_t)blockIdx.x * kRadix + tid] = sum;
   }
 }
 
-// Row d of the histogram (tiles 0 .. ceil(A/4096)) becomes its exclusive
-// prefix; rowsum[d] the digit total.  One block per digit.
+// The histogram is stored by tile, hist[t * 512 + d]: a tile's counts are
+// one contiguous 2 KB row, written and read back by its own tile's
+// workgroups with whole-sector accesses (a column-major layout costs a
+// 32-byte sector per 4-byte count on both sides).  Column d (tiles
+// 0 .. ceil(A/4096)) becomes its exclusive prefix; rowsum[d] the digit
+// total.  Block j scans the kScanDigits digits from j * kScanDigits: lane
+// (part, d) = (tid / kScanDigits, tid % kScanDigits) sums kScanRun
+// consecutive tiles, so the kScanDigits lanes of a part read and write one
+// 128-byte line per tile.  The parts of a wave (the lanes kScanDigits
+// apart) are scanned by shuffles, the waves through LDS.
+constexpr int kScanDigits = 32;
+constexpr int kScanRun = 32;
+static_assert(kRadix % kScanDigits == 0 && kWave % kScanDigits == 0,
+              "digit blocks");
+constexpr int kScanBlocks = kRadix / kScanDigits;
+
 template <int NT>
 __global__ __launch_bounds__(NT) void k_rs_rowscan(
     uint32_t* hist, int64_t nb, uint32_t* rowsum, const uint32_t* state,
     int round) {
+  constexpr int NW = NT / kWave;
+  constexpr int kChunk = NT / kScanDigits * kScanRun;  // tiles per pass
   if (radix_idle(state, round)) return;
-  __shared__ uint32_t red[NT / kWave];
+  __shared__ uint32_t wtot[NW][kScanDigits];
+  const int ln = lane_id();
+  const int wv = threadIdx.x / kWave;
+  const int dl = threadIdx.x % kScanDigits;
+  const int part = threadIdx.x / kScanDigits;
+  uint32_t* col = hist + (int64_t)blockIdx.x * kScanDigits + dl;
   const int64_t nbA = tiles_of(state[kLen]);
-  uint32_t* row = hist + (int64_t)blockIdx.x * nb;
   uint32_t carry = 0;
-  for (int64_t c0 = 0; c0 < nbA; c0 += NT) {
-    const int64_t t = c0 + threadIdx.x;
-    const uint32_t v = t < nbA ? row[t] : 0u;
-    uint32_t tot;
-    const uint32_t ex = block_exscan1<NT>(v, red, &tot);
-    if (t < nbA) row[t] = carry + ex;
-    carry += tot;
+  for (int64_t c0 = 0; c0 < nbA; c0 += kChunk) {
+    const int64_t t0 = c0 + (int64_t)part * kScanRun;
+    uint32_t v[kScanRun];
+#pragma unroll
+    for (int r = 0; r < kScanRun; ++r)
+      v[r] = t0 + r < nbA ? col[(t0 + r) * kRadix] : 0u;
+    uint32_t sum = 0;
+#pragma unroll
+    for (int r = 0; r < kScanRun; ++r) {
+      const uint32_t x = v[r];
+      v[r] = sum;
+      sum += x;
+    }
+    // inclusive over the wave's parts of digit dl
+    uint32_t inc = sum;
+#pragma unroll
+    for (int off = kScanDigits; off < kWave; off <<= 1) {
+      const uint32_t o = __shfl_up(inc, off);
+      if (ln >= off) inc += o;
+    }
+    if (ln >= kWave - kScanDigits) wtot[wv][dl] = inc;
+    __syncthreads();
+    uint32_t before = inc - sum, all = 0;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const uint32_t x = wtot[w][dl];
+      if (w < wv) before += x;
+      all += x;
+    }
+    __syncthreads();  // wtot is rewritten by the next pass
+#pragma unroll
+    for (int r = 0; r < kScanRun; ++r)
+      if (t0 + r < nbA) col[(t0 + r) * kRadix] = carry + before + v[r];
+    carry += all;
   }
-  if (threadIdx.x == 0) rowsum[blockIdx.x] = carry;
+  if (part == 0) rowsum[(int64_t)blockIdx.x * kScanDigits + dl] = carry;
 }
 
 // Stable scatter of one tile.  Wave w owns the tile's contiguous span
@@ -431,12 +502,17 @@ __global__ __launch_bounds__(NT) void k_rs_rowscan(
 // order.  The tile is then written out from LDS by consecutive threads, so
 // each store instruction writes the runs of a few digits contiguously
 // instead of up to 64 scattered words.  Four barriers per tile.
-template <int NT, bool kVal = true>
+// kText: the token round's first pass (packed keys, sh = vb), which keys
+// position idx from text[idx], text[idx + 1] as k_sa_init does instead of
+// reading keys (kin unused).
+template <int NT, bool kVal = true, bool kText = false>
 __global__ __launch_bounds__(NT) void k_rs_scatter(
     const uint64_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint64_t* __restrict__ kout, uint32_t* __restrict__ vout, int sh,
     const uint32_t* __restrict__ hist, int64_t nb,
-    const uint32_t* __restrict__ rowsum, const uint32_t* state, int round) {
+    const uint32_t* __restrict__ rowsum, const uint32_t* state, int round,
+    const int32_t* __restrict__ text) {
+  static_assert(!(kText && kVal), "the text pass packs the position");
   constexpr int NW = NT / kWave;
   constexpr int kSpan = kTile / NW;
   constexpr int kSteps = kSpan / kWave;
@@ -458,11 +534,26 @@ __global__ __launch_bounds__(NT) void k_rs_scatter(
   uint64_t k[kSteps];
   uint32_t v[kSteps];
   uint64_t peers[kSteps];  // lanes of the same step holding the same digit
+  if (kText) {
+    const TokenCoding tc =
+        token_coding((int32_t)state[kTokLo], (int32_t)state[kTokHi]);
 #pragma unroll
-  for (int s = 0; s < kSteps; ++s) {
-    const int64_t idx = wbase + s * kWave + ln;
-    k[s] = idx < A ? kin[idx] : 0;
-    v[s] = kVal && idx < A ? vin[idx] : 0;
+    for (int s = 0; s < kSteps; ++s) {
+      const int64_t idx = wbase + s * kWave + ln;
+      const int32_t t0 = idx < A ? text[idx] : 0;
+      const int32_t t1 = idx + 1 < A ? text[idx + 1] : 0;
+      k[s] = idx < A ? (token_key(tc, t0, t1, idx + 1 < A) << sh) |
+                           (uint64_t)idx
+                     : 0;
+      v[s] = 0;
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+      const int64_t idx = wbase + s * kWave + ln;
+      k[s] = idx < A ? kin[idx] : 0;
+      v[s] = kVal && idx < A ? vin[idx] : 0;
+    }
   }
   for (int e = tid; e < NW * kRadix; e += NT) (&woff[0][0])[e] = 0;
   // Digit d's first output slot: the totals of the digits below it.
@@ -490,7 +581,7 @@ __global__ __launch_bounds__(NT) void k_rs_scatter(
   uint32_t ttot;
   const uint32_t ls = block_exscan1<NT>(cnt, red, &ttot);
   if (tid < kRadix) {
-    gdelta[tid] = dbase + hist[(int64_t)tid * nb + blockIdx.x] - ls;
+    gdelta[tid] = dbase + hist[(int64_t)blockIdx.x * kRadix + tid] - ls;
     uint32_t run = ls;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
@@ -940,8 +1031,12 @@ __device__ __forceinline__ int count_below(const uint64_t* c, int len,
 // Groups above kCap are left to the round's radix launches; when the
 // caller enqueued none (global_follows == 0) this launch marks the round
 // stalled and does nothing.  A round with no group left sets the done
-// flag.
-template <int NT>
+// flag.  kExpectDone: the caller expects the array to be final by this
+// round (a rebuild's margin rounds), so the launch reads the state words
+// before the tile's group marks, which it then reads only if the round
+// has work after all.  (A separate instantiation: a run-time switch
+// changed the load schedule of every round.)
+template <int NT, bool kExpectDone>
 __global__ __launch_bounds__(NT) void k_sa_local(
     uint32_t* __restrict__ gp, uint32_t* __restrict__ gsz,
     uint32_t* __restrict__ sa, const uint32_t* __restrict__ rank_cur,
@@ -968,7 +1063,7 @@ __global__ __launch_bounds__(NT) void k_sa_local(
 #pragma unroll
   for (int k = 0; k < kWT; ++k) {
     const int64_t p = ts + (wv + k * NW) * kWave + ln;
-    gt[k] = p < m ? gp[p] : kFinished;
+    gt[k] = !kExpectDone && p < m ? gp[p] : kFinished;
   }
   // every word the launch decides on, loaded at once
   const uint32_t done = state[kDone];
@@ -998,6 +1093,13 @@ __global__ __launch_bounds__(NT) void k_sa_local(
   // a resumed round clears its stall mark before its radix launches
   if (stalled != 0 && blockIdx.x == 0 && threadIdx.x == 0)
     state[kStalled] = 0;
+  if (kExpectDone) {
+#pragma unroll
+    for (int k = 0; k < kWT; ++k) {
+      const int64_t p = ts + (wv + k * NW) * kWave + ln;
+      gt[k] = p < m ? gp[p] : kFinished;
+    }
+  }
   // Every group fits this launch: sort by (rank[i + h], rank[i + 2h]) and
   // the round triples h; a round with a radix part doubles it.
   const bool triple = mg <= (uint32_t)kCap && m <= kTripleMaxM;
@@ -1267,7 +1369,7 @@ static int token_round_vb(int64_t m) {
 // `nbits` bits of its keys (above the vb value bits of the token round's
 // packed keys), then the group heads of the sorted order.
 static int sort_and_rank(SaWs& w, int64_t nb, int64_t m, int round,
-                         hipStream_t stream) {
+                         const int32_t* text, hipStream_t stream) {
   const int vb = round == 0 ? token_round_vb(m) : 0;
   const int nbits = round == 0 ? 2 * kPairBits : round_bits(m);
   uint64_t* keys[2] = {w.keyA, w.keyB};
@@ -1279,19 +1381,25 @@ static int sort_and_rank(SaWs& w, int64_t nb, int64_t m, int round,
       hipLaunchKernelGGL(k_rs_hist<kRsThreads>, dim3((unsigned)nb),
                          dim3(kRsThreads), 0, stream, keys[x], sh, w.hist, nb,
                          w.state, round);
-    hipLaunchKernelGGL(k_rs_rowscan<kRsThreads>, dim3(kRadix),
+    hipLaunchKernelGGL(k_rs_rowscan<kRsThreads>, dim3(kScanBlocks),
                        dim3(kRsThreads), 0, stream, w.hist, nb, w.rowsum,
                        w.state, round);
-    if (vb)
+    // (the token round's first pass keys the text itself)
+    if (vb && sh == vb)
+      hipLaunchKernelGGL((k_rs_scatter<kRsThreads, false, true>),
+                         dim3((unsigned)nb), dim3(kRsThreads), 0, stream,
+                         nullptr, nullptr, keys[x ^ 1], nullptr, sh, w.hist,
+                         nb, w.rowsum, w.state, round, text);
+    else if (vb)
       hipLaunchKernelGGL((k_rs_scatter<kRsThreads, false>),
                          dim3((unsigned)nb), dim3(kRsThreads), 0, stream,
                          keys[x], nullptr, keys[x ^ 1], nullptr, sh, w.hist,
-                         nb, w.rowsum, w.state, round);
+                         nb, w.rowsum, w.state, round, nullptr);
     else
       hipLaunchKernelGGL(k_rs_scatter<kRsThreads>, dim3((unsigned)nb),
                          dim3(kRsThreads), 0, stream, keys[x], vals[x],
                          keys[x ^ 1], vals[x ^ 1], sh, w.hist, nb, w.rowsum,
-                         w.state, round);
+                         w.state, round, nullptr);
     x ^= 1;
   }
   const int nx = (round + 1) & 1;
@@ -1309,7 +1417,8 @@ static int sort_and_rank(SaWs& w, int64_t nb, int64_t m, int round,
 // also finishes the build or stalls it), then, when `global_path`, the
 // radix launches for the groups above kCap.
 static int doubling_round(SaWs& w, int64_t nb, int64_t m, int round,
-                          int global_path, hipStream_t stream) {
+                          int global_path, int expect_done,
+                          hipStream_t stream) {
   const int cur = round & 1, nx = (round + 1) & 1;
   const int64_t nl = (m + kPosTile - 1) / kPosTile;
   // A round enqueued with its radix part has groups above the cap, and
@@ -1319,11 +1428,20 @@ static int doubling_round(SaWs& w, int64_t nb, int64_t m, int round,
   if (global_path)
     hipLaunchKernelGGL(k_sa_order<1024>, dim3(1), dim3(1024), 0, stream,
                        w.tmax[cur], w.tmax[nx], w.order, nl, w.state);
-  hipLaunchKernelGGL(k_sa_local<kSaLocalThreads>, dim3((unsigned)nl),
-                     dim3(kSaLocalThreads), 0, stream, w.gp, w.gsz, w.sa,
-                     w.rank[cur], w.rank[nx], w.skip[cur], w.skip[nx],
-                     global_path ? w.order : nullptr, m, nl, round,
-                     global_path, w.state);
+  if (expect_done)
+    hipLaunchKernelGGL((k_sa_local<kSaLocalThreads, true>),
+                       dim3((unsigned)nl), dim3(kSaLocalThreads), 0, stream,
+                       w.gp, w.gsz, w.sa, w.rank[cur], w.rank[nx],
+                       w.skip[cur], w.skip[nx],
+                       global_path ? w.order : nullptr, m, nl, round,
+                       global_path, w.state);
+  else
+    hipLaunchKernelGGL((k_sa_local<kSaLocalThreads, false>),
+                       dim3((unsigned)nl), dim3(kSaLocalThreads), 0, stream,
+                       w.gp, w.gsz, w.sa, w.rank[cur], w.rank[nx],
+                       w.skip[cur], w.skip[nx],
+                       global_path ? w.order : nullptr, m, nl, round,
+                       global_path, w.state);
   if (!global_path) return (int)hipGetLastError();
   // (blkmax holds the head counts until the group-head pass needs it)
   hipLaunchKernelGGL(k_pos_count<kRsThreads>, dim3((unsigned)nb),
@@ -1333,7 +1451,7 @@ static int doubling_round(SaWs& w, int64_t nb, int64_t m, int round,
                      dim3(kRsThreads), 0, stream, w.gp, w.gsz, w.sa,
                      w.rank[cur], w.tcnt, w.blkmax, m, nb, round, w.keyA,
                      w.valA, w.pos, w.state);
-  return sort_and_rank(w, nb, m, round, stream);
+  return sort_and_rank(w, nb, m, round, nullptr, stream);
 }
 
 // ---------------------------------------------------------- delta index
@@ -1354,7 +1472,7 @@ struct DixWs {
   uint64_t* keyB;    // [D]
   uint32_t* pos;     // [D] positions; sorted after the second pass
   uint32_t* valB;    // [D]
-  uint32_t* hist;    // [512][NB]
+  uint32_t* hist;    // [NB][512]
   uint32_t* rowsum;  // [512]
   uint32_t* state;   // [kStateWords]
 };
@@ -1508,20 +1626,25 @@ int build_begin(const int32_t* text, int64_t m, void* workspace,
                      m, w.keyA, w.valA, w.pos, token_round_vb(m), plo, phi,
                      parts, w.skip[0], w.skip[1], w.tmax[0], w.tmax[1],
                      (m + kPosTile - 1) / kPosTile, w.hist, nb, w.state);
-  return sort_and_rank(w, nb, m, 0, stream);
+  return sort_and_rank(w, nb, m, 0, text, stream);
 }
 
 // Rounds first .. first + count - 1 (round r doubles h = h0 * 2^(r-1),
 // h0 = 1 or 2 as round 0 decided; with h0 = 2 the last round finds none).
-int build_rounds(int64_t m, int first, int count, int global_path,
+// flags: SFX_SA_ROUNDS_RADIX enqueues the radix launches,
+// SFX_SA_ROUNDS_EXPECT_FINAL has the local launches read the state first.
+int build_rounds(int64_t m, int first, int count, int flags,
                  void* workspace, hipStream_t stream) {
   if (m <= 1) return 0;
   SaWs w;
   sa_ws_layout(m, workspace, &w);
   const int64_t nb = (m + kTile - 1) / kTile;
   const int last = total_rounds(m);
+  const int global_path = (flags & SFX_SA_ROUNDS_RADIX) ? 1 : 0;
+  const int expect_done = (flags & SFX_SA_ROUNDS_EXPECT_FINAL) ? 1 : 0;
   for (int r = first < 1 ? 1 : first; r < first + count && r <= last; ++r) {
-    const int rc = doubling_round(w, nb, m, r, global_path, stream);
+    const int rc =
+        doubling_round(w, nb, m, r, global_path, expect_done, stream);
     if (rc) return rc;
   }
   return (int)hipGetLastError();
@@ -1547,7 +1670,8 @@ extern "C" int sfx_sa_build(const int32_t* text, int64_t m, int64_t n_total,
   if (!ws_ok(m, workspace, workspace_bytes)) return SFX_EINVAL;
   int rc = build_begin(text, m, workspace, stream);
   if (rc) return rc;
-  rc = build_rounds(m, 1, total_rounds(m), 1, workspace, stream);
+  rc = build_rounds(m, 1, total_rounds(m), SFX_SA_ROUNDS_RADIX, workspace,
+                    stream);
   if (rc) return rc;
   return build_finish(m, n_total, sa_out, sa_is64, workspace, stream);
 }
@@ -1577,13 +1701,14 @@ extern "C" int sfx_sa_build_begin(const int32_t* text, int64_t m,
 }
 
 extern "C" int sfx_sa_build_rounds(int64_t m, int32_t first, int32_t count,
-                                   int32_t global_path, void* workspace,
+                                   int32_t flags, void* workspace,
                                    size_t workspace_bytes,
                                    hipStream_t stream) {
   if (m < 0 || m > 0x7fffffffLL || first < 1 || count < 0) return SFX_EINVAL;
   if (!ws_ok(m, workspace, workspace_bytes)) return SFX_EINVAL;
-  if (global_path != 0 && global_path != 1) return SFX_EINVAL;
-  return build_rounds(m, first, count, global_path, workspace, stream);
+  if (flags & ~(SFX_SA_ROUNDS_RADIX | SFX_SA_ROUNDS_EXPECT_FINAL))
+    return SFX_EINVAL;
+  return build_rounds(m, first, count, flags, workspace, stream);
 }
 
 extern "C" int sfx_sa_build_finish(int64_t m, int64_t n_total, void* sa_out,
@@ -1635,13 +1760,13 @@ extern "C" int sfx_delta_index_build(const int32_t* delta,
     hipLaunchKernelGGL(k_rs_hist<kRsThreads>, dim3((unsigned)nb),
                        dim3(kRsThreads), 0, stream, keys[x], sh, w.hist, nb,
                        w.state, 0);
-    hipLaunchKernelGGL(k_rs_rowscan<kRsThreads>, dim3(kRadix),
+    hipLaunchKernelGGL(k_rs_rowscan<kRsThreads>, dim3(kScanBlocks),
                        dim3(kRsThreads), 0, stream, w.hist, nb, w.rowsum,
                        w.state, 0);
     hipLaunchKernelGGL(k_rs_scatter<kRsThreads>, dim3((unsigned)nb),
                        dim3(kRsThreads), 0, stream, keys[x], vals[x],
                        keys[x ^ 1], vals[x ^ 1], sh, w.hist, nb, w.rowsum,
-                       w.state, 0);
+                       w.state, 0, nullptr);
     x ^= 1;
   }
   // two passes (keys of at most 18 bits): the sorted data is back in

@@ -188,9 +188,12 @@ class GlobalIndex:
         # margin), with the radix path enqueued for the rounds that took it
         # then; the rest only if the device reports the array is not final
         # yet, or is stalled at a round that needs the radix path (a pinned
-        # copy of the build's state block).
+        # copy of the build's state block).  The rounds past those the
+        # previous build needed (sa_final_hint on; 0: no build yet) are
+        # enqueued as expected to find the array final.
         self.sa_round_hint = 12
         self.sa_radix_hint = DEFAULT_RADIX_MASK
+        self.sa_final_hint = 0
         # (m, next_round) while rounds may remain; (m, None) once the suffix
         # array is final and its n-gram table is being built
         self._build_state = None
@@ -514,7 +517,7 @@ class GlobalIndex:
         check(L.sfx_sa_build_begin(dst.data_ptr(), m, ws.data_ptr(),
                                    ws.numel(), st), "SA rebuild")
         enqueue_rounds(m, 1, first, self.sa_radix_hint, ws.data_ptr(),
-                       ws.numel(), st)
+                       ws.numel(), st, self.sa_final_hint)
         self._copy_build_state(m)
         self._staged_build_finish(dst, m)
         # Kept even when every round was enqueued: the state copy then
@@ -558,6 +561,7 @@ class GlobalIndex:
         if state.done:
             self.sa_round_hint = state.needed + 2
             self.sa_radix_hint = state.radix_mask & ~1
+            self.sa_final_hint = state.needed + 1
             return True
         if state.stalled:
             nxt, radix = state.stalled, 1 << state.stalled
@@ -566,6 +570,7 @@ class GlobalIndex:
             # have raised the flag, so the array is final as it stands.
             self.sa_round_hint = total
             self.sa_radix_hint = state.radix_mask & ~1
+            self.sa_final_hint = 0
             return True
         else:
             radix = 0

@@ -11,7 +11,8 @@ from __future__ import annotations
 
 import torch
 
-from suffixgpu_amd._lib import check, lib, require_gpu, stream_of
+from suffixgpu_amd._lib import (SA_ROUNDS_EXPECT_FINAL, SA_ROUNDS_RADIX,
+                                check, lib, require_gpu, stream_of)
 
 
 def sa_workspace_bytes(n: int) -> int:
@@ -123,11 +124,14 @@ def build_suffix_array(tokens: torch.Tensor) -> torch.Tensor:
 
 def build_suffix_array_rounds(text: torch.Tensor, m: int, out: torch.Tensor,
                               workspace: torch.Tensor, rounds: int,
-                              radix_mask: int = DEFAULT_RADIX_MASK) -> None:
+                              radix_mask: int = DEFAULT_RADIX_MASK,
+                              final_from: int = 0) -> None:
     """The build with only its first ``rounds`` doubling rounds enqueued
     (then the output copy): the background rebuild's first chunk.  Rounds
-    whose bit is set in ``radix_mask`` enqueue the radix path too.  The
-    result is final iff :func:`build_state` says so afterwards."""
+    whose bit is set in ``radix_mask`` enqueue the radix path too; rounds
+    from ``final_from`` on (0: none) are enqueued as expected to find the
+    array final (see :func:`enqueue_rounds`).  The result is final iff
+    :func:`build_state` says so afterwards."""
     require_gpu(text, out, workspace)
     workspace = _workspace_ok(workspace, text, sa_workspace_bytes(m))
     L = lib()
@@ -135,26 +139,37 @@ def build_suffix_array_rounds(text: torch.Tensor, m: int, out: torch.Tensor,
     ws, nbytes = workspace.data_ptr(), workspace.numel()
     check(L.sfx_sa_build_begin(text.data_ptr(), m, ws, nbytes, st),
           "SA build")
-    enqueue_rounds(m, 1, max(0, rounds), radix_mask, ws, nbytes, st)
+    enqueue_rounds(m, 1, max(0, rounds), radix_mask, ws, nbytes, st,
+                   final_from)
     check(L.sfx_sa_build_finish(m, out.shape[0], out.data_ptr(),
                                 int(out.dtype == torch.int64), ws, nbytes,
                                 st), "SA build")
 
 
 def enqueue_rounds(m: int, first: int, count: int, radix_mask: int,
-                   ws: int, nbytes: int, stream) -> None:
+                   ws: int, nbytes: int, stream, final_from: int = 0) -> None:
     """Doubling rounds first .. first+count-1 on ``stream``: a round r with
     bit r of ``radix_mask`` set enqueues the radix path too, the others
     only the local launch (a round that needs the radix path then stalls
-    the build, see :class:`BuildState`)."""
+    the build, see :class:`BuildState`).  Rounds r >= ``final_from`` (when
+    it is positive) are flagged as expected to find the array final, as a
+    rebuild's margin rounds are: their launches check the build state
+    before reading their tiles.  The flag changes no result."""
     L = lib()
+
+    def flags(r: int) -> int:
+        f = SA_ROUNDS_RADIX if (radix_mask >> r) & 1 else 0
+        if 0 < final_from <= r:
+            f |= SA_ROUNDS_EXPECT_FINAL
+        return f
+
     r, end = first, first + count
     while r < end:
-        g = (radix_mask >> r) & 1
+        f = flags(r)
         r2 = r + 1
-        while r2 < end and ((radix_mask >> r2) & 1) == g:
+        while r2 < end and flags(r2) == f:
             r2 += 1
-        check(L.sfx_sa_build_rounds(m, r, r2 - r, g, ws, nbytes, stream),
+        check(L.sfx_sa_build_rounds(m, r, r2 - r, f, ws, nbytes, stream),
               "SA build")
         r = r2
 

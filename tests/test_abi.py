@@ -71,6 +71,9 @@ def test_abi_version_and_constants(so):
     so.sfx_sa_group_cap.restype = ctypes.c_int32
     assert so.sfx_sa_group_cap() == 2048  # the value the header documents
     assert _lib.NOALLOC_MAX_ROWS == header_define("SFX_NOALLOC_MAX_ROWS")
+    assert _lib.SA_ROUNDS_RADIX == header_define("SFX_SA_ROUNDS_RADIX")
+    assert (_lib.SA_ROUNDS_EXPECT_FINAL
+            == header_define("SFX_SA_ROUNDS_EXPECT_FINAL"))
 
 
 def test_workspace_sizes_are_host_only(so):
@@ -92,6 +95,11 @@ def test_argument_errors_are_reported_before_any_launch():
     # first4 must be 16-byte aligned (checked before any launch)
     assert lib.sfx_sa_keys(None, None, 16, 0, 32, None, 8, None) == -1
     assert lib.sfx_sa_build(None, -1, 0, None, 0, None, 0, None) == -1
+    # sfx_sa_build_rounds takes two flag bits; m = 1 needs no workspace,
+    # so only the flags can be wrong (a valid call enqueues nothing)
+    assert lib.sfx_sa_build_rounds(1, 1, 1, 4, None, 0, None) == -1
+    assert lib.sfx_sa_build_rounds(1, 1, 1, -1, None, 0, None) == -1
+    assert lib.sfx_sa_build_rounds(1, 1, 1, 3, None, 0, None) == 0
     assert lib.sfx_index_swap(None, None, None, None, -1, None, 0,
                               None) == -1
     assert lib.sfx_index_swap(None, None, None, None, 16, None, 0,

@@ -187,6 +187,33 @@ def test_build_suffix_array_stall_and_resume(gpu):
     np.testing.assert_array_equal(N(out), o_build_sa(t))
 
 
+@pytest.mark.parametrize("final_from", [1, 2, 4])
+def test_build_suffix_array_expect_final_flag(gpu, final_from):
+    """Rounds flagged as expected to find the array final (a rebuild's
+    margin rounds) give the same array whether the flag is right or wrong:
+    from round 1 every round is flagged, including the token pairs' radix
+    round and the rounds that still have groups to sort."""
+    from suffixgpu_amd.suffix_array import (build_suffix_array_rounds,
+                                            read_build_state,
+                                            sa_workspace_bytes)
+    rng = np.random.default_rng(11)
+    period = rng.integers(0, 5, size=37).astype(I32)
+    texts = [_planted_bigram_text(5000, 3),
+             np.concatenate([np.tile(period, 300),
+                             rng.integers(0, 5, size=900).astype(I32)])]
+    for t in texts:
+        m = t.shape[0]
+        ws = torch.empty(sa_workspace_bytes(m), dtype=torch.uint8,
+                         device=gpu)
+        out = torch.empty(m, dtype=torch.int32, device=gpu)
+        build_suffix_array_rounds(T(t, gpu), m, out, ws, 40,
+                                  radix_mask=(1 << 40) - 2,
+                                  final_from=final_from)
+        st = read_build_state(ws, m)
+        assert st.done and not st.stalled
+        np.testing.assert_array_equal(N(out), o_build_sa(t))
+
+
 def test_build_suffix_array_identity_tail(gpu):
     from suffixgpu_amd.suffix_array import build_suffix_array_into
     rng = np.random.default_rng(4)
