@@ -101,6 +101,77 @@ __device__ __forceinline__ void kary_narrow(uint32_t& lo, uint32_t& hi,
   hi = nhi;
 }
 
+// Key-row comparison of a group's G probes at once (G % 8 == 0, keys not
+// NULL).  Instruction i loads the rows of probes i * G/8 .. + G/8 - 1, one
+// 16-byte part per lane: lanes 8s .. 8s + 7 of the group read probe
+// i * G/8 + s's row, so each load instruction of the wave touches one
+// line per 8 lanes.  (With one row per lane it touched 64 lines, and the
+// CU's vector L1 serves the distinct lines of an instruction one after
+// another: the waves of a workgroup then queued behind each other, about
+// 0.4 us apart.)  Two ballots per instruction give every row's first
+// differing token and its sign; each lane keeps its own probe's result
+// (probe gl: instruction gl / (G/8), octet gl % (G/8)) and finishes it in
+// the corpus when the pattern is longer than the row and the row ties.
+// pc holds pattern tokens 4 * (gl % 8) .. + 3.  probe_of(q) is probe q's
+// rank.  Returns -1 / 0 / +1 for the lane's own probe.
+template <int G, class ProbeFn, class PatFn>
+__device__ __forceinline__ int cmp_probes_key(
+    const int32_t* __restrict__ keys, int kw,
+    const int32_t* __restrict__ sa, const int32_t* __restrict__ corpus,
+    int64_t n, ProbeFn probe_of, const int32_t (&pc)[4], PatFn pat_at,
+    int plen) {
+  constexpr int kParts = 8;             // 16-byte parts of a 128-byte row
+  constexpr int kRows = G / kParts;     // rows per load instruction
+  constexpr int kInstr = G / kRows;     // load instructions per round
+  static_assert(G % kParts == 0, "whole rows per group");
+  const int ln = lane_id();
+  const int gl = ln % G;
+  const int gbase = ln - gl;
+  const int part = gl % kParts;
+  const int sub = gl / kParts;
+  const int kn = plen < kw ? plen : kw;
+  const bool live = 4 * part < kn;
+  int4 v[kInstr];
+#pragma unroll
+  for (int i = 0; i < kInstr; ++i) {
+    v[i] = make_int4(0, 0, 0, 0);
+    if (live) {
+      const int64_t pr = probe_of(i * kRows + sub);
+      v[i] = reinterpret_cast<const int4*>(keys + pr * kw)[part];
+    }
+  }
+  int cv = 0;
+#pragma unroll
+  for (int i = 0; i < kInstr; ++i) {
+    const int32_t t4[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+    bool mis = false, neg = false;
+#pragma unroll
+    for (int j = 3; j >= 0; --j) {  // the lowest differing token wins
+      if (live && 4 * part + j < kn && t4[j] != pc[j]) {
+        mis = true;
+        neg = t4[j] < pc[j];
+      }
+    }
+    const uint64_t bm = ballot(mis);
+    const uint64_t bn = ballot(mis && neg);
+    const int ob = gbase + kParts * (gl % kRows);  // own probe's octet
+    const uint32_t seg = (uint32_t)(bm >> ob) & 0xffu;
+    const int lb = seg ? __builtin_ctz(seg) : 0;
+    const bool nb = (bn >> (ob + lb)) & 1ull;
+    const int r = seg == 0 ? 0 : (nb ? -1 : 1);
+    cv = i == gl / kRows ? r : cv;
+  }
+  if (cv != 0 || plen <= kw) return cv;
+  const int64_t pos = sa[probe_of(gl)];
+  for (int j = kw; j < plen; ++j) {
+    const int64_t idx = pos + j;
+    const int32_t t = idx < n ? corpus[idx] : -1;
+    const int32_t pj = pat_at(j);
+    if (t != pj) return t < pj ? -1 : 1;
+  }
+  return 0;
+}
+
 // Exact lower bound (first rank with cmp >= 0) and upper bound (first rank
 // with cmp > 0) of one pattern.  Called by all G lanes of an aligned group
 // with identical arguments; returns the bounds on every lane of the group.
@@ -125,10 +196,14 @@ __device__ __forceinline__ void kary_bounds(
   const int ln = lane_id();
   const int gl = ln % G;
   const int gbase = ln - gl;
-  int32_t pt[32];
+  constexpr bool kCoop = G % 8 == 0;  // rows read by lane octets
+  int32_t pt[kCoop ? 4 : 32];
   if (keys) {
+    // cooperative: pattern tokens 4 * (gl % 8) .. + 3; else all of them
+    const int j0 = kCoop ? 4 * (gl % 8) : 0;
 #pragma unroll
-    for (int j = 0; j < 32; ++j) pt[j] = j < plen ? pat_at(j) : 0;
+    for (int j = 0; j < (kCoop ? 4 : 32); ++j)
+      pt[j] = j0 + j < plen ? pat_at(j0 + j) : 0;
   }
   uint32_t lo1 = r0, hi1 = r1, lo2 = r0, hi2 = r1;
   while (lo1 < hi1 || lo2 < hi2) {
@@ -137,17 +212,26 @@ __device__ __forceinline__ void kary_bounds(
     const bool only2 = !shared && lo1 == hi1;
     const bool split = !shared && !only1 && !only2;
     // G probes over the one live range, or G/2 per bound once they split
-    const bool upper_half = split && gl >= H;
-    const bool use2 = only2 || upper_half;
     const uint32_t c = split ? cH : cG;
     const int np = split ? H : G;
-    const int k = upper_half ? gl - H : gl;
-    const int64_t probe = (int64_t)kary_at(use2 ? lo2 : lo1, use2 ? hi2 : hi1,
-                                           (uint32_t)(k + 1) * c);
-    const int cv =
-        keys ? cmp_suffix_key(keys, kw, sa, corpus, n, probe, pt, pat_at,
-                              plen)
-             : cmp_suffix(sa, corpus, n, probe, pat_at, plen);
+    // probe q of the group (lane q's own probe)
+    auto probe_of = [&](int q) -> int64_t {
+      const bool uh = split && q >= H;
+      const bool u2 = only2 || uh;
+      const int kq = uh ? q - H : q;
+      return (int64_t)kary_at(u2 ? lo2 : lo1, u2 ? hi2 : hi1,
+                              (uint32_t)(kq + 1) * c);
+    };
+    int cv;
+    if constexpr (kCoop) {
+      cv = keys ? cmp_probes_key<G>(keys, kw, sa, corpus, n, probe_of, pt,
+                                    pat_at, plen)
+                : cmp_suffix(sa, corpus, n, probe_of(gl), pat_at, plen);
+    } else {
+      cv = keys ? cmp_suffix_key(keys, kw, sa, corpus, n, probe_of(gl), pt,
+                                 pat_at, plen)
+                : cmp_suffix(sa, corpus, n, probe_of(gl), pat_at, plen);
+    }
     const uint64_t m1 = ballot(cv >= 0);
     const uint64_t m2 = ballot(cv > 0);
     const uint32_t full = G == 32 ? 0xffffffffu : ((1u << G) - 1u);
