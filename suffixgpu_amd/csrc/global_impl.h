@@ -897,10 +897,10 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
     // Early gathers (decode step).  With one length per search group,
     // wave 0's groups search lengths 1 .. 4, which the n-gram table
     // answers with one lookup, and wave 0 then waits for the longest
-    // searches.  Meanwhile it gathers the continuation blocks of the caps
+    // searches.  Meanwhile it gathers the continuation block of one cap
     // whose candidate it already knows (cap <= the table's longest run
-    // length) into the LDS areas of the waves that will expand them: wave
-    // c for the run of equal candidate lengths that cap c heads.  A cap
+    // length) into the LDS area of the wave that will expand it: wave c
+    // for the run of equal candidate lengths that cap c heads.  A cap
     // whose run head it cannot know yet (the cap before lies beyond the
     // table) is gathered as if it were one; pre[c] is the length gathered
     // for cap c, -1 for none.
@@ -909,7 +909,12 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
     const bool early = kEarly && a.step && gram && ngroups >= P;
     if (early && wv == 0) {
       wave_lds_sync();  // this wave's groups wrote lengths 1 .. 4
+      // One gather: the smallest cap's (its short candidate has the most
+      // distinct continuations, the longest expansion).  A second one
+      // held the block barrier past the longest searches (two gathers of
+      // about 3.8 us each from 3.6 us, searches ending at 7.5-9.3 us).
       int prev = -1;  // candidate length of cap c - 1, if known
+      int gc = -1, glen = 0;  // the cap to gather and its candidate length
       for (int c = 0; c < C; ++c) {
         const int cap = p.caps[c];
         int best = -1;
@@ -920,17 +925,20 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
           const uint64_t m = ballot(f);
           best = m ? 64 - __builtin_clzll(m) : 0;
         }
-        int got = -1;
         if (best > 0 && c < nmw && best != prev) {
-          const int64_t s0 = lbs[best - 1];
-          const int64_t ilen = ubs[best - 1] - s0;
-          gather_expand(a, L, smem, b, c, 1, best, (int)(ilen < R ? ilen : R),
-                        s0, ilen, nullptr, nullptr, false, nullptr, nullptr, c,
-                        false);
-          got = best;
+          gc = c;
+          glen = best;
         }
-        if (ln == 0) pre[c] = got;
+        if (ln == 0) pre[c] = -1;
         prev = best;
+      }
+      if (gc >= 0) {
+        const int64_t s0 = lbs[glen - 1];
+        const int64_t ilen = ubs[glen - 1] - s0;
+        gather_expand(a, L, smem, b, gc, 1, glen,
+                      (int)(ilen < R ? ilen : R), s0, ilen, nullptr, nullptr,
+                      false, nullptr, nullptr, gc, false);
+        if (ln == 0) pre[gc] = glen;
       }
     }
     __syncthreads();
