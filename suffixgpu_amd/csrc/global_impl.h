@@ -988,7 +988,7 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
                     a.ws.sa_nv, a.ws.sa_score, a.ws.sa_chain, nullptr,
                     early ? pre : nullptr);
       SFX_TRACE_POINT(4);
-      if (block_arrive(a.ws.pick + b, 3u, misc + 1))
+      if (block_arrive<false>(a.ws.pick + b, 3u, misc + 1))
         final_pick(p, a.ws, b, a.draft, a.num_valid, misc + 4);
       return;
     }
@@ -1055,7 +1055,7 @@ __device__ __forceinline__ void global_body(const GlobalArgs& a,
       source_expand(a, L, smem, b, 2, dlen, dcnt, nullptr, dpc, a.ws.dn_nv,
                     a.ws.dn_score, a.ws.dn_chain, need);
       SFX_TRACE_POINT(6);
-      if (block_arrive(a.ws.pick + b, 3u, misc + 2))
+      if (block_arrive<false>(a.ws.pick + b, 3u, misc + 2))
         final_pick(p, a.ws, b, a.draft, a.num_valid, misc + 4);
       return;
     }

@@ -542,7 +542,7 @@ __device__ __forceinline__ void local_body(const LocalArgs& a,
     ws_store(a.ws.l_emit + b, emit);
     ws_store(a.ws.l_score + b, res_score[best]);
   }
-  if (block_arrive(a.ws.pick + b, 3u, misc + 2))
+  if (block_arrive<false>(a.ws.pick + b, 3u, misc + 2))
     final_pick(p, a.ws, b, a.draft, a.num_valid, misc + 4);
 }
 

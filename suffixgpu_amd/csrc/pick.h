@@ -30,16 +30,17 @@ __device__ __forceinline__ void final_pick(const sfx_params& p,
     const int64_t i = (int64_t)b * C + (on ? c : 0);
     int sl = 0, dl = 0, snv = 0, dnv = 0;
     float ssc = 0.0f, dsc = 0.0f;
+    // (ws_load: the handover into this pick does not invalidate caches)
     if (on) {
-      sl = ws.sa_len[i];
-      dl = ws.dl_c[i];
-      ssc = ws.sa_score[i];
-      dsc = ws.dn_score[i];
-      snv = ws.sa_nv[i];
-      dnv = ws.dn_nv[i];
+      sl = ws_load(ws.sa_len + i);
+      dl = ws_load(ws.dl_c + i);
+      ssc = ws_load(ws.sa_score + i);
+      dsc = ws_load(ws.dn_score + i);
+      snv = ws_load(ws.sa_nv + i);
+      dnv = ws_load(ws.dn_nv + i);
     }
-    const float lscore = ws.l_score[b];
-    const int lemit = ws.l_emit[b];
+    const float lscore = ws_load(ws.l_score + b);
+    const int lemit = ws_load(ws.l_emit + b);
     // the SA lengths published for the delta workgroups: every producer
     // has arrived, so none reads them again this step
     if (on) ws.sa_known[(int64_t)b * SFX_MAX_CANDIDATES + c] = 0;
@@ -84,7 +85,7 @@ __device__ __forceinline__ void final_pick(const sfx_params& p,
                          : which == 1 ? ws.sa_chain + i * K
                                       : ws.dn_chain + i * K;
   for (int j = threadIdx.x; j < K; j += blockDim.x)
-    draft[(int64_t)b * K + j] = j < nv ? chain[j] : -1;
+    draft[(int64_t)b * K + j] = j < nv ? ws_load(chain + j) : -1;
   if (threadIdx.x == 0) num_valid[b] = nv;
   SFX_TRACE_POINT(14);
 }

@@ -149,6 +149,19 @@ __device__ __forceinline__ void ws_store(float* p, float v) {
   __hip_atomic_store(reinterpret_cast<uint32_t*>(p), __float_as_uint(v),
                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// The matching reads after a handover without the acquire's cache
+// invalidation (block_arrive<false>): agent-scope relaxed atomic loads,
+// which read the coherent copy that the writers' stores and release
+// reached, not a line a cache of this XCD may still hold.
+__device__ __forceinline__ int32_t ws_load(const int32_t* p) {
+  return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ws_load(const float* p) {
+  return __uint_as_float(__hip_atomic_load(
+      reinterpret_cast<uint32_t*>(const_cast<float*>(p)), __ATOMIC_RELAXED,
+      __HIP_MEMORY_SCOPE_AGENT));
+}
 
 // ------------------------------------------------------------ fp32 rules
 // The chain probability and scores follow torch's fp32 CPU arithmetic:
@@ -843,6 +856,10 @@ __device__ __forceinline__ void compact_first_r(MbPtr mb, int64_t n,
 // release writes that L2 back before the counter update, and only the last
 // arriver's thread 0 invalidates (its CU's L1 and XCD's L2) before the
 // barrier that lets the block read the other workgroups' results.
+// kAcquire false: no invalidation; the last arriver then reads the other
+// workgroups' results only with ws_load (every such load is issued after
+// the counter update has returned, behind the barrier).
+template <bool kAcquire = true>
 __device__ __forceinline__ bool block_arrive(unsigned* ctr,
                                              unsigned expected,
                                              int* lds_flag) {
@@ -853,7 +870,7 @@ __device__ __forceinline__ bool block_arrive(unsigned* ctr,
     const int last = old == expected - 1;
     if (last) {
       atomicExch(ctr, 0u);
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      if (kAcquire) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     *lds_flag = last;
   }
