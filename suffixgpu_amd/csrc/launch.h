@@ -63,6 +63,9 @@ constexpr int kMinStreamChunk = 1024;
 // Two workgroups of a kernel share a CU when each takes at most this much
 // LDS (the step kernels' register use allows two 512-thread groups per CU).
 constexpr size_t kHalfLds = kMaxLds / 2;
+// Three share a CU at this much LDS each (256-byte aligned): the step
+// kernels stay at or below 80 VGPRs, 6 waves per SIMD.
+constexpr size_t kThirdLds = (kMaxLds / 3) & ~size_t(255);
 
 int check_local(const sfx_params& p, const sfx_batch& bt);
 // Local layout within `cap` bytes of LDS for `nthreads` per row: 0 = whole

@@ -116,17 +116,20 @@ int launch_step(const sfx_params* p, const sfx_index* ix, const sfx_batch* bt,
   const unsigned blocks =
       (unsigned)(bt->batch * (global_on ? 2 + dparts : 1));
   // A grid larger than the CU count runs in waves of workgroups; when every
-  // role fits half a CU's LDS, two groups share each CU and the waves halve.
-  // Otherwise each role takes the LDS layout that suits it best.
+  // role fits half a CU's LDS, two groups share each CU and the waves halve,
+  // and past twice the CU count, a third: three groups per CU.  Otherwise
+  // each role takes the LDS layout that suits it best.
   size_t cap = kMaxLds;
-  if (blocks > (unsigned)device_cus()) {
+  auto fits = [&](size_t c) {
     size_t glds = 0;
-    const bool fits =
-        local_chunk(*p, bt->seq, kHalfLds) >= 0 &&
-        (!global_on ||
-         merge_waves_for(*p, *ix, dparts, &glds, kHalfLds) > 0);
-    if (fits) cap = kHalfLds;
-  }
+    return local_chunk(*p, bt->seq, c) >= 0 &&
+           (!global_on || merge_waves_for(*p, *ix, dparts, &glds, c) > 0);
+  };
+  const unsigned cus = (unsigned)device_cus();
+  if (blocks > 2 * cus && fits(kThirdLds))
+    cap = kThirdLds;
+  else if (blocks > cus && fits(kHalfLds))
+    cap = kHalfLds;
   a.l.chunk = local_chunk(*p, bt->seq, cap, kLocalThreadsDefault,
                           &a.l.mb_full);
   size_t lds = local_lds_bytes(*p, bt->seq, a.l.chunk, kLocalThreadsDefault,
