@@ -4,7 +4,9 @@ resource report (hipcc cross-compiles for gfx950 without a GPU).
 Two 512-thread workgroups of the fused step share a CU only while it needs
 at most 128 VGPRs (4 waves per SIMD); spilling to scratch would put every
 step on the slow path.  Both happened once by accident, so they are
-checked here."""
+checked here.  The fused step kernel's launches past twice the CU count
+size every role for three workgroups per CU, which needs at most 80 VGPRs
+(6 waves per SIMD)."""
 
 from __future__ import annotations
 
@@ -53,6 +55,8 @@ def test_step_kernels_fit_two_workgroups_per_cu(src, kernel, tmp_path):
         assert r["ScratchSize"] == 0, (name, r)
         assert r["VGPRs"] <= 128, (name, r)
         assert r["Occupancy"] >= 4, (name, r)
+        if kernel == "k_step":
+            assert r["VGPRs"] <= 80 and r["Occupancy"] >= 6, (name, r)
 
 
 @pytest.mark.skipif(shutil.which(HIPCC) is None and
