@@ -95,6 +95,39 @@ def test_global_step_vs_oracle(gpu):
     np.testing.assert_array_equal(N(new), enew)
 
 
+def test_global_step_patterns_past_key_rows_vs_oracle(gpu):
+    """Patterns of up to 48 tokens against 32-token key rows: a search
+    probe whose row ties with the pattern finishes the comparison in the
+    corpus.  The template corpus has matches longer than the rows."""
+    from oracle.sa import suffix_match_backoff
+    p = 48
+    w, d, o = _global_pair(gpu, seed=5, max_pattern_len=p, num_backoff=5)
+    bt = w.batch
+    gi = o.global_index
+    # the SA match lengths of the rows' tails, as the step will see them
+    # after the update: some pass the key rows' 32 tokens
+    q = np.zeros((bt.tokens.shape[0], p), dtype=np.int32)
+    ql = np.zeros(bt.tokens.shape[0], dtype=np.int64)
+    for i in range(bt.tokens.shape[0]):
+        acc = int((bt.sampled[i] != -1).sum())
+        ctx = np.concatenate([bt.tokens[i, :bt.num_tokens[i]],
+                              bt.sampled[i, :acc]])
+        n = min(len(ctx), p)
+        q[i, :n] = ctx[len(ctx) - n:]
+        ql[i] = n
+    sa_len, _, _ = suffix_match_backoff(gi.sa, gi.corpus, q, ql, p,
+                                        np.array([p], dtype=np.int64))
+    assert (sa_len[:, 0] > 32).sum() >= 4, sa_len[:, 0]
+    tg = T(bt.tokens, gpu)
+    draft, nv, new = d.propose_with_update(T(bt.num_tokens, gpu), tg,
+                                           T(bt.sampled, gpu))
+    to = bt.tokens.copy()
+    ed, env, enew = o.propose_with_update(bt.num_tokens, to, bt.sampled)
+    np.testing.assert_array_equal(N(new), enew)
+    np.testing.assert_array_equal(N(draft), ed)
+    np.testing.assert_array_equal(N(nv), env)
+
+
 def test_serial_equals_parallel_paths(gpu):
     w, d, o = _global_pair(gpu)
     d2, _, _ = None, None, None
