@@ -90,6 +90,20 @@ def test_build_suffix_array(gpu, n, vocab):
     np.testing.assert_array_equal(N(got), o_build_sa(t))
 
 
+@pytest.mark.parametrize("n", [5000, 70000])
+def test_build_suffix_array_wide_tokens(gpu, n):
+    """Tokens spanning 2^31 values (no pair keys: the token round keys
+    each position by its own token, signed order), over several radix
+    tiles, with runs that need several doubling rounds."""
+    from suffixgpu_amd.suffix_array import build_suffix_array
+    rng = np.random.default_rng(n)
+    vals = np.array([-2 ** 31, -5, 0, 7, 2 ** 30, 2 ** 31 - 2], np.int64)
+    t = vals[rng.integers(0, len(vals), size=n)].astype(I32)
+    t[n // 3:n // 3 + 900] = np.tile(t[:30], 30)  # a long repeat
+    got = build_suffix_array(T(t, gpu))
+    np.testing.assert_array_equal(N(got), o_build_sa(t))
+
+
 def test_build_suffix_array_structured(gpu):
     from suffixgpu_amd.suffix_array import build_suffix_array
     for toks in ([1, 2, 3, 1, 2, 3, 1, 2], [5] * 5000, [0],
